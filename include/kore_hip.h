@@ -1,0 +1,150 @@
+/*
+ * kore_hip.h -- C ABI of libkore_hip.so: KORE's fused layer ops as
+ * hand-written gfx950 (MI355X) HIP kernels.
+ *
+ * Contract shared by every entry point:
+ *   - All tensors are row-major, contiguous, little-endian, resident in device
+ *     memory (hipMalloc or any allocator that hands out device pointers).  The
+ *     caller owns every buffer: no entry point allocates, frees or copies
+ *     between host and device, so nothing hidden lands in a timed region.
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Work is only
+ *     enqueued; nothing synchronises.  The caller syncs before reading results.
+ *   - Return value: 0 on success; a negative KORE_HIP_ERR_* code for a bad
+ *     argument (checked on the host before anything is launched); a positive
+ *     hipError_t value when the launch itself fails.  No entry point aborts.
+ *   - A call with zero elements of work returns 0 and launches nothing, as the
+ *     reference CPU ops return empty tensors.
+ *   - Pointers that are not 16-byte aligned, or rows whose length is not a
+ *     multiple of 4 floats, take a scalar path with identical results.
+ *   - Entry points are reentrant and keep no state between calls.
+ *
+ * Each declaration names the reference function it replaces (paths relative
+ * to the KidIkaros/KORE tree) and what its results match: "bit-exact" means
+ * byte-identical to the reference CPU function on the same input; "f32 tol"
+ * means |gpu - ref| <= 1e-6 or <= 1e-5 * |ref| per element.
+ */
+#ifndef KORE_HIP_H
+#define KORE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *kore_stream_t; /* hipStream_t */
+
+#define KORE_HIP_OK 0
+#define KORE_HIP_ERR_NULL_PTR (-1)  /* a required pointer is NULL        */
+#define KORE_HIP_ERR_BAD_DIM (-2)   /* a dimension is invalid (odd head_dim, cols == 0 with rows > 0, ...) */
+#define KORE_HIP_ERR_OVERFLOW (-3)  /* an element count overflows 64-bit or exceeds the kernel's index range */
+#define KORE_HIP_ERR_ALIAS (-4)     /* input/output overlap the op does not allow */
+
+/* Library version as 10000*major + 100*minor + patch. */
+int kore_hip_version(void);
+
+/* Static text for a status code (never NULL). */
+const char *kore_hip_status_string(int status);
+
+/* ---------------------------------------------------------------- RMSNorm
+ * out[r, :] = (x[r, :] * inv_rms_r) * weight[:],
+ * inv_rms_r = 1 / sqrt((sum_i x[r,i]^2 summed left to right) / cols + eps).
+ * Replaces cuda_rms_norm_f32 (crates/kore-kernels/src/cuda/ops.rs:517-541)
+ * and is the device twin of kore_kernels::cpu_fused::fused_rms_norm
+ * (crates/kore-kernels/src/cpu_fused.rs:160-190).  Bit-exact: the row sum
+ * keeps the reference's sequential f32 order.  out may equal x. */
+int kore_hip_rms_norm_f32(const float *x, const float *weight, float *out,
+                          uint64_t rows, uint64_t cols, float eps,
+                          kore_stream_t stream);
+
+/* ------------------------------------------------------------ activations
+ * out[i] = gelu_tanh(x[i]).  Replaces cuda_gelu_f32
+ * (crates/kore-kernels/src/cuda/ops.rs:197-204); twin of
+ * kore_nn::activations::gelu (crates/kore-nn/src/activations.rs:14-32).
+ * f32 tol.  out may equal x. */
+int kore_hip_gelu_f32(const float *x, float *out, uint64_t n,
+                      kore_stream_t stream);
+
+/* out[i] = x[i] / (1 + exp(-x[i])).  Replaces cuda_silu_f32
+ * (crates/kore-kernels/src/cuda/ops.rs:206-213); twin of
+ * kore_nn::activations::silu (crates/kore-nn/src/activations.rs:35-45).
+ * f32 tol.  out may equal x. */
+int kore_hip_silu_f32(const float *x, float *out, uint64_t n,
+                      kore_stream_t stream);
+
+/* out[i] = a[i] * b[i].  Replaces cuda_mul_f32
+ * (crates/kore-kernels/src/cuda/ops.rs:100-108); twin of Tensor::mul's
+ * same-shape path (crates/kore-core/src/ops/arithmetic.rs:482-509).
+ * Bit-exact.  out may equal a or b. */
+int kore_hip_mul_f32(const float *a, const float *b, float *out, uint64_t n,
+                     kore_stream_t stream);
+
+/* out[i] = silu(gate[i]) * up[i] in one HBM pass.  Replaces the reference's
+ * two-op composition silu(gate) then mul(up)
+ * (crates/kore-serve/src/layered/engine.rs:633-643,
+ *  crates/kore-edge/src/runtime.rs:253-255).  f32 tol.  out may equal gate
+ * or up. */
+int kore_hip_swiglu_f32(const float *gate, const float *up, float *out,
+                        uint64_t n, kore_stream_t stream);
+
+/* ------------------------------------------------------------------- RoPE
+ * Host helper (no device work): inv_freq[i] = 1 / base^((2i)/head_dim) for
+ * i < head_dim/2, written to HOST memory.  The caller uploads it once per
+ * (head_dim, base).  Same expression as precompute_rope_inv_freq
+ * (crates/kore-serve/src/layered/engine.rs:694-700) and the per-element freq
+ * of kore_edge::ops::rope::apply_rope (crates/kore-edge/src/ops/rope.rs:24);
+ * it plays the role of cuda_rope_freqs_f32
+ * (crates/kore-kernels/src/cuda/ops.rs:549-567). */
+int kore_hip_rope_inv_freq_f32(float *inv_freq_host, uint32_t head_dim,
+                               float base);
+
+/* In-place rotary embedding of data[batch, seq_len, num_heads, head_dim] at
+ * positions start_pos + s (the same for every batch entry).
+ * interleaved = 0: pairs (i, i + head_dim/2), as kore_edge apply_rope
+ *   (crates/kore-edge/src/ops/rope.rs:9-36) and the CUDA rope_f32 kernel
+ *   (crates/kore-kernels/src/cuda/kernels/rope.cu:36-37);
+ * interleaved = 1: pairs (2i, 2i+1), as kore-serve's apply_rope
+ *   (crates/kore-serve/src/layered/engine.rs:706-727).
+ * inv_freq: device buffer from kore_hip_rope_inv_freq_f32.  Replaces
+ * cuda_rope_f32 (crates/kore-kernels/src/cuda/ops.rs:572-599).  f32 tol. */
+int kore_hip_rope_f32(float *data, const float *inv_freq, uint64_t batch,
+                      uint64_t seq_len, uint32_t num_heads, uint32_t head_dim,
+                      uint64_t start_pos, int interleaved,
+                      kore_stream_t stream);
+
+/* Q and K of one attention layer (GQA: q_heads != k_heads allowed) rotated in
+ * one launch; identical results to two kore_hip_rope_f32 calls. */
+int kore_hip_rope_qk_f32(float *q, float *k, const float *inv_freq,
+                         uint64_t batch, uint64_t seq_len, uint32_t q_heads,
+                         uint32_t k_heads, uint32_t head_dim,
+                         uint64_t start_pos, int interleaved,
+                         kore_stream_t stream);
+
+/* -------------------------------------------------------------- Embedding
+ * out[t, :] = table[ids[t], :] if ids[t] < vocab, else zeros.  ids are read
+ * as unsigned 32-bit (an int32 buffer is accepted as-is; negative ids are
+ * out of range).  Twin of kore_nn::Embedding::lookup
+ * (crates/kore-nn/src/embedding.rs:55-72) and kore_edge embedding_lookup
+ * (crates/kore-edge/src/ops/embedding.rs:8-27).  Bit-exact. */
+int kore_hip_embedding_f32(const float *table, const uint32_t *ids,
+                           float *out, uint64_t n_ids, uint64_t vocab,
+                           uint64_t dim, kore_stream_t stream);
+
+/* ----------------------------------------------------- BitLinear pre-quant
+ * Per row r: xn = RMSNorm(x[r,:]) exactly as kore_hip_rms_norm_f32;
+ * amax = max_i |xn_i| (1.0 if amax < 1e-8); scale[r] = amax / 127;
+ * q[r,i] = clamp(round_half_away((xn_i * 127) / amax), -128, 127) (NaN -> 0).
+ * The reference has no such op (BitLinear::forward,
+ * crates/kore-nn/src/bit_linear.rs:175-237, feeds f32 activations to the
+ * ternary GEMM); it composes fused_rms_norm (cpu_fused.rs:160-190) with the
+ * absmax convention of kore_btes::quantize (crates/kore-btes/src/quantize.rs:8-10).
+ * One HBM pass.  Bit-exact codes and scales. */
+int kore_hip_rms_norm_quant_i8(const float *x, const float *weight,
+                               int8_t *q, float *scale, uint64_t rows,
+                               uint64_t cols, float eps, kore_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KORE_HIP_H */

@@ -1,0 +1,54 @@
+// common.hpp -- shared device helpers for the gfx950 fused layer kernels.
+//
+// Everything here is written for CDNA4 (gfx950): wave64, 128-bit vector
+// memory operations, LDS, DPP/ds_swizzle cross-lane moves.  No MFMA is used
+// anywhere in this library: every op is bound by HBM bandwidth.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kore {
+
+// Native 128-bit vector types (clang ext_vector_type maps 1:1 onto a
+// global_load_dwordx4 / global_store_dwordx4 operand).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Streaming loads/stores: data touched once.  The nontemporal hint keeps
+// the 2+ GB element-wise streams from evicting reusable lines in L2/MALL.
+__device__ __forceinline__ f32x4 ld_stream(const f32x4* p) {
+    return __builtin_nontemporal_load(p);
+}
+__device__ __forceinline__ void st_stream(f32x4* p, f32x4 v) {
+    __builtin_nontemporal_store(v, p);
+}
+__device__ __forceinline__ f32x4 ld_cached(const f32x4* p) { return *p; }
+
+// Exact wave-wide max.  max is order-free, so any reduction tree gives the
+// same bits; NaN operands are dropped like Rust's f32::max.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Read lane `src`'s value of v into every lane (v_readlane -> SGPR).
+__device__ __forceinline__ float read_lane(float v, int src) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace kore

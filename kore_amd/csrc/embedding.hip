@@ -1,0 +1,82 @@
+// embedding.hip -- token-embedding gather  out[t, :] = table[ids[t], :].
+//
+// Roofline: HBM.  Bytes per token: dim*4 read + dim*4 written + 4 for the id.
+// A pure copy, so results are bit-exact by construction; out-of-range ids
+// (ids[t] >= vocab, ids read as uint32) produce a zero row, as
+// crates/kore-nn/src/embedding.rs:63-68 and
+// crates/kore-edge/src/ops/embedding.rs:18-25 do.
+//
+// Vector path: one workgroup per kEmbTokens tokens; each wave copies whole
+// rows with global_load_dwordx4 / global_store_dwordx4, all of a thread's
+// loads issued before its first store.  Table reads use the default cache
+// policy (repeated ids hit L2/MALL); output stores are nontemporal.
+#include "common.hpp"
+#include "kore_hip_internal.hpp"
+
+namespace kore {
+
+constexpr int kEmbBlock = 256;
+constexpr int kEmbUnroll = 4;  // float4 per thread per pass
+
+__global__ __launch_bounds__(kEmbBlock) void embedding_vec_kernel(const f32x4* __restrict__ table,
+                                                                  const uint32_t* __restrict__ ids,
+                                                                  f32x4* __restrict__ out, uint64_t vocab,
+                                                                  uint64_t dim4) {
+    const uint64_t t = blockIdx.x;
+    const uint32_t id = ids[t];
+    f32x4* dst = out + t * dim4;
+    if ((uint64_t)id >= vocab) {
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        for (uint64_t i = threadIdx.x; i < dim4; i += kEmbBlock) st_stream(dst + i, z);
+        return;
+    }
+    const f32x4* src = table + (uint64_t)id * dim4;
+    uint64_t i = threadIdx.x;
+    for (; i + (kEmbUnroll - 1) * kEmbBlock < dim4; i += kEmbUnroll * kEmbBlock) {
+        f32x4 v[kEmbUnroll];
+#pragma unroll
+        for (int u = 0; u < kEmbUnroll; ++u) v[u] = ld_cached(src + i + u * kEmbBlock);
+#pragma unroll
+        for (int u = 0; u < kEmbUnroll; ++u) st_stream(dst + i + u * kEmbBlock, v[u]);
+    }
+    for (; i < dim4; i += kEmbBlock) st_stream(dst + i, ld_cached(src + i));
+}
+
+// Scalar path: dim % 4 != 0 or unaligned table/out.
+__global__ __launch_bounds__(kEmbBlock) void embedding_scalar_kernel(const float* __restrict__ table,
+                                                                     const uint32_t* __restrict__ ids,
+                                                                     float* __restrict__ out, uint64_t vocab,
+                                                                     uint64_t dim) {
+    const uint64_t t = blockIdx.x;
+    const uint32_t id = ids[t];
+    float* dst = out + t * dim;
+    if ((uint64_t)id >= vocab) {
+        for (uint64_t i = threadIdx.x; i < dim; i += kEmbBlock) dst[i] = 0.0f;
+        return;
+    }
+    const float* src = table + (uint64_t)id * dim;
+    for (uint64_t i = threadIdx.x; i < dim; i += kEmbBlock) dst[i] = src[i];
+}
+
+}  // namespace kore
+
+using namespace kore;
+
+extern "C" int kore_hip_embedding_f32(const float* table, const uint32_t* ids, float* out, uint64_t n_ids,
+                                      uint64_t vocab, uint64_t dim, kore_stream_t stream) {
+    if (n_ids == 0 || dim == 0) return KORE_HIP_OK;
+    if (!ids || !out || (vocab && !table)) return KORE_HIP_ERR_NULL_PTR;
+    uint64_t out_elems, table_elems;
+    if (!mul_ok(n_ids, dim, &out_elems) || !mul_ok(vocab, dim, &table_elems) || out_elems > kMaxElements ||
+        table_elems > kMaxElements || n_ids > 0x7fffffffull)
+        return KORE_HIP_ERR_OVERFLOW;
+    hipStream_t s = (hipStream_t)stream;
+    dim3 grid((uint32_t)n_ids), block(kEmbBlock);
+    if (dim % 4 == 0 && aligned16(out) && (vocab == 0 || aligned16(table))) {
+        hipLaunchKernelGGL(embedding_vec_kernel, grid, block, 0, s, reinterpret_cast<const f32x4*>(table), ids,
+                           reinterpret_cast<f32x4*>(out), vocab, dim / 4);
+    } else {
+        hipLaunchKernelGGL(embedding_scalar_kernel, grid, block, 0, s, table, ids, out, vocab, dim);
+    }
+    return launch_status();
+}

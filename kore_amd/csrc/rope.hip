@@ -1,0 +1,197 @@
+// rope.hip -- in-place rotary position embedding over [batch, seq, heads, D].
+//
+// Roofline: HBM.  Bytes per token (b, s): 2 * heads * D * 4 (read + write,
+// in place); the inv_freq table (D/2 floats) stays in L2.
+//
+// One workgroup per token.  Its first D/2 threads compute the token's
+// (cos, sin) pairs once into LDS: angle = (start_pos + s) * inv_freq[i] is
+// the reference's f32 product (crates/kore-edge/src/ops/rope.rs:22-26 /
+// crates/kore-serve/src/layered/engine.rs:716-719) and sincosf is ocml's
+// accurate version with full range reduction (angles reach ~2047 rad), never
+// the __sinf fast path.  Every head of Q and K then reuses those pairs, so the
+// transcendental cost is D/2 per token instead of heads*D/2.
+//
+// Half-split layout (pairs i, i+D/2): a task is a float4 at i and its partner
+// float4 at i+D/2 -> D/8 tasks per head.  Interleaved (pairs 2p, 2p+1): a task
+// is one float4 holding two pairs -> D/4 tasks per head.  Consecutive threads
+// take consecutive tasks, so each wave-wide access is 16 contiguous 16-byte
+// words per head segment.
+//
+// The rotation is the reference's: d[i] = x0*c - x1*s, d[j] = x0*s + x1*c,
+// with every product rounded on its own (-ffp-contract=off).
+#include "common.hpp"
+#include "kore_hip_internal.hpp"
+
+namespace kore {
+
+constexpr int kRopeBlock = 128;
+constexpr uint32_t kRopeMaxHeadDim = 4096;
+
+struct RopeTensor {
+    float* data;     // [batch*seq, heads, D]
+    uint32_t heads;
+};
+
+__device__ __forceinline__ float2 rot(float x0, float x1, float c, float s) {
+    float a0 = x0 * c, b0 = x1 * s;
+    float a1 = x0 * s, b1 = x1 * c;
+    return make_float2(a0 - b0, a1 + b1);
+}
+
+// Vector path: D % 8 == 0 and both tensors 16-byte aligned.
+template <bool Interleaved>
+__global__ __launch_bounds__(kRopeBlock) void rope_vec_kernel(RopeTensor t0, RopeTensor t1,
+                                                              const float* __restrict__ inv_freq,
+                                                              uint64_t seq_len, uint32_t head_dim,
+                                                              uint64_t start_pos) {
+    extern __shared__ f32x4 cs_raw[];  // [D/2] (cos, sin), 16-byte aligned base
+    float2* cs = reinterpret_cast<float2*>(cs_raw);
+    const uint64_t token = blockIdx.x;
+    const uint32_t half = head_dim >> 1;
+    const float pos = (float)(start_pos + token % seq_len);
+    for (uint32_t i = threadIdx.x; i < half; i += kRopeBlock) {
+        float angle = pos * inv_freq[i];
+        float s, c;
+        sincosf(angle, &s, &c);
+        cs[i] = make_float2(c, s);
+    }
+    __syncthreads();
+
+    const uint32_t tasks_per_head = Interleaved ? (head_dim >> 2) : (head_dim >> 3);
+    const uint32_t n0 = t0.heads * tasks_per_head;
+    const uint32_t n_all = n0 + t1.heads * tasks_per_head;
+    for (uint32_t task = threadIdx.x; task < n_all; task += kRopeBlock) {
+        const bool first = task < n0;
+        const uint32_t local = first ? task : task - n0;
+        const uint32_t heads = first ? t0.heads : t1.heads;
+        float* row = (first ? t0.data : t1.data) + token * (uint64_t)heads * head_dim;
+        const uint32_t h = local / tasks_per_head;
+        const uint32_t k = local - h * tasks_per_head;
+        float* v = row + (uint64_t)h * head_dim;
+        if (Interleaved) {
+            f32x4* p = reinterpret_cast<f32x4*>(v + 4 * k);
+            f32x4 x = *p;
+            const f32x4 csv = *reinterpret_cast<const f32x4*>(&cs[2 * k]);  // c0 s0 c1 s1
+            float2 r0 = rot(x.x, x.y, csv.x, csv.y);
+            float2 r1 = rot(x.z, x.w, csv.z, csv.w);
+            f32x4 o;
+            o.x = r0.x; o.y = r0.y; o.z = r1.x; o.w = r1.y;
+            *p = o;
+        } else {
+            f32x4* p0 = reinterpret_cast<f32x4*>(v + 4 * k);
+            f32x4* p1 = reinterpret_cast<f32x4*>(v + half + 4 * k);
+            f32x4 x0 = *p0, x1 = *p1;
+            const f32x4 ca = *reinterpret_cast<const f32x4*>(&cs[4 * k]);      // c0 s0 c1 s1
+            const f32x4 cb = *reinterpret_cast<const f32x4*>(&cs[4 * k + 2]);  // c2 s2 c3 s3
+            float2 r0 = rot(x0.x, x1.x, ca.x, ca.y);
+            float2 r1 = rot(x0.y, x1.y, ca.z, ca.w);
+            float2 r2 = rot(x0.z, x1.z, cb.x, cb.y);
+            float2 r3 = rot(x0.w, x1.w, cb.z, cb.w);
+            f32x4 o0, o1;
+            o0.x = r0.x; o0.y = r1.x; o0.z = r2.x; o0.w = r3.x;
+            o1.x = r0.y; o1.y = r1.y; o1.z = r2.y; o1.w = r3.y;
+            *p0 = o0;
+            *p1 = o1;
+        }
+    }
+}
+
+// Scalar path: any even D, any 4-byte alignment.  One task per pair.
+template <bool Interleaved>
+__global__ __launch_bounds__(kRopeBlock) void rope_scalar_kernel(RopeTensor t0, RopeTensor t1,
+                                                                 const float* __restrict__ inv_freq,
+                                                                 uint64_t seq_len, uint32_t head_dim,
+                                                                 uint64_t start_pos) {
+    extern __shared__ f32x4 cs_raw[];
+    float2* cs = reinterpret_cast<float2*>(cs_raw);
+    const uint64_t token = blockIdx.x;
+    const uint32_t half = head_dim >> 1;
+    const float pos = (float)(start_pos + token % seq_len);
+    for (uint32_t i = threadIdx.x; i < half; i += kRopeBlock) {
+        float angle = pos * inv_freq[i];
+        float s, c;
+        sincosf(angle, &s, &c);
+        cs[i] = make_float2(c, s);
+    }
+    __syncthreads();
+    const uint32_t n0 = t0.heads * half;
+    const uint32_t n_all = n0 + t1.heads * half;
+    for (uint32_t task = threadIdx.x; task < n_all; task += kRopeBlock) {
+        const bool first = task < n0;
+        const uint32_t local = first ? task : task - n0;
+        const uint32_t heads = first ? t0.heads : t1.heads;
+        float* row = (first ? t0.data : t1.data) + token * (uint64_t)heads * head_dim;
+        const uint32_t h = local / half;
+        const uint32_t i = local - h * half;
+        float* v = row + (uint64_t)h * head_dim;
+        const uint32_t j0 = Interleaved ? 2 * i : i;
+        const uint32_t j1 = Interleaved ? 2 * i + 1 : i + half;
+        float2 r = rot(v[j0], v[j1], cs[i].x, cs[i].y);
+        v[j0] = r.x;
+        v[j1] = r.y;
+    }
+}
+
+static int rope_launch(float* q, uint32_t q_heads, float* k, uint32_t k_heads, const float* inv_freq,
+                       uint64_t batch, uint64_t seq_len, uint32_t head_dim, uint64_t start_pos,
+                       int interleaved, hipStream_t s) {
+    uint64_t tokens;
+    if (!mul_ok(batch, seq_len, &tokens)) return KORE_HIP_ERR_OVERFLOW;
+    const uint64_t heads_all = (uint64_t)q_heads + k_heads;
+    if (tokens == 0 || heads_all == 0 || head_dim == 0) return KORE_HIP_OK;
+    if ((head_dim & 1u) || head_dim > kRopeMaxHeadDim) return KORE_HIP_ERR_BAD_DIM;
+    if (!inv_freq || (q_heads && !q) || (k_heads && !k)) return KORE_HIP_ERR_NULL_PTR;
+    uint64_t elems;
+    if (!mul_ok(tokens, (uint64_t)heads_all * head_dim, &elems) || elems > kMaxElements ||
+        tokens > 0x7fffffffull)
+        return KORE_HIP_ERR_OVERFLOW;
+    if ((uint64_t)heads_all * (head_dim / 2) > 0xffffffffull) return KORE_HIP_ERR_OVERFLOW;
+    if (start_pos + seq_len < start_pos) return KORE_HIP_ERR_OVERFLOW;
+    if (q && k && q_heads && k_heads) {
+        // Overlapping Q and K would rotate shared elements twice.
+        const char* q0 = (const char*)q;
+        const char* q1 = q0 + tokens * (uint64_t)q_heads * head_dim * 4;
+        const char* k0 = (const char*)k;
+        const char* k1 = k0 + tokens * (uint64_t)k_heads * head_dim * 4;
+        if (q0 < k1 && k0 < q1) return KORE_HIP_ERR_ALIAS;
+    }
+    RopeTensor t0{q_heads ? q : k, q_heads ? q_heads : k_heads};
+    RopeTensor t1{q_heads ? k : nullptr, q_heads ? k_heads : 0u};
+    const bool vec = (head_dim % 8 == 0) && aligned16(t0.data) && (t1.heads == 0 || aligned16(t1.data));
+    const size_t lds = ((size_t)(head_dim / 2) * sizeof(float2) + 15) & ~(size_t)15;
+    dim3 grid((uint32_t)tokens), block(kRopeBlock);
+    if (vec) {
+        if (interleaved)
+            hipLaunchKernelGGL(rope_vec_kernel<true>, grid, block, lds, s, t0, t1, inv_freq, seq_len, head_dim,
+                               start_pos);
+        else
+            hipLaunchKernelGGL(rope_vec_kernel<false>, grid, block, lds, s, t0, t1, inv_freq, seq_len, head_dim,
+                               start_pos);
+    } else {
+        if (interleaved)
+            hipLaunchKernelGGL(rope_scalar_kernel<true>, grid, block, lds, s, t0, t1, inv_freq, seq_len,
+                               head_dim, start_pos);
+        else
+            hipLaunchKernelGGL(rope_scalar_kernel<false>, grid, block, lds, s, t0, t1, inv_freq, seq_len,
+                               head_dim, start_pos);
+    }
+    return launch_status();
+}
+
+}  // namespace kore
+
+using namespace kore;
+
+extern "C" int kore_hip_rope_f32(float* data, const float* inv_freq, uint64_t batch, uint64_t seq_len,
+                                 uint32_t num_heads, uint32_t head_dim, uint64_t start_pos, int interleaved,
+                                 kore_stream_t stream) {
+    return rope_launch(data, num_heads, nullptr, 0, inv_freq, batch, seq_len, head_dim, start_pos, interleaved,
+                       (hipStream_t)stream);
+}
+
+extern "C" int kore_hip_rope_qk_f32(float* q, float* k, const float* inv_freq, uint64_t batch,
+                                    uint64_t seq_len, uint32_t q_heads, uint32_t k_heads, uint32_t head_dim,
+                                    uint64_t start_pos, int interleaved, kore_stream_t stream) {
+    return rope_launch(q, q_heads, k, k_heads, inv_freq, batch, seq_len, head_dim, start_pos, interleaved,
+                       (hipStream_t)stream);
+}

@@ -1,0 +1,227 @@
+/*
+ * kore_oracle.c -- CPU restatement of KORE's reference CPU path for the fused
+ * layer ops.  TEST INFRASTRUCTURE ONLY (the parity checker and the CPU
+ * baseline); the product library never links it.
+ *
+ * Build: see oracle/Makefile (gcc -O2 -ffp-contract=off -fno-fast-math
+ * -fno-builtin, glibc libm).  Each function names the reference Rust function
+ * it restates; the declarations in kore_oracle.h carry the file:line.
+ */
+#include "kore_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <string.h>
+
+/* cpu_fused.rs:175-187: per row, sum_sq is `row.iter().map(|x| x*x).sum()`,
+ * a left-to-right f32 fold; rms = sqrt(sum_sq / D + eps); inv = 1/rms;
+ * y = row[i] * inv * g[i] evaluated as (row[i]*inv)*g[i]. */
+void kore_oracle_rms_norm_f32(const float *x, const float *gamma, float *y,
+                              size_t rows, size_t cols, float eps) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float *row = x + r * cols;
+        float *out = y + r * cols;
+        float sum_sq = 0.0f;
+        for (size_t i = 0; i < cols; ++i) {
+            float sq = row[i] * row[i];
+            sum_sq = sum_sq + sq;
+        }
+        float rms = sqrtf(sum_sq / (float)cols + eps);
+        float inv_rms = 1.0f / rms;
+        for (size_t i = 0; i < cols; ++i) {
+            float t = row[i] * inv_rms;
+            out[i] = t * gamma[i];
+        }
+    }
+}
+
+/* activations.rs:23-29.  FRAC_2_SQRT_PI * FRAC_1_SQRT_2 is a product of two
+ * f32 constants, folded in f32 (0x3F4C422A); 0.044715*x*x*x associates left. */
+void kore_oracle_gelu_f32(const float *x, float *y, size_t n) {
+    const float frac_2_sqrt_pi = 1.12837916709551257390f;
+    const float frac_1_sqrt_2 = 0.707106781186547524401f;
+    const float k = frac_2_sqrt_pi * frac_1_sqrt_2;
+    for (size_t i = 0; i < n; ++i) {
+        float v = x[i];
+        float cube = ((0.044715f * v) * v) * v;
+        float inner = k * (v + cube);
+        float half_x = 0.5f * v;
+        y[i] = half_x * (1.0f + tanhf(inner));
+    }
+}
+
+/* activations.rs:43: x / (1.0 + (-x).exp()). */
+void kore_oracle_silu_f32(const float *x, float *y, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        float v = x[i];
+        y[i] = v / (1.0f + expf(-v));
+    }
+}
+
+struct mul_job {
+    const float *a, *b;
+    float *out;
+    size_t lo, hi;
+};
+
+static void *mul_worker(void *arg) {
+    struct mul_job *j = (struct mul_job *)arg;
+    for (size_t i = j->lo; i < j->hi; ++i) j->out[i] = j->a[i] * j->b[i];
+    return NULL;
+}
+
+/* arithmetic.rs:499-509: result[i] = a[i] * b[i], rayon-parallel above
+ * PAR_THRESHOLD; element-wise, so the split never changes a bit. */
+void kore_oracle_mul_f32(const float *a, const float *b, float *out, size_t n,
+                         int nthreads) {
+    if (nthreads <= 1 || n < 8192) {
+        for (size_t i = 0; i < n; ++i) out[i] = a[i] * b[i];
+        return;
+    }
+    if (nthreads > 256) nthreads = 256;
+    pthread_t tid[256];
+    struct mul_job jobs[256];
+    size_t chunk = (n + (size_t)nthreads - 1) / (size_t)nthreads;
+    int started = 0;
+    for (int t = 0; t < nthreads; ++t) {
+        size_t lo = (size_t)t * chunk, hi = lo + chunk;
+        if (lo >= n) break;
+        if (hi > n) hi = n;
+        jobs[t].a = a; jobs[t].b = b; jobs[t].out = out;
+        jobs[t].lo = lo; jobs[t].hi = hi;
+        if (pthread_create(&tid[t], NULL, mul_worker, &jobs[t]) != 0) {
+            mul_worker(&jobs[t]);
+            tid[t] = 0;
+        }
+        started = t + 1;
+    }
+    for (int t = 0; t < started; ++t)
+        if (tid[t]) pthread_join(tid[t], NULL);
+}
+
+/* engine.rs:633-643: silu(gate) into a fresh tensor, then Tensor::mul. */
+void kore_oracle_swiglu_f32(const float *gate, const float *up, float *out,
+                            float *tmp, size_t n, int mul_threads) {
+    kore_oracle_silu_f32(gate, tmp, n);
+    kore_oracle_mul_f32(tmp, up, out, n, mul_threads);
+}
+
+/* engine.rs:694-700: 1.0 / base.powf(2.0 * i as f32 / head_dim as f32). */
+void kore_oracle_rope_inv_freq_f32(float *inv_freq, size_t head_dim, float base) {
+    size_t half = head_dim / 2;
+    for (size_t i = 0; i < half; ++i) {
+        float e = (2.0f * (float)i) / (float)head_dim;
+        inv_freq[i] = 1.0f / powf(base, e);
+    }
+}
+
+/* rope.rs:18-35.  freq is recomputed per element with the same expression as
+ * the inv_freq table above; angle = (start_pos + pos) as f32 * freq. */
+void kore_oracle_rope_f32(float *data, size_t seq_len, size_t n_heads,
+                          size_t head_dim, size_t start_pos, float base) {
+    size_t half = head_dim / 2;
+    for (size_t pos = 0; pos < seq_len; ++pos) {
+        float abs_pos = (float)(start_pos + pos);
+        for (size_t h = 0; h < n_heads; ++h) {
+            size_t off = pos * n_heads * head_dim + h * head_dim;
+            for (size_t i = 0; i < half; ++i) {
+                float e = (2.0f * (float)i) / (float)head_dim;
+                float freq = 1.0f / powf(base, e);
+                float angle = abs_pos * freq;
+                float c = cosf(angle);
+                float s = sinf(angle);
+                float x0 = data[off + i];
+                float x1 = data[off + half + i];
+                float a0 = x0 * c, b0 = x1 * s;
+                float a1 = x0 * s, b1 = x1 * c;
+                data[off + i] = a0 - b0;
+                data[off + half + i] = a1 + b1;
+            }
+        }
+    }
+}
+
+/* engine.rs:715-724, per head: pairs (2*pair, 2*pair+1) of each head vector,
+ * angle = abs_pos * inv_freq[pair]. */
+void kore_oracle_rope_interleaved_f32(float *data, size_t seq_len,
+                                      size_t n_heads, size_t head_dim,
+                                      size_t start_pos, const float *inv_freq) {
+    size_t half = head_dim / 2;
+    for (size_t pos = 0; pos < seq_len; ++pos) {
+        float abs_pos = (float)(start_pos + pos);
+        for (size_t h = 0; h < n_heads; ++h) {
+            float *v = data + pos * n_heads * head_dim + h * head_dim;
+            for (size_t p = 0; p < half; ++p) {
+                float angle = abs_pos * inv_freq[p];
+                float c = cosf(angle);
+                float s = sinf(angle);
+                float x0 = v[2 * p];
+                float x1 = v[2 * p + 1];
+                float a0 = x0 * c, b0 = x1 * s;
+                float a1 = x0 * s, b1 = x1 * c;
+                v[2 * p] = a0 - b0;
+                v[2 * p + 1] = a1 + b1;
+            }
+        }
+    }
+}
+
+/* embedding.rs (edge) :16-26: copy the row when id < vocab, else zeros. */
+void kore_oracle_embedding_f32(const float *table, const uint32_t *ids,
+                               float *out, size_t n_ids, size_t vocab,
+                               size_t dim) {
+    for (size_t t = 0; t < n_ids; ++t) {
+        size_t id = (size_t)ids[t];
+        float *dst = out + t * dim;
+        if (id < vocab) {
+            memcpy(dst, table + id * dim, dim * sizeof(float));
+        } else {
+            for (size_t i = 0; i < dim; ++i) dst[i] = 0.0f;
+        }
+    }
+}
+
+/* ((xn * 127.0) / amax).round().clamp(-128.0, 127.0) as i8.
+ * f32::round rounds half away from zero (= C roundf); f32::clamp keeps NaN;
+ * `as i8` saturates and maps NaN to 0. */
+int8_t kore_oracle_quant_code(float xn, float amax_guarded) {
+    float t = (xn * 127.0f) / amax_guarded;
+    float r = roundf(t);
+    if (r != r) return 0;
+    if (r < -128.0f) r = -128.0f;
+    if (r > 127.0f) r = 127.0f;
+    return (int8_t)(int)r;
+}
+
+/* f32::max: returns the non-NaN operand when exactly one is NaN. */
+static float rust_fmax(float a, float b) {
+    if (a != a) return b;
+    if (b != b) return a;
+    return a > b ? a : b;
+}
+
+void kore_oracle_rms_norm_quant_i8(const float *x, const float *gamma,
+                                   int8_t *q, float *scale, size_t rows,
+                                   size_t cols, float eps) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float *row = x + r * cols;
+        float sum_sq = 0.0f;
+        for (size_t i = 0; i < cols; ++i) {
+            float sq = row[i] * row[i];
+            sum_sq = sum_sq + sq;
+        }
+        float rms = sqrtf(sum_sq / (float)cols + eps);
+        float inv_rms = 1.0f / rms;
+        float amax = 0.0f;
+        for (size_t i = 0; i < cols; ++i) {
+            float xn = (row[i] * inv_rms) * gamma[i];
+            amax = rust_fmax(amax, fabsf(xn));
+        }
+        float a = amax < 1e-8f ? 1.0f : amax;
+        for (size_t i = 0; i < cols; ++i) {
+            float xn = (row[i] * inv_rms) * gamma[i];
+            q[r * cols + i] = kore_oracle_quant_code(xn, a);
+        }
+        scale[r] = a / 127.0f;
+    }
+}

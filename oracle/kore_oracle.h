@@ -1,0 +1,95 @@
+/*
+ * kore_oracle.h -- CPU restatement of KORE's reference CPU path for the fused
+ * layer ops (RMSNorm, SiLU/GELU/SwiGLU, RoPE, embedding gather, BitLinear
+ * pre-quant).
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker and the CPU
+ * baseline: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg load it.  The product (libkore_hip.so) never links or calls it.
+ *
+ * Every function follows one reference Rust function, statement for
+ * statement, in IEEE binary32 with the same operation order; the file:line
+ * of the function it restates is given beside each declaration (paths are
+ * relative to the KidIkaros/KORE checkout).  Rust never contracts a*b+c into
+ * an FMA and folds iterator sums left to right, so this file is built with
+ * -ffp-contract=off -fno-fast-math -fno-builtin and calls glibc libm, which is
+ * what Rust's f32::{exp,tanh,sin,cos,powf} resolve to on linux-gnu.
+ */
+#ifndef KORE_ORACLE_H
+#define KORE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* crates/kore-kernels/src/cpu_fused.rs:160-190 (fused_rms_norm); identical
+ * arithmetic in crates/kore-edge/src/ops/norm.rs:7-20. */
+void kore_oracle_rms_norm_f32(const float *x, const float *gamma, float *y,
+                              size_t rows, size_t cols, float eps);
+
+/* crates/kore-nn/src/activations.rs:14-32 (gelu, tanh form). */
+void kore_oracle_gelu_f32(const float *x, float *y, size_t n);
+
+/* crates/kore-nn/src/activations.rs:35-45 (silu); same formula as
+ * crates/kore-edge/src/ops/activation.rs:21-26. */
+void kore_oracle_silu_f32(const float *x, float *y, size_t n);
+
+/* crates/kore-core/src/ops/arithmetic.rs:482-509 (binary_op, same-shape fast
+ * path, op = a*b).  nthreads > 1 splits the index range like rayon's
+ * par_iter_mut; the result does not depend on the split. */
+void kore_oracle_mul_f32(const float *a, const float *b, float *out, size_t n,
+                         int nthreads);
+
+/* SwiGLU as the reference composes it: silu(gate) (activations.rs:35-45)
+ * followed by Tensor::mul (arithmetic.rs:76-95); see
+ * crates/kore-serve/src/layered/engine.rs:633-643 and
+ * crates/kore-edge/src/runtime.rs:253-255.  `tmp` holds the silu tensor. */
+void kore_oracle_swiglu_f32(const float *gate, const float *up, float *out,
+                            float *tmp, size_t n, int mul_threads);
+
+/* crates/kore-serve/src/layered/engine.rs:694-700 (precompute_rope_inv_freq):
+ * inv_freq[i] = 1 / base^(2i/head_dim), i < head_dim/2. */
+void kore_oracle_rope_inv_freq_f32(float *inv_freq, size_t head_dim, float base);
+
+/* crates/kore-edge/src/ops/rope.rs:9-36 (apply_rope, half-split pairs
+ * (i, i+D/2), in place on [seq_len, n_heads, head_dim]). */
+void kore_oracle_rope_f32(float *data, size_t seq_len, size_t n_heads,
+                          size_t head_dim, size_t start_pos, float base);
+
+/* crates/kore-serve/src/layered/engine.rs:706-727 (apply_rope, interleaved
+ * pairs (2i, 2i+1), inv_freq table), applied in place to every head of a
+ * [seq_len, n_heads, head_dim] buffer. */
+void kore_oracle_rope_interleaved_f32(float *data, size_t seq_len,
+                                      size_t n_heads, size_t head_dim,
+                                      size_t start_pos, const float *inv_freq);
+
+/* crates/kore-edge/src/ops/embedding.rs:8-27 and
+ * crates/kore-nn/src/embedding.rs:55-72: out[t,:] = table[id_t,:] when
+ * id_t < vocab (ids read as unsigned 32-bit), else a zero row. */
+void kore_oracle_embedding_f32(const float *table, const uint32_t *ids,
+                               float *out, size_t n_ids, size_t vocab,
+                               size_t dim);
+
+/* BitLinear pre-quant.  The reference has no such function; this is the
+ * composition the build defines:
+ *   xn    = fused_rms_norm(x, gamma, eps)   (cpu_fused.rs:160-190)
+ *   amax  = fold(0, f32::max) of |xn|       (kore-btes/src/quantize.rs:9)
+ *   amax  = 1.0 if amax < 1e-8              (kore-btes/src/quantize.rs:10)
+ *   q     = ((xn*127)/amax).round().clamp(-128,127) as i8
+ *           (f32::round = ties away from zero; `as i8` saturates, NaN -> 0)
+ *   scale = amax / 127                      (x ~= q * scale)            */
+void kore_oracle_rms_norm_quant_i8(const float *x, const float *gamma,
+                                   int8_t *q, float *scale, size_t rows,
+                                   size_t cols, float eps);
+
+/* One element of the pre-quant code: the shared definition used above.  */
+int8_t kore_oracle_quant_code(float xn, float amax_guarded);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KORE_ORACLE_H */

@@ -1,0 +1,169 @@
+"""numpy front end of the C oracle (kore_oracle.c).  TEST INFRASTRUCTURE ONLY.
+
+Each wrapper names the reference function the C code restates; see
+kore_oracle.h for file:line citations.  Inputs are converted to contiguous
+float32 / uint32 arrays; outputs are new arrays.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_build", "libkore_oracle.so")
+
+_c = ctypes
+_sz = _c.c_size_t
+_p = _c.c_void_p
+_f = _c.c_float
+_i = _c.c_int
+
+_SIGS = {
+    "kore_oracle_rms_norm_f32": (None, [_p, _p, _p, _sz, _sz, _f]),
+    "kore_oracle_gelu_f32": (None, [_p, _p, _sz]),
+    "kore_oracle_silu_f32": (None, [_p, _p, _sz]),
+    "kore_oracle_mul_f32": (None, [_p, _p, _p, _sz, _i]),
+    "kore_oracle_swiglu_f32": (None, [_p, _p, _p, _p, _sz, _i]),
+    "kore_oracle_rope_inv_freq_f32": (None, [_p, _sz, _f]),
+    "kore_oracle_rope_f32": (None, [_p, _sz, _sz, _sz, _sz, _f]),
+    "kore_oracle_rope_interleaved_f32": (None, [_p, _sz, _sz, _sz, _sz, _p]),
+    "kore_oracle_embedding_f32": (None, [_p, _p, _p, _sz, _sz, _sz]),
+    "kore_oracle_rms_norm_quant_i8": (None, [_p, _p, _p, _p, _sz, _sz, _f]),
+    "kore_oracle_quant_code": (_c.c_int8, [_f, _f]),
+}
+
+_lib = None
+
+
+def build() -> None:
+    """Compile the oracle with its Makefile (gcc, no FMA contraction)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def rms_norm(x, gamma, eps: float) -> np.ndarray:
+    """fused_rms_norm (crates/kore-kernels/src/cpu_fused.rs:160-190) over the last axis."""
+    x = _f32(x)
+    g = _f32(gamma)
+    cols = x.shape[-1]
+    rows = x.size // cols if cols else 0
+    y = np.empty_like(x)
+    lib().kore_oracle_rms_norm_f32(_ptr(x), _ptr(g), _ptr(y), rows, cols, eps)
+    return y
+
+
+def gelu(x) -> np.ndarray:
+    """kore_nn::activations::gelu (crates/kore-nn/src/activations.rs:14-32)."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().kore_oracle_gelu_f32(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def silu(x) -> np.ndarray:
+    """kore_nn::activations::silu (crates/kore-nn/src/activations.rs:35-45)."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().kore_oracle_silu_f32(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def mul(a, b, threads: int = 1) -> np.ndarray:
+    """Tensor::mul same-shape path (crates/kore-core/src/ops/arithmetic.rs:482-509)."""
+    a = _f32(a)
+    b = _f32(b)
+    out = np.empty_like(a)
+    lib().kore_oracle_mul_f32(_ptr(a), _ptr(b), _ptr(out), a.size, threads)
+    return out
+
+
+def swiglu(gate, up, threads: int = 1) -> np.ndarray:
+    """silu(gate) then Tensor::mul(up) (crates/kore-serve/src/layered/engine.rs:633-643)."""
+    g = _f32(gate)
+    u = _f32(up)
+    out = np.empty_like(g)
+    tmp = np.empty_like(g)
+    lib().kore_oracle_swiglu_f32(_ptr(g), _ptr(u), _ptr(out), _ptr(tmp), g.size, threads)
+    return out
+
+
+def rope_inv_freq(head_dim: int, base: float) -> np.ndarray:
+    """precompute_rope_inv_freq (crates/kore-serve/src/layered/engine.rs:694-700)."""
+    out = np.zeros(max(head_dim // 2, 1), dtype=np.float32)
+    lib().kore_oracle_rope_inv_freq_f32(_ptr(out), head_dim, base)
+    return out[: head_dim // 2]
+
+
+def rope(data, start_pos: int, base: float, interleaved: bool = False) -> np.ndarray:
+    """RoPE on data[..., seq, heads, head_dim] (leading axes = batch, same
+    positions per batch entry).  Half-split: kore_edge apply_rope
+    (crates/kore-edge/src/ops/rope.rs:9-36); interleaved: kore-serve apply_rope
+    (crates/kore-serve/src/layered/engine.rs:706-727)."""
+    d = _f32(data).copy()
+    seq, heads, hd = d.shape[-3:]
+    batch = d.size // (seq * heads * hd) if d.size else 0
+    inv = rope_inv_freq(hd, base)
+    stride = seq * heads * hd
+    for b in range(batch):
+        view = d.reshape(-1)[b * stride:(b + 1) * stride]
+        ptr = view.ctypes.data
+        if interleaved:
+            lib().kore_oracle_rope_interleaved_f32(ptr, seq, heads, hd, start_pos, _ptr(inv))
+        else:
+            lib().kore_oracle_rope_f32(ptr, seq, heads, hd, start_pos, base)
+    return d
+
+
+def embedding(table, ids) -> np.ndarray:
+    """Embedding::lookup (crates/kore-nn/src/embedding.rs:55-72) /
+    embedding_lookup (crates/kore-edge/src/ops/embedding.rs:8-27)."""
+    t = _f32(table)
+    vocab, dim = t.shape
+    i = np.ascontiguousarray(ids).astype(np.int64).astype(np.uint32)  # i32 -> u32 bit pattern
+    out = np.empty((i.size, dim), dtype=np.float32)
+    lib().kore_oracle_embedding_f32(_ptr(t), _ptr(i), _ptr(out), i.size, vocab, dim)
+    return out
+
+
+def rms_norm_quant_i8(x, gamma, eps: float):
+    """fused_rms_norm + per-row absmax int8 (composition defined in kore_oracle.h)."""
+    x = _f32(x)
+    g = _f32(gamma)
+    cols = x.shape[-1]
+    rows = x.size // cols if cols else 0
+    q = np.empty(x.shape, dtype=np.int8)
+    s = np.empty(x.shape[:-1], dtype=np.float32)
+    lib().kore_oracle_rms_norm_quant_i8(_ptr(x), _ptr(g), _ptr(q), _ptr(s), rows, cols, eps)
+    return q, s
+
+
+def quant_code(xn: float, amax: float) -> int:
+    return int(lib().kore_oracle_quant_code(xn, amax))
+
+
+__all__ = ["build", "lib", "rms_norm", "gelu", "silu", "mul", "swiglu", "rope_inv_freq", "rope", "embedding",
+           "rms_norm_quant_i8", "quant_code"]

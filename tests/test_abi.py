@@ -1,0 +1,77 @@
+"""The C ABI library loads, exports every entry point include/kore_hip.h
+declares, and rejects bad arguments on the host (no GPU needed: argument
+checks run before anything is enqueued)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+from kore_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "kore_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kore_hip_\w+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+    # the ctypes binding covers every compute entry point
+    assert set(names) - {"kore_hip_status_string"} == set(_lib.SIGNATURES)
+
+
+def test_version_and_status_text():
+    lib = _lib.load()
+    assert lib.kore_hip_version() == 100
+    assert _lib.status_string(0) == "ok"
+    assert "null" in _lib.status_string(-1)
+    assert "HIP" in _lib.status_string(700)
+
+
+P = 0x1000  # a fake, never-dereferenced non-null pointer
+
+
+def test_argument_errors_are_reported_on_host():
+    lib = _lib.load()
+    s = None
+    # zero work: OK and nothing launched, even with null pointers
+    assert lib.kore_hip_gelu_f32(None, None, 0, s) == 0
+    assert lib.kore_hip_rms_norm_f32(None, None, None, 0, 128, 1e-6, s) == 0
+    assert lib.kore_hip_embedding_f32(None, None, None, 0, 10, 4, s) == 0
+    # null pointers with work
+    assert lib.kore_hip_gelu_f32(None, P, 16, s) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert lib.kore_hip_swiglu_f32(P, None, P, 16, s) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert lib.kore_hip_rms_norm_f32(P, None, P, 4, 128, 1e-6, s) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert lib.kore_hip_rms_norm_quant_i8(P, P, P, None, 4, 128, 1e-6, s) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert lib.kore_hip_embedding_f32(P, None, P, 3, 10, 4, s) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert lib.kore_hip_rope_f32(P, None, 1, 4, 2, 8, 0, 0, s) == _lib.KORE_HIP_ERR_NULL_PTR
+    # bad dims
+    assert lib.kore_hip_rope_f32(P, P, 1, 4, 2, 7, 0, 0, s) == _lib.KORE_HIP_ERR_BAD_DIM
+    assert lib.kore_hip_rms_norm_f32(P, P, P, 4, 0, 1e-6, s) == _lib.KORE_HIP_ERR_BAD_DIM
+    assert lib.kore_hip_rope_inv_freq_f32(P, 7, 10000.0) == _lib.KORE_HIP_ERR_BAD_DIM
+    # overflow
+    assert lib.kore_hip_gelu_f32(P, P, 2**62, s) == _lib.KORE_HIP_ERR_OVERFLOW
+    assert lib.kore_hip_rms_norm_f32(P, P, P, 2**40, 2**40, 1e-6, s) == _lib.KORE_HIP_ERR_OVERFLOW
+    assert lib.kore_hip_embedding_f32(P, P, P, 2**33, 2**33, 4, s) == _lib.KORE_HIP_ERR_OVERFLOW
+    # overlapping Q and K
+    assert lib.kore_hip_rope_qk_f32(P, P + 64, P, 1, 4, 2, 2, 8, 0, 0, s) == _lib.KORE_HIP_ERR_ALIAS
+
+
+@pytest.mark.parametrize("head_dim", [2, 8, 64, 128, 256])
+@pytest.mark.parametrize("base", [10000.0, 500000.0, 10.0])
+def test_rope_inv_freq_table_matches_oracle_bit_exact(head_dim, base):
+    half = head_dim // 2
+    got = np.zeros(half, np.float32)
+    assert _lib.load().kore_hip_rope_inv_freq_f32(got.ctypes.data, head_dim, base) == 0
+    want = oracle.rope_inv_freq(head_dim, base)
+    assert got.tobytes() == want.tobytes()

@@ -1,0 +1,304 @@
+"""GPU parity: every entry point of libkore_hip.so against the CPU oracle on
+identical seeded inputs, through KORE's rocm_* op API (kore_amd.rocm).
+
+Bar: embedding gather, RMSNorm and int8 codes/scales
+bit-exact; GELU / SiLU / SwiGLU / RoPE within |d| <= 1e-6 or |d| <= 1e-5*|ref|
+(inputs.assert_close).  Cases cover the reference's edge cases (empty work,
+ragged rows, out-of-range ids, zero rows, NaN/Inf) plus every BASELINE config
+at full size.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from inputs import (assert_bitexact, assert_close, embedding_ids, max_err, normal, prequant_inputs, rmsnorm_inputs)
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+from kore_amd import rocm  # noqa: E402
+from kore_amd.rocm import HipBuffer  # noqa: E402
+
+DEV = 0
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def up(arr) -> HipBuffer:
+    return HipBuffer.from_host(DEV, np.ascontiguousarray(arr))
+
+
+def down(buf: HipBuffer, dtype, shape):
+    return buf.to_host(dtype)[: int(np.prod(shape))].reshape(shape)
+
+
+def unaligned(arr: np.ndarray) -> HipBuffer:
+    """Device copy of arr starting 4 bytes past a 16-byte boundary."""
+    t = torch.empty(arr.size + 1, dtype=torch.float32, device="cuda")
+    t[1:].copy_(torch.from_numpy(np.ascontiguousarray(arr, np.float32).ravel()))
+    return HipBuffer.from_tensor(t[1:])
+
+
+# ----------------------------------------------------------------- RMSNorm
+RMS_SHAPES = [(1, 1), (3, 7), (2, 4), (5, 256), (17, 260), (6, 1000), (32, 2048), (9, 2560), (7, 4096),
+              (3, 5000), (65, 512)]
+
+
+@pytest.mark.parametrize("rows,cols", RMS_SHAPES)
+def test_rms_norm_bit_exact(rows, cols):
+    log(f"rms_norm rows={rows} cols={cols}")
+    x, g = rmsnorm_inputs(rows, cols, seed=rows * 131 + cols)
+    out = rocm.rocm_rms_norm_f32(DEV, up(x), up(g), rows, cols, 1e-6)
+    got = down(out, np.float32, (rows, cols))
+    want = oracle.rms_norm(x, g, 1e-6)
+    assert_bitexact(got, want, "rms_norm")
+
+
+def test_rms_norm_baseline_config0_and_sweep():
+    # x[32,2048] ~ N(0,1), w ~ N(1,0.02), eps 1e-6, seed 0
+    for rows, cols in [(32, 2048), (16384, 2048)]:
+        log(f"rms_norm baseline rows={rows} cols={cols}")
+        x, g = rmsnorm_inputs(rows, cols, seed=0)
+        got = down(rocm.rocm_rms_norm_f32(DEV, up(x), up(g), rows, cols, 1e-6), np.float32, (rows, cols))
+        assert_bitexact(got, oracle.rms_norm(x, g, 1e-6), "rms_norm baseline")
+
+
+def test_rms_norm_in_place_and_unaligned():
+    rows, cols = 10, 768
+    x, g = rmsnorm_inputs(rows, cols, seed=3)
+    want = oracle.rms_norm(x, g, 1e-6)
+    buf = up(x)
+    rocm.rocm_rms_norm_f32(DEV, buf, up(g), rows, cols, 1e-6, out=buf)
+    assert_bitexact(down(buf, np.float32, (rows, cols)), want, "in place")
+    xb = unaligned(x)
+    out = rocm.rocm_rms_norm_f32(DEV, xb, up(g), rows, cols, 1e-6)
+    assert_bitexact(down(out, np.float32, (rows, cols)), want, "unaligned")
+
+
+def test_rms_norm_special_rows():
+    cols = 300
+    x = normal((6, cols), 8)
+    x[1] = 0.0
+    x[2, 5] = np.nan
+    x[3, 7] = np.inf
+    x[4] *= 1e20  # sum of squares overflows to inf -> inv 0
+    x[5, :] = 1e-30  # underflowing squares
+    g = np.ones(cols, np.float32)
+    for eps in (1e-6, 0.0):
+        got = down(rocm.rocm_rms_norm_f32(DEV, up(x), up(g), 6, cols, eps), np.float32, (6, cols))
+        want = oracle.rms_norm(x, g, eps)
+        assert_bitexact(got, want, f"special rows eps={eps}")
+
+
+# --------------------------------------------------------------- pre-quant
+@pytest.mark.parametrize("rows,cols", [(1, 2560), (64, 2560), (4096, 2560), (5, 33), (9, 300), (3, 8),
+                                       (20, 2048), (7, 4096), (2, 4100)])
+def test_prequant_bit_exact(rows, cols):
+    log(f"prequant rows={rows} cols={cols}")
+    x, g = prequant_inputs(rows, cols, seed=rows + 17 * cols)
+    q, s = rocm.rocm_rms_norm_quant_i8(DEV, up(x), up(g), rows, cols, 1e-6)
+    gq = down(q, np.int8, (rows, cols))
+    gs = down(s, np.float32, (rows,))
+    wq, ws = oracle.rms_norm_quant_i8(x, g, 1e-6)
+    assert gs.tobytes() == ws.tobytes()
+    diff = np.argwhere(gq != wq)
+    assert diff.size == 0, f"{len(diff)} codes differ, first {diff[:3].tolist()}"
+
+
+def test_prequant_baseline_seed0():
+    # BASELINE configs[4] at T = 4096, 64, 1 with seed 0
+    for rows in (4096, 64, 1):
+        log(f"prequant baseline T={rows}")
+        x, g = prequant_inputs(rows, 2560, seed=0)
+        q, s = rocm.rocm_rms_norm_quant_i8(DEV, up(x), up(g), rows, 2560, 1e-6)
+        wq, ws = oracle.rms_norm_quant_i8(x, g, 1e-6)
+        assert down(q, np.int8, (rows, 2560)).tobytes() == wq.tobytes()
+        assert down(s, np.float32, (rows,)).tobytes() == ws.tobytes()
+
+
+def test_prequant_special_rows_and_unaligned_q():
+    cols = 512
+    x = normal((7, cols), 4)
+    x[0] = 0.0                        # amax guard -> codes 0, scale 1/127
+    x[1, 3] = np.nan                  # NaN row -> all codes 0
+    x[2, 9] = np.inf
+    x[3] = 1e-12                      # tiny but non-zero
+    x[4, ::2] = 0.0
+    x[5] *= 1e20
+    g = normal((cols,), 5, 1.0, 0.02)
+    g[6] = np.nan                     # one NaN weight: its code is 0, the rest quantise
+    wq, ws = oracle.rms_norm_quant_i8(x, g, 1e-6)
+    q, s = rocm.rocm_rms_norm_quant_i8(DEV, up(x), up(g), 7, cols, 1e-6)
+    assert down(q, np.int8, (7, cols)).tobytes() == wq.tobytes()
+    assert down(s, np.float32, (7,)).tobytes() == ws.tobytes()
+    # q buffer at an odd byte offset takes the scalar path
+    qt = torch.empty(7 * cols + 1, dtype=torch.int8, device="cuda")
+    qb = HipBuffer(qt[1:].view(torch.uint8), DEV)
+    rocm.rocm_rms_norm_quant_i8(DEV, up(x), up(g), 7, cols, 1e-6, out_q=qb)
+    assert qt[1:].cpu().numpy().tobytes() == wq.tobytes()
+
+
+# ------------------------------------------------------------- activations
+ACT_SIZES = [1, 3, 4, 5, 255, 1024, 1027, (1 << 20) + 3]
+
+
+def special_values():
+    return np.array([0.0, -0.0, 1.0, -1.0, np.inf, -np.inf, np.nan, 88.0, -88.0, 89.0, -89.0, 100.0, -100.0,
+                     1e-38, -1e-38, 1e-45, 3.0e38, -3.0e38, 0.5, -0.5, 10.0, -10.0, 20.0, -20.0], np.float32)
+
+
+@pytest.mark.parametrize("op", ["gelu", "silu"])
+@pytest.mark.parametrize("n", ACT_SIZES)
+def test_unary_activation(op, n):
+    log(f"{op} n={n}")
+    x = normal((n,), n) * 3
+    x[: min(n, 24)] = special_values()[: min(n, 24)]
+    got = down(getattr(rocm, f"rocm_{op}_f32")(DEV, up(x), n), np.float32, (n,))
+    want = getattr(oracle, op)(x)
+    assert_close(got, want, what=op)
+
+
+@pytest.mark.parametrize("op", ["mul", "swiglu"])
+@pytest.mark.parametrize("n", ACT_SIZES)
+def test_binary_op(op, n):
+    log(f"{op} n={n}")
+    a = normal((n,), n) * 3
+    b = normal((n,), n + 1)
+    a[: min(n, 24)] = special_values()[: min(n, 24)]
+    got = down(getattr(rocm, f"rocm_{op}_f32")(DEV, up(a), up(b), n), np.float32, (n,))
+    if op == "mul":
+        assert_bitexact(got, oracle.mul(a, b), "mul")
+    else:
+        assert_close(got, oracle.swiglu(a, b), what=op)
+
+
+def test_activation_unaligned_and_in_place():
+    n = 4099
+    a, b = normal((n,), 1), normal((n,), 2)
+    got = down(rocm.rocm_gelu_f32(DEV, unaligned(a), n), np.float32, (n,))
+    assert_close(got, oracle.gelu(a), what="gelu unaligned")
+    got = down(rocm.rocm_swiglu_f32(DEV, unaligned(a), up(b), n), np.float32, (n,))
+    assert_close(got, oracle.swiglu(a, b), what="swiglu unaligned")
+    buf = up(a)
+    rocm.rocm_silu_f32(DEV, buf, n, out=buf)
+    assert_close(down(buf, np.float32, (n,)), oracle.silu(a), what="silu in place")
+
+
+@pytest.mark.slow
+def test_swiglu_gelu_baseline_full():
+    # gate, up [16384, 14336] ~ N(0,1); GELU on the same shape
+    shape = (16384, 14336)
+    n = shape[0] * shape[1]
+    log("swiglu/gelu baseline full: generating inputs")
+    gate = normal(shape, 0)
+    upv = normal(shape, 1)
+    out = rocm.rocm_swiglu_f32(DEV, up(gate), up(upv), n)
+    got = down(out, np.float32, shape)
+    del out
+    log("swiglu: oracle")
+    want = oracle.swiglu(gate, upv, threads=16)
+    assert_close(got, want, what="swiglu full")
+    log(f"swiglu max abs/rel err {max_err(got, want)}")
+    del got, want, upv
+    out = rocm.rocm_gelu_f32(DEV, up(gate), n)
+    got = down(out, np.float32, shape)
+    del out
+    log("gelu: oracle")
+    want = oracle.gelu(gate)
+    assert_close(got, want, what="gelu full")
+    log(f"gelu max abs/rel err {max_err(got, want)}")
+
+
+# -------------------------------------------------------------------- RoPE
+@pytest.mark.parametrize("interleaved", [False, True])
+@pytest.mark.parametrize("batch,seq,heads,hd,start", [(1, 1, 1, 4, 0), (2, 5, 3, 8, 7), (1, 3, 2, 6, 0),
+                                                      (2, 9, 4, 128, 100000), (1, 17, 5, 64, 3),
+                                                      (3, 4, 2, 2, 1)])
+def test_rope_small(interleaved, batch, seq, heads, hd, start):
+    log(f"rope b={batch} s={seq} h={heads} d={hd} start={start} interleaved={interleaved}")
+    x = normal((batch, seq, heads, hd), seq * hd + heads)
+    buf = up(x)
+    inv = rocm.rocm_rope_inv_freq_f32(DEV, hd, 10000.0)
+    rocm.rocm_rope_f32(DEV, buf, inv, batch, seq, heads, hd, start, interleaved)
+    got = down(buf, np.float32, x.shape)
+    want = oracle.rope(x, start, 10000.0, interleaved)
+    assert_close(got, want, what="rope")
+
+
+def test_rope_unaligned_scalar_path():
+    x = normal((2, 6, 3, 16), 5)
+    buf = unaligned(x)
+    inv = rocm.rocm_rope_inv_freq_f32(DEV, 16, 10000.0)
+    rocm.rocm_rope_f32(DEV, buf, inv, 2, 6, 3, 16, 11, False)
+    assert_close(buf.tensor(torch.float32).cpu().numpy().reshape(x.shape), oracle.rope(x, 11, 10000.0),
+                 what="rope unaligned")
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_rope_qk_baseline_full(interleaved):
+    # Q[8,2048,32,128], K[8,2048,8,128] ~ N(0,1), theta 1e4, positions 0..2047
+    log(f"rope qk baseline full interleaved={interleaved}")
+    q = normal((8, 2048, 32, 128), 0)
+    k = normal((8, 2048, 8, 128), 1)
+    qb, kb = up(q), up(k)
+    inv = rocm.rocm_rope_inv_freq_f32(DEV, 128, 10000.0)
+    rocm.rocm_rope_qk_f32(DEV, qb, kb, inv, 8, 2048, 32, 8, 128, 0, interleaved)
+    gq = down(qb, np.float32, q.shape)
+    gk = down(kb, np.float32, k.shape)
+    wq = oracle.rope(q, 0, 10000.0, interleaved)
+    assert_close(gq, wq, what="rope q")
+    log(f"rope q max abs/rel err {max_err(gq, wq)}")
+    wk = oracle.rope(k, 0, 10000.0, interleaved)
+    assert_close(gk, wk, what="rope k")
+    # the fused launch equals two single-tensor launches
+    qb2 = up(q)
+    rocm.rocm_rope_f32(DEV, qb2, inv, 8, 2048, 32, 128, 0, interleaved)
+    assert down(qb2, np.float32, q.shape).tobytes() == gq.tobytes()
+
+
+# --------------------------------------------------------------- Embedding
+@pytest.mark.parametrize("vocab,dim,n_ids", [(10, 4, 3), (50, 7, 20), (1000, 256, 513), (64, 4096, 100),
+                                             (3, 2, 3), (100, 4100, 9)])
+def test_embedding_bit_exact(vocab, dim, n_ids):
+    log(f"embedding vocab={vocab} dim={dim} n={n_ids}")
+    table = normal((vocab, dim), vocab, 0.0, 0.02)
+    ids = embedding_ids(n_ids, vocab, seed=n_ids)
+    ids[0] = vocab          # out of range -> zeros
+    if n_ids > 2:
+        ids[1] = -1         # negative int32 -> u32 max -> zeros
+        ids[2] = vocab - 1
+    out = rocm.rocm_embedding_f32(DEV, up(table), up(ids), n_ids, vocab, dim)
+    got = down(out, np.float32, (n_ids, dim))
+    assert got.tobytes() == oracle.embedding(table, ids).tobytes()
+
+
+def test_embedding_reference_kat_on_device():
+    # crates/kore-edge/src/ops/embedding.rs:33-41
+    w = np.array([1, 2, 3, 4, 5, 6], np.float32)
+    out = rocm.rocm_embedding_f32(DEV, up(w), up(np.array([0, 2, 1], np.uint32)), 3, 3, 2)
+    assert down(out, np.float32, (6,)).tolist() == [1.0, 2.0, 5.0, 6.0, 3.0, 4.0]
+
+
+def test_embedding_unaligned():
+    table = normal((20, 8), 2)
+    ids = np.array([3, 19, 0, 25], np.int32)
+    out = rocm.rocm_embedding_f32(DEV, unaligned(table), up(ids), 4, 20, 8)
+    assert down(out, np.float32, (4, 8)).tobytes() == oracle.embedding(table, ids).tobytes()
+
+
+@pytest.mark.slow
+def test_embedding_baseline_full():
+    # table[128256,4096] ~ N(0,0.02), ids int32[8192], 5% repeats
+    log("embedding baseline full")
+    table = normal((128256, 4096), 0, 0.0, 0.02)
+    ids = embedding_ids(8192, 128256, seed=0)
+    assert len(np.unique(ids)) < 8192  # repeats present
+    out = rocm.rocm_embedding_f32(DEV, up(table), up(ids), 8192, 128256, 4096)
+    got = down(out, np.float32, (8192, 4096))
+    assert got.tobytes() == oracle.embedding(table, ids).tobytes()

@@ -1,0 +1,229 @@
+"""Pins the CPU oracle (oracle/kore_oracle.c) before anything is compared with it.
+
+Three kinds of check, chosen so that a plausible restatement mistake -- a
+dropped term, a wrong sign or index, pairwise instead of sequential summation,
+half-split vs interleaved pairing, ties-to-even instead of ties-away -- fails
+at least one of them:
+
+  * the reference's own known-answer tests, tightened where the answer is
+    exact (file:line of each);
+  * closed forms / invariants / f64 recomputations of the mathematics;
+  * an independent library (torch, f64) for the transcendental formulas.
+"""
+import math
+import struct
+
+import numpy as np
+import pytest
+
+import oracle
+from inputs import normal, rmsnorm_inputs
+
+
+def f32_bits(x: float) -> int:
+    return struct.unpack("<I", struct.pack("<f", x))[0]
+
+
+# --------------------------------------------------------------- embedding
+def test_embedding_reference_kat():
+    # crates/kore-edge/src/ops/embedding.rs:33-41 (exact assert_eq)
+    w = np.array([1, 2, 3, 4, 5, 6], np.float32).reshape(3, 2)
+    out = oracle.embedding(w, np.array([0, 2, 1], np.uint32))
+    assert out.ravel().tolist() == [1.0, 2.0, 5.0, 6.0, 3.0, 4.0]
+
+
+def test_embedding_out_of_range_reference_kat():
+    # crates/kore-edge/src/ops/embedding.rs:44-50 and kore-nn embedding.rs:146-151
+    w = np.array([1, 2, 3, 4], np.float32).reshape(2, 2)
+    assert oracle.embedding(w, np.array([10], np.uint32)).ravel().tolist() == [0.0, 0.0]
+
+
+def test_embedding_brute_force_and_negative_ids():
+    table = normal((50, 7), 3)
+    ids = np.array([0, 49, 50, -1, 3, 3, 2**31 - 1, -(2**31)], np.int64).astype(np.int32)
+    out = oracle.embedding(table, ids)
+    for t, i in enumerate(ids):
+        u = int(np.uint32(np.int64(i) & 0xFFFFFFFF))
+        want = table[u] if u < 50 else np.zeros(7, np.float32)
+        assert out[t].tobytes() == want.tobytes()
+
+
+# ----------------------------------------------------------------- RMSNorm
+def test_rms_norm_unit_input_reference_kat():
+    # crates/kore-nn/src/rms_norm.rs:193-202 (ones -> 1.0 within 1e-3)
+    y = oracle.rms_norm(np.ones((2, 8), np.float32), np.ones(8, np.float32), 1e-6)
+    assert np.allclose(y, 1.0, atol=1e-3)
+    # exact f32 closed form: sum = 8 -> 8/8 + eps, inv = 1/sqrt(1+1e-6)
+    inv = np.float32(1.0) / np.sqrt(np.float32(1.0) + np.float32(1e-6))
+    assert (y == np.float32(1.0) * inv).all()
+
+
+def test_rms_norm_123_closed_form():
+    # crates/kore-edge/src/ops/norm.rs:44-52 ([1,2,3]: rms = sqrt(14/3))
+    y = oracle.rms_norm(np.array([[1, 2, 3]], np.float32), np.ones(3, np.float32), 1e-5)
+    rms = math.sqrt(14.0 / 3.0 + 1e-5)
+    assert np.allclose(y[0], np.array([1, 2, 3]) / rms, rtol=1e-6)
+    assert 0 < y[0, 0] < 1 and y[0, 2] > 1
+
+
+def test_rms_norm_sum_is_sequential():
+    # Squares [2^24, 1, 1, ...]: a left-to-right f32 fold absorbs every +1
+    # (2^24 + 1 rounds back to 2^24), a pairwise/f64 sum would not.  This pins
+    # the reference's sequential `row.iter().map(|x| x*x).sum()` (cpu_fused.rs:180).
+    cols = 64
+    x = np.ones((1, cols), np.float32)
+    x[0, 0] = 4096.0
+    y = oracle.rms_norm(x, np.ones(cols, np.float32), 0.0)
+    ss = np.float32(2.0**24)
+    inv = np.float32(1.0) / np.sqrt(ss / np.float32(cols))
+    assert y[0, 1] == np.float32(1.0) * inv
+    pairwise = np.float32(1.0) / np.sqrt(np.float32((2.0**24 + cols - 1) / cols))
+    assert y[0, 1] != pairwise
+
+
+def test_rms_norm_weight_and_order():
+    # y_i = (x_i * inv) * g_i: scaling g by 2 scales y exactly by 2; the
+    # invariant mean((y/g)^2) ~= 1 holds to f32 precision; f64 recomputation.
+    x, g = rmsnorm_inputs(16, 256, seed=5)
+    y = oracle.rms_norm(x, g, 1e-6)
+    y2 = oracle.rms_norm(x, 2 * g, 1e-6)
+    assert (y2 == 2 * y).all()
+    assert np.allclose(((y / g) ** 2).mean(axis=1), 1.0, atol=1e-5)
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt((x64**2).mean(axis=1, keepdims=True) + 1e-6) * g
+    assert np.max(np.abs(y - ref) / np.abs(ref)) < 2e-6
+
+
+# ------------------------------------------------------------- activations
+def test_gelu_constant_bits():
+    # FRAC_2_SQRT_PI * FRAC_1_SQRT_2 folded in f32 (activations.rs:25-26) ==
+    # edge's 0.797_884_6 (activation.rs:12) == 0x3F4C422A
+    k = np.float32(1.12837916709551257390) * np.float32(0.707106781186547524401)
+    assert f32_bits(float(k)) == 0x3F4C422A == f32_bits(0.7978846)
+
+
+def test_gelu_reference_kat_and_torch():
+    # crates/kore-nn/src/activations.rs:152-159: gelu(0)=0, gelu(1)>0.8, gelu(-1)<0
+    y = oracle.gelu(np.array([0.0, 1.0, -1.0], np.float32))
+    assert abs(y[0]) < 1e-4 and y[1] > 0.8 and y[2] < 0
+    torch = pytest.importorskip("torch")
+    x = np.concatenate([normal((20000,), 11) * 3, np.linspace(-10, 10, 2001, dtype=np.float32)])
+    ref = torch.nn.functional.gelu(torch.from_numpy(x.astype(np.float64)), approximate="tanh").numpy()
+    got = oracle.gelu(x)
+    assert np.max(np.abs(got - ref)) < 2e-6  # f32 evaluation vs f64 library
+
+
+def test_silu_reference_kat_and_torch():
+    # crates/kore-serve/src/layered/engine.rs:877-886: silu(1)~0.7311, silu(-1)~-0.2689
+    y = oracle.silu(np.array([1.0, -1.0], np.float32))
+    assert abs(y[0] - 0.7311) < 1e-3 and abs(y[1] + 0.2689) < 1e-3
+    torch = pytest.importorskip("torch")
+    x = np.concatenate([normal((20000,), 12) * 4, np.linspace(-30, 30, 3001, dtype=np.float32)])
+    ref = torch.nn.functional.silu(torch.from_numpy(x.astype(np.float64))).numpy()
+    got = oracle.silu(x)
+    rel = np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert np.max(rel[np.abs(ref) > 1e-30]) < 1e-6
+
+
+def test_mul_and_swiglu_composition():
+    a, b = normal((10001,), 1), normal((10001,), 2)
+    assert (oracle.mul(a, b) == a * b).all()  # IEEE f32 product, bit-exact
+    assert (oracle.mul(a, b, threads=4) == a * b).all()
+    s = oracle.swiglu(a, b, threads=3)
+    assert (s == oracle.silu(a) * b).all()
+
+
+# -------------------------------------------------------------------- RoPE
+def test_rope_identity_at_position_zero():
+    # crates/kore-edge/src/ops/rope.rs:43-51
+    d = np.array([1, 2, 3, 4], np.float32).reshape(1, 1, 4)
+    assert (oracle.rope(d, 0, 10000.0) == d).all()
+    assert (oracle.rope(d, 0, 10000.0, interleaved=True) == d).all()
+
+
+def test_rope_changes_values_and_preserves_pair_norm():
+    # rope.rs:53-74 (values change at pos 5; pair (0, 2) norm preserved at pos 7)
+    d = np.array([3, 4, 1, 2], np.float32).reshape(1, 1, 4)
+    assert (np.abs(oracle.rope(d, 5, 10000.0) - d) > 1e-5).any()
+    r = oracle.rope(d, 7, 10000.0)[0, 0]
+    assert abs(math.hypot(r[0], r[2]) - math.hypot(3, 1)) < 1e-5
+
+
+def test_rope_f64_closed_form_both_pairings():
+    seq, heads, hd, start = 37, 3, 16, 1000
+    x = normal((seq, heads, hd), 21)
+    inv = oracle.rope_inv_freq(hd, 10000.0)
+    # inv_freq table is 1/base^(2i/D): check against f64
+    assert np.allclose(inv, 1.0 / 10000.0 ** (np.arange(hd // 2) * 2.0 / hd), rtol=1e-6)
+    pos = (start + np.arange(seq)).astype(np.float32)
+    ang = (pos[:, None] * inv[None, :]).astype(np.float64)  # the reference's f32 product
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    x64 = x.astype(np.float64)
+    half = hd // 2
+    want = x64.copy()
+    want[..., :half] = x64[..., :half] * c - x64[..., half:] * s
+    want[..., half:] = x64[..., :half] * s + x64[..., half:] * c
+    got = oracle.rope(x, start, 10000.0)
+    assert np.max(np.abs(got - want)) < 2e-6
+    want_i = x64.copy()
+    want_i[..., 0::2] = x64[..., 0::2] * c - x64[..., 1::2] * s
+    want_i[..., 1::2] = x64[..., 0::2] * s + x64[..., 1::2] * c
+    got_i = oracle.rope(x, start, 10000.0, interleaved=True)
+    assert np.max(np.abs(got_i - want_i)) < 2e-6
+    # the two pairings really differ
+    assert np.max(np.abs(got - got_i)) > 1e-2
+
+
+def test_rope_batch_positions_restart():
+    x = normal((2, 5, 2, 8), 4)
+    got = oracle.rope(x, 3, 10000.0)
+    assert (got[0] == oracle.rope(x[0], 3, 10000.0)).all()
+    assert (got[1] == oracle.rope(x[1], 3, 10000.0)).all()
+
+
+# --------------------------------------------------------------- pre-quant
+def test_quant_code_ties_away_from_zero():
+    # amax = 127 makes t = (xn*127)/127 == xn exactly for these xn
+    for xn, want in [(2.5, 3), (-2.5, -3), (0.5, 1), (-0.5, -1), (1.5, 2), (126.5, 127),
+                     (0.49999997, 0), (-0.49999997, 0), (127.0, 127), (-127.0, -127), (0.0, 0)]:
+        assert oracle.quant_code(xn, 127.0) == want, xn
+
+
+def test_quant_code_clamp_and_nan():
+    assert oracle.quant_code(float("nan"), 1.0) == 0
+    assert oracle.quant_code(10.0, 1.0) == 127
+    assert oracle.quant_code(-10.0, 1.0) == -128
+    assert oracle.quant_code(float("inf"), 1.0) == 127
+
+
+def test_prequant_brute_force_small_rows():
+    rng = np.random.default_rng(9)
+    for cols in (1, 3, 8, 33):
+        x = rng.standard_normal((5, cols)).astype(np.float32)
+        x[1] = 0.0  # zero row -> amax guard
+        g = (1 + 0.02 * rng.standard_normal(cols)).astype(np.float32)
+        q, s = oracle.rms_norm_quant_i8(x, g, 1e-6)
+        xn = oracle.rms_norm(x, g, 1e-6)  # the same normalisation, shared definition
+        for r in range(5):
+            amax = float(np.max(np.abs(xn[r])))
+            a = 1.0 if amax < 1e-8 else amax
+            assert s[r] == np.float32(np.float32(a) / np.float32(127.0))
+            # every code reconstructs within half a step (f64 check)
+            recon = q[r].astype(np.float64) * (a / 127.0)
+            assert np.all(np.abs(recon - xn[r]) <= a / 127.0 * 0.5 * (1 + 1e-5) + 1e-12)
+            if amax >= 1e-8:
+                assert np.max(np.abs(q[r])) == 127  # the absmax element maps to +-127
+        assert (q[1] == 0).all() and s[1] == np.float32(1.0 / 127.0)
+
+
+def test_quant_math_identities_compiled(tmp_path):
+    """The GPU kernel's fast quotient (Markstein) and ties-away rounding
+    identities, checked in IEEE f32 on the CPU (tests/csrc/check_quant_math.c)."""
+    import os
+    import subprocess
+
+    src = os.path.join(os.path.dirname(__file__), "csrc", "check_quant_math.c")
+    exe = str(tmp_path / "cqm")
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-mfma", "-o", exe, src, "-lm"], check=True)
+    r = subprocess.run([exe, "3000000"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
