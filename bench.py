@@ -1,0 +1,468 @@
+#!/usr/bin/env python3
+"""Benchmark of KORE's fused layer ops on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME[,NAME]] [--no-cpu]
+
+A step is one launch of a fused kernel over one full BASELINE.json config with
+its inputs already resident in HBM.  The headline line is BASELINE configs[1]
+(RoPE over Q[8,2048,32,128] + K[8,2048,8,128], one fused Q+K launch); every
+other config is measured the same way and reported under "kernels".
+
+Per workload:
+  * W untimed warmup launches, then K timed launches bracketed by
+    torch.cuda.synchronize(); HIP events recorded on the stream the kernels are
+    launched on give the average kernel duration;
+  * algorithmic bytes = every input read once + every output written once;
+    achieved GB/s = bytes / average duration; frac = achieved / 8000 GB/s;
+  * inputs are rotated over enough buffer sets to exceed the 256 MB MALL, so
+    HBM is measured, not cache;
+  * cpu_baseline: the oracle (a C restatement of the reference's CPU
+    functions) timed on this host on a bounded sample of the same workload.
+
+Prints ONE JSON line (rank 0).  `--gpus N` with N > 1 exits: this build runs
+on one GPU (see DESIGN.md for how the path shards).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--only", type=str, default="")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU work per baseline sample")
+    return p.parse_args()
+
+
+# ----------------------------------------------------------------- workloads
+class Workload:
+    name = ""
+    desc = ""
+    tokens = 1
+    bytes = 0
+    kernel = ""       # device kernel symbol prefix (for rocprof cross-checks)
+    dtype = "f32"
+
+    def setup(self, torch, lib):  # allocate inputs, return None
+        raise NotImplementedError
+
+    def launch(self, i: int, stream: int) -> int:
+        raise NotImplementedError
+
+    def cpu_sample(self):
+        """-> (callable running the oracle once on the sample, sample_bytes,
+        sample_tokens, threads, description)"""
+        raise NotImplementedError
+
+    def free(self):
+        for k in list(self.__dict__):
+            if k.startswith("_d"):
+                delattr(self, k)
+
+
+def n_sets(bytes_per_set: int, cap: int = 8) -> int:
+    return max(1, min(cap, math.ceil(2 * MALL_BYTES / max(bytes_per_set, 1))))
+
+
+def randn(torch, shape, seed, mean=0.0, std=1.0):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    t = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
+    if std != 1.0:
+        t.mul_(std)
+    if mean != 0.0:
+        t.add_(mean)
+    return t
+
+
+class RopeQK(Workload):
+    name = "rope_qk"
+    B, S, HQ, HK, D = 8, 2048, 32, 8, 128
+    kernel = "rope_vec_kernel"
+
+    def __init__(self, interleaved=False):
+        self.interleaved = interleaved
+        if interleaved:
+            self.name = "rope_qk_interleaved"
+        self.tokens = self.B * self.S
+        self.bytes = 2 * self.B * self.S * (self.HQ + self.HK) * self.D * 4
+        self.desc = (f"RoPE f32 in place, Q[{self.B},{self.S},{self.HQ},{self.D}] + K[{self.B},{self.S},{self.HK},"
+                     f"{self.D}], theta 1e4, positions 0..{self.S - 1}, "
+                     f"{'interleaved' if interleaved else 'half-split'} pairs, one Q+K launch")
+
+    def setup(self, torch, lib):
+        from kore_amd import rocm
+
+        self.lib = lib
+        self._dq = randn(torch, (self.B, self.S, self.HQ, self.D), 0)
+        self._dk = randn(torch, (self.B, self.S, self.HK, self.D), 1)
+        self._dinv = torch.from_numpy(rocm.rope_inv_freq_host(self.D, 10000.0)).cuda()
+
+    def launch(self, i, stream):
+        return self.lib.kore_hip_rope_qk_f32(self._dq.data_ptr(), self._dk.data_ptr(), self._dinv.data_ptr(),
+                                             self.B, self.S, self.HQ, self.HK, self.D, 0, int(self.interleaved),
+                                             stream)
+
+    def cpu_sample(self):
+        import oracle
+        from inputs import normal
+
+        q = normal((1, self.S, self.HQ, self.D), 0)
+        k = normal((1, self.S, self.HK, self.D), 1)
+
+        def run():
+            oracle.rope(q, 0, 10000.0, self.interleaved)
+            oracle.rope(k, 0, 10000.0, self.interleaved)
+
+        return run, self.bytes // self.B, self.S, 1, "batch 0 of Q and K (1/8 of the config), single thread"
+
+
+class RMSNorm(Workload):
+    kernel = "row_norm_kernel"
+
+    def __init__(self, rows, cols):
+        self.rows, self.cols = rows, cols
+        self.name = f"rms_norm_{rows}x{cols}"
+        self.tokens = rows
+        self.bytes = rows * cols * 4 * 2 + cols * 4
+        self.desc = f"RMSNorm f32 x[{rows},{cols}] ~ N(0,1), w ~ N(1,0.02), eps 1e-6 (bit-exact)"
+
+    def setup(self, torch, lib):
+        self.lib = lib
+        per = self.rows * self.cols * 8
+        self.k = n_sets(per)
+        self._dx = [randn(torch, (self.rows, self.cols), s) for s in range(self.k)]
+        self._dy = [torch.empty_like(self._dx[0]) for _ in range(self.k)]
+        self._dw = randn(torch, (self.cols,), 100, 1.0, 0.02)
+
+    def launch(self, i, stream):
+        j = i % self.k
+        return self.lib.kore_hip_rms_norm_f32(self._dx[j].data_ptr(), self._dw.data_ptr(), self._dy[j].data_ptr(),
+                                              self.rows, self.cols, 1e-6, stream)
+
+    def cpu_sample(self):
+        import oracle
+        from inputs import rmsnorm_inputs
+
+        rows = min(self.rows, 4096)
+        x, g = rmsnorm_inputs(rows, self.cols, 0)
+        return (lambda: oracle.rms_norm(x, g, 1e-6)), rows * self.cols * 8 + self.cols * 4, rows, 1, \
+            f"{rows} rows, single thread"
+
+
+class Swiglu(Workload):
+    name = "swiglu"
+    T, F = 16384, 14336
+    kernel = "binary_vec_kernel"
+
+    def __init__(self):
+        self.tokens = self.T
+        self.bytes = 3 * self.T * self.F * 4
+        self.desc = f"SwiGLU f32 out = silu(gate) * up, gate/up/out [{self.T},{self.F}] ~ N(0,1)"
+
+    def setup(self, torch, lib):
+        self.lib = lib
+        self._dg = randn(torch, (self.T, self.F), 0)
+        self._du = randn(torch, (self.T, self.F), 1)
+        self._do = torch.empty_like(self._dg)
+
+    def launch(self, i, stream):
+        return self.lib.kore_hip_swiglu_f32(self._dg.data_ptr(), self._du.data_ptr(), self._do.data_ptr(),
+                                            self.T * self.F, stream)
+
+    def cpu_sample(self):
+        import oracle
+        from inputs import normal
+
+        rows = 512
+        g, u = normal((rows, self.F), 0), normal((rows, self.F), 1)
+        thr = os.cpu_count() or 1
+        return (lambda: oracle.swiglu(g, u, threads=thr)), 3 * rows * self.F * 4, rows, thr, \
+            f"{rows} of {self.T} rows; silu single thread, mul on {thr} threads (rayon in the reference)"
+
+
+class Gelu(Workload):
+    name = "gelu"
+    T, F = 16384, 14336
+    kernel = "unary_vec_kernel"
+
+    def __init__(self):
+        self.tokens = self.T
+        self.bytes = 2 * self.T * self.F * 4
+        self.desc = f"GELU (tanh form) f32 x[{self.T},{self.F}] ~ N(0,1)"
+
+    def setup(self, torch, lib):
+        self.lib = lib
+        self._dx = randn(torch, (self.T, self.F), 0)
+        self._dy = torch.empty_like(self._dx)
+
+    def launch(self, i, stream):
+        return self.lib.kore_hip_gelu_f32(self._dx.data_ptr(), self._dy.data_ptr(), self.T * self.F, stream)
+
+    def cpu_sample(self):
+        import oracle
+        from inputs import normal
+
+        rows = 256
+        x = normal((rows, self.F), 0)
+        return (lambda: oracle.gelu(x)), 2 * rows * self.F * 4, rows, 1, f"{rows} of {self.T} rows, single thread"
+
+
+class Embedding(Workload):
+    name = "embedding"
+    V, D, N = 128256, 4096, 8192
+    kernel = "embedding_vec_kernel"
+
+    def __init__(self):
+        self.tokens = self.N
+        self.bytes = self.N * self.D * 4 * 2 + self.N * 4
+        self.desc = (f"Embedding gather f32 table[{self.V},{self.D}] ~ N(0,0.02), ids int32[{self.N}] "
+                     "uniform with 5% repeats (bit-exact)")
+
+    def setup(self, torch, lib):
+        from inputs import embedding_ids
+
+        self.lib = lib
+        self._dt = randn(torch, (self.V, self.D), 0, 0.0, 0.02)
+        self.k = 4
+        self._dids = [torch.from_numpy(embedding_ids(self.N, self.V, seed=s)).cuda() for s in range(self.k)]
+        self._do = [torch.empty((self.N, self.D), device="cuda") for _ in range(self.k)]
+
+    def launch(self, i, stream):
+        j = i % self.k
+        return self.lib.kore_hip_embedding_f32(self._dt.data_ptr(), self._dids[j].data_ptr(), self._do[j].data_ptr(),
+                                               self.N, self.V, self.D, stream)
+
+    def cpu_sample(self):
+        import oracle
+        from inputs import embedding_ids
+
+        table = np.full((self.V, self.D), 0.5, np.float32)  # values do not change copy speed
+        ids = embedding_ids(self.N, self.V, 0)
+        return (lambda: oracle.embedding(table, ids)), self.bytes, self.N, 1, \
+            "full config (values constant), single thread"
+
+
+class Prequant(Workload):
+    kernel = "row_norm_kernel"
+
+    def __init__(self, rows, cols=2560):
+        self.rows, self.cols = rows, cols
+        self.name = f"prequant_{rows}x{cols}"
+        self.tokens = rows
+        self.bytes = rows * cols * 4 + rows * cols + rows * 4 + cols * 4
+        self.desc = (f"BitLinear pre-quant x[{rows},{cols}] (1% outliers x20) -> RMSNorm -> int8 codes + f32 "
+                     "scale per row (bit-exact)")
+
+    def setup(self, torch, lib):
+        self.lib = lib
+        self.k = n_sets(self.rows * self.cols * 5, cap=16)
+        self._dx = []
+        for s in range(self.k):
+            x = randn(torch, (self.rows, self.cols), s)
+            g = torch.Generator(device="cuda")
+            g.manual_seed(1000 + s)
+            m = torch.rand((self.rows, self.cols), generator=g, device="cuda") < 0.01
+            x[m] *= 20.0
+            self._dx.append(x)
+        self._dq = [torch.empty((self.rows, self.cols), dtype=torch.int8, device="cuda") for _ in range(self.k)]
+        self._ds = [torch.empty((self.rows,), device="cuda") for _ in range(self.k)]
+        self._dw = randn(torch, (self.cols,), 100, 1.0, 0.02)
+
+    def launch(self, i, stream):
+        j = i % self.k
+        return self.lib.kore_hip_rms_norm_quant_i8(self._dx[j].data_ptr(), self._dw.data_ptr(),
+                                                   self._dq[j].data_ptr(), self._ds[j].data_ptr(), self.rows,
+                                                   self.cols, 1e-6, stream)
+
+    def cpu_sample(self):
+        import oracle
+        from inputs import prequant_inputs
+
+        x, g = prequant_inputs(self.rows, self.cols, 0)
+        return (lambda: oracle.rms_norm_quant_i8(x, g, 1e-6)), self.bytes, self.rows, 1, \
+            "full config, single thread"
+
+
+class Copy(Workload):
+    """A plain 1 GiB device copy through the gather kernel with ids = 0..N-1;
+    used to calibrate rocprof's FETCH_SIZE / WRITE_SIZE counters."""
+    name = "copy_1gib"
+    N, D = 65536, 4096
+    kernel = "embedding_vec_kernel"
+
+    def __init__(self):
+        self.tokens = self.N
+        self.bytes = self.N * self.D * 4 * 2 + self.N * 4
+        self.desc = "calibration copy: 1 GiB read + 1 GiB written (gather with ids 0..N-1)"
+
+    def setup(self, torch, lib):
+        self.lib = lib
+        self._dt = randn(torch, (self.N, self.D), 0)
+        self._dids = torch.arange(self.N, dtype=torch.int32, device="cuda")
+        self._do = torch.empty_like(self._dt)
+
+    def launch(self, i, stream):
+        return self.lib.kore_hip_embedding_f32(self._dt.data_ptr(), self._dids.data_ptr(), self._do.data_ptr(),
+                                               self.N, self.N, self.D, stream)
+
+    def cpu_sample(self):
+        return None
+
+
+def all_workloads():
+    return [RopeQK(False), RopeQK(True), RMSNorm(32, 2048), RMSNorm(16384, 2048), Swiglu(), Gelu(), Embedding(),
+            Prequant(4096), Prequant(64), Prequant(1), Copy()]
+
+
+# ------------------------------------------------------------------ measure
+def time_gpu(torch, w: Workload, steps: int, warmup: int):
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    for i in range(warmup):
+        rc = w.launch(i, sp)
+        if rc != 0:
+            raise RuntimeError(f"{w.name}: launch returned {rc}")
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(steps):
+        rc = w.launch(warmup + i, sp)
+        if rc != 0:
+            raise RuntimeError(f"{w.name}: launch returned {rc}")
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = ev0.elapsed_time(ev1)
+    return ev_ms / steps, wall
+
+
+def time_cpu(w: Workload, budget_s: float):
+    s = w.cpu_sample()
+    if s is None:
+        return None
+    run, nbytes, ntok, threads, desc = s
+    run()  # warm (page-in, libm init)
+    reps, t = 0, 0.0
+    t0 = time.perf_counter()
+    while True:
+        run()
+        reps += 1
+        t = time.perf_counter() - t0
+        if t >= budget_s or reps >= 1000:
+            break
+    per = t / reps
+    return {"value": round(nbytes / per / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "ns_per_token": round(per / ntok * 1e9, 1), "seconds": round(t, 2), "reps": reps,
+            "sample": desc, "host_cores": os.cpu_count()}
+
+
+def load_traffic():
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE, scaled by the copy-kernel calibration), if a committed summary
+    exists: profiles/hbm_traffic.txt, lines `workload fetch_bytes write_bytes`."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+    out = {}
+    if os.path.exists(path):
+        for line in open(path):
+            f = line.split()
+            if len(f) == 3 and not line.startswith("#"):
+                try:
+                    out[f[0]] = int(float(f[1])) + int(float(f[2]))
+                except ValueError:
+                    pass
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested). The fused layer ops are "
+              "row/element independent and shard by token rows with no exchange; see DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import kore_amd
+
+    lib = kore_amd.load_library()
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    only = set(filter(None, args.only.split(",")))
+    works = [w for w in all_workloads() if not only or w.name in only]
+    if not only:
+        works = [w for w in works if w.name != "copy_1gib"]
+    traffic = load_traffic()
+    results = {}
+    for w in works:
+        print(f"[bench] {w.name}: setup", file=sys.stderr, flush=True)
+        w.setup(torch, lib)
+        torch.cuda.synchronize()
+        steps = args.steps if w.bytes >= (64 << 20) else max(args.steps, 200)
+        print(f"[bench] {w.name}: {args.warmup} warmup + {steps} timed launches", file=sys.stderr, flush=True)
+        ms, wall = time_gpu(torch, w, steps, args.warmup)
+        gbs = w.bytes / (ms * 1e-3) / 1e9
+        r = {
+            "workload": w.desc, "kernel": w.kernel, "bytes_per_launch": w.bytes, "tokens": w.tokens,
+            "kernel_us": round(ms * 1e3, 3), "achieved_gbs": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
+            "ns_per_token": round(ms * 1e6 / w.tokens, 3), "steps": steps, "wall_s": round(wall, 4),
+            "wall_gbs": round(w.bytes * steps / wall / 1e9, 1),
+        }
+        if w.name in traffic:
+            r["hbm_traffic_bytes"] = traffic[w.name]
+        w.free()
+        torch.cuda.empty_cache()
+        if not args.no_cpu:
+            print(f"[bench] {w.name}: cpu baseline", file=sys.stderr, flush=True)
+            r["cpu_baseline"] = time_cpu(w, args.cpu_seconds if w.name == "rope_qk" else args.cpu_seconds / 3)
+        results[w.name] = r
+        print(f"[bench] {w.name}: {r['kernel_us']} us, {r['achieved_gbs']} GB/s ({100 * r['frac_of_peak']:.1f}% "
+              f"of peak), {r['ns_per_token']} ns/token", file=sys.stderr, flush=True)
+
+    head_name = "rope_qk" if "rope_qk" in results else next(iter(results))
+    h = results[head_name]
+    steps = h["steps"]
+    line = {
+        "metric": "achieved HBM GB/s and % of MI355X HBM peak per fused kernel; ns/token",
+        "value": round(h["bytes_per_launch"] * steps / h["wall_s"] / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(h["wall_s"] / steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) inputs of the BASELINE shapes)",
+        "config": {"workload": h["workload"], "kernel": h["kernel"], "bytes_per_step": h["bytes_per_launch"],
+                   "tokens_per_step": h["tokens"], "ns_per_token": h["ns_per_token"]},
+        "roofline": {"bound": "hbm", "achieved": h["achieved_gbs"], "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": h["frac_of_peak"], "traffic": h.get("hbm_traffic_bytes")},
+        "cpu_baseline": h.get("cpu_baseline"),
+        "kernels": results,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -4,52 +4,72 @@
 // Roofline: HBM.  Bytes per row: cols*4 read, plus cols*4 written (RMSNorm)
 // or cols + 4 written (pre-quant); the weight vector stays in L2.
 //
-// Why a "row engine" instead of a tree reduction: the reference sums x^2 with
-// a left-to-right f32 fold (crates/kore-kernels/src/cpu_fused.rs:180).  A tree
-// sum lands a few ulps away, which moves inv_rms and flips int8 codes that sit
-// on a rounding boundary.  The engine reproduces the fold exactly and still
-// keeps every HBM access coalesced:
+// The reference sums x^2 with a left-to-right f32 fold
+// (crates/kore-kernels/src/cpu_fused.rs:180).  A tree sum lands a few ulps
+// away, which moves inv_rms and flips int8 codes on rounding boundaries, so
+// the fold must be reproduced exactly.  A plain sequential walk costs one
+// dependent add (~8 cycles on gfx950) per element -- ~8.5 us for a 2560-wide
+// row, longer than the whole HBM budget of the pre-quant config.  The engine
+// below computes the same bits with a *segmented exact fold*:
 //
-//   * one wave owns kRowsPerWave rows.  It loads them with wave-wide
-//     global_load_dwordx4 (64 lanes x 16 B = 256 columns of one row per
-//     instruction), all loads in flight before the first use, and keeps the
-//     values in VGPRs until the output is written (one HBM read per byte);
-//   * per 256-column chunk, every lane squares its float4s and writes them to
-//     the wave's private LDS tile [kRowsPerWave][256 + pad];
-//   * lane r of the wave then walks row r of the tile in column order adding
-//     one square at a time -- the reference's exact fold -- with the tile read
-//     as ds_read_b128.  The pad (4 floats) puts the rows' reads on disjoint
-//     banks;
-//   * inv_rms = 1 / sqrt(ss / cols + eps) with IEEE sqrt and division (the
-//     library is built with correctly rounded f32 divide/sqrt), broadcast with
-//     v_readlane; the epilogue is element-parallel over all 64 lanes.
+//   Row split into 64 contiguous segments, segment j owned by lane j.
+//   phase 0  every lane sums its segment (any order) and a wave scan turns the
+//            sums into an estimate of the running sum at its segment start;
+//   phase 1  the estimate names a binade E = [2^E, 2^(E+1)) (grid g = 2^(E-23));
+//            the lane folds its segment twice, from sigma_0 = 2^E and
+//            sigma_1 = 2^E + g (E = -126: from 0 and 2^-149), giving increments
+//            d_p = w_p - sigma_p (NaN if the walk left the binade);
+//   resolve  walk the segments in order with the exact running sum s: if s is
+//            in the segment's binade, p = lsb(s), and t = s + d_p < 2^(E+1),
+//            the segment's true end is t; otherwise fold it sequentially from
+//            s.
+// Exactness: inside one binade s -> RN(s + a) commutes with a shift of s by
+// an even number of ulps (round-half-even only looks at the last bit), so the
+// walk from s is the walk from sigma_p shifted by s - sigma_p, as long as it
+// stays below 2^(E+1) -- which t < 2^(E+1) certifies.  Lane 0 folds from the
+// true start 0, so its result is exact with no condition.  The estimate only
+// decides how often the resolve falls back (binade crossings: ~log2(sum)
+// segments per row); it never affects a bit of the result.  The algorithm is
+// checked against the plain fold on adversarial rows by the CPU test suite
+// (tests/csrc/check_segmented_fold.c restates this kernel in scalar C).
 //
-// A wave's LDS traffic never crosses waves, so there is no barrier: LDS
+// Data movement per wave (R rows):
+//   * rows loaded with wave-wide global_load_dwordx4 (coalesced, 1 KiB per
+//     instruction), all in flight before first use, kept in VGPRs for the
+//     epilogue: one HBM read per byte;
+//   * per row, squares pass through a wave-private LDS tile once to put
+//     segment j into lane j (odd float4 pitch: conflict-free ds_read_b128);
+//   * each segment's (d_0, d_1, 2^E, 2^(E+1)) goes to an LDS table; the
+//     resolve runs lane-parallel over the wave's rows (lane r <-> row r);
+//   * segments predicted to fail (walk left the binade, or the estimate sits
+//     within 2^-10 of a binade edge) keep their squares in LDS slots so the
+//     fallback fold reads LDS; an unpredicted failure re-reads the segment
+//     from global memory (L2/MALL) -- rare, and still exact.
+// A wave's LDS traffic never crosses waves, so there are no barriers: LDS
 // operations from one wave complete in issue order.
 //
-// Pre-quant epilogue (one pass, codes bit-exact):
-//   xn   = (x * inv) * w                          (cpu_fused.rs:185)
+// Epilogue (element-parallel over all 64 lanes, coalesced layout):
+//   inv  = 1 / sqrt(ss / cols + eps)   IEEE sqrt and division (cpu_fused.rs:181-182)
+//   xn   = (x * inv) * w                                      (cpu_fused.rs:185)
+// Pre-quant additionally:
 //   amax = max |xn| (wave max: order-free, exact); 1.0 if amax < 1e-8
-//   t    = (xn * 127) / amax                      IEEE quotient, obtained with
+//   t    = (xn * 127) / amax  as the IEEE quotient, obtained with
 //          y = 1/amax (IEEE), q0 = a*y, r = fma(-amax, q0, a), t = fma(r, y, q0)
-//          (Markstein's correction: with y the correctly rounded reciprocal,
-//          t is the correctly rounded quotient -- checked exhaustively against
-//          IEEE division on the CPU by the test suite)
-//   code = trunc(t + copysign(0.5 - 2^-25, t)), then clamp to [-128, 127];
-//          equal to round-half-away(t) for |t| < 2^23 (also checked on the
-//          CPU over every float in range); v_cvt_i32_f32 maps NaN to 0 and
-//          saturates, like Rust's `as i8` after clamp.
+//          (Markstein: with y the correctly rounded reciprocal, t is the
+//          correctly rounded quotient -- checked on the CPU by the test suite)
+//   code = trunc(t + copysign(0.5 - 2^-25, t)) clamped to [-128, 127];
+//          equal to round-half-away(t) for |t| < 2^23 (checked on the CPU over
+//          every float in range); v_cvt_i32_f32 maps NaN to 0 and saturates,
+//          like Rust's `as i8` after clamp.
 #include "common.hpp"
 #include "kore_hip_internal.hpp"
 
 namespace kore {
 
-constexpr int kRowsPerWave = 4;
 constexpr int kWavesPerBlock = 4;
 constexpr int kNormBlock = kWave * kWavesPerBlock;
-constexpr int kChunk = 256;                 // columns per wave-wide float4 load
-constexpr int kPitch = kChunk + 4;          // LDS row pitch (floats)
-constexpr int kTileFloats = kRowsPerWave * kPitch;
+constexpr int kSegs = kWave;  // segments per row: one per lane
+constexpr int kSlots = 8;     // LDS fallback slots per row
 
 enum class NormOut { F32, I8 };
 
@@ -64,6 +84,15 @@ struct NormArgs {
     float eps;
 };
 
+// Odd pitch (in float4) of the transpose tile: 64 lanes reading 16 B at
+// segment starts j*pitch hit 16 distinct 16-byte bank groups per 16 lanes.
+__host__ __device__ constexpr uint32_t tile_pitch4(uint32_t sl4) { return sl4 + ((sl4 & 1u) ? 2u : 1u); }
+
+// Per-wave LDS: transpose tile, run table, fallback slots, run-end bytes.
+__host__ __device__ constexpr uint32_t wave_lds_f4(uint32_t sl4, uint32_t rows) {
+    return kSegs * tile_pitch4(sl4) + rows * kSegs + rows * kSlots * sl4 + (rows * kSegs + 15) / 16;
+}
+
 __device__ __forceinline__ int32_t cvt_i32_sat(float v) {
     // v_cvt_i32_f32: round toward zero, saturating, NaN -> 0.  Written as asm
     // because a C++ float->int cast of NaN is undefined.
@@ -72,8 +101,6 @@ __device__ __forceinline__ int32_t cvt_i32_sat(float v) {
     return r;
 }
 
-// int8 code of one normalised value; see the header comment for the proof
-// obligations (both are exercised by the CPU test suite).
 __device__ __forceinline__ uint32_t quant_code(float xn, float amax, float rcp_amax) {
     float a = xn * 127.0f;
     float q0 = a * rcp_amax;
@@ -93,127 +120,343 @@ __device__ __forceinline__ float abs_max4(float m, f32x4 v) {
     return m;
 }
 
-// Adds the 256 squares of this lane's tile row to ss in column order.  The
-// reads are issued in blocks of 8 float4 ahead of the adds that consume them.
-__device__ __forceinline__ float fold_tile_row(const f32x4* __restrict__ tp, float ss) {
-    constexpr int kBlk = 8;
-    constexpr int kN = kChunk / 4;  // 64 float4
-    f32x4 a[kBlk], b[kBlk];
-#pragma unroll
-    for (int j = 0; j < kBlk; ++j) a[j] = tp[j];
-    // Rolled loop: a fully unrolled fold lets the scheduler hoist all 64
-    // reads (256 VGPRs) above the adds and evict the row cache to AGPRs.
-#pragma unroll 1
-    for (int blk = 0; blk < kN / kBlk; blk += 2) {
-#pragma unroll
-        for (int j = 0; j < kBlk; ++j) b[j] = tp[(blk + 1) * kBlk + j];
-#pragma unroll
-        for (int j = 0; j < kBlk; ++j) {
-            ss = ss + a[j].x;
-            ss = ss + a[j].y;
-            ss = ss + a[j].z;
-            ss = ss + a[j].w;
-        }
-        if (blk + 2 < kN / kBlk) {
-#pragma unroll
-            for (int j = 0; j < kBlk; ++j) a[j] = tp[(blk + 2) * kBlk + j];
-        }
-#pragma unroll
-        for (int j = 0; j < kBlk; ++j) {
-            ss = ss + b[j].x;
-            ss = ss + b[j].y;
-            ss = ss + b[j].z;
-            ss = ss + b[j].w;
-        }
-    }
-    return ss;
+__device__ __forceinline__ float fold4(float s, f32x4 a) {
+    s = s + a.x;
+    s = s + a.y;
+    s = s + a.z;
+    s = s + a.w;
+    return s;
 }
 
-// Vector path: cols % 4 == 0, cols <= NCH * 256, x/w/y 16-byte aligned and q
-// 4-byte aligned.  Grid: one block per kWavesPerBlock * kRowsPerWave rows.
-template <NormOut Out, int NCH>
+__device__ __forceinline__ float sum4(f32x4 a) { return (a.x + a.y) + (a.z + a.w); }
+
+// Orders this wave's LDS accesses across lanes.  A lane reading what another
+// lane of the same wave wrote (or overwriting what another lane read) needs
+// it: the compiler reasons per thread, sees different addresses, and would
+// otherwise move the load above the store.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// DPP move of v with lanes that have no source reading 0 (bound_ctrl off,
+// old = 0).  ctrl/row_mask follow the gfx9 DPP encoding.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp0(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, kRowMask, 0xf, false));
+}
+
+// Inclusive wave64 prefix sum in DPP: row_shr 1/2/4/8 within each row of 16
+// lanes, then row_bcast:15 and row_bcast:31 carry the row totals forward.
+// Used only for the segment-start estimates, so its summation order is free.
+__device__ __forceinline__ float wave_incl_scan(float v) {
+    v += dpp0<0x111, 0xf>(v);  // row_shr:1
+    v += dpp0<0x112, 0xf>(v);  // row_shr:2
+    v += dpp0<0x114, 0xf>(v);  // row_shr:4
+    v += dpp0<0x118, 0xf>(v);  // row_shr:8
+    v += dpp0<0x142, 0xa>(v);  // row_bcast:15 -> rows 1, 3
+    v += dpp0<0x143, 0xc>(v);  // row_bcast:31 -> rows 2, 3
+    return v;
+}
+
+// Identity element of the run scan: F(p) = p (bits 0b10), D = 0, no head.
+constexpr int kIdBits = 2;
+
+// One element of the suffix scan over a run of segments.
+//   bits: F(0) | F(1) << 1 | head << 2 ; F(p) = parity after the span given
+//         entry parity p; head = the span already reaches its run's end.
+//   d0/d1: exact increment of the span for entry parity 0 / 1.
+struct RunElem {
+    int bits;
+    float d0, d1;
+};
+
+// x = (span that starts first) then y = (span that follows).  Exact: inside a
+// run every increment is a multiple of one ulp and sums stay below the binade
+// top whenever the resolve accepts them (see the header comment).
+__device__ __forceinline__ RunElem run_compose(RunElem x, RunElem y) {
+    const int f0 = x.bits & 1, f1 = (x.bits >> 1) & 1;
+    RunElem r;
+    r.bits = ((y.bits >> f0) & 1) | (((y.bits >> f1) & 1) << 1);
+    r.d0 = x.d0 + (f0 ? y.d1 : y.d0);
+    r.d1 = x.d1 + (f1 ? y.d1 : y.d0);
+    return r;
+}
+
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ int dppi(int v, int id) {
+    return __builtin_amdgcn_update_dpp(id, v, kCtrl, kRowMask, 0xf, false);
+}
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, kRowMask, 0xf, false));
+}
+
+// One Hillis-Steele step of the segmented scan: lane L takes the element k
+// lanes below it (a LATER span, since lanes hold segments in reverse order)
+// unless L's own span already ends its run.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ void run_scan_step(RunElem& e) {
+    RunElem lo;
+    lo.bits = dppi<kCtrl, kRowMask>(e.bits, kIdBits);
+    lo.d0 = dppf<kCtrl, kRowMask>(e.d0);
+    lo.d1 = dppf<kCtrl, kRowMask>(e.d1);
+    if (!(e.bits & 4)) {
+        RunElem c = run_compose(e, lo);
+        e.bits = c.bits | (lo.bits & 4);
+        e.d0 = c.d0;
+        e.d1 = c.d1;
+    }
+}
+
+__device__ __forceinline__ void run_scan(RunElem& e) {
+    run_scan_step<0x111, 0xf>(e);  // row_shr:1
+    run_scan_step<0x112, 0xf>(e);  // row_shr:2
+    run_scan_step<0x114, 0xf>(e);  // row_shr:4
+    run_scan_step<0x118, 0xf>(e);  // row_shr:8
+    run_scan_step<0x142, 0xa>(e);  // row_bcast:15 -> rows 1, 3
+    run_scan_step<0x143, 0xc>(e);  // row_bcast:31 -> rows 2, 3
+}
+
+// Vector path: cols % 4 == 0, x/w/y 16-byte aligned, q 4-byte aligned,
+// ceil(cols/4 / 64) <= SL4.  Segment j covers float4 [j*SL4, (j+1)*SL4).
+// Grid: one block per kWavesPerBlock * R rows; dynamic LDS =
+// kWavesPerBlock * wave_lds_f4(SL4, R) float4.
+template <NormOut Out, int SL4, int R>
 __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
-    __shared__ f32x4 lds[kWavesPerBlock * kTileFloats / 4];
+    constexpr int NCH = SL4;  // 64*SL4 float4 cover the row: SL4 wave-wide chunks
+    constexpr int TP4 = (int)tile_pitch4(SL4);
+    constexpr uint32_t kWaveF4 = wave_lds_f4(SL4, R);
+    extern __shared__ f32x4 lds4[];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const uint64_t row0 = ((uint64_t)blockIdx.x * kWavesPerBlock + wave) * kRowsPerWave;
+    const uint64_t row0 = ((uint64_t)blockIdx.x * kWavesPerBlock + wave) * R;
     if (row0 >= args.rows) return;  // uniform per wave; no block barrier follows
     const uint64_t left = args.rows - row0;
-    const int nrows = left < (uint64_t)kRowsPerWave ? (int)left : kRowsPerWave;
-    const uint32_t cols = args.cols;
-    const uint32_t cols4 = cols >> 2;
-    const int nch = (int)((cols4 + kWave - 1) / kWave);
-    float* tile = reinterpret_cast<float*>(lds) + wave * kTileFloats;
-    const f32x4* x4 = reinterpret_cast<const f32x4*>(args.x) + row0 * cols4;
-    const f32x4* w4 = reinterpret_cast<const f32x4*>(args.w);
+    const int nrows = left < (uint64_t)R ? (int)left : R;
+    const uint32_t cols4 = args.cols >> 2;
+    const int nseg = (int)((cols4 + SL4 - 1) / SL4);
+    f32x4* tile = lds4 + (size_t)wave * kWaveF4;
+    f32x4* table = tile + kSegs * TP4;        // [R][64] (D0, D1, bot, top)
+    f32x4* slots = table + R * kSegs;         // [R][kSlots][SL4]
+    uint8_t* nexts = reinterpret_cast<uint8_t*>(slots + R * kSlots * SL4);  // [R][64]
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(args.x);
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    const float inf = __builtin_inff();
+    const float qnan = __builtin_nanf("");
 
-    // All HBM reads of the wave, chunk-major so chunk 0 of every row lands
-    // first and the fold can start while the rest streams in.
-    f32x4 xv[NCH][kRowsPerWave];
+    // ---- HBM reads: coalesced, chunk-major, all in flight.
+    f32x4 xv[R][NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const uint32_t f = (uint32_t)c * kWave + lane;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            xv[r][c] = (f < cols4 && r < nrows) ? ld_stream(x4 + (row0 + r) * cols4 + f) : zero;
+    }
+
+    // Lane L holds segment j = 63 - L, so a forward (lane-increasing) scan
+    // composes each segment with the segments after it.
+    const int seg_id = kSegs - 1 - lane;
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+
+    // ---- per row: transpose, estimate, artificial walks, run scan.
+    uint64_t pmask[R];  // predicted-fallback segments, bit j = segment j
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        pmask[r] = 0;
+        if (r < nrows) {
+            wave_lds_sync();  // previous row's tile reads precede these writes
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const int f = c * kWave + lane;  // float4 index in the row
+                tile[(f / SL4) * TP4 + (f % SL4)] = xv[r][c] * xv[r][c];  // zero past the end
+            }
+            wave_lds_sync();
+            f32x4 seg[SL4];
+            float ssum = 0.0f;
+#pragma unroll
+            for (int k = 0; k < SL4; ++k) {
+                seg[k] = tile[seg_id * TP4 + k];
+                ssum += sum4(seg[k]);
+            }
+            // Estimate of the running sum at this segment's start = sum over
+            // the segments before it = lanes above this one.
+            const float incl = wave_incl_scan(ssum);
+            const float total = read_lane(incl, kWave - 1);
+            const float est = total - incl;  // any summation order: an estimate
+            const bool empty = seg_id >= nseg;
+            float sig0, sig1, bot, top;
+            int key;
+            if (empty) {
+                sig0 = 0.0f; sig1 = 0.0f; bot = 0.0f; top = inf; key = 1024;
+            } else if (seg_id == 0) {
+                // The true start of segment 0 is +0: fold from it exactly.
+                sig0 = 0.0f; sig1 = 0.0f; bot = 0.0f; top = inf; key = 1025;
+            } else {
+                const uint32_t ef = __float_as_uint(est) >> 23;  // est >= 0
+                key = (int)ef;
+                if (ef >= 255u) {           // Inf/NaN estimate: always fall back
+                    sig0 = 0.0f; sig1 = 0.0f; bot = inf; top = 0.0f;
+                } else if (ef <= 1u) {      // [0, 2^-125): one grid of 2^-149
+                    sig0 = 0.0f; sig1 = __uint_as_float(1u); bot = 0.0f; top = __uint_as_float(2u << 23);
+                    key = 1;
+                } else {
+                    sig0 = __uint_as_float(ef << 23);
+                    sig1 = __uint_as_float((ef << 23) | 1u);
+                    bot = sig0;
+                    top = __uint_as_float((ef + 1u) << 23);  // ef + 1 == 255 -> +Inf
+                }
+            }
+            float w0 = sig0, w1 = sig1;
+#pragma unroll
+            for (int k = 0; k < SL4; ++k) {
+                const f32x4 a = seg[k];
+                w0 = w0 + a.x; w1 = w1 + a.x;
+                w0 = w0 + a.y; w1 = w1 + a.y;
+                w0 = w0 + a.z; w1 = w1 + a.z;
+                w0 = w0 + a.w; w1 = w1 + a.w;
+            }
+            const bool ok0 = w0 < top;
+            const bool ok1 = (seg_id == 0 || empty) ? ok0 : (w1 < top);
+            // A segment whose estimated span touches a binade edge (within
+            // 2^-10; the estimate's own error is below cols * 2^-24 relative)
+            // will most likely cross it: keep it out of runs so that it is
+            // folded alone, from its LDS slot, instead of breaking a jump.
+            const bool edge = seg_id != 0 && !empty &&
+                              (est < bot * 1.0009765625f || est + ssum >= top * 0.9990234375f);
+            const bool valid = ok0 && ok1 && !edge;
+            // Scan element of this single segment.
+            RunElem e;
+            if (empty) {
+                e.bits = kIdBits; e.d0 = 0.0f; e.d1 = 0.0f;
+            } else {
+                e.d0 = ok0 ? w0 - sig0 : qnan;
+                e.d1 = (seg_id == 0) ? e.d0 : (ok1 ? w1 - sig1 : qnan);
+                e.bits = (int)(__float_as_uint(w0) & 1u) |
+                         (seg_id == 0 ? 0 : (int)((__float_as_uint(w1) & 1u) << 1));
+            }
+            // Runs: maximal spans of valid segments with one binade key.  An
+            // invalid segment is a run of its own.  This lane's span ends
+            // its run when the next segment (lane - 1) is in another run.
+            const int key_me = valid ? key : 2048 + seg_id;
+            const int key_next = __shfl_up(key_me, 1, kWave);  // segment j+1
+            if (lane == 0 || key_next != key_me) e.bits |= 4;
+            run_scan(e);
+            // How far the span reaches: first run end at or after segment j.
+            const uint64_t ends = __ballot(lane == 0 || key_next != key_me);
+            // ends bit L = lane L ends a run; the run of lane L ends at the
+            // highest lane <= L with its bit set.
+            const uint64_t below = ends & (lt_mask | (1ull << lane));
+            const int end_lane = 63 - __builtin_clzll(below);
+            const int next_seg = kSegs - end_lane;  // (63 - end_lane) + 1
+            f32x4 ent;
+            ent.x = e.d0; ent.y = e.d1; ent.z = bot; ent.w = top;
+            table[r * kSegs + seg_id] = ent;
+            nexts[r * kSegs + seg_id] = (uint8_t)next_seg;
+            // Predicted fallback: the segment cannot join a run.
+            const bool pred = !empty && !valid;
+            const uint64_t m = __builtin_bitreverse64(__ballot(pred));  // bit j = segment j
+            pmask[r] = m;
+            const int slot = __popcll(m & ((1ull << seg_id) - 1ull));
+            if (pred && slot < kSlots) {
+                f32x4* dst = slots + (r * kSlots + slot) * SL4;
+#pragma unroll
+                for (int k = 0; k < SL4; ++k) dst[k] = seg[k];
+            }
+        }
+    }
+
+    // Weights for the epilogue: L2 hits, in flight during the resolve.
+    const f32x4* w4 = reinterpret_cast<const f32x4*>(args.w);
     f32x4 wv[NCH];
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-        const uint32_t c4 = (uint32_t)c * kWave + lane;
-        const bool in_row = c < nch && c4 < cols4;
-#pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r)
-            xv[c][r] = (in_row && r < nrows) ? ld_stream(x4 + (uint64_t)r * cols4 + c4) : zero;
-        wv[c] = in_row ? ld_cached(w4 + c4) : zero;
+        const uint32_t f = (uint32_t)c * kWave + lane;
+        wv[c] = (f < cols4) ? ld_cached(w4 + f) : zero;
     }
 
-    // Sequential sum of squares, lane r <-> row r.  Columns past the end are
-    // zero: adding +0.0 to a non-negative running sum leaves it bit-identical.
+    // ---- resolve: lane r owns row r; one step per run or fallback.
+    wave_lds_sync();  // table, run ends and slots were written by other lanes
+    uint64_t my_mask = pmask[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r) my_mask = (lane == r) ? pmask[r] : my_mask;
     float ss = 0.0f;
+    if (lane < nrows) {
+        const f32x4* trow = table + lane * kSegs;
+        const uint8_t* nrow = nexts + lane * kSegs;
+        const f32x4* xrow = x4 + (row0 + lane) * cols4;
+        int j = 0;
+        while (j < nseg) {
+            const f32x4 e = trow[j];
+            const int nj = nrow[j];
+            const float d = (__float_as_uint(ss) & 1u) ? e.y : e.x;
+            const float t = ss + d;
+            if (ss >= e.z && t < e.w) {
+                ss = t;
+                j = nj;
+            } else {
+                // Sequential fold of segment j from the exact start: the
+                // segment's data is fetched first, then folded in order.
+                f32x4 v[SL4];
+                const int slot = __popcll(my_mask & ((1ull << j) - 1ull));
+                if (((my_mask >> j) & 1ull) && slot < kSlots) {
+                    const f32x4* src = slots + (lane * kSlots + slot) * SL4;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        if (c < nch) {
+                    for (int k = 0; k < SL4; ++k) v[k] = src[k];
+                } else {
 #pragma unroll
-            for (int r = 0; r < kRowsPerWave; ++r) {
-                f32x4 v = xv[c][r];
-                *reinterpret_cast<f32x4*>(tile + r * kPitch + 4 * lane) = v * v;
+                    for (int k = 0; k < SL4; ++k) {
+                        const uint32_t f = (uint32_t)(j * SL4 + k);
+                        const f32x4 xv1 = (f < cols4) ? xrow[f] : zero;
+                        v[k] = xv1 * xv1;
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < SL4; ++k) ss = fold4(ss, v[k]);
+                ++j;
             }
-            if (lane < nrows) ss = fold_tile_row(reinterpret_cast<const f32x4*>(tile + lane * kPitch), ss);
         }
     }
 
     // cpu_fused.rs:181-182 with IEEE sqrt and division.
     float inv_lane = 0.0f;
     if (lane < nrows) {
-        float rms = sqrtf(ss / (float)cols + args.eps);
+        float rms = sqrtf(ss / (float)args.cols + args.eps);
         inv_lane = 1.0f / rms;
     }
-    float inv[kRowsPerWave];
+    float inv[R];
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r) inv[r] = read_lane(inv_lane, r);
+    for (int r = 0; r < R; ++r) inv[r] = read_lane(inv_lane, r);
 
     if (Out == NormOut::F32) {
-        f32x4* y4 = reinterpret_cast<f32x4*>(args.y) + row0 * cols4;
+        f32x4* y4 = reinterpret_cast<f32x4*>(args.y);
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
-            const uint32_t c4 = (uint32_t)c * kWave + lane;
-            if (c < nch && c4 < cols4) {
+            const uint32_t f = (uint32_t)c * kWave + lane;
+            if (f < cols4) {
 #pragma unroll
-                for (int r = 0; r < kRowsPerWave; ++r)
-                    if (r < nrows) st_stream(y4 + (uint64_t)r * cols4 + c4, (xv[c][r] * inv[r]) * wv[c]);
+                for (int r = 0; r < R; ++r)
+                    if (r < nrows) st_stream(y4 + (row0 + r) * cols4 + f, (xv[r][c] * inv[r]) * wv[c]);
             }
         }
     } else {
-        float amax[kRowsPerWave];
+        float amax[R];
 #pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r) amax[r] = 0.0f;
+        for (int r = 0; r < R; ++r) amax[r] = 0.0f;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
 #pragma unroll
-            for (int r = 0; r < kRowsPerWave; ++r) {
-                f32x4 xn = (xv[c][r] * inv[r]) * wv[c];
-                xv[c][r] = xn;
+            for (int r = 0; r < R; ++r) {
+                f32x4 xn = (xv[r][c] * inv[r]) * wv[c];
+                xv[r][c] = xn;
                 amax[r] = abs_max4(amax[r], xn);
             }
         }
-        float rcp[kRowsPerWave];
+        float rcp[R];
 #pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r) {
+        for (int r = 0; r < R; ++r) {
             float m = wave_max(amax[r]);
             m = m < 1e-8f ? 1.0f : m;  // kore-btes/src/quantize.rs:10
             amax[r] = m;
@@ -221,21 +464,21 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
         }
         float my_amax = amax[0];
 #pragma unroll
-        for (int r = 1; r < kRowsPerWave; ++r) my_amax = lane == r ? amax[r] : my_amax;
+        for (int r = 1; r < R; ++r) my_amax = lane == r ? amax[r] : my_amax;
         if (lane < nrows) args.scale[row0 + lane] = my_amax / 127.0f;
-        uint32_t* q4 = reinterpret_cast<uint32_t*>(args.q) + row0 * cols4;
+        uint32_t* q4 = reinterpret_cast<uint32_t*>(args.q);
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
-            const uint32_t c4 = (uint32_t)c * kWave + lane;
-            if (c < nch && c4 < cols4) {
+            const uint32_t f = (uint32_t)c * kWave + lane;
+            if (f < cols4) {
 #pragma unroll
-                for (int r = 0; r < kRowsPerWave; ++r) {
+                for (int r = 0; r < R; ++r) {
                     if (r < nrows) {
-                        const f32x4 v = xv[c][r];
+                        const f32x4 v = xv[r][c];
                         uint32_t p = quant_code(v.x, amax[r], rcp[r]) | (quant_code(v.y, amax[r], rcp[r]) << 8) |
                                      (quant_code(v.z, amax[r], rcp[r]) << 16) |
                                      (quant_code(v.w, amax[r], rcp[r]) << 24);
-                        q4[(uint64_t)r * cols4 + c4] = p;
+                        q4[(row0 + r) * cols4 + f] = p;
                     }
                 }
             }
@@ -244,7 +487,8 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
 }
 
 // Scalar path for any shape/alignment: one thread per row, the reference loop
-// verbatim.  Used for cols % 4 != 0, unaligned views and very long rows.
+// verbatim.  Used for cols % 4 != 0, unaligned views and rows longer than
+// the vector path's register budget.
 template <NormOut Out>
 __global__ __launch_bounds__(64) void row_norm_scalar_kernel(NormArgs args) {
     const uint64_t row = (uint64_t)blockIdx.x * 64 + threadIdx.x;
@@ -272,8 +516,34 @@ __global__ __launch_bounds__(64) void row_norm_scalar_kernel(NormArgs args) {
     }
 }
 
+template <NormOut Out, int SL4, int R>
+static int launch_vec(NormArgs a, hipStream_t s) {
+    const size_t lds = (size_t)kWavesPerBlock * wave_lds_f4(SL4, R) * sizeof(f32x4);
+    const uint64_t rows_per_block = (uint64_t)kWavesPerBlock * R;
+    const uint64_t blocks = (a.rows + rows_per_block - 1) / rows_per_block;
+    if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
+    hipLaunchKernelGGL((row_norm_kernel<Out, SL4, R>), dim3((uint32_t)blocks), dim3(kNormBlock), lds, s, a);
+    return launch_status();
+}
+
+template <NormOut Out, int R>
+static int launch_sl4(NormArgs a, uint32_t nch, hipStream_t s) {
+    if (nch <= 1) return launch_vec<Out, 1, R>(a, s);
+    if (nch <= 2) return launch_vec<Out, 2, R>(a, s);
+    if (nch <= 4) return launch_vec<Out, 4, R>(a, s);
+    if (nch <= 6) return launch_vec<Out, 6, R>(a, s);
+    if (nch <= 8) return launch_vec<Out, 8, R>(a, s);
+    if (R > 2 || nch <= 10) return launch_vec<Out, 10, R>(a, s);
+    if (nch <= 12) return launch_vec<Out, 12, (R < 2 ? R : 2)>(a, s);
+    if (R > 1 || nch <= 16) return launch_vec<Out, 16, (R < 2 ? R : 2)>(a, s);
+    if (nch <= 24) return launch_vec<Out, 24, 1>(a, s);
+    return launch_vec<Out, 32, 1>(a, s);
+}
+
+// Rows per wave: 4 amortises the resolve over more rows when the grid has
+// enough rows to fill the chip; 1 minimises latency for small batches.
 template <NormOut Out>
-static int norm_launch(const NormArgs& a, hipStream_t s) {
+static int norm_launch(NormArgs a, hipStream_t s) {
     if (a.rows == 0) return KORE_HIP_OK;
     if (a.cols == 0) return KORE_HIP_ERR_BAD_DIM;
     if (!a.x || !a.w) return KORE_HIP_ERR_NULL_PTR;
@@ -282,8 +552,8 @@ static int norm_launch(const NormArgs& a, hipStream_t s) {
     uint64_t elems;
     if (!mul_ok(a.rows, a.cols, &elems) || elems > kMaxElements) return KORE_HIP_ERR_OVERFLOW;
     const uint32_t cols4 = a.cols / 4;
-    const int nch = (int)((cols4 + kWave - 1) / kWave);
-    bool vec = a.cols % 4 == 0 && aligned16(a.x) && aligned16(a.w) && nch <= 16;
+    const uint32_t nch = (cols4 + kWave - 1) / kWave;
+    bool vec = a.cols % 4 == 0 && aligned16(a.x) && aligned16(a.w) && nch <= 32;
     if (Out == NormOut::F32) vec = vec && aligned16(a.y);
     else vec = vec && (reinterpret_cast<uintptr_t>(a.q) & 3u) == 0;
     if (!vec) {
@@ -292,24 +562,10 @@ static int norm_launch(const NormArgs& a, hipStream_t s) {
         hipLaunchKernelGGL(row_norm_scalar_kernel<Out>, dim3((uint32_t)blocks), dim3(64), 0, s, a);
         return launch_status();
     }
-    const uint64_t rows_per_block = (uint64_t)kWavesPerBlock * kRowsPerWave;
-    const uint64_t blocks = (a.rows + rows_per_block - 1) / rows_per_block;
-    if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
-    dim3 grid((uint32_t)blocks), block(kNormBlock);
-#define KORE_NORM_CASE(N)                                                           \
-    if (nch <= N) {                                                                 \
-        hipLaunchKernelGGL((row_norm_kernel<Out, N>), grid, block, 0, s, a);         \
-        return launch_status();                                                     \
-    }
-    KORE_NORM_CASE(1)
-    KORE_NORM_CASE(2)
-    KORE_NORM_CASE(4)
-    KORE_NORM_CASE(8)
-    KORE_NORM_CASE(10)
-    KORE_NORM_CASE(12)
-    KORE_NORM_CASE(16)
-#undef KORE_NORM_CASE
-    return KORE_HIP_ERR_BAD_DIM;
+    const bool many = a.rows > 2048;
+    if (many && nch <= 10) return launch_sl4<Out, 4>(a, nch, s);
+    if (many && nch <= 16) return launch_sl4<Out, 2>(a, nch, s);
+    return launch_sl4<Out, 1>(a, nch, s);
 }
 
 }  // namespace kore

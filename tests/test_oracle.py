@@ -227,3 +227,19 @@ def test_quant_math_identities_compiled(tmp_path):
     subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-mfma", "-o", exe, src, "-lm"], check=True)
     r = subprocess.run([exe, "3000000"], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+def test_segmented_exact_fold_compiled(tmp_path):
+    """The row kernels' segmented exact fold (kore_amd/csrc/norm.hip),
+    restated in scalar C with the kernel's segment sizes, estimates, run
+    composition and checks, equals the plain left-to-right f32 fold on
+    adversarial rows (ties, subnormals, overflow, NaN/Inf, zeros, outliers)."""
+    import os
+    import subprocess
+
+    src = os.path.join(os.path.dirname(__file__), "csrc", "check_segmented_fold.c")
+    exe = str(tmp_path / "csf")
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-o", exe, src, "-lm"], check=True)
+    r = subprocess.run([exe, "40000"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "MISMATCH" not in r.stdout
