@@ -66,6 +66,11 @@
 
 namespace kore {
 
+// Rows per wave when the grid has enough rows to fill the chip (cols <= 2560).
+#ifndef KORE_NORM_ROWS_MANY
+#define KORE_NORM_ROWS_MANY 2
+#endif
+
 constexpr int kWavesPerBlock = 4;
 constexpr int kNormBlock = kWave * kWavesPerBlock;
 constexpr int kSegs = kWave;  // segments per row: one per lane
@@ -101,15 +106,25 @@ __device__ __forceinline__ int32_t cvt_i32_sat(float v) {
     return r;
 }
 
-__device__ __forceinline__ uint32_t quant_code(float xn, float amax, float rcp_amax) {
+// Code of one normalised value xn of a row with absmax amax (>= every |xn|
+// of the row, or 1.0 when the row's absmax is below 1e-8).  |t| cannot exceed
+// 127 * (1 + 2^-23) -- |xn| <= amax and both roundings are faithful -- so the
+// reference's clamp to [-128, 127] never binds and is not evaluated; NaN
+// (from NaN inputs or an infinite amax) converts to 0.
+__device__ __forceinline__ int32_t quant_code(float xn, float amax, float rcp_amax) {
     float a = xn * 127.0f;
     float q0 = a * rcp_amax;
     float r = __builtin_fmaf(-amax, q0, a);
     float t = __builtin_fmaf(r, rcp_amax, q0);
     float b = t + __builtin_copysignf(0.49999997f, t);
-    int32_t c = cvt_i32_sat(b);
-    c = c < -128 ? -128 : (c > 127 ? 127 : c);
-    return (uint32_t)c & 0xffu;
+    return cvt_i32_sat(b);
+}
+
+// Four codes -> one dword, byte k = code k (v_perm_b32 byte selects).
+__device__ __forceinline__ uint32_t pack4(int32_t c0, int32_t c1, int32_t c2, int32_t c3) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)c1, (uint32_t)c0, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)c3, (uint32_t)c2, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 __device__ __forceinline__ float abs_max4(float m, f32x4 v) {
@@ -247,13 +262,17 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
     const float qnan = __builtin_nanf("");
 
     // ---- HBM reads: coalesced, chunk-major, all in flight.
+    // Row-major issue order: row 0 lands first and its fold starts while the
+    // other rows are still streaming in.
     f32x4 xv[R][NCH];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const uint32_t f = (uint32_t)c * kWave + lane;
+    for (int r = 0; r < R; ++r) {
+        const f32x4* xr = x4 + (row0 + r) * cols4;
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            xv[r][c] = (f < cols4 && r < nrows) ? ld_stream(x4 + (row0 + r) * cols4 + f) : zero;
+        for (int c = 0; c < NCH; ++c) {
+            const uint32_t f = (uint32_t)c * kWave + lane;
+            xv[r][c] = (f < cols4 && r < nrows) ? ld_stream(xr + f) : zero;
+        }
     }
 
     // Lane L holds segment j = 63 - L, so a forward (lane-increasing) scan
@@ -261,109 +280,124 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
     const int seg_id = kSegs - 1 - lane;
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
-    // ---- per row: transpose, estimate, artificial walks, run scan.
+    // ---- transpose every row through the wave's tile (sequentially: one
+    // tile), then run the per-row phases for all rows at once so their
+    // dependency chains interleave.  Rows past nrows compute on zeros and are
+    // never stored or resolved.
+    f32x4 seg[R][SL4];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        wave_lds_sync();  // previous tile reads precede these writes
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int f = c * kWave + lane;  // float4 index in the row
+            tile[(f / SL4) * TP4 + (f % SL4)] = xv[r][c] * xv[r][c];  // zero past the end
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int k = 0; k < SL4; ++k) seg[r][k] = tile[seg_id * TP4 + k];
+    }
+
+    const bool empty = seg_id >= nseg;
+    float ssum[R], est[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < SL4; ++k) acc += sum4(seg[r][k]);
+        ssum[r] = acc;
+    }
+    // Estimate of the running sum at this segment's start = sum over the
+    // segments before it = lanes above this one (any summation order).
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float incl = wave_incl_scan(ssum[r]);
+        est[r] = read_lane(incl, kWave - 1) - incl;
+    }
+
+    RunElem el[R];
+    float bot[R], top[R];
+    bool valid[R];
+    int key_me[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        // Binade of the estimate (exponent field ef; ef <= 1 is the uniform
+        // grid [0, 2^-125) of step 2^-149), selected branch-free.  Segment 0
+        // folds from its true start +0; an Inf/NaN estimate gets an empty
+        // window so the segment always falls back.
+        const uint32_t ef_raw = __float_as_uint(est[r]) >> 23;  // est >= 0
+        const uint32_t ef = ef_raw < 1u ? 1u : ef_raw;
+        const bool sub = ef == 1u;
+        const bool first = seg_id == 0 || empty;
+        const bool bad = !first && ef >= 255u;
+        float sig0 = sub ? 0.0f : __uint_as_float(ef << 23);
+        float sig1 = sub ? __uint_as_float(1u) : __uint_as_float((ef << 23) | 1u);
+        float b = sig0;
+        float t = __uint_as_float((ef + 1u) << 23);  // ef + 1 == 255 -> +Inf
+        sig0 = first ? 0.0f : sig0;
+        sig1 = first ? 0.0f : sig1;
+        b = first ? 0.0f : (bad ? inf : b);
+        t = first ? inf : (bad ? 0.0f : t);
+        bot[r] = b;
+        top[r] = t;
+        float w0 = sig0, w1 = sig1;
+#pragma unroll
+        for (int k = 0; k < SL4; ++k) {
+            const f32x4 a = seg[r][k];
+            w0 = w0 + a.x; w1 = w1 + a.x;
+            w0 = w0 + a.y; w1 = w1 + a.y;
+            w0 = w0 + a.z; w1 = w1 + a.z;
+            w0 = w0 + a.w; w1 = w1 + a.w;
+        }
+        const bool ok0 = w0 < t;
+        const bool ok1 = first ? ok0 : (w1 < t);
+        // A segment whose estimated span touches a binade edge (within 2^-10;
+        // the estimate's own error is below cols * 2^-24 relative) will most
+        // likely cross it: keep it out of runs so that it is folded alone,
+        // from its LDS slot, instead of breaking a jump.
+        const bool edge = !first && (est[r] < b * 1.0009765625f || est[r] + ssum[r] >= t * 0.9990234375f);
+        valid[r] = ok0 && ok1 && !edge;
+        // Scan element of this single segment.
+        RunElem e;
+        e.d0 = ok0 ? w0 - sig0 : qnan;
+        e.d1 = (seg_id == 0) ? e.d0 : (ok1 ? w1 - sig1 : qnan);
+        e.bits = (int)(__float_as_uint(w0) & 1u) | (seg_id == 0 ? 0 : (int)((__float_as_uint(w1) & 1u) << 1));
+        if (empty) {
+            e.bits = kIdBits; e.d0 = 0.0f; e.d1 = 0.0f;
+        }
+        // Runs: maximal spans of valid segments with one binade key; an
+        // invalid segment is a run of its own.
+        key_me[r] = empty ? 1024 : (seg_id == 0 ? 1025 : (valid[r] ? (int)ef : 2048 + seg_id));
+        el[r] = e;
+    }
+
     uint64_t pmask[R];  // predicted-fallback segments, bit j = segment j
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        pmask[r] = 0;
+        // This lane's span ends its run when the next segment (lane - 1) is
+        // in another run; wave_shr:1 moves lane - 1's key here.
+        const int key_next = __builtin_amdgcn_update_dpp(key_me[r], key_me[r], 0x138, 0xf, 0xf, false);
+        const bool ends_here = lane == 0 || key_next != key_me[r];
+        if (ends_here) el[r].bits |= 4;
+        const uint64_t ends = __ballot(ends_here);
+        run_scan(el[r]);
+        // The run of lane L ends at the highest lane <= L with its bit set.
+        const uint64_t below = ends & (lt_mask | (1ull << lane));
+        const int end_lane = 63 - __builtin_clzll(below);
+        f32x4 ent;
+        ent.x = el[r].d0; ent.y = el[r].d1; ent.z = bot[r]; ent.w = top[r];
+        // Predicted fallback: the segment cannot join a run.
+        const bool pred = !empty && !valid[r];
+        const uint64_t m = __builtin_bitreverse64(__ballot(pred));  // bit j = segment j
+        pmask[r] = m;
         if (r < nrows) {
-            wave_lds_sync();  // previous row's tile reads precede these writes
-#pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-                const int f = c * kWave + lane;  // float4 index in the row
-                tile[(f / SL4) * TP4 + (f % SL4)] = xv[r][c] * xv[r][c];  // zero past the end
-            }
-            wave_lds_sync();
-            f32x4 seg[SL4];
-            float ssum = 0.0f;
-#pragma unroll
-            for (int k = 0; k < SL4; ++k) {
-                seg[k] = tile[seg_id * TP4 + k];
-                ssum += sum4(seg[k]);
-            }
-            // Estimate of the running sum at this segment's start = sum over
-            // the segments before it = lanes above this one.
-            const float incl = wave_incl_scan(ssum);
-            const float total = read_lane(incl, kWave - 1);
-            const float est = total - incl;  // any summation order: an estimate
-            const bool empty = seg_id >= nseg;
-            float sig0, sig1, bot, top;
-            int key;
-            if (empty) {
-                sig0 = 0.0f; sig1 = 0.0f; bot = 0.0f; top = inf; key = 1024;
-            } else if (seg_id == 0) {
-                // The true start of segment 0 is +0: fold from it exactly.
-                sig0 = 0.0f; sig1 = 0.0f; bot = 0.0f; top = inf; key = 1025;
-            } else {
-                const uint32_t ef = __float_as_uint(est) >> 23;  // est >= 0
-                key = (int)ef;
-                if (ef >= 255u) {           // Inf/NaN estimate: always fall back
-                    sig0 = 0.0f; sig1 = 0.0f; bot = inf; top = 0.0f;
-                } else if (ef <= 1u) {      // [0, 2^-125): one grid of 2^-149
-                    sig0 = 0.0f; sig1 = __uint_as_float(1u); bot = 0.0f; top = __uint_as_float(2u << 23);
-                    key = 1;
-                } else {
-                    sig0 = __uint_as_float(ef << 23);
-                    sig1 = __uint_as_float((ef << 23) | 1u);
-                    bot = sig0;
-                    top = __uint_as_float((ef + 1u) << 23);  // ef + 1 == 255 -> +Inf
-                }
-            }
-            float w0 = sig0, w1 = sig1;
-#pragma unroll
-            for (int k = 0; k < SL4; ++k) {
-                const f32x4 a = seg[k];
-                w0 = w0 + a.x; w1 = w1 + a.x;
-                w0 = w0 + a.y; w1 = w1 + a.y;
-                w0 = w0 + a.z; w1 = w1 + a.z;
-                w0 = w0 + a.w; w1 = w1 + a.w;
-            }
-            const bool ok0 = w0 < top;
-            const bool ok1 = (seg_id == 0 || empty) ? ok0 : (w1 < top);
-            // A segment whose estimated span touches a binade edge (within
-            // 2^-10; the estimate's own error is below cols * 2^-24 relative)
-            // will most likely cross it: keep it out of runs so that it is
-            // folded alone, from its LDS slot, instead of breaking a jump.
-            const bool edge = seg_id != 0 && !empty &&
-                              (est < bot * 1.0009765625f || est + ssum >= top * 0.9990234375f);
-            const bool valid = ok0 && ok1 && !edge;
-            // Scan element of this single segment.
-            RunElem e;
-            if (empty) {
-                e.bits = kIdBits; e.d0 = 0.0f; e.d1 = 0.0f;
-            } else {
-                e.d0 = ok0 ? w0 - sig0 : qnan;
-                e.d1 = (seg_id == 0) ? e.d0 : (ok1 ? w1 - sig1 : qnan);
-                e.bits = (int)(__float_as_uint(w0) & 1u) |
-                         (seg_id == 0 ? 0 : (int)((__float_as_uint(w1) & 1u) << 1));
-            }
-            // Runs: maximal spans of valid segments with one binade key.  An
-            // invalid segment is a run of its own.  This lane's span ends
-            // its run when the next segment (lane - 1) is in another run.
-            const int key_me = valid ? key : 2048 + seg_id;
-            const int key_next = __shfl_up(key_me, 1, kWave);  // segment j+1
-            if (lane == 0 || key_next != key_me) e.bits |= 4;
-            run_scan(e);
-            // How far the span reaches: first run end at or after segment j.
-            const uint64_t ends = __ballot(lane == 0 || key_next != key_me);
-            // ends bit L = lane L ends a run; the run of lane L ends at the
-            // highest lane <= L with its bit set.
-            const uint64_t below = ends & (lt_mask | (1ull << lane));
-            const int end_lane = 63 - __builtin_clzll(below);
-            const int next_seg = kSegs - end_lane;  // (63 - end_lane) + 1
-            f32x4 ent;
-            ent.x = e.d0; ent.y = e.d1; ent.z = bot; ent.w = top;
             table[r * kSegs + seg_id] = ent;
-            nexts[r * kSegs + seg_id] = (uint8_t)next_seg;
-            // Predicted fallback: the segment cannot join a run.
-            const bool pred = !empty && !valid;
-            const uint64_t m = __builtin_bitreverse64(__ballot(pred));  // bit j = segment j
-            pmask[r] = m;
+            nexts[r * kSegs + seg_id] = (uint8_t)(kSegs - end_lane);  // (63 - end_lane) + 1
             const int slot = __popcll(m & ((1ull << seg_id) - 1ull));
             if (pred && slot < kSlots) {
                 f32x4* dst = slots + (r * kSlots + slot) * SL4;
 #pragma unroll
-                for (int k = 0; k < SL4; ++k) dst[k] = seg[k];
+                for (int k = 0; k < SL4; ++k) dst[k] = seg[r][k];
             }
         }
     }
@@ -431,14 +465,15 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
     for (int r = 0; r < R; ++r) inv[r] = read_lane(inv_lane, r);
 
     if (Out == NormOut::F32) {
-        f32x4* y4 = reinterpret_cast<f32x4*>(args.y);
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const uint32_t f = (uint32_t)c * kWave + lane;
-            if (f < cols4) {
+        for (int r = 0; r < R; ++r) {
+            if (r < nrows) {
+                f32x4* yr = reinterpret_cast<f32x4*>(args.y) + (row0 + r) * cols4;
 #pragma unroll
-                for (int r = 0; r < R; ++r)
-                    if (r < nrows) st_stream(y4 + (row0 + r) * cols4 + f, (xv[r][c] * inv[r]) * wv[c]);
+                for (int c = 0; c < NCH; ++c) {
+                    const uint32_t f = (uint32_t)c * kWave + lane;
+                    if (f < cols4) st_stream(yr + f, (xv[r][c] * inv[r]) * wv[c]);
+                }
             }
         }
     } else {
@@ -466,19 +501,17 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
 #pragma unroll
         for (int r = 1; r < R; ++r) my_amax = lane == r ? amax[r] : my_amax;
         if (lane < nrows) args.scale[row0 + lane] = my_amax / 127.0f;
-        uint32_t* q4 = reinterpret_cast<uint32_t*>(args.q);
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const uint32_t f = (uint32_t)c * kWave + lane;
-            if (f < cols4) {
+        for (int r = 0; r < R; ++r) {
+            if (r < nrows) {
+                uint32_t* qr = reinterpret_cast<uint32_t*>(args.q) + (row0 + r) * cols4;
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    if (r < nrows) {
+                for (int c = 0; c < NCH; ++c) {
+                    const uint32_t f = (uint32_t)c * kWave + lane;
+                    if (f < cols4) {
                         const f32x4 v = xv[r][c];
-                        uint32_t p = quant_code(v.x, amax[r], rcp[r]) | (quant_code(v.y, amax[r], rcp[r]) << 8) |
-                                     (quant_code(v.z, amax[r], rcp[r]) << 16) |
-                                     (quant_code(v.w, amax[r], rcp[r]) << 24);
-                        q4[(row0 + r) * cols4 + f] = p;
+                        qr[f] = pack4(quant_code(v.x, amax[r], rcp[r]), quant_code(v.y, amax[r], rcp[r]),
+                                      quant_code(v.z, amax[r], rcp[r]), quant_code(v.w, amax[r], rcp[r]));
                     }
                 }
             }
@@ -563,7 +596,7 @@ static int norm_launch(NormArgs a, hipStream_t s) {
         return launch_status();
     }
     const bool many = a.rows > 2048;
-    if (many && nch <= 10) return launch_sl4<Out, 4>(a, nch, s);
+    if (many && nch <= 10) return launch_sl4<Out, KORE_NORM_ROWS_MANY>(a, nch, s);
     if (many && nch <= 16) return launch_sl4<Out, 2>(a, nch, s);
     return launch_sl4<Out, 1>(a, nch, s);
 }
