@@ -2,10 +2,10 @@
 // fused SwiGLU  out = silu(gate) * up.
 //
 // Roofline: HBM.  Bytes per element: 8 (GELU, SiLU), 12 (mul, SwiGLU).
-// Layout: flat f32 arrays.  Each thread owns UNROLL float4 slots spaced one
-// block-width apart, so every wave-wide global_load_dwordx4 covers 1 KiB of
-// contiguous memory and all UNROLL loads are in flight before the first use.
-// Loads and stores carry the nontemporal hint: each byte is touched once.
+// Layout: flat f32 arrays.  Each thread owns kEwUnroll float4 slots spaced
+// one block-width apart, so every wave-wide global_load_dwordx4 covers 1 KiB
+// of contiguous memory.  Loads and stores carry the nontemporal hint: each
+// byte is touched once.
 //
 // Arithmetic follows the reference op order (crates/kore-nn/src/activations.rs
 // :23-29 for GELU, :43 for SiLU) so that only the transcendental differs; the
@@ -59,8 +59,11 @@ struct SwigluOp {
     __device__ __forceinline__ float operator()(float g, float u) const { return silu_f(g) * u; }
 };
 
+// One float4 per thread per operand: on MI355X many short waves keep more
+// independent requests in flight than fewer threads with unrolled loads
+// (a plain copy reaches ~82% of 8 TB/s this way, ~76% at 4 float4/thread).
 constexpr int kEwBlock = 256;
-constexpr int kEwUnroll = 4;
+constexpr int kEwUnroll = 1;  // float4 per thread
 
 constexpr uint64_t kEwTile = (uint64_t)kEwBlock * kEwUnroll;  // float4 per block
 

@@ -6,17 +6,17 @@
 // crates/kore-nn/src/embedding.rs:63-68 and
 // crates/kore-edge/src/ops/embedding.rs:18-25 do.
 //
-// Vector path: one workgroup per kEmbTokens tokens; each wave copies whole
-// rows with global_load_dwordx4 / global_store_dwordx4, all of a thread's
-// loads issued before its first store.  Table reads use the default cache
-// policy (repeated ids hit L2/MALL); output stores are nontemporal.
+// Vector path: one float4 per thread over a (token, row chunk) grid; rows
+// longer than 65535 chunks use a workgroup-per-token loop.  Table reads use
+// the default cache policy (repeated ids hit L2/MALL); output stores are
+// nontemporal.
 #include "common.hpp"
 #include "kore_hip_internal.hpp"
 
 namespace kore {
 
 constexpr int kEmbBlock = 256;
-constexpr int kEmbUnroll = 4;  // float4 per thread per pass
+constexpr int kEmbUnroll = 4;  // float4 per thread per pass (rows > 16M floats)
 
 __global__ __launch_bounds__(kEmbBlock) void embedding_vec_kernel(const f32x4* __restrict__ table,
                                                                   const uint32_t* __restrict__ ids,
@@ -40,6 +40,22 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_vec_kernel(const f32x4* _
         for (int u = 0; u < kEmbUnroll; ++u) st_stream(dst + i + u * kEmbBlock, v[u]);
     }
     for (; i < dim4; i += kEmbBlock) st_stream(dst + i, ld_cached(src + i));
+}
+
+// One float4 per thread: grid (token, chunk of kEmbBlock float4).  Many
+// small, short-lived waves keep more independent requests in flight than a
+// few long ones (measured best on MI355X for mixed read/write streams).
+__global__ __launch_bounds__(kEmbBlock) void embedding_vec1_kernel(const f32x4* __restrict__ table,
+                                                                   const uint32_t* __restrict__ ids,
+                                                                   f32x4* __restrict__ out, uint64_t vocab,
+                                                                   uint64_t dim4) {
+    const uint64_t t = blockIdx.x;
+    const uint64_t i = (uint64_t)blockIdx.y * kEmbBlock + threadIdx.x;
+    if (i >= dim4) return;
+    const uint32_t id = ids[t];
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    const f32x4 v = ((uint64_t)id < vocab) ? ld_cached(table + (uint64_t)id * dim4 + i) : z;
+    st_stream(out + t * dim4 + i, v);
 }
 
 // Scalar path: dim % 4 != 0 or unaligned table/out.
@@ -73,6 +89,13 @@ extern "C" int kore_hip_embedding_f32(const float* table, const uint32_t* ids, f
     hipStream_t s = (hipStream_t)stream;
     dim3 grid((uint32_t)n_ids), block(kEmbBlock);
     if (dim % 4 == 0 && aligned16(out) && (vocab == 0 || aligned16(table))) {
+        const uint64_t chunks = (dim / 4 + kEmbBlock - 1) / kEmbBlock;
+        if (chunks <= 65535) {
+            hipLaunchKernelGGL(embedding_vec1_kernel, dim3((uint32_t)n_ids, (uint32_t)chunks), block, 0, s,
+                               reinterpret_cast<const f32x4*>(table), ids, reinterpret_cast<f32x4*>(out), vocab,
+                               dim / 4);
+            return launch_status();
+        }
         hipLaunchKernelGGL(embedding_vec_kernel, grid, block, 0, s, reinterpret_cast<const f32x4*>(table), ids,
                            reinterpret_cast<f32x4*>(out), vocab, dim / 4);
     } else {

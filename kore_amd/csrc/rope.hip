@@ -24,7 +24,8 @@
 
 namespace kore {
 
-constexpr int kRopeBlock = 128;
+constexpr int kRopeBlock = 128;      // scalar path
+constexpr int kRopeMaxBlock = 1024;  // vector path: blockDim chosen per call
 constexpr uint32_t kRopeMaxHeadDim = 4096;
 
 struct RopeTensor {
@@ -38,9 +39,15 @@ __device__ __forceinline__ float2 rot(float x0, float x1, float c, float s) {
     return make_float2(a0 - b0, a1 + b1);
 }
 
-// Vector path: D % 8 == 0 and both tensors 16-byte aligned.
+// Vector path: D % 8 == 0 and both tensors 16-byte aligned.  blockDim covers
+// a token's tasks in at most kRopeBatch slots per thread (one float4 pair per
+// slot: many short waves, as for the other streams); a pass issues all of its
+// global loads first, so the token's sincos work (first pass only) and the
+// barrier overlap the memory latency instead of delaying the loads.
+constexpr int kRopeBatch = 2;
+
 template <bool Interleaved>
-__global__ __launch_bounds__(kRopeBlock) void rope_vec_kernel(RopeTensor t0, RopeTensor t1,
+__global__ __launch_bounds__(kRopeMaxBlock) void rope_vec_kernel(RopeTensor t0, RopeTensor t1,
                                                               const float* __restrict__ inv_freq,
                                                               uint64_t seq_len, uint32_t head_dim,
                                                               uint64_t start_pos) {
@@ -48,50 +55,76 @@ __global__ __launch_bounds__(kRopeBlock) void rope_vec_kernel(RopeTensor t0, Rop
     float2* cs = reinterpret_cast<float2*>(cs_raw);
     const uint64_t token = blockIdx.x;
     const uint32_t half = head_dim >> 1;
-    const float pos = (float)(start_pos + token % seq_len);
-    for (uint32_t i = threadIdx.x; i < half; i += kRopeBlock) {
-        float angle = pos * inv_freq[i];
-        float s, c;
-        sincosf(angle, &s, &c);
-        cs[i] = make_float2(c, s);
-    }
-    __syncthreads();
-
     const uint32_t tasks_per_head = Interleaved ? (head_dim >> 2) : (head_dim >> 3);
     const uint32_t n0 = t0.heads * tasks_per_head;
     const uint32_t n_all = n0 + t1.heads * tasks_per_head;
-    for (uint32_t task = threadIdx.x; task < n_all; task += kRopeBlock) {
-        const bool first = task < n0;
-        const uint32_t local = first ? task : task - n0;
-        const uint32_t heads = first ? t0.heads : t1.heads;
-        float* row = (first ? t0.data : t1.data) + token * (uint64_t)heads * head_dim;
-        const uint32_t h = local / tasks_per_head;
-        const uint32_t k = local - h * tasks_per_head;
-        float* v = row + (uint64_t)h * head_dim;
-        if (Interleaved) {
-            f32x4* p = reinterpret_cast<f32x4*>(v + 4 * k);
-            f32x4 x = *p;
-            const f32x4 csv = *reinterpret_cast<const f32x4*>(&cs[2 * k]);  // c0 s0 c1 s1
-            float2 r0 = rot(x.x, x.y, csv.x, csv.y);
-            float2 r1 = rot(x.z, x.w, csv.z, csv.w);
-            f32x4 o;
-            o.x = r0.x; o.y = r0.y; o.z = r1.x; o.w = r1.y;
-            *p = o;
-        } else {
-            f32x4* p0 = reinterpret_cast<f32x4*>(v + 4 * k);
-            f32x4* p1 = reinterpret_cast<f32x4*>(v + half + 4 * k);
-            f32x4 x0 = *p0, x1 = *p1;
-            const f32x4 ca = *reinterpret_cast<const f32x4*>(&cs[4 * k]);      // c0 s0 c1 s1
-            const f32x4 cb = *reinterpret_cast<const f32x4*>(&cs[4 * k + 2]);  // c2 s2 c3 s3
-            float2 r0 = rot(x0.x, x1.x, ca.x, ca.y);
-            float2 r1 = rot(x0.y, x1.y, ca.z, ca.w);
-            float2 r2 = rot(x0.z, x1.z, cb.x, cb.y);
-            float2 r3 = rot(x0.w, x1.w, cb.z, cb.w);
-            f32x4 o0, o1;
-            o0.x = r0.x; o0.y = r1.x; o0.z = r2.x; o0.w = r3.x;
-            o1.x = r0.y; o1.y = r1.y; o1.z = r2.y; o1.w = r3.y;
-            *p0 = o0;
-            *p1 = o1;
+    float* row0 = t0.data + token * (uint64_t)t0.heads * head_dim;
+    float* row1 = t1.data + token * (uint64_t)t1.heads * head_dim;
+
+    const uint32_t nthr = blockDim.x;
+    for (uint32_t base = 0; base < n_all; base += kRopeBatch * nthr) {
+        f32x4* p0[kRopeBatch];
+        f32x4* p1[kRopeBatch];
+        f32x4 x0[kRopeBatch], x1[kRopeBatch];
+        uint32_t kk[kRopeBatch];
+#pragma unroll
+        for (int u = 0; u < kRopeBatch; ++u) {
+            const uint32_t task = base + u * nthr + threadIdx.x;
+            const bool ok = task < n_all;
+            const bool first = task < n0;
+            const uint32_t local = first ? task : task - n0;
+            const uint32_t h = local / tasks_per_head;
+            const uint32_t k = local - h * tasks_per_head;
+            float* v = (first ? row0 : row1) + (uint64_t)h * head_dim;
+            kk[u] = k;
+            if (Interleaved) {
+                p0[u] = reinterpret_cast<f32x4*>(v + 4 * k);
+                p1[u] = p0[u];
+                if (ok) x0[u] = *p0[u];
+            } else {
+                p0[u] = reinterpret_cast<f32x4*>(v + 4 * k);
+                p1[u] = reinterpret_cast<f32x4*>(v + half + 4 * k);
+                if (ok) {
+                    x0[u] = *p0[u];
+                    x1[u] = *p1[u];
+                }
+            }
+        }
+        if (base == 0) {
+            const float pos = (float)(start_pos + token % seq_len);
+            for (uint32_t i = threadIdx.x; i < half; i += nthr) {
+                float angle = pos * inv_freq[i];
+                float s, c;
+                sincosf(angle, &s, &c);
+                cs[i] = make_float2(c, s);
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int u = 0; u < kRopeBatch; ++u) {
+            const uint32_t task = base + u * nthr + threadIdx.x;
+            if (task >= n_all) continue;
+            const uint32_t k = kk[u];
+            if (Interleaved) {
+                const f32x4 csv = *reinterpret_cast<const f32x4*>(&cs[2 * k]);  // c0 s0 c1 s1
+                float2 r0 = rot(x0[u].x, x0[u].y, csv.x, csv.y);
+                float2 r1 = rot(x0[u].z, x0[u].w, csv.z, csv.w);
+                f32x4 o;
+                o.x = r0.x; o.y = r0.y; o.z = r1.x; o.w = r1.y;
+                *p0[u] = o;
+            } else {
+                const f32x4 ca = *reinterpret_cast<const f32x4*>(&cs[4 * k]);      // c0 s0 c1 s1
+                const f32x4 cb = *reinterpret_cast<const f32x4*>(&cs[4 * k + 2]);  // c2 s2 c3 s3
+                float2 r0 = rot(x0[u].x, x1[u].x, ca.x, ca.y);
+                float2 r1 = rot(x0[u].y, x1[u].y, ca.z, ca.w);
+                float2 r2 = rot(x0[u].z, x1[u].z, cb.x, cb.y);
+                float2 r3 = rot(x0[u].w, x1[u].w, cb.z, cb.w);
+                f32x4 o0, o1;
+                o0.x = r0.x; o0.y = r1.x; o0.z = r2.x; o0.w = r3.x;
+                o1.x = r0.y; o1.y = r1.y; o1.z = r2.y; o1.w = r3.y;
+                *p0[u] = o0;
+                *p1[u] = o1;
+            }
         }
     }
 }
@@ -161,6 +194,13 @@ static int rope_launch(float* q, uint32_t q_heads, float* k, uint32_t k_heads, c
     const size_t lds = ((size_t)(head_dim / 2) * sizeof(float2) + 15) & ~(size_t)15;
     dim3 grid((uint32_t)tokens), block(kRopeBlock);
     if (vec) {
+        // Threads per token: the token's tasks in at most kRopeBatch slots,
+        // rounded to whole waves, capped at kRopeMaxBlock.
+        const uint64_t tasks = heads_all * (interleaved ? head_dim / 4 : head_dim / 8);
+        uint64_t thr = (tasks + kRopeBatch - 1) / kRopeBatch;
+        if (tasks <= (uint64_t)kRopeMaxBlock) thr = tasks;
+        thr = (thr + 63) / 64 * 64;
+        block = dim3((uint32_t)(thr > (uint64_t)kRopeMaxBlock ? kRopeMaxBlock : thr));
         if (interleaved)
             hipLaunchKernelGGL(rope_vec_kernel<true>, grid, block, lds, s, t0, t1, inv_freq, seq_len, head_dim,
                                start_pos);
