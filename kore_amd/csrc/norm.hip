@@ -66,11 +66,6 @@
 
 namespace kore {
 
-// Rows per wave when the grid has enough rows to fill the chip (cols <= 2560).
-#ifndef KORE_NORM_ROWS_MANY
-#define KORE_NORM_ROWS_MANY 2
-#endif
-
 constexpr int kWavesPerBlock = 4;
 constexpr int kNormBlock = kWave * kWavesPerBlock;
 constexpr int kSegs = kWave;  // segments per row: one per lane
@@ -93,9 +88,11 @@ struct NormArgs {
 // segment starts j*pitch hit 16 distinct 16-byte bank groups per 16 lanes.
 __host__ __device__ constexpr uint32_t tile_pitch4(uint32_t sl4) { return sl4 + ((sl4 & 1u) ? 2u : 1u); }
 
-// Per-wave LDS: transpose tile, run table, fallback slots, run-end bytes.
+// Per-wave LDS: half-row transpose tile (32 segments), run table, fallback
+// slots, run-end bytes.
+constexpr int kHalfSegs = kSegs / 2;
 __host__ __device__ constexpr uint32_t wave_lds_f4(uint32_t sl4, uint32_t rows) {
-    return kSegs * tile_pitch4(sl4) + rows * kSegs + rows * kSlots * sl4 + (rows * kSegs + 15) / 16;
+    return kHalfSegs * tile_pitch4(sl4) + rows * kSegs + rows * kSlots * sl4 + (rows * kSegs + 15) / 16;
 }
 
 __device__ __forceinline__ int32_t cvt_i32_sat(float v) {
@@ -253,7 +250,7 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
     const uint32_t cols4 = args.cols >> 2;
     const int nseg = (int)((cols4 + SL4 - 1) / SL4);
     f32x4* tile = lds4 + (size_t)wave * kWaveF4;
-    f32x4* table = tile + kSegs * TP4;        // [R][64] (D0, D1, bot, top)
+    f32x4* table = tile + kHalfSegs * TP4;    // [R][64] (D0, D1, bot, top)
     f32x4* slots = table + R * kSegs;         // [R][kSlots][SL4]
     uint8_t* nexts = reinterpret_cast<uint8_t*>(slots + R * kSlots * SL4);  // [R][64]
     const f32x4* x4 = reinterpret_cast<const f32x4*>(args.x);
@@ -284,18 +281,28 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
     // tile), then run the per-row phases for all rows at once so their
     // dependency chains interleave.  Rows past nrows compute on zeros and are
     // never stored or resolved.
+    // The tile holds half a row (32 segments): pass h moves segments
+    // [32h, 32h + 32), which lanes 63 - seg read back.
     f32x4 seg[R][SL4];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        wave_lds_sync();  // previous tile reads precede these writes
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const int f = c * kWave + lane;  // float4 index in the row
-            tile[(f / SL4) * TP4 + (f % SL4)] = xv[r][c] * xv[r][c];  // zero past the end
+        for (int h = 0; h < 2; ++h) {
+            wave_lds_sync();  // previous tile reads precede these writes
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const int f = c * kWave + lane;  // float4 index in the row
+                const int sg = f / SL4 - h * kHalfSegs;
+                if (sg >= 0 && sg < kHalfSegs)
+                    tile[sg * TP4 + (f % SL4)] = xv[r][c] * xv[r][c];  // zero past the end
+            }
+            wave_lds_sync();
+            const int my = seg_id - h * kHalfSegs;
+            if (my >= 0 && my < kHalfSegs) {
+#pragma unroll
+                for (int k = 0; k < SL4; ++k) seg[r][k] = tile[my * TP4 + k];
+            }
         }
-        wave_lds_sync();
-#pragma unroll
-        for (int k = 0; k < SL4; ++k) seg[r][k] = tile[seg_id * TP4 + k];
     }
 
     const bool empty = seg_id >= nseg;
@@ -402,15 +409,6 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
         }
     }
 
-    // Weights for the epilogue: L2 hits, in flight during the resolve.
-    const f32x4* w4 = reinterpret_cast<const f32x4*>(args.w);
-    f32x4 wv[NCH];
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const uint32_t f = (uint32_t)c * kWave + lane;
-        wv[c] = (f < cols4) ? ld_cached(w4 + f) : zero;
-    }
-
     // ---- resolve: lane r owns row r; one step per run or fallback.
     wave_lds_sync();  // table, run ends and slots were written by other lanes
     uint64_t my_mask = pmask[0];
@@ -452,6 +450,16 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
                 ++j;
             }
         }
+    }
+
+    // Weights for the epilogue (L2 hits), loaded after the resolve so their
+    // registers are free while it runs.
+    const f32x4* w4 = reinterpret_cast<const f32x4*>(args.w);
+    f32x4 wv[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const uint32_t f = (uint32_t)c * kWave + lane;
+        wv[c] = (f < cols4) ? ld_cached(w4 + f) : zero;
     }
 
     // cpu_fused.rs:181-182 with IEEE sqrt and division.
@@ -559,22 +567,24 @@ static int launch_vec(NormArgs a, hipStream_t s) {
     return launch_status();
 }
 
-template <NormOut Out, int R>
+template <NormOut Out>
 static int launch_sl4(NormArgs a, uint32_t nch, hipStream_t s) {
-    if (nch <= 1) return launch_vec<Out, 1, R>(a, s);
-    if (nch <= 2) return launch_vec<Out, 2, R>(a, s);
-    if (nch <= 4) return launch_vec<Out, 4, R>(a, s);
-    if (nch <= 6) return launch_vec<Out, 6, R>(a, s);
-    if (nch <= 8) return launch_vec<Out, 8, R>(a, s);
-    if (R > 2 || nch <= 10) return launch_vec<Out, 10, R>(a, s);
-    if (nch <= 12) return launch_vec<Out, 12, (R < 2 ? R : 2)>(a, s);
-    if (R > 1 || nch <= 16) return launch_vec<Out, 16, (R < 2 ? R : 2)>(a, s);
+    if (nch <= 1) return launch_vec<Out, 1, 1>(a, s);
+    if (nch <= 2) return launch_vec<Out, 2, 1>(a, s);
+    if (nch <= 4) return launch_vec<Out, 4, 1>(a, s);
+    if (nch <= 6) return launch_vec<Out, 6, 1>(a, s);
+    if (nch <= 8) return launch_vec<Out, 8, 1>(a, s);
+    if (nch <= 10) return launch_vec<Out, 10, 1>(a, s);
+    if (nch <= 12) return launch_vec<Out, 12, 1>(a, s);
+    if (nch <= 16) return launch_vec<Out, 16, 1>(a, s);
     if (nch <= 24) return launch_vec<Out, 24, 1>(a, s);
     return launch_vec<Out, 32, 1>(a, s);
 }
 
-// Rows per wave: 4 amortises the resolve over more rows when the grid has
-// enough rows to fill the chip; 1 minimises latency for small batches.
+// One row per wave: with the half-row tile a wave needs ~8 KB of LDS and
+// ~110 VGPRs (2560 columns), so four waves share each SIMD and hide each
+// other's latency -- measured faster than amortising the resolve over two or
+// four rows per wave at lower occupancy.
 template <NormOut Out>
 static int norm_launch(NormArgs a, hipStream_t s) {
     if (a.rows == 0) return KORE_HIP_OK;
@@ -595,10 +605,7 @@ static int norm_launch(NormArgs a, hipStream_t s) {
         hipLaunchKernelGGL(row_norm_scalar_kernel<Out>, dim3((uint32_t)blocks), dim3(64), 0, s, a);
         return launch_status();
     }
-    const bool many = a.rows > 2048;
-    if (many && nch <= 10) return launch_sl4<Out, KORE_NORM_ROWS_MANY>(a, nch, s);
-    if (many && nch <= 16) return launch_sl4<Out, 2>(a, nch, s);
-    return launch_sl4<Out, 1>(a, nch, s);
+    return launch_sl4<Out>(a, nch, s);
 }
 
 }  // namespace kore
