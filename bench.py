@@ -302,6 +302,43 @@ class Prequant(Workload):
             "full config, single thread"
 
 
+class RmsNormSiluGate(Workload):
+    """SURVEY next-row: y = RMSNorm(x) * silu(z) (cuda/ops.rs:717-751) on the
+    pre-quant activation shape."""
+    kernel = "row_norm_kernel"
+
+    def __init__(self, rows=4096, cols=2560):
+        self.rows, self.cols = rows, cols
+        self.name = f"rms_norm_silu_gate_{rows}x{cols}"
+        self.tokens = rows
+        self.bytes = rows * cols * 4 * 3 + cols * 4
+        self.desc = f"RMSNorm(x) * silu(z) f32, x, z [{rows},{cols}] ~ N(0,1), w ~ N(1,0.02), eps 1e-6"
+
+    def setup(self, torch, lib):
+        self.lib = lib
+        self.k = n_sets(self.rows * self.cols * 12)
+        self._dx = [randn(torch, (self.rows, self.cols), s) for s in range(self.k)]
+        self._dz = [randn(torch, (self.rows, self.cols), 50 + s) for s in range(self.k)]
+        self._dy = [torch.empty_like(self._dx[0]) for _ in range(self.k)]
+        self._dw = randn(torch, (self.cols,), 100, 1.0, 0.02)
+
+    def launch(self, i, stream):
+        j = i % self.k
+        return self.lib.kore_hip_rms_norm_silu_gate_f32(self._dx[j].data_ptr(), self._dw.data_ptr(),
+                                                        self._dz[j].data_ptr(), self._dy[j].data_ptr(), self.rows,
+                                                        self.cols, 1e-6, stream)
+
+    def cpu_sample(self):
+        import oracle
+        from inputs import normal, rmsnorm_inputs
+
+        rows = min(self.rows, 1024)
+        x, g = rmsnorm_inputs(rows, self.cols, 0)
+        z = normal((rows, self.cols), 5)
+        return (lambda: oracle.rms_norm_silu_gate(x, g, z, 1e-6)), rows * self.cols * 12 + self.cols * 4, rows, 1, \
+            f"{rows} rows, single thread"
+
+
 class Copy(Workload):
     """A plain 1 GiB device copy through the gather kernel with ids = 0..N-1;
     used to calibrate rocprof's FETCH_SIZE / WRITE_SIZE counters."""
@@ -330,7 +367,7 @@ class Copy(Workload):
 
 def all_workloads():
     return [RopeQK(False), RopeQK(True), RMSNorm(32, 2048), RMSNorm(16384, 2048), Swiglu(), Gelu(), Embedding(),
-            Prequant(4096), Prequant(64), Prequant(1), Copy()]
+            Prequant(4096), Prequant(64), Prequant(1), RmsNormSiluGate(), Copy()]
 
 
 # ------------------------------------------------------------------ measure

@@ -143,6 +143,18 @@ int kore_hip_rms_norm_quant_i8(const float *x, const float *weight,
                                int8_t *q, float *scale, uint64_t rows,
                                uint64_t cols, float eps, kore_stream_t stream);
 
+/* ------------------------------------------------- RMSNorm with SiLU gate
+ * out[r, :] = RMSNorm(x)[r, :] * silu(z[r, :]), silu(v) = v / (1 + exp(-v)),
+ * with the RMSNorm part computed exactly as kore_hip_rms_norm_f32.  Replaces
+ * cuda_fused_rms_norm_silu_gate_f32 (crates/kore-kernels/src/cuda/ops.rs:717-751,
+ * kernel crates/kore-kernels/src/cuda/kernels/fused_norm_proj.cu:204-253),
+ * whose CPU definition is the test at crates/kore-kernels/src/cpu_fused.rs:451-483.
+ * f32 tol.  out may equal x or z. */
+int kore_hip_rms_norm_silu_gate_f32(const float *x, const float *weight,
+                                    const float *z, float *out, uint64_t rows,
+                                    uint64_t cols, float eps,
+                                    kore_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

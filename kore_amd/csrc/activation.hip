@@ -42,9 +42,6 @@ struct GeluOp {
     }
 };
 
-// activations.rs:43  x / (1 + exp(-x)), IEEE division.
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
-
 struct SiluOp {
     __device__ __forceinline__ float operator()(float x) const { return silu_f(x); }
 };

@@ -49,6 +49,10 @@ __device__ __forceinline__ float read_lane(float v, int src) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
 }
 
+// SiLU as the reference writes it (crates/kore-nn/src/activations.rs:43):
+// x / (1 + exp(-x)) with ocml's accurate expf and IEEE division.
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace kore

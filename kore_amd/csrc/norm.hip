@@ -71,7 +71,9 @@ constexpr int kNormBlock = kWave * kWavesPerBlock;
 constexpr int kSegs = kWave;  // segments per row: one per lane
 constexpr int kSlots = 8;     // LDS fallback slots per row
 
-enum class NormOut { F32, I8 };
+// F32: y = RMSNorm(x); I8: pre-quant codes + scales; SiluGate: y = RMSNorm(x)
+// * silu(z) (the Mamba input-path gate).
+enum class NormOut { F32, I8, SiluGate };
 
 struct NormArgs {
     const float* x;
@@ -79,6 +81,7 @@ struct NormArgs {
     float* y;        // NormOut::F32
     int8_t* q;       // NormOut::I8
     float* scale;    // NormOut::I8
+    const float* z;  // NormOut::SiluGate
     uint64_t rows;
     uint32_t cols;
     float eps;
@@ -484,6 +487,34 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
                 }
             }
         }
+    } else if (Out == NormOut::SiluGate) {
+        // cpu_fused.rs:466-471: x_hat = (x*inv)*g; y = x_hat * silu(z).
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r < nrows) {
+                const f32x4* zr = reinterpret_cast<const f32x4*>(args.z) + (row0 + r) * cols4;
+                f32x4* yr = reinterpret_cast<f32x4*>(args.y) + (row0 + r) * cols4;
+                f32x4 zv[NCH];
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) {
+                    const uint32_t f = (uint32_t)c * kWave + lane;
+                    zv[c] = (f < cols4) ? ld_stream(zr + f) : zero;
+                }
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) {
+                    const uint32_t f = (uint32_t)c * kWave + lane;
+                    if (f < cols4) {
+                        const f32x4 xh = (xv[r][c] * inv[r]) * wv[c];
+                        f32x4 g;
+                        g.x = silu_f(zv[c].x);
+                        g.y = silu_f(zv[c].y);
+                        g.z = silu_f(zv[c].z);
+                        g.w = silu_f(zv[c].w);
+                        st_stream(yr + f, xh * g);
+                    }
+                }
+            }
+        }
     } else {
         float amax[R];
 #pragma unroll
@@ -546,6 +577,10 @@ __global__ __launch_bounds__(64) void row_norm_scalar_kernel(NormArgs args) {
     if (Out == NormOut::F32) {
         float* yr = args.y + row * cols;
         for (uint32_t i = 0; i < cols; ++i) yr[i] = (xr[i] * inv) * args.w[i];
+    } else if (Out == NormOut::SiluGate) {
+        float* yr = args.y + row * cols;
+        const float* zr = args.z + row * cols;
+        for (uint32_t i = 0; i < cols; ++i) yr[i] = ((xr[i] * inv) * args.w[i]) * silu_f(zr[i]);
     } else {
         float m = 0.0f;
         for (uint32_t i = 0; i < cols; ++i) m = fmaxf(m, fabsf((xr[i] * inv) * args.w[i]));
@@ -590,7 +625,8 @@ static int norm_launch(NormArgs a, hipStream_t s) {
     if (a.rows == 0) return KORE_HIP_OK;
     if (a.cols == 0) return KORE_HIP_ERR_BAD_DIM;
     if (!a.x || !a.w) return KORE_HIP_ERR_NULL_PTR;
-    if (Out == NormOut::F32 && !a.y) return KORE_HIP_ERR_NULL_PTR;
+    if (Out != NormOut::I8 && !a.y) return KORE_HIP_ERR_NULL_PTR;
+    if (Out == NormOut::SiluGate && !a.z) return KORE_HIP_ERR_NULL_PTR;
     if (Out == NormOut::I8 && (!a.q || !a.scale)) return KORE_HIP_ERR_NULL_PTR;
     uint64_t elems;
     if (!mul_ok(a.rows, a.cols, &elems) || elems > kMaxElements) return KORE_HIP_ERR_OVERFLOW;
@@ -598,6 +634,7 @@ static int norm_launch(NormArgs a, hipStream_t s) {
     const uint32_t nch = (cols4 + kWave - 1) / kWave;
     bool vec = a.cols % 4 == 0 && aligned16(a.x) && aligned16(a.w) && nch <= 32;
     if (Out == NormOut::F32) vec = vec && aligned16(a.y);
+    else if (Out == NormOut::SiluGate) vec = vec && aligned16(a.y) && aligned16(a.z);
     else vec = vec && (reinterpret_cast<uintptr_t>(a.q) & 3u) == 0;
     if (!vec) {
         uint64_t blocks = (a.rows + 63) / 64;
@@ -615,13 +652,20 @@ using namespace kore;
 extern "C" int kore_hip_rms_norm_f32(const float* x, const float* weight, float* out, uint64_t rows,
                                      uint64_t cols, float eps, kore_stream_t stream) {
     if (cols > 0xffffffffull) return KORE_HIP_ERR_OVERFLOW;
-    NormArgs a{x, weight, out, nullptr, nullptr, rows, (uint32_t)cols, eps};
+    NormArgs a{x, weight, out, nullptr, nullptr, nullptr, rows, (uint32_t)cols, eps};
     return norm_launch<NormOut::F32>(a, (hipStream_t)stream);
 }
 
 extern "C" int kore_hip_rms_norm_quant_i8(const float* x, const float* weight, int8_t* q, float* scale,
                                           uint64_t rows, uint64_t cols, float eps, kore_stream_t stream) {
     if (cols > 0xffffffffull) return KORE_HIP_ERR_OVERFLOW;
-    NormArgs a{x, weight, nullptr, q, scale, rows, (uint32_t)cols, eps};
+    NormArgs a{x, weight, nullptr, q, scale, nullptr, rows, (uint32_t)cols, eps};
     return norm_launch<NormOut::I8>(a, (hipStream_t)stream);
+}
+
+extern "C" int kore_hip_rms_norm_silu_gate_f32(const float* x, const float* weight, const float* z, float* out,
+                                               uint64_t rows, uint64_t cols, float eps, kore_stream_t stream) {
+    if (cols > 0xffffffffull) return KORE_HIP_ERR_OVERFLOW;
+    NormArgs a{x, weight, out, nullptr, nullptr, z, rows, (uint32_t)cols, eps};
+    return norm_launch<NormOut::SiluGate>(a, (hipStream_t)stream);
 }

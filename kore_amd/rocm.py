@@ -18,7 +18,6 @@ dims imply raises ``RocmError.MemoryError`` instead of reaching the GPU.
 """
 from __future__ import annotations
 
-import ctypes
 from typing import Optional, Tuple
 
 import numpy as np
@@ -151,6 +150,22 @@ def rocm_rms_norm_f32(device_idx: int, input: HipBuffer, weight: HipBuffer, rows
     return o
 
 
+def rocm_fused_rms_norm_silu_gate_f32(device_idx: int, input: HipBuffer, gamma: HipBuffer, gate: HipBuffer,
+                                      rows: int, cols: int, eps: float,
+                                      out: Optional[HipBuffer] = None) -> HipBuffer:
+    """``cuda_fused_rms_norm_silu_gate_f32`` (cuda/ops.rs:717-751):
+    y = RMSNorm(x) * silu(z), RMSNorm bit-exact as ``rocm_rms_norm_f32``."""
+    _require_device(device_idx)
+    n = rows * cols * 4
+    _need(input, n, "rms_norm_silu_gate input")
+    _need(gamma, cols * 4, "rms_norm_silu_gate gamma")
+    _need(gate, n, "rms_norm_silu_gate gate")
+    o = _out(device_idx, out, n, "rms_norm_silu_gate out")
+    _check(_lib.load().kore_hip_rms_norm_silu_gate_f32(input.ptr, gamma.ptr, gate.ptr, o.ptr, rows, cols, eps,
+                                                       _stream(device_idx)), "rms_norm_silu_gate_f32")
+    return o
+
+
 # ------------------------------------------------------------ activations
 def _unary(name: str, device_idx: int, a: HipBuffer, n: int, out: Optional[HipBuffer]) -> HipBuffer:
     _require_device(device_idx)
@@ -269,5 +284,5 @@ def rocm_rms_norm_quant_i8(device_idx: int, input: HipBuffer, weight: HipBuffer,
 __all__ = [
     "RocmError", "HipBuffer", "rocm_rms_norm_f32", "rocm_gelu_f32", "rocm_silu_f32", "rocm_mul_f32",
     "rocm_swiglu_f32", "rope_inv_freq_host", "rocm_rope_inv_freq_f32", "rocm_rope_f32", "rocm_rope_qk_f32",
-    "rocm_embedding_f32", "rocm_rms_norm_quant_i8",
+    "rocm_embedding_f32", "rocm_rms_norm_quant_i8", "rocm_fused_rms_norm_silu_gate_f32",
 ]

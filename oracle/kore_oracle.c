@@ -225,3 +225,26 @@ void kore_oracle_rms_norm_quant_i8(const float *x, const float *gamma,
         scale[r] = a / 127.0f;
     }
 }
+
+/* cpu_fused.rs:459-473: sum_sq fold, inv_rms = 1/sqrt(sum_sq/cols + eps),
+ * x_hat = row[c]*inv_rms*gamma[c], y = x_hat * silu(z). */
+void kore_oracle_rms_norm_silu_gate_f32(const float *x, const float *gamma,
+                                        const float *z, float *y, size_t rows,
+                                        size_t cols, float eps) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float *row = x + r * cols;
+        float sum_sq = 0.0f;
+        for (size_t i = 0; i < cols; ++i) {
+            float sq = row[i] * row[i];
+            sum_sq = sum_sq + sq;
+        }
+        float rms = sqrtf(sum_sq / (float)cols + eps);
+        float inv_rms = 1.0f / rms;
+        for (size_t i = 0; i < cols; ++i) {
+            float xh = (row[i] * inv_rms) * gamma[i];
+            float zv = z[r * cols + i];
+            float sz = zv / (1.0f + expf(-zv));
+            y[r * cols + i] = xh * sz;
+        }
+    }
+}

@@ -85,6 +85,15 @@ void kore_oracle_rms_norm_quant_i8(const float *x, const float *gamma,
                                    int8_t *q, float *scale, size_t rows,
                                    size_t cols, float eps);
 
+/* RMSNorm with a SiLU gate, y = RMSNorm(x) * silu(z): the CPU definition of
+ * fused_rms_norm_silu_gate_f32 in crates/kore-kernels/src/cpu_fused.rs:451-483
+ * (x_hat = (x*inv)*g with the sequential sum of squares; silu(z) =
+ * z/(1+exp(-z)); y = x_hat * silu(z)); the CUDA kernel is
+ * crates/kore-kernels/src/cuda/kernels/fused_norm_proj.cu:204-253. */
+void kore_oracle_rms_norm_silu_gate_f32(const float *x, const float *gamma,
+                                        const float *z, float *y, size_t rows,
+                                        size_t cols, float eps);
+
 /* One element of the pre-quant code: the shared definition used above.  */
 int8_t kore_oracle_quant_code(float xn, float amax_guarded);
 

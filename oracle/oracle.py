@@ -33,6 +33,7 @@ _SIGS = {
     "kore_oracle_embedding_f32": (None, [_p, _p, _p, _sz, _sz, _sz]),
     "kore_oracle_rms_norm_quant_i8": (None, [_p, _p, _p, _p, _sz, _sz, _f]),
     "kore_oracle_quant_code": (_c.c_int8, [_f, _f]),
+    "kore_oracle_rms_norm_silu_gate_f32": (None, [_p, _p, _p, _p, _sz, _sz, _f]),
 }
 
 _lib = None
@@ -161,9 +162,21 @@ def rms_norm_quant_i8(x, gamma, eps: float):
     return q, s
 
 
+def rms_norm_silu_gate(x, gamma, z, eps: float) -> np.ndarray:
+    """RMSNorm(x) * silu(z) (crates/kore-kernels/src/cpu_fused.rs:451-483)."""
+    x = _f32(x)
+    g = _f32(gamma)
+    zz = _f32(z)
+    cols = x.shape[-1]
+    rows = x.size // cols if cols else 0
+    y = np.empty_like(x)
+    lib().kore_oracle_rms_norm_silu_gate_f32(_ptr(x), _ptr(g), _ptr(zz), _ptr(y), rows, cols, eps)
+    return y
+
+
 def quant_code(xn: float, amax: float) -> int:
     return int(lib().kore_oracle_quant_code(xn, amax))
 
 
 __all__ = ["build", "lib", "rms_norm", "gelu", "silu", "mul", "swiglu", "rope_inv_freq", "rope", "embedding",
-           "rms_norm_quant_i8", "quant_code"]
+           "rms_norm_quant_i8", "rms_norm_silu_gate", "quant_code"]

@@ -95,6 +95,36 @@ def test_rms_norm_special_rows():
         assert_bitexact(got, want, f"special rows eps={eps}")
 
 
+# ------------------------------------------------------- RMSNorm + SiLU gate
+@pytest.mark.parametrize("rows,cols", [(1, 4), (3, 7), (2, 8), (32, 2048), (17, 260), (64, 2560), (4096, 2560),
+                                       (5, 5000)])
+def test_rms_norm_silu_gate(rows, cols):
+    log(f"rms_norm_silu_gate rows={rows} cols={cols}")
+    x, g = rmsnorm_inputs(rows, cols, seed=rows + cols)
+    z = normal((rows, cols), rows * 7 + cols) * 3
+    z.ravel()[: min(z.size, 24)] = special_values()[: min(z.size, 24)]
+    out = rocm.rocm_fused_rms_norm_silu_gate_f32(DEV, up(x), up(g), up(z), rows, cols, 1e-6)
+    got = down(out, np.float32, (rows, cols))
+    want = oracle.rms_norm_silu_gate(x, g, z, 1e-6)
+    assert_close(got, want, what="rms_norm_silu_gate")
+    # the normalisation factor is the bit-exact RMSNorm one: where silu(z) == 1
+    # the output is bit-identical to rms_norm
+    ones = np.full_like(z, 1e30)
+    got1 = down(rocm.rocm_fused_rms_norm_silu_gate_f32(DEV, up(x), up(g), up(ones), rows, cols, 1e-6),
+                np.float32, (rows, cols))
+    assert_bitexact(got1, oracle.rms_norm(x, g, 1e-6) * np.float32(1e30), "silu gate = identity")
+
+
+def test_rms_norm_silu_gate_reference_kat_on_device():
+    # crates/kore-kernels/src/cpu_fused.rs:451-483
+    x = np.arange(1, 9, dtype=np.float32).reshape(2, 4)
+    z = np.array([0.5, 1.0, -0.5, 2.0, -1.0, 0.0, 1.5, -2.0], np.float32).reshape(2, 4)
+    got = down(rocm.rocm_fused_rms_norm_silu_gate_f32(DEV, up(x), up(np.ones(4, np.float32)), up(z), 2, 4, 1e-6),
+               np.float32, (2, 4))
+    assert np.isfinite(got).all() and got.ravel()[5] == 0.0
+    assert_close(got, oracle.rms_norm_silu_gate(x, np.ones(4), z, 1e-6), what="silu gate kat")
+
+
 # --------------------------------------------------------------- pre-quant
 @pytest.mark.parametrize("rows,cols", [(1, 2560), (64, 2560), (4096, 2560), (5, 33), (9, 300), (3, 8),
                                        (20, 2048), (7, 4096), (2, 4100)])

@@ -243,3 +243,21 @@ def test_segmented_exact_fold_compiled(tmp_path):
     r = subprocess.run([exe, "40000"], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "MISMATCH" not in r.stdout
+
+
+# ------------------------------------------------------- RMSNorm + SiLU gate
+def test_rms_norm_silu_gate_reference_kat_and_f64():
+    # crates/kore-kernels/src/cpu_fused.rs:451-483: x = 1..8 (2x4), gamma = 1,
+    # z as below; all finite and SiLU(0) = 0 zeroes element 5.
+    x = np.arange(1, 9, dtype=np.float32).reshape(2, 4)
+    z = np.array([0.5, 1.0, -0.5, 2.0, -1.0, 0.0, 1.5, -2.0], np.float32).reshape(2, 4)
+    y = oracle.rms_norm_silu_gate(x, np.ones(4, np.float32), z, 1e-6)
+    assert np.isfinite(y).all() and y.ravel()[5] == 0.0
+    # it is exactly RMSNorm (the pinned oracle) times the pinned silu
+    assert (y == oracle.rms_norm(x, np.ones(4), 1e-6) * oracle.silu(z)).all()
+    xg, g = rmsnorm_inputs(8, 96, seed=2)
+    zz = normal((8, 96), 3) * 3
+    y = oracle.rms_norm_silu_gate(xg, g, zz, 1e-6)
+    x64 = xg.astype(np.float64)
+    ref = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6) * g * (zz / (1 + np.exp(-zz.astype(np.float64))))
+    assert np.max(np.abs(y - ref) / np.maximum(np.abs(ref), 1e-6)) < 5e-6
