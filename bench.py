@@ -229,7 +229,7 @@ class Gelu(Workload):
 class Embedding(Workload):
     name = "embedding"
     V, D, N = 128256, 4096, 8192
-    kernel = "embedding_vec_kernel"
+    kernel = "embedding_vec1_kernel"
 
     def __init__(self):
         self.tokens = self.N
@@ -344,7 +344,7 @@ class Copy(Workload):
     used to calibrate rocprof's FETCH_SIZE / WRITE_SIZE counters."""
     name = "copy_1gib"
     N, D = 65536, 4096
-    kernel = "embedding_vec_kernel"
+    kernel = "embedding_vec1_kernel"
 
     def __init__(self):
         self.tokens = self.N

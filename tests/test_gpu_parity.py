@@ -115,6 +115,19 @@ def test_rms_norm_silu_gate(rows, cols):
     assert_bitexact(got1, oracle.rms_norm(x, g, 1e-6) * np.float32(1e30), "silu gate = identity")
 
 
+@pytest.mark.parametrize("cols", [2560, 2562])  # vector path and scalar path
+def test_rms_norm_silu_gate_wide_gate_range(cols):
+    # The gate's error grows with |z| (exp argument rounding); sweep the
+    # whole range where e^-z is finite, both signs, plus overflow territory.
+    log(f"rms_norm_silu_gate wide z cols={cols}")
+    rows = 64
+    x, g = rmsnorm_inputs(rows, cols, seed=9)
+    z = np.linspace(-100.0, 100.0, rows * cols, dtype=np.float32).reshape(rows, cols)
+    out = rocm.rocm_fused_rms_norm_silu_gate_f32(DEV, up(x), up(g), up(z), rows, cols, 1e-6)
+    got = down(out, np.float32, (rows, cols))
+    assert_close(got, oracle.rms_norm_silu_gate(x, g, z, 1e-6), what="rms_norm_silu_gate wide z")
+
+
 def test_rms_norm_silu_gate_reference_kat_on_device():
     # crates/kore-kernels/src/cpu_fused.rs:451-483
     x = np.arange(1, 9, dtype=np.float32).reshape(2, 4)
@@ -123,6 +136,13 @@ def test_rms_norm_silu_gate_reference_kat_on_device():
                np.float32, (2, 4))
     assert np.isfinite(got).all() and got.ravel()[5] == 0.0
     assert_close(got, oracle.rms_norm_silu_gate(x, np.ones(4), z, 1e-6), what="silu gate kat")
+    # cpu_fused.rs:660-697
+    xe = np.array([[100.0, -100.0, 0.0001, -0.0001]], np.float32)
+    ze = np.array([[50.0, -50.0, 0.0, 100.0]], np.float32)
+    ge = down(rocm.rocm_fused_rms_norm_silu_gate_f32(DEV, up(xe), up(np.ones(4, np.float32)), up(ze), 1, 4, 1e-6),
+              np.float32, (1, 4))
+    assert np.isfinite(ge).all() and abs(ge[0, 1]) < 1e-10 and abs(ge[0, 2]) < 1e-10
+    assert_close(ge, oracle.rms_norm_silu_gate(xe, np.ones(4), ze, 1e-6), what="silu gate extreme kat")
 
 
 # --------------------------------------------------------------- pre-quant

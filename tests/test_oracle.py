@@ -255,6 +255,12 @@ def test_rms_norm_silu_gate_reference_kat_and_f64():
     assert np.isfinite(y).all() and y.ravel()[5] == 0.0
     # it is exactly RMSNorm (the pinned oracle) times the pinned silu
     assert (y == oracle.rms_norm(x, np.ones(4), 1e-6) * oracle.silu(z)).all()
+    # cpu_fused.rs:660-697: extreme x and z; finite, silu(-50) and silu(0) gate to ~0
+    xe = np.array([[100.0, -100.0, 0.0001, -0.0001]], np.float32)
+    ze = np.array([[50.0, -50.0, 0.0, 100.0]], np.float32)
+    ye = oracle.rms_norm_silu_gate(xe, np.ones(4, np.float32), ze, 1e-6)
+    assert np.isfinite(ye).all() and abs(ye[0, 1]) < 1e-10 and abs(ye[0, 2]) < 1e-10
+    assert abs(ye[0, 0] - 50.0 * 100.0 / np.sqrt(5000.000005)) < 1e-4
     xg, g = rmsnorm_inputs(8, 96, seed=2)
     zz = normal((8, 96), 3) * 3
     y = oracle.rms_norm_silu_gate(xg, g, zz, 1e-6)
