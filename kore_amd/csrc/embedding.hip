@@ -15,7 +15,8 @@
 
 namespace kore {
 
-constexpr int kEmbBlock = 256;
+constexpr int kEmbBlock = 256;      // per-token loop and scalar kernels
+constexpr int kEmbMaxBlock = 1024;  // one-float4 kernel: blockDim chosen per call
 constexpr int kEmbUnroll = 4;  // float4 per thread per pass (rows > 16M floats)
 
 __global__ __launch_bounds__(kEmbBlock) void embedding_vec_kernel(const f32x4* __restrict__ table,
@@ -42,15 +43,18 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_vec_kernel(const f32x4* _
     for (; i < dim4; i += kEmbBlock) st_stream(dst + i, ld_cached(src + i));
 }
 
-// One float4 per thread: grid (token, chunk of kEmbBlock float4).  Many
-// small, short-lived waves keep more independent requests in flight than a
-// few long ones (measured best on MI355X for mixed read/write streams).
-__global__ __launch_bounds__(kEmbBlock) void embedding_vec1_kernel(const f32x4* __restrict__ table,
-                                                                   const uint32_t* __restrict__ ids,
-                                                                   f32x4* __restrict__ out, uint64_t vocab,
-                                                                   uint64_t dim4) {
+// One float4 per thread: grid (token, chunk of blockDim float4), blockDim =
+// the row's float4 count rounded up to a wave, at most 1024.  Short-lived
+// workgroups that each move one contiguous row chunk keep the most
+// independent requests in flight (measured on MI355X: a 1 GiB gather-copy
+// runs at 74.6% of 8 TB/s with 256-thread chunks, 81.5% with 1024, and
+// worse with several tokens per workgroup).
+__global__ __launch_bounds__(kEmbMaxBlock) void embedding_vec1_kernel(const f32x4* __restrict__ table,
+                                                                      const uint32_t* __restrict__ ids,
+                                                                      f32x4* __restrict__ out, uint64_t vocab,
+                                                                      uint64_t dim4) {
     const uint64_t t = blockIdx.x;
-    const uint64_t i = (uint64_t)blockIdx.y * kEmbBlock + threadIdx.x;
+    const uint64_t i = (uint64_t)blockIdx.y * blockDim.x + threadIdx.x;
     if (i >= dim4) return;
     const uint32_t id = ids[t];
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
@@ -89,9 +93,11 @@ extern "C" int kore_hip_embedding_f32(const float* table, const uint32_t* ids, f
     hipStream_t s = (hipStream_t)stream;
     dim3 grid((uint32_t)n_ids), block(kEmbBlock);
     if (dim % 4 == 0 && aligned16(out) && (vocab == 0 || aligned16(table))) {
-        const uint64_t chunks = (dim / 4 + kEmbBlock - 1) / kEmbBlock;
+        const uint64_t dim4 = dim / 4;
+        const uint32_t thr = dim4 >= (uint64_t)kEmbMaxBlock ? kEmbMaxBlock : (uint32_t)((dim4 + 63) / 64 * 64);
+        const uint64_t chunks = (dim4 + thr - 1) / thr;
         if (chunks <= 65535) {
-            hipLaunchKernelGGL(embedding_vec1_kernel, dim3((uint32_t)n_ids, (uint32_t)chunks), block, 0, s,
+            hipLaunchKernelGGL(embedding_vec1_kernel, dim3((uint32_t)n_ids, (uint32_t)chunks), dim3(thr), 0, s,
                                reinterpret_cast<const f32x4*>(table), ids, reinterpret_cast<f32x4*>(out), vocab,
                                dim / 4);
             return launch_status();

@@ -15,7 +15,8 @@
 // float4 at i+D/2 -> D/8 tasks per head.  Interleaved (pairs 2p, 2p+1): a task
 // is one float4 holding two pairs -> D/4 tasks per head.  Consecutive threads
 // take consecutive tasks, so each wave-wide access is 16 contiguous 16-byte
-// words per head segment.
+// words per head segment.  Q/K are touched once, so loads and stores are
+// nontemporal (measured 108.7 -> 106.5 us on the 8x2048x(32+8)x128 config).
 //
 // The rotation is the reference's: d[i] = x0*c - x1*s, d[j] = x0*s + x1*c,
 // with every product rounded on its own (-ffp-contract=off).
@@ -45,6 +46,7 @@ __device__ __forceinline__ float2 rot(float x0, float x1, float c, float s) {
 // global loads first, so the token's sincos work (first pass only) and the
 // barrier overlap the memory latency instead of delaying the loads.
 constexpr int kRopeBatch = 2;
+
 
 template <bool Interleaved>
 __global__ __launch_bounds__(kRopeMaxBlock) void rope_vec_kernel(RopeTensor t0, RopeTensor t1,
@@ -80,13 +82,13 @@ __global__ __launch_bounds__(kRopeMaxBlock) void rope_vec_kernel(RopeTensor t0, 
             if (Interleaved) {
                 p0[u] = reinterpret_cast<f32x4*>(v + 4 * k);
                 p1[u] = p0[u];
-                if (ok) x0[u] = *p0[u];
+                if (ok) x0[u] = ld_stream(p0[u]);
             } else {
                 p0[u] = reinterpret_cast<f32x4*>(v + 4 * k);
                 p1[u] = reinterpret_cast<f32x4*>(v + half + 4 * k);
                 if (ok) {
-                    x0[u] = *p0[u];
-                    x1[u] = *p1[u];
+                    x0[u] = ld_stream(p0[u]);
+                    x1[u] = ld_stream(p1[u]);
                 }
             }
         }
@@ -111,7 +113,7 @@ __global__ __launch_bounds__(kRopeMaxBlock) void rope_vec_kernel(RopeTensor t0, 
                 float2 r1 = rot(x0[u].z, x0[u].w, csv.z, csv.w);
                 f32x4 o;
                 o.x = r0.x; o.y = r0.y; o.z = r1.x; o.w = r1.y;
-                *p0[u] = o;
+                st_stream(p0[u], o);
             } else {
                 const f32x4 ca = *reinterpret_cast<const f32x4*>(&cs[4 * k]);      // c0 s0 c1 s1
                 const f32x4 cb = *reinterpret_cast<const f32x4*>(&cs[4 * k + 2]);  // c2 s2 c3 s3
@@ -122,8 +124,8 @@ __global__ __launch_bounds__(kRopeMaxBlock) void rope_vec_kernel(RopeTensor t0, 
                 f32x4 o0, o1;
                 o0.x = r0.x; o0.y = r1.x; o0.z = r2.x; o0.w = r3.x;
                 o1.x = r0.y; o1.y = r1.y; o1.z = r2.y; o1.w = r3.y;
-                *p0[u] = o0;
-                *p1[u] = o1;
+                st_stream(p0[u], o0);
+                st_stream(p1[u], o1);
             }
         }
     }
