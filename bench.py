@@ -20,7 +20,8 @@ Per workload:
     functions) timed on this host on a bounded sample of the same workload.
 
 Prints ONE JSON line (rank 0).  `--gpus N` with N > 1 exits: this build runs
-on one GPU (see DESIGN.md for how the path shards).
+on one GPU (every op is row- or element-independent, so a multi-GPU version
+shards token rows across processes with no exchange).
 """
 from __future__ import annotations
 
@@ -303,7 +304,7 @@ class Prequant(Workload):
 
 
 class RmsNormSiluGate(Workload):
-    """SURVEY next-row: y = RMSNorm(x) * silu(z) (cuda/ops.rs:717-751) on the
+    """y = RMSNorm(x) * silu(z) (cuda/ops.rs:717-751) on the
     pre-quant activation shape."""
     kernel = "row_norm_kernel"
 
@@ -339,6 +340,113 @@ class RmsNormSiluGate(Workload):
             f"{rows} rows, single thread"
 
 
+class Softmax(Workload):
+    """row softmax (cuda/ops.rs:486-511, cpu_fused.rs:195-231)
+    over attention-probability rows [16 heads x 2048 queries, 2048 keys]."""
+    kernel = "softmax_reg_kernel"
+
+    def __init__(self, rows=32768, cols=2048):
+        self.rows, self.cols = rows, cols
+        self.name = f"softmax_{rows}x{cols}"
+        self.tokens = rows
+        self.bytes = rows * cols * 8
+        self.desc = f"softmax f32 over the last dim of x[{rows},{cols}] ~ N(0,4^2)"
+
+    def setup(self, torch, lib):
+        self.lib = lib
+        self.k = n_sets(self.bytes)
+        self._dx = [randn(torch, (self.rows, self.cols), 200 + s, 0.0, 4.0) for s in range(self.k)]
+        self._dy = [torch.empty_like(self._dx[0]) for _ in range(self.k)]
+
+    def launch(self, i, stream):
+        j = i % self.k
+        return self.lib.kore_hip_softmax_f32(self._dx[j].data_ptr(), self._dy[j].data_ptr(), self.rows, self.cols,
+                                             stream)
+
+    def cpu_sample(self):
+        import oracle
+        from inputs import normal
+
+        rows = 2048
+        x = normal((rows, self.cols), 0) * 4
+        return (lambda: oracle.softmax(x)), rows * self.cols * 8, rows, 1, f"{rows} rows, single thread"
+
+
+class SoftmaxBackward(Workload):
+    """fused_softmax_backward (cpu_fused_backward.rs:86-115)."""
+    kernel = "softmax_reg_kernel"
+
+    def __init__(self, rows=32768, cols=2048):
+        self.rows, self.cols = rows, cols
+        self.name = f"softmax_backward_{rows}x{cols}"
+        self.tokens = rows
+        self.bytes = rows * cols * 12
+        self.desc = f"softmax backward f32 dx = y*(dy - sum(y*dy)), y, dy, dx [{rows},{cols}]"
+
+    def setup(self, torch, lib):
+        self.lib = lib
+        self.k = n_sets(self.bytes)
+        self._dy_ = [torch.softmax(randn(torch, (self.rows, self.cols), 300 + s), dim=-1) for s in range(self.k)]
+        self._dg = [randn(torch, (self.rows, self.cols), 400 + s) for s in range(self.k)]
+        self._do = [torch.empty_like(self._dg[0]) for _ in range(self.k)]
+
+    def launch(self, i, stream):
+        j = i % self.k
+        return self.lib.kore_hip_softmax_backward_f32(self._dg[j].data_ptr(), self._dy_[j].data_ptr(),
+                                                      self._do[j].data_ptr(), self.rows, self.cols, stream)
+
+    def cpu_sample(self):
+        import oracle
+        from inputs import normal
+
+        rows = 2048
+        y = oracle.softmax(normal((rows, self.cols), 0))
+        dy = normal((rows, self.cols), 1)
+        return (lambda: oracle.softmax_backward(dy, y)), rows * self.cols * 12, rows, 1, f"{rows} rows, single thread"
+
+
+class RmsNormBackward(Workload):
+    """fused_rms_norm_backward (cpu_fused_backward.rs:20-81):
+    dx and dgamma; three launches (row pass, partial sums, final sum)."""
+    kernel = "rms_bwd_rows_kernel"
+
+    def __init__(self, rows=16384, cols=2048):
+        self.rows, self.cols = rows, cols
+        self.name = f"rms_norm_backward_{rows}x{cols}"
+        self.tokens = rows
+        self.bytes = rows * cols * 12 + cols * 8
+        self.desc = (f"RMSNorm backward f32: dy, x [{rows},{cols}] -> dx [{rows},{cols}], dgamma [{cols}] "
+                     f"(eps 1e-5, deterministic dgamma)")
+
+    def setup(self, torch, lib):
+        self.lib = lib
+        self.k = n_sets(self.bytes)
+        self._dx_ = [randn(torch, (self.rows, self.cols), 500 + s) for s in range(self.k)]
+        self._ddy = [randn(torch, (self.rows, self.cols), 600 + s) for s in range(self.k)]
+        self._dout = [torch.empty_like(self._dx_[0]) for _ in range(self.k)]
+        self._dg = randn(torch, (self.cols,), 700, 1.0, 0.02)
+        self._dgg = torch.empty_like(self._dg)
+        self.wsb = lib.kore_hip_rms_norm_backward_workspace_bytes(self.rows, self.cols)
+        self._dws = torch.empty(self.wsb, dtype=torch.uint8, device="cuda")
+
+    def launch(self, i, stream):
+        j = i % self.k
+        return self.lib.kore_hip_rms_norm_backward_f32(self._ddy[j].data_ptr(), self._dx_[j].data_ptr(),
+                                                       self._dg.data_ptr(), self._dout[j].data_ptr(),
+                                                       self._dgg.data_ptr(), self._dws.data_ptr(), self.wsb,
+                                                       self.rows, self.cols, 1e-5, stream)
+
+    def cpu_sample(self):
+        import oracle
+        from inputs import normal, rmsnorm_inputs
+
+        rows = 2048
+        x, g = rmsnorm_inputs(rows, self.cols, 0)
+        dy = normal((rows, self.cols), 1)
+        return (lambda: oracle.rms_norm_backward(dy, x, g, 1e-5)), rows * self.cols * 12 + self.cols * 8, rows, 1, \
+            f"{rows} rows, single thread"
+
+
 class Copy(Workload):
     """A plain 1 GiB device copy through the gather kernel with ids = 0..N-1;
     used to calibrate rocprof's FETCH_SIZE / WRITE_SIZE counters."""
@@ -367,7 +475,8 @@ class Copy(Workload):
 
 def all_workloads():
     return [RopeQK(False), RopeQK(True), RMSNorm(32, 2048), RMSNorm(16384, 2048), Swiglu(), Gelu(), Embedding(),
-            Prequant(4096), Prequant(64), Prequant(1), RmsNormSiluGate(), Copy()]
+            Prequant(4096), Prequant(64), Prequant(1), RmsNormSiluGate(), Softmax(), SoftmaxBackward(),
+            RmsNormBackward(), Copy()]
 
 
 # ------------------------------------------------------------------ measure
@@ -435,7 +544,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested). The fused layer ops are "
-              "row/element independent and shard by token rows with no exchange; see DESIGN.md.", file=sys.stderr)
+              "row/element independent and shard by token rows with no exchange.", file=sys.stderr)
         sys.exit(2)
     import torch
 

@@ -155,6 +155,57 @@ int kore_hip_rms_norm_silu_gate_f32(const float *x, const float *weight,
                                     uint64_t cols, float eps,
                                     kore_stream_t stream);
 
+/* ---------------------------------------------------------------- Softmax
+ * Row softmax over the last dimension of x[rows, cols]:
+ * out[r, :] = e * (1 / sum(e)), e = exp(x[r, :] - max(x[r, :])), the max
+ * skipping NaN like f32::max.  Replaces cuda_softmax_f32
+ * (crates/kore-kernels/src/cuda/ops.rs:486-511, kernel
+ * crates/kore-kernels/src/cuda/kernels/softmax.cu:26-86); twin of
+ * fused_softmax (crates/kore-kernels/src/cpu_fused.rs:195-231).  f32 tol.
+ * out may equal x. */
+int kore_hip_softmax_f32(const float *x, float *out, uint64_t rows,
+                         uint64_t cols, kore_stream_t stream);
+
+/* Causal row softmax: row r (counting all rows of the call) keeps columns
+ * c < seq_offset + r + 1; the others are excluded from the max and written as
+ * 0; a row whose kept sum is not > 0 is scaled by 0.  Replaces the
+ * softmax_causal_f32 kernel (crates/kore-kernels/src/cuda/kernels/softmax.cu:88-157),
+ * which the reference launches from no host wrapper.  f32 tol.  out may
+ * equal x. */
+int kore_hip_softmax_causal_f32(const float *x, float *out, uint64_t rows,
+                                uint64_t cols, uint64_t seq_offset,
+                                kore_stream_t stream);
+
+/* Softmax backward: grad_in[r, :] = out[r, :] * (grad_out[r, :] - dot_r),
+ * dot_r = sum(out[r, :] * grad_out[r, :]).  Twin of fused_softmax_backward
+ * (crates/kore-kernels/src/cpu_fused_backward.rs:86-115); the reference has
+ * no GPU version.  f32 tol.  grad_in may equal out or grad_out. */
+int kore_hip_softmax_backward_f32(const float *grad_out, const float *out,
+                                  float *grad_in, uint64_t rows, uint64_t cols,
+                                  kore_stream_t stream);
+
+/* --------------------------------------------------------- RMSNorm backward
+ * For y = RMSNorm(x) * gamma (rows x cols), given grad_out = dL/dy:
+ *   inv_r = 1 / sqrt(sum_i x^2 / cols + eps)
+ *   grad_x[r, i]  = (gamma[i] * inv_r) * grad_out[r, i] - coeff_r * x[r, i],
+ *   coeff_r = (sum_i (x * grad_out) * gamma * inv_r) / (sum_i x^2 + eps * cols)
+ *   grad_gamma[i] = sum_r (grad_out[r, i] * x[r, i]) * inv_r   (overwritten)
+ * Twin of fused_rms_norm_backward
+ * (crates/kore-kernels/src/cpu_fused_backward.rs:20-81); the reference has no
+ * GPU version.  f32 tol.  grad_gamma is deterministic (fixed reduction order).
+ * workspace: device scratch of at least
+ * kore_hip_rms_norm_backward_workspace_bytes(rows, cols) bytes (the dgamma
+ * partial sums), else KORE_HIP_ERR_BAD_DIM.  grad_x must not overlap
+ * grad_out or x (KORE_HIP_ERR_ALIAS).  rows == 0 zeroes grad_gamma. */
+uint64_t kore_hip_rms_norm_backward_workspace_bytes(uint64_t rows, uint64_t cols);
+
+int kore_hip_rms_norm_backward_f32(const float *grad_out, const float *x,
+                                   const float *gamma, float *grad_x,
+                                   float *grad_gamma, float *workspace,
+                                   uint64_t workspace_bytes, uint64_t rows,
+                                   uint64_t cols, float eps,
+                                   kore_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

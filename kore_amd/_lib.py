@@ -40,6 +40,15 @@ SIGNATURES = {
     "kore_hip_embedding_f32": [_ptr, _ptr, _ptr, _u64, _u64, _u64, _ptr],
     "kore_hip_rms_norm_quant_i8": [_ptr, _ptr, _ptr, _ptr, _u64, _u64, _f32, _ptr],
     "kore_hip_rms_norm_silu_gate_f32": [_ptr, _ptr, _ptr, _ptr, _u64, _u64, _f32, _ptr],
+    "kore_hip_softmax_f32": [_ptr, _ptr, _u64, _u64, _ptr],
+    "kore_hip_softmax_causal_f32": [_ptr, _ptr, _u64, _u64, _u64, _ptr],
+    "kore_hip_softmax_backward_f32": [_ptr, _ptr, _ptr, _u64, _u64, _ptr],
+    "kore_hip_rms_norm_backward_f32": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _f32, _ptr],
+}
+
+# Entry points whose return type is not int.
+RESTYPES = {
+    "kore_hip_rms_norm_backward_workspace_bytes": ([_u64, _u64], _u64),
 }
 
 
@@ -71,6 +80,12 @@ def load() -> ctypes.CDLL:
                 raise KoreLibraryError(f"{LIB_PATH} does not export {name}")
             fn.argtypes = argtypes
             fn.restype = _int
+        for name, (argtypes, restype) in RESTYPES.items():
+            fn = getattr(lib, name, None)
+            if fn is None:
+                raise KoreLibraryError(f"{LIB_PATH} does not export {name}")
+            fn.argtypes = argtypes
+            fn.restype = restype
         lib.kore_hip_status_string.argtypes = [_int]
         lib.kore_hip_status_string.restype = ctypes.c_char_p
         _lib = lib

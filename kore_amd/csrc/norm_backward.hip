@@ -1,0 +1,347 @@
+// norm_backward.hip -- RMSNorm backward: dx and dgamma in one pass over the
+// rows plus a small deterministic column reduction.
+//
+// Definition: crates/kore-kernels/src/cpu_fused_backward.rs:20-81
+// (fused_rms_norm_backward), per row r with d = cols:
+//   sum_sq = sum_i x^2;  inv = 1 / sqrt(sum_sq / d + eps)
+//   dgamma[i] += (dy[i] * x[i]) * inv                 (accumulated over rows)
+//   dot = sum_i (x[i] * dy[i]) * g[i]
+//   coeff = (dot * inv) / (sum_sq + eps * d)
+//   dx[i] = (g[i] * inv) * dy[i] - coeff * x[i]
+// Sums are tree reductions (f32 tolerance; the reference has no GPU version).
+//
+// Roofline: HBM.  Algorithmic bytes: x and dy read once, dx written once
+// (12 * rows * cols), plus gamma and dgamma.  The dgamma partials add
+// 2 * P * cols * 4 bytes (P = the workgroup count, ~1024 for large batches:
+// 4% of the traffic at 16384 x 2048).
+//
+// Vector path (cols % 4 == 0, 16-byte aligned, cols <= 4096):
+//   1. rms_bwd_rows_kernel: a row is split over S = 1, 2 or 4 waves (at
+//      most 4 float4 columns per wave and operand); a workgroup of 4 waves
+//      runs up to 16 row iterations; each wave's dgamma partial stays in
+//      registers (gamma is re-read from cache per row); the row slots'
+//      partials are added in a fixed order through LDS and written as
+//      workspace row p = the block index.
+//   2. rms_bwd_partials_kernel: block (column chunk of 64 float4, group of 64
+//      partials) sums its group in a fixed order -> level-2 rows.
+//   3. rms_bwd_final_kernel: one thread per float4 column sums the level-2
+//      rows in order -> dgamma.
+// Generic path (any shape): one workgroup per row writes dx and inv[r] to the
+// workspace; then one thread per column folds its dgamma over the rows in
+// the reference's order.
+#include "common.hpp"
+#include "kore_hip_internal.hpp"
+
+namespace kore {
+
+constexpr int kBwBlock = 256;
+constexpr int kBwWaves = kBwBlock / kWave;
+constexpr uint32_t kBwGroup = 64;  // partial rows per level-2 row
+
+struct BwArgs {
+    const float* dy;
+    const float* x;
+    const float* g;
+    float* dx;
+    float* dgamma;
+    float* ws;
+    uint64_t rows;
+    uint64_t cols;
+    float eps;
+    uint32_t rpw;       // row iterations per workgroup (vector path)
+    uint64_t partials;  // P
+    uint64_t groups;    // level-2 rows
+};
+
+__device__ __forceinline__ float sum4(f32x4 a) { return (a.x + a.y) + (a.z + a.w); }
+
+// A row is split over S waves (wave w: row slot j = w / S, column part
+// q = w % S, float4 columns (q*NCHW + k)*64 + lane, k < NCHW), so a wave holds
+// at most 4 float4 per operand.  The workgroup covers rows
+// [b*rpb, (b+1)*rpb), rpb = iters * (4 / S): iteration i takes rows
+// b*rpb + i*(4/S) + j.  Per row, the S waves' partial sums meet in LDS (slot
+// parity double-buffered, one barrier per iteration) and are added in q
+// order.  Each wave keeps its dgamma partial in registers; at the end the
+// row slots' partials are added in j order through LDS and written as
+// workspace row b.
+template <int NCHW, int S>
+__global__ __launch_bounds__(kBwBlock) void rms_bwd_rows_kernel(BwArgs a) {
+    constexpr int kSlots = kBwWaves / S;
+    extern __shared__ f32x4 part[];  // [cols4]
+    __shared__ float red[2][kBwWaves][2];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int j = wave / S, q = wave % S;
+    const uint32_t cols4 = (uint32_t)(a.cols >> 2);
+    const float fcols = (float)a.cols;
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    const uint64_t rpb = (uint64_t)a.rpw * kSlots;
+    const uint64_t rbase = (uint64_t)blockIdx.x * rpb;
+
+    f32x4 acc[NCHW];
+#pragma unroll
+    for (int k = 0; k < NCHW; ++k) acc[k] = zero;
+    for (uint32_t it = 0; it < a.rpw; ++it) {
+        const uint64_t r = rbase + (uint64_t)it * kSlots + j;
+        const bool live = r < a.rows;
+        const uint64_t rr = live ? r : 0;
+        const f32x4* xr = reinterpret_cast<const f32x4*>(a.x) + rr * cols4;
+        const f32x4* dr = reinterpret_cast<const f32x4*>(a.dy) + rr * cols4;
+        // gamma is re-read per row (an L1/L2 hit) instead of held in
+        // registers: the empty asm makes its base opaque so the loads stay
+        // inside the loop.
+        uint64_t gaddr = reinterpret_cast<uint64_t>(a.g);
+        asm volatile("" : "+s"(gaddr));
+        const f32x4* g4 = reinterpret_cast<const f32x4*>(gaddr);
+        f32x4 xv[NCHW], dv[NCHW];
+#pragma unroll
+        for (int k = 0; k < NCHW; ++k) {
+            const uint32_t f = (uint32_t)(q * NCHW + k) * kWave + lane;
+            xv[k] = (live && f < cols4) ? ld_stream(xr + f) : zero;
+            dv[k] = (live && f < cols4) ? ld_stream(dr + f) : zero;
+        }
+        float ss = 0.0f, dot = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NCHW; ++k) {
+            const uint32_t f = (uint32_t)(q * NCHW + k) * kWave + lane;
+            const f32x4 gv = f < cols4 ? ld_cached(g4 + f) : zero;
+            ss += sum4(xv[k] * xv[k]);
+            dot += sum4((xv[k] * dv[k]) * gv);
+        }
+        ss = wave_sum(ss);
+        dot = wave_sum(dot);
+        if (S > 1) {
+            const int par = it & 1;
+            if (lane == 0) {
+                red[par][wave][0] = ss;
+                red[par][wave][1] = dot;
+            }
+            __syncthreads();
+            ss = red[par][j * S][0];
+            dot = red[par][j * S][1];
+#pragma unroll
+            for (int t = 1; t < S; ++t) {
+                ss += red[par][j * S + t][0];
+                dot += red[par][j * S + t][1];
+            }
+        }
+        const float inv = 1.0f / sqrtf(ss / fcols + a.eps);
+        const float coeff = (dot * inv) / (ss + a.eps * fcols);
+        if (live) {
+            f32x4* orow = reinterpret_cast<f32x4*>(a.dx) + r * cols4;
+            asm volatile("" : "+s"(gaddr));
+            const f32x4* g4b = reinterpret_cast<const f32x4*>(gaddr);
+#pragma unroll
+            for (int k = 0; k < NCHW; ++k) {
+                const uint32_t f = (uint32_t)(q * NCHW + k) * kWave + lane;
+                if (f < cols4) st_stream(orow + f, (ld_cached(g4b + f) * inv) * dv[k] - coeff * xv[k]);
+                acc[k] = acc[k] + (dv[k] * xv[k]) * inv;
+            }
+        }
+    }
+    // Row slots' partials added in j order through LDS, then one partial row.
+#pragma unroll 1
+    for (int jj = 0; jj < kSlots; ++jj) {
+        if (j == jj) {
+#pragma unroll
+            for (int k = 0; k < NCHW; ++k) {
+                const uint32_t f = (uint32_t)(q * NCHW + k) * kWave + lane;
+                if (f < cols4) part[f] = (jj == 0) ? acc[k] : part[f] + acc[k];
+            }
+        }
+        __syncthreads();
+    }
+    f32x4* wrow = reinterpret_cast<f32x4*>(a.ws) + (uint64_t)blockIdx.x * cols4;
+    for (uint32_t f = threadIdx.x; f < cols4; f += kBwBlock) wrow[f] = part[f];
+}
+
+// grid (ceil(cols4 / 64), groups): wave w of the block sums partial rows
+// g*64 + w*16 + k (k = 0..15, in order) of column float4 cx*64 + lane; the 4
+// wave sums are then added in wave order.
+__global__ __launch_bounds__(kBwBlock) void rms_bwd_partials_kernel(BwArgs a) {
+    __shared__ f32x4 red[kBwWaves][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const uint64_t cols4 = a.cols >> 2;
+    const uint64_t col = (uint64_t)blockIdx.x * kWave + lane;
+    const uint64_t grp = blockIdx.y;
+    const f32x4* w4 = reinterpret_cast<const f32x4*>(a.ws);
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    constexpr int kPer = kBwGroup / kBwWaves;
+    f32x4 v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint64_t p = grp * kBwGroup + (uint64_t)wave * kPer + k;
+        v[k] = (p < a.partials && col < cols4) ? w4[p * cols4 + col] : zero;
+    }
+    f32x4 s = v[0];
+#pragma unroll
+    for (int k = 1; k < kPer; ++k) s = s + v[k];
+    red[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && col < cols4) {
+        f32x4 t = red[0][lane];
+#pragma unroll
+        for (int w = 1; w < kBwWaves; ++w) t = t + red[w][lane];
+        reinterpret_cast<f32x4*>(a.ws)[(a.partials + grp) * cols4 + col] = t;
+    }
+}
+
+__global__ __launch_bounds__(kBwBlock) void rms_bwd_final_kernel(BwArgs a) {
+    const uint64_t cols4 = a.cols >> 2;
+    const uint64_t col = (uint64_t)blockIdx.x * kBwBlock + threadIdx.x;
+    if (col >= cols4) return;
+    const f32x4* l2 = reinterpret_cast<const f32x4*>(a.ws) + a.partials * cols4;
+    f32x4 t = l2[col];
+    for (uint64_t g = 1; g < a.groups; ++g) t = t + l2[g * cols4 + col];
+    reinterpret_cast<f32x4*>(a.dgamma)[col] = t;
+}
+
+// ---- generic path
+__global__ __launch_bounds__(kBwBlock) void rms_bwd_row_generic_kernel(BwArgs a) {
+    __shared__ float red[2][kBwWaves];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const uint64_t r = blockIdx.x;
+    const float* xr = a.x + r * a.cols;
+    const float* dr = a.dy + r * a.cols;
+    float ss = 0.0f, dot = 0.0f;
+    for (uint64_t i = threadIdx.x; i < a.cols; i += kBwBlock) {
+        const float xv = xr[i];
+        ss += xv * xv;
+        dot += (xv * dr[i]) * a.g[i];
+    }
+    ss = wave_sum(ss);
+    dot = wave_sum(dot);
+    if (lane == 0) {
+        red[0][wave] = ss;
+        red[1][wave] = dot;
+    }
+    __syncthreads();
+    ss = red[0][0];
+    dot = red[1][0];
+#pragma unroll
+    for (int w = 1; w < kBwWaves; ++w) {
+        ss += red[0][w];
+        dot += red[1][w];
+    }
+    const float fcols = (float)a.cols;
+    const float inv = 1.0f / sqrtf(ss / fcols + a.eps);
+    const float coeff = (dot * inv) / (ss + a.eps * fcols);
+    for (uint64_t i = threadIdx.x; i < a.cols; i += kBwBlock)
+        a.dx[r * a.cols + i] = (a.g[i] * inv) * dr[i] - coeff * xr[i];
+    if (threadIdx.x == 0) a.ws[r] = inv;
+}
+
+// One thread per column: dgamma[c] = sum over rows, in row order.
+__global__ __launch_bounds__(kBwBlock) void rms_bwd_col_generic_kernel(BwArgs a) {
+    const uint64_t c = (uint64_t)blockIdx.x * kBwBlock + threadIdx.x;
+    if (c >= a.cols) return;
+    float acc = 0.0f;
+    for (uint64_t r = 0; r < a.rows; ++r) acc = acc + (a.dy[r * a.cols + c] * a.x[r * a.cols + c]) * a.ws[r];
+    a.dgamma[c] = acc;
+}
+
+__global__ __launch_bounds__(kBwBlock) void fill_zero_kernel(float* p, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * kBwBlock + threadIdx.x;
+    if (i < n) p[i] = 0.0f;
+}
+
+static bool bwd_vec(uint64_t cols) { return cols % 4 == 0 && cols / 4 <= 1024; }
+
+// Waves per row for the vector path: each wave holds <= 4 float4 columns.
+static uint32_t bwd_split(uint64_t cols) {
+    const uint64_t c4 = cols / 4;
+    return c4 <= 256 ? 1u : (c4 <= 512 ? 2u : 4u);
+}
+
+// Row iterations per workgroup: ~1024 workgroups (4 waves each) fill the
+// chip; at most 16 iterations so that large batches keep few partial rows.
+static uint32_t bwd_iters(uint64_t rows, uint32_t split) {
+    const uint64_t per_iter = kBwWaves / split;
+    uint64_t it = (rows + 1024 * per_iter - 1) / (1024 * per_iter);
+    if (it < 1) it = 1;
+    if (it > 16) it = 16;
+    return (uint32_t)it;
+}
+
+// Workspace floats for the vector and generic plans (the larger is required).
+static uint64_t bwd_ws_floats(uint64_t rows, uint64_t cols, uint64_t* partials, uint64_t* groups,
+                              uint32_t* iters) {
+    const uint32_t split = bwd_split(cols);
+    const uint32_t it = bwd_iters(rows, split);
+    const uint64_t rpb = (uint64_t)it * (kBwWaves / split);  // rows per block = per partial row
+    const uint64_t p = (rows + rpb - 1) / rpb;
+    const uint64_t g = (p + kBwGroup - 1) / kBwGroup;
+    if (partials) *partials = p;
+    if (groups) *groups = g;
+    if (iters) *iters = it;
+    const uint64_t vec = bwd_vec(cols) ? (p + g) * cols : 0;
+    return vec > rows ? vec : rows;
+}
+
+template <int NCHW, int S>
+static void launch_rows(const BwArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((rms_bwd_rows_kernel<NCHW, S>), dim3((uint32_t)a.partials), dim3(kBwBlock),
+                       (a.cols / 4) * sizeof(f32x4), s, a);
+}
+
+}  // namespace kore
+
+using namespace kore;
+
+extern "C" uint64_t kore_hip_rms_norm_backward_workspace_bytes(uint64_t rows, uint64_t cols) {
+    if (rows == 0 || cols == 0) return 0;
+    uint64_t elems;
+    if (!mul_ok(rows, cols, &elems) || elems > kMaxElements) return 0;
+    return bwd_ws_floats(rows, cols, nullptr, nullptr, nullptr) * sizeof(float);
+}
+
+extern "C" int kore_hip_rms_norm_backward_f32(const float* grad_out, const float* x, const float* gamma,
+                                              float* grad_x, float* grad_gamma, float* workspace,
+                                              uint64_t workspace_bytes, uint64_t rows, uint64_t cols, float eps,
+                                              kore_stream_t stream) {
+    if (cols == 0) return KORE_HIP_OK;
+    if (!grad_gamma || !gamma) return KORE_HIP_ERR_NULL_PTR;
+    hipStream_t s = (hipStream_t)stream;
+    if (rows == 0) {  // dgamma of an empty batch is zero (the reference's vec![0.0; d])
+        if (cols > kMaxElements) return KORE_HIP_ERR_OVERFLOW;
+        // A fill kernel rather than hipMemsetAsync, so the call can be captured in a graph.
+        hipLaunchKernelGGL(fill_zero_kernel, dim3((uint32_t)((cols + kBwBlock - 1) / kBwBlock)), dim3(kBwBlock), 0, s,
+                           grad_gamma, cols);
+        return launch_status();
+    }
+    if (!grad_out || !x || !grad_x || !workspace) return KORE_HIP_ERR_NULL_PTR;
+    uint64_t elems;
+    if (!mul_ok(rows, cols, &elems) || elems > kMaxElements || rows > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
+    BwArgs a{grad_out, x, gamma, grad_x, grad_gamma, workspace, rows, cols, eps, 0, 0, 0};
+    const uint64_t need = bwd_ws_floats(rows, cols, &a.partials, &a.groups, &a.rpw) * sizeof(float);
+    if (a.groups > 65535) return KORE_HIP_ERR_OVERFLOW;  // grid.y of the partial reduction
+    if (workspace_bytes < need) return KORE_HIP_ERR_BAD_DIM;
+    // grad_x must not overlap the inputs (the row pass reads a row ahead).
+    const char* o0 = (const char*)grad_x;
+    const char* o1 = o0 + elems * sizeof(float);
+    for (const float* in : {grad_out, x}) {
+        const char* i0 = (const char*)in;
+        if (i0 < o1 && o0 < i0 + elems * sizeof(float)) return KORE_HIP_ERR_ALIAS;
+    }
+    const bool vec = bwd_vec(cols) && aligned16(grad_out) && aligned16(x) && aligned16(gamma) &&
+                     aligned16(grad_x) && aligned16(grad_gamma) && aligned16(workspace);
+    if (vec) {
+        const uint64_t cols4 = cols / 4;
+        if (cols4 <= 64) launch_rows<1, 1>(a, s);
+        else if (cols4 <= 128) launch_rows<2, 1>(a, s);
+        else if (cols4 <= 256) launch_rows<4, 1>(a, s);
+        else if (cols4 <= 512) launch_rows<4, 2>(a, s);
+        else launch_rows<4, 4>(a, s);
+        hipLaunchKernelGGL(rms_bwd_partials_kernel, dim3((uint32_t)((cols4 + kWave - 1) / kWave), (uint32_t)a.groups),
+                           dim3(kBwBlock), 0, s, a);
+        hipLaunchKernelGGL(rms_bwd_final_kernel, dim3((uint32_t)((cols4 + kBwBlock - 1) / kBwBlock)),
+                           dim3(kBwBlock), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(rms_bwd_row_generic_kernel, dim3((uint32_t)rows), dim3(kBwBlock), 0, s, a);
+        hipLaunchKernelGGL(rms_bwd_col_generic_kernel, dim3((uint32_t)((cols + kBwBlock - 1) / kBwBlock)),
+                           dim3(kBwBlock), 0, s, a);
+    }
+    return launch_status();
+}

@@ -286,3 +286,69 @@ __all__ = [
     "rocm_swiglu_f32", "rope_inv_freq_host", "rocm_rope_inv_freq_f32", "rocm_rope_f32", "rocm_rope_qk_f32",
     "rocm_embedding_f32", "rocm_rms_norm_quant_i8", "rocm_fused_rms_norm_silu_gate_f32",
 ]
+
+
+# ---------------------------------------------------------------- softmax
+def rocm_softmax_f32(device_idx: int, a: HipBuffer, rows: int, cols: int,
+                     out: Optional[HipBuffer] = None) -> HipBuffer:
+    """``cuda_softmax_f32`` (cuda/ops.rs:486-511); twin of ``fused_softmax``
+    (cpu_fused.rs:195-231)."""
+    _require_device(device_idx)
+    n = rows * cols * 4
+    _need(a, n, "softmax input")
+    o = _out(device_idx, out, n, "softmax out")
+    _check(_lib.load().kore_hip_softmax_f32(a.ptr, o.ptr, rows, cols, _stream(device_idx)), "softmax_f32")
+    return o
+
+
+def rocm_softmax_causal_f32(device_idx: int, a: HipBuffer, rows: int, cols: int, seq_offset: int = 0,
+                            out: Optional[HipBuffer] = None) -> HipBuffer:
+    """The ``softmax_causal_f32`` kernel (cuda/kernels/softmax.cu:88-157): row r
+    keeps columns < seq_offset + r + 1."""
+    _require_device(device_idx)
+    n = rows * cols * 4
+    _need(a, n, "softmax_causal input")
+    o = _out(device_idx, out, n, "softmax_causal out")
+    _check(_lib.load().kore_hip_softmax_causal_f32(a.ptr, o.ptr, rows, cols, seq_offset, _stream(device_idx)),
+           "softmax_causal_f32")
+    return o
+
+
+def rocm_softmax_backward_f32(device_idx: int, grad_output: HipBuffer, output: HipBuffer, rows: int, cols: int,
+                              out: Optional[HipBuffer] = None) -> HipBuffer:
+    """``fused_softmax_backward`` (cpu_fused_backward.rs:86-115) on the device:
+    grad_input = y * (dy - sum(y * dy))."""
+    _require_device(device_idx)
+    n = rows * cols * 4
+    _need(grad_output, n, "softmax_backward grad_output")
+    _need(output, n, "softmax_backward output")
+    o = _out(device_idx, out, n, "softmax_backward grad_input")
+    _check(_lib.load().kore_hip_softmax_backward_f32(grad_output.ptr, output.ptr, o.ptr, rows, cols,
+                                                     _stream(device_idx)), "softmax_backward_f32")
+    return o
+
+
+# ------------------------------------------------------- RMSNorm backward
+def rocm_rms_norm_backward_workspace_bytes(rows: int, cols: int) -> int:
+    """Device scratch ``rocm_rms_norm_backward_f32`` needs for (rows, cols)."""
+    return int(_lib.load().kore_hip_rms_norm_backward_workspace_bytes(rows, cols))
+
+
+def rocm_rms_norm_backward_f32(device_idx: int, grad_output: HipBuffer, input: HipBuffer, gamma: HipBuffer,
+                               rows: int, cols: int, eps: float, workspace: Optional[HipBuffer] = None,
+                               grad_input: Optional[HipBuffer] = None, grad_gamma: Optional[HipBuffer] = None):
+    """``fused_rms_norm_backward`` (cpu_fused_backward.rs:20-81) on the device
+    -> (grad_input, grad_gamma).  The workspace is allocated when not given."""
+    _require_device(device_idx)
+    n = rows * cols * 4
+    _need(grad_output, n, "rms_norm_backward grad_output")
+    _need(input, n, "rms_norm_backward input")
+    _need(gamma, cols * 4, "rms_norm_backward gamma")
+    gx = _out(device_idx, grad_input, n, "rms_norm_backward grad_input")
+    gg = _out(device_idx, grad_gamma, cols * 4, "rms_norm_backward grad_gamma")
+    wsb = rocm_rms_norm_backward_workspace_bytes(rows, cols)
+    ws = workspace if workspace is not None else HipBuffer.empty(device_idx, max(wsb, 16))
+    _check(_lib.load().kore_hip_rms_norm_backward_f32(grad_output.ptr, input.ptr, gamma.ptr, gx.ptr, gg.ptr, ws.ptr,
+                                                      ws.nbytes, rows, cols, eps, _stream(device_idx)),
+           "rms_norm_backward_f32")
+    return gx, gg

@@ -248,3 +248,81 @@ void kore_oracle_rms_norm_silu_gate_f32(const float *x, const float *gamma,
         }
     }
 }
+
+/* cpu_fused.rs:208-227. */
+void kore_oracle_softmax_f32(const float *x, float *y, size_t rows, size_t cols) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float *row = x + r * cols;
+        float *out = y + r * cols;
+        float max_val = -INFINITY;
+        for (size_t i = 0; i < cols; ++i) max_val = rust_fmax(max_val, row[i]);
+        float sum = 0.0f;
+        for (size_t i = 0; i < cols; ++i) {
+            float e = expf(row[i] - max_val);
+            out[i] = e;
+            sum = sum + e;
+        }
+        float inv_sum = 1.0f / sum;
+        for (size_t i = 0; i < cols; ++i) out[i] = out[i] * inv_sum;
+    }
+}
+
+/* softmax.cu:101-156 with sequential sums; fmaxf is IEEE maxNum like f32::max. */
+void kore_oracle_softmax_causal_f32(const float *x, float *y, size_t rows,
+                                    size_t cols, size_t seq_offset) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float *row = x + r * cols;
+        float *out = y + r * cols;
+        size_t limit = seq_offset + r + 1;
+        float max_val = -INFINITY;
+        for (size_t c = 0; c < cols; ++c) {
+            float v = c < limit ? row[c] : -INFINITY;
+            max_val = rust_fmax(max_val, v);
+        }
+        float sum = 0.0f;
+        for (size_t c = 0; c < cols; ++c) {
+            float v = c < limit ? expf(row[c] - max_val) : 0.0f;
+            out[c] = v;
+            sum = sum + v;
+        }
+        float inv_sum = sum > 0.0f ? 1.0f / sum : 0.0f;
+        for (size_t c = 0; c < cols; ++c) out[c] = out[c] * inv_sum;
+    }
+}
+
+/* cpu_fused_backward.rs:102-112. */
+void kore_oracle_softmax_backward_f32(const float *dy, const float *y,
+                                      float *dx, size_t rows, size_t cols) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float *yr = y + r * cols;
+        const float *dyr = dy + r * cols;
+        float dot = 0.0f;
+        for (size_t i = 0; i < cols; ++i) dot = dot + yr[i] * dyr[i];
+        for (size_t i = 0; i < cols; ++i) dx[r * cols + i] = yr[i] * (dyr[i] - dot);
+    }
+}
+
+/* cpu_fused_backward.rs:43-78. */
+void kore_oracle_rms_norm_backward_f32(const float *dy, const float *x,
+                                       const float *gamma, float *dx,
+                                       float *dgamma, size_t rows, size_t cols,
+                                       float eps) {
+    for (size_t i = 0; i < cols; ++i) dgamma[i] = 0.0f;
+    for (size_t r = 0; r < rows; ++r) {
+        const float *xr = x + r * cols;
+        const float *gr = dy + r * cols;
+        float sum_sq = 0.0f;
+        for (size_t i = 0; i < cols; ++i) sum_sq = sum_sq + xr[i] * xr[i];
+        float rms = sqrtf(sum_sq / (float)cols + eps);
+        float inv_rms = 1.0f / rms;
+        for (size_t i = 0; i < cols; ++i) dgamma[i] = dgamma[i] + (gr[i] * xr[i]) * inv_rms;
+        float dot = 0.0f;
+        for (size_t i = 0; i < cols; ++i) dot = dot + (xr[i] * gr[i]) * gamma[i];
+        float coeff = (dot * inv_rms) / (sum_sq + eps * (float)cols);
+        for (size_t i = 0; i < cols; ++i) {
+            float a = (gamma[i] * inv_rms) * gr[i];
+            float b = coeff * xr[i];
+            dx[r * cols + i] = a - b;
+        }
+    }
+}

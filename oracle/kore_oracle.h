@@ -97,6 +97,35 @@ void kore_oracle_rms_norm_silu_gate_f32(const float *x, const float *gamma,
 /* One element of the pre-quant code: the shared definition used above.  */
 int8_t kore_oracle_quant_code(float xn, float amax_guarded);
 
+/* crates/kore-kernels/src/cpu_fused.rs:195-231 (fused_softmax): max by an
+ * f32::max fold from -inf (NaN elements skipped), e = exp(x - max), sum folded
+ * left to right, y = e * (1 / sum). */
+void kore_oracle_softmax_f32(const float *x, float *y, size_t rows, size_t cols);
+
+/* crates/kore-kernels/src/cuda/kernels/softmax.cu:88-157 (softmax_causal_f32;
+ * GPU-only in the reference, no CPU twin): row r keeps columns
+ * c < seq_offset + r + 1, the rest are -inf in the max and 0 in the output;
+ * inv_sum = sum > 0 ? 1/sum : 0.  Sums are folded left to right here (the CUDA
+ * kernel uses a tree; both are within the f32 tolerance). */
+void kore_oracle_softmax_causal_f32(const float *x, float *y, size_t rows,
+                                    size_t cols, size_t seq_offset);
+
+/* crates/kore-kernels/src/cpu_fused_backward.rs:86-115
+ * (fused_softmax_backward): dot = sum(y*dy) folded left to right,
+ * dx = y * (dy - dot). */
+void kore_oracle_softmax_backward_f32(const float *dy, const float *y,
+                                      float *dx, size_t rows, size_t cols);
+
+/* crates/kore-kernels/src/cpu_fused_backward.rs:20-81
+ * (fused_rms_norm_backward): per row sum_sq, inv_rms = 1/sqrt(sum_sq/d + eps);
+ * dgamma[i] += (go*x)*inv_rms (rows in order);
+ * dot = sum((x*go)*g); coeff = (dot*inv_rms) / (sum_sq + eps*d);
+ * dx = ((g*inv_rms)*go) - coeff*x.  dgamma is overwritten. */
+void kore_oracle_rms_norm_backward_f32(const float *dy, const float *x,
+                                       const float *gamma, float *dx,
+                                       float *dgamma, size_t rows, size_t cols,
+                                       float eps);
+
 #ifdef __cplusplus
 }
 #endif

@@ -34,6 +34,10 @@ _SIGS = {
     "kore_oracle_rms_norm_quant_i8": (None, [_p, _p, _p, _p, _sz, _sz, _f]),
     "kore_oracle_quant_code": (_c.c_int8, [_f, _f]),
     "kore_oracle_rms_norm_silu_gate_f32": (None, [_p, _p, _p, _p, _sz, _sz, _f]),
+    "kore_oracle_softmax_f32": (None, [_p, _p, _sz, _sz]),
+    "kore_oracle_softmax_causal_f32": (None, [_p, _p, _sz, _sz, _sz]),
+    "kore_oracle_softmax_backward_f32": (None, [_p, _p, _p, _sz, _sz]),
+    "kore_oracle_rms_norm_backward_f32": (None, [_p, _p, _p, _p, _p, _sz, _sz, _f]),
 }
 
 _lib = None
@@ -179,4 +183,47 @@ def quant_code(xn: float, amax: float) -> int:
 
 
 __all__ = ["build", "lib", "rms_norm", "gelu", "silu", "mul", "swiglu", "rope_inv_freq", "rope", "embedding",
-           "rms_norm_quant_i8", "rms_norm_silu_gate", "quant_code"]
+           "rms_norm_quant_i8", "rms_norm_silu_gate", "quant_code", "softmax", "softmax_causal",
+           "softmax_backward", "rms_norm_backward"]
+
+
+def _rows_cols(x: np.ndarray):
+    cols = x.shape[-1] if x.ndim else 1
+    return (x.size // cols if cols else 0), cols
+
+
+def softmax(x) -> np.ndarray:
+    """cpu_fused.rs:195-231 (fused_softmax) over the last dimension."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    rows, cols = _rows_cols(x)
+    lib().kore_oracle_softmax_f32(_ptr(x), _ptr(y), rows, cols)
+    return y
+
+
+def softmax_causal(x, seq_offset: int = 0) -> np.ndarray:
+    """softmax.cu:88-157 (softmax_causal_f32): row r keeps columns < seq_offset + r + 1."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    rows, cols = _rows_cols(x)
+    lib().kore_oracle_softmax_causal_f32(_ptr(x), _ptr(y), rows, cols, seq_offset)
+    return y
+
+
+def softmax_backward(dy, y) -> np.ndarray:
+    """cpu_fused_backward.rs:86-115: dx = y * (dy - sum(y*dy))."""
+    dy, y = _f32(dy), _f32(y)
+    dx = np.empty_like(y)
+    rows, cols = _rows_cols(y)
+    lib().kore_oracle_softmax_backward_f32(_ptr(dy), _ptr(y), _ptr(dx), rows, cols)
+    return dx
+
+
+def rms_norm_backward(dy, x, gamma, eps: float):
+    """cpu_fused_backward.rs:20-81 -> (dx, dgamma)."""
+    dy, x, gamma = _f32(dy), _f32(x), _f32(gamma)
+    rows, cols = _rows_cols(x)
+    dx = np.empty_like(x)
+    dgamma = np.empty(cols, np.float32)
+    lib().kore_oracle_rms_norm_backward_f32(_ptr(dy), _ptr(x), _ptr(gamma), _ptr(dx), _ptr(dgamma), rows, cols, eps)
+    return dx, dgamma

@@ -109,3 +109,24 @@ def assert_bitexact(got, ref, what: str = "") -> None:
         i = tuple(bad[0])
         raise AssertionError(f"{what}: {len(bad)} of {gb.size} elements differ; first at {i}: "
                              f"got {got[i]!r} ref {ref[i]!r}")
+
+
+def assert_close_scaled(got, ref, scale, rtol: float = 1e-5, atol: float = 1e-6, what: str = "") -> None:
+    """|got - ref| <= atol + rtol * scale per element, for outputs that are a
+    difference of rounded terms (backward passes): `scale` is the magnitude of
+    the terms (e.g. |a| + |b| for a - b), so cancellation in the result does
+    not turn the reference's own rounding into a relative error.  NaN must
+    meet NaN."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    scale = np.broadcast_to(np.asarray(scale, dtype=np.float64), ref.shape)
+    nan_g, nan_r = np.isnan(got), np.isnan(ref)
+    with np.errstate(invalid="ignore"):
+        ok = np.abs(got - ref) <= atol + rtol * scale
+    ok |= nan_g & nan_r
+    ok &= nan_g == nan_r
+    if not ok.all():
+        bad = np.argwhere(~ok)
+        i = tuple(bad[0])
+        raise AssertionError(f"{what}: {len(bad)} of {ok.size} elements outside tol (rtol={rtol} of scale, "
+                             f"atol={atol}); first at {i}: got {got[i]!r} ref {ref[i]!r} scale {scale[i]!r}")

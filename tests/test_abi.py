@@ -27,7 +27,7 @@ def test_every_declared_symbol_is_exported():
     for n in names:
         assert hasattr(lib, n), n
     # the ctypes binding covers every compute entry point
-    assert set(names) - {"kore_hip_status_string"} == set(_lib.SIGNATURES)
+    assert set(names) - {"kore_hip_status_string"} == set(_lib.SIGNATURES) | set(_lib.RESTYPES)
 
 
 def test_version_and_status_text():
@@ -65,6 +65,36 @@ def test_argument_errors_are_reported_on_host():
     assert lib.kore_hip_embedding_f32(P, P, P, 2**33, 2**33, 4, s) == _lib.KORE_HIP_ERR_OVERFLOW
     # overlapping Q and K
     assert lib.kore_hip_rope_qk_f32(P, P + 64, P, 1, 4, 2, 2, 8, 0, 0, s) == _lib.KORE_HIP_ERR_ALIAS
+    # softmax family
+    assert lib.kore_hip_softmax_f32(None, None, 0, 16, s) == 0
+    assert lib.kore_hip_softmax_f32(None, P, 4, 16, s) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert lib.kore_hip_softmax_backward_f32(P, None, P, 4, 16, s) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert lib.kore_hip_softmax_f32(P, P, 2**40, 2**40, s) == _lib.KORE_HIP_ERR_OVERFLOW
+    assert lib.kore_hip_softmax_causal_f32(P, P, 4, 16, 2**64 - 2, s) == _lib.KORE_HIP_ERR_OVERFLOW
+    # RMSNorm backward: workspace, aliasing, nulls
+    ws = lib.kore_hip_rms_norm_backward_workspace_bytes
+    need = ws(16, 64)
+    assert need > 0
+    assert lib.kore_hip_rms_norm_backward_f32(P, P, P, P + 2**20, P, None, need, 16, 64, 1e-5, s) == \
+        _lib.KORE_HIP_ERR_NULL_PTR
+    assert lib.kore_hip_rms_norm_backward_f32(P, P + 2**20, P, P + 2**21, P, P, need - 4, 16, 64, 1e-5, s) == \
+        _lib.KORE_HIP_ERR_BAD_DIM
+    assert lib.kore_hip_rms_norm_backward_f32(P, P + 2**20, P, P + 64, P, P, need, 16, 64, 1e-5, s) == \
+        _lib.KORE_HIP_ERR_ALIAS
+
+
+def test_rms_norm_backward_workspace_size():
+    ws = _lib.load().kore_hip_rms_norm_backward_workspace_bytes
+    assert ws(0, 128) == 0 and ws(128, 0) == 0 and ws(2**40, 2**40) == 0
+    # vector plan: a row split over S = 1/2/4 waves (cols <= 1024/2048/4096),
+    # 4/S rows per iteration, iters = clamp(ceil(rows / (1024 * 4/S)), 1, 16),
+    # P = ceil(rows / (iters * 4/S)) partial rows + ceil(P / 64) level-2 rows;
+    # generic plan: one float per row.
+    assert ws(16384, 2048) == (1024 + 16) * 2048 * 4
+    assert ws(100, 256) == (25 + 1) * 256 * 4
+    assert ws(1 << 20, 4096) == (65536 + 1024) * 4096 * 4
+    assert ws(16384, 2050) == 16384 * 4       # cols % 4 != 0 -> generic
+    assert ws(4, 8192) == 4 * 4               # cols > 4096 -> generic
 
 
 @pytest.mark.parametrize("head_dim", [2, 8, 64, 128, 256])

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 import oracle
-from inputs import (assert_bitexact, assert_close, embedding_ids, max_err, normal, prequant_inputs, rmsnorm_inputs)
+from inputs import (assert_bitexact, assert_close, assert_close_scaled, embedding_ids, max_err, normal,
+                    prequant_inputs, rmsnorm_inputs)
 
 pytestmark = pytest.mark.gpu
 
@@ -352,3 +353,160 @@ def test_embedding_baseline_full():
     out = rocm.rocm_embedding_f32(DEV, up(table), up(ids), 8192, 128256, 4096)
     got = down(out, np.float32, (8192, 4096))
     assert got.tobytes() == oracle.embedding(table, ids).tobytes()
+
+
+# ----------------------------------------------------------------- softmax
+# Tolerances.  The reference folds its sums left to right in f32, so its own
+# result is only within the recursive-summation bound gamma_n = n * 2^-24
+# (relative to the sum of |terms|) of the exact value; the kernel sums in a
+# tree.  Each test therefore checks (a) accuracy: the kernel is within the
+# plain f32 tolerance (1e-5 relative / 1e-6 absolute) of an f64 evaluation,
+# and (b) parity with the oracle (semantics of NaN, inf, masks, padding) with
+# rtol = 1e-5 + n * 2^-24, n = the number of terms the reference folds.
+U32 = 2.0 ** -24
+
+
+def _softmax64(x):
+    x = np.asarray(x, np.float64)
+    e = np.exp(x - x.max(axis=-1, keepdims=True))
+    return e / e.sum(axis=-1, keepdims=True)
+
+# one shape per kernel path: wave per row (<= 256/512/1024/2048/4096 cols),
+# workgroup per row (<= 8192/16384), looped (longer rows, cols % 4 != 0)
+SOFTMAX_SHAPES = [(1, 1), (3, 7), (5, 4), (4, 256), (7, 260), (9, 512), (6, 1000), (33, 2048), (5, 4096),
+                  (3, 8192), (2, 16384), (2, 20000), (3, 4099), (2, 128256)]
+
+
+@pytest.mark.parametrize("rows,cols", SOFTMAX_SHAPES)
+def test_softmax(rows, cols):
+    log(f"softmax rows={rows} cols={cols}")
+    x = normal((rows, cols), rows * 31 + cols) * 4
+    got = down(rocm.rocm_softmax_f32(DEV, up(x), rows, cols), np.float32, (rows, cols))
+    assert_close(got, _softmax64(x), what="softmax vs f64")
+    assert_close(got, oracle.softmax(x), rtol=1e-5 + cols * U32, what="softmax vs oracle")
+
+
+def test_softmax_special_rows_in_place_and_unaligned():
+    log("softmax special rows")
+    cols = 300
+    x = normal((8, cols), 3) * 2
+    x[0, 5] = np.nan
+    x[1, :] = -np.inf
+    x[2, 7] = np.inf
+    x[3, ::3] = -np.inf
+    x[4] = 1000.0 + x[4]
+    x[5] = -3e38
+    x[6, 0] = 3e38
+    want = oracle.softmax(x)
+    got = down(rocm.rocm_softmax_f32(DEV, up(x), 8, cols), np.float32, (8, cols))
+    assert_close(got, want, rtol=1e-5 + cols * U32, what="softmax special")
+    for c in (256, 1024, 4096):  # in place, register paths
+        xx = normal((5, c), c) * 3
+        b = up(xx)
+        rocm.rocm_softmax_f32(DEV, b, 5, c, out=b)
+        assert_close(down(b, np.float32, (5, c)), _softmax64(xx), what=f"softmax in place {c}")
+    xu = normal((4, 512), 11)
+    got = down(rocm.rocm_softmax_f32(DEV, unaligned(xu), 4, 512), np.float32, (4, 512))
+    assert_close(got, _softmax64(xu), what="softmax unaligned")
+
+
+@pytest.mark.parametrize("rows,cols,offset", [(6, 8, 0), (6, 8, 3), (40, 64, 0), (300, 256, 0), (17, 2048, 1000),
+                                              (3, 8192, 4000), (2, 20000, 9999), (9, 4099, 10), (4, 33, 100)])
+def test_softmax_causal(rows, cols, offset):
+    log(f"softmax_causal rows={rows} cols={cols} offset={offset}")
+    x = normal((rows, cols), rows + cols + offset) * 3
+    got = down(rocm.rocm_softmax_causal_f32(DEV, up(x), rows, cols, offset), np.float32, (rows, cols))
+    want = oracle.softmax_causal(x, offset)
+    lim = np.minimum(offset + np.arange(rows) + 1, cols)
+    assert_close(got, want, rtol=1e-5 + int(lim.max()) * U32, what="softmax_causal vs oracle")
+    exact = np.zeros((rows, cols))
+    for r in range(rows):
+        exact[r, :lim[r]] = _softmax64(x[r, :lim[r]])
+    assert_close(got, exact, what="softmax_causal vs f64")
+    # masked entries are exact zeros
+    mask = np.arange(cols)[None, :] >= lim[:, None]
+    assert (got[mask] == 0.0).all()
+
+
+def _softmax_bwd_scale(y, dy):
+    y64, dy64 = y.astype(np.float64), dy.astype(np.float64)
+    dot_abs = np.abs(y64 * dy64).sum(axis=-1, keepdims=True)
+    return np.abs(y64) * (np.abs(dy64) + dot_abs)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 7), (4, 256), (9, 512), (33, 2048), (5, 4096), (3, 8192),
+                                       (2, 16384), (2, 20000), (3, 4099)])
+def test_softmax_backward(rows, cols):
+    log(f"softmax_backward rows={rows} cols={cols}")
+    y = oracle.softmax(normal((rows, cols), cols) * 3)
+    dy = normal((rows, cols), cols + 1)
+    got = down(rocm.rocm_softmax_backward_f32(DEV, up(dy), up(y), rows, cols), np.float32, (rows, cols))
+    want = oracle.softmax_backward(dy, y)
+    assert_close_scaled(got, want, _softmax_bwd_scale(y, dy), rtol=1e-5 + cols * U32, what="softmax_backward")
+
+
+def test_softmax_backward_reference_kat_on_device():
+    # cpu_fused_backward.rs:236-248: uniform upstream gradient -> ~0
+    y = np.array([[0.2, 0.3, 0.5]], np.float32)
+    got = down(rocm.rocm_softmax_backward_f32(DEV, up(np.ones((1, 3), np.float32)), up(y), 1, 3), np.float32, (1, 3))
+    assert np.abs(got).max() < 1e-6
+
+
+# -------------------------------------------------------- RMSNorm backward
+def _rms_bwd_scales(dy, x, g, eps):
+    x64, dy64, g64 = x.astype(np.float64), dy.astype(np.float64), g.astype(np.float64)
+    cols = x.shape[1]
+    ss = (x64 * x64).sum(axis=1, keepdims=True)
+    inv = 1.0 / np.sqrt(ss / cols + eps)
+    coeff_abs = np.abs(x64 * dy64 * g64).sum(axis=1, keepdims=True) * inv / (ss + eps * cols)
+    sdx = np.abs(g64) * inv * np.abs(dy64) + coeff_abs * np.abs(x64)
+    sdg = (np.abs(dy64 * x64) * inv).sum(axis=0)
+    return sdx, sdg
+
+
+# vector path split over 1/2/4 waves, several row iterations, generic path
+RMS_BWD_SHAPES = [(1, 4), (3, 7), (16, 64), (100, 256), (33, 1000), (64, 2048), (10, 4096), (5, 8192), (4099, 512),
+                  (2000, 2050), (20000, 1024)]
+
+
+@pytest.mark.parametrize("rows,cols", RMS_BWD_SHAPES)
+def test_rms_norm_backward(rows, cols):
+    log(f"rms_norm_backward rows={rows} cols={cols}")
+    x, g = rmsnorm_inputs(rows, cols, seed=rows + cols)
+    dy = normal((rows, cols), rows * 3 + cols)
+    gx, gg = rocm.rocm_rms_norm_backward_f32(DEV, up(dy), up(x), up(g), rows, cols, 1e-5)
+    dx_w, dg_w = oracle.rms_norm_backward(dy, x, g, 1e-5)
+    sdx, sdg = _rms_bwd_scales(dy, x, g, 1e-5)
+    assert_close_scaled(down(gx, np.float32, (rows, cols)), dx_w, sdx, rtol=1e-5 + cols * U32,
+                        what="rms_norm_backward dx")
+    assert_close_scaled(down(gg, np.float32, (cols,)), dg_w, sdg, rtol=1e-5 + rows * U32,
+                        what="rms_norm_backward dgamma")
+
+
+def test_rms_norm_backward_deterministic_and_edge_cases():
+    log("rms_norm_backward determinism / edges")
+    rows, cols = 3000, 2048
+    x, g = rmsnorm_inputs(rows, cols, seed=1)
+    dy = normal((rows, cols), 2)
+    a = rocm.rocm_rms_norm_backward_f32(DEV, up(dy), up(x), up(g), rows, cols, 1e-5)
+    b = rocm.rocm_rms_norm_backward_f32(DEV, up(dy), up(x), up(g), rows, cols, 1e-5)
+    assert a[0].to_host(np.uint8).tobytes() == b[0].to_host(np.uint8).tobytes()
+    assert a[1].to_host(np.uint8).tobytes() == b[1].to_host(np.uint8).tobytes()
+    # zero upstream gradient -> zeros (cpu_fused_backward.rs:220-234)
+    gx, gg = rocm.rocm_rms_norm_backward_f32(DEV, up(np.zeros((1, 3), np.float32)),
+                                             up(np.array([[1.0, 2.0, 3.0]], np.float32)), up(np.ones(3, np.float32)),
+                                             1, 3, 1e-5)
+    assert np.abs(gx.to_host(np.float32)[:3]).max() < 1e-6 and np.abs(gg.to_host(np.float32)[:3]).max() < 1e-6
+    # rows == 0 zeroes grad_gamma
+    gg0 = up(np.full(64, 7.0, np.float32))
+    rocm.rocm_rms_norm_backward_f32(DEV, up(np.zeros(4, np.float32)), up(np.zeros(4, np.float32)),
+                                    up(np.ones(64, np.float32)), 0, 64, 1e-5, grad_gamma=gg0)
+    assert (gg0.to_host(np.float32)[:64] == 0.0).all()
+    # unaligned views take the generic path
+    xu, dyu = normal((7, 256), 3), normal((7, 256), 4)
+    gu = np.ones(256, np.float32)
+    gx, gg = rocm.rocm_rms_norm_backward_f32(DEV, unaligned(dyu), unaligned(xu), up(gu), 7, 256, 1e-5)
+    dx_w, dg_w = oracle.rms_norm_backward(dyu, xu, gu, 1e-5)
+    sdx, sdg = _rms_bwd_scales(dyu, xu, gu, 1e-5)
+    assert_close_scaled(down(gx, np.float32, (7, 256)), dx_w, sdx, rtol=1e-5 + 256 * U32, what="unaligned dx")
+    assert_close_scaled(down(gg, np.float32, (256,)), dg_w, sdg, rtol=1e-5 + 7 * U32, what="unaligned dgamma")

@@ -267,3 +267,98 @@ def test_rms_norm_silu_gate_reference_kat_and_f64():
     x64 = xg.astype(np.float64)
     ref = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6) * g * (zz / (1 + np.exp(-zz.astype(np.float64))))
     assert np.max(np.abs(y - ref) / np.maximum(np.abs(ref), 1e-6)) < 5e-6
+
+
+# ----------------------------------------------------------------- softmax
+def _softmax64(x):
+    x = np.asarray(x, np.float64)
+    e = np.exp(x - x.max(axis=-1, keepdims=True))
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def test_softmax_reference_kats():
+    # cpu_fused.rs:278-304
+    y = oracle.softmax(np.array([[1.0, 2.0, 3.0], [1.0, 2.0, 3.0]], np.float32))
+    assert abs(y[0].sum() - 1) < 1e-6 and abs(y[1].sum() - 1) < 1e-6
+    assert y[0, 2] > y[0, 1] > y[0, 0]
+    y = oracle.softmax(np.array([[1000.0, 1001.0, 1002.0]], np.float32))
+    assert np.isfinite(y).all() and abs(y.sum() - 1) < 1e-6
+
+
+def test_softmax_f64_and_special_values():
+    x = normal((16, 300), 4) * 8
+    y = oracle.softmax(x)
+    ref = _softmax64(x)
+    assert np.allclose(y, ref, rtol=5e-6, atol=1e-9)
+    # f32::max skips NaN, but exp(NaN - m) poisons the sum: the whole row is NaN
+    r = oracle.softmax(np.array([[1.0, np.nan, 2.0]], np.float32))
+    assert np.isnan(r).all()
+    # -inf entries get 0; an all -inf row is NaN (exp(-inf - -inf))
+    r = oracle.softmax(np.array([[0.0, -np.inf, 0.0]], np.float32))
+    assert r[0, 1] == 0.0 and r[0, 0] == r[0, 2] == 0.5
+    assert np.isnan(oracle.softmax(np.full((1, 3), -np.inf, np.float32))).all()
+    # +inf: inf - inf = NaN at that entry -> NaN row
+    assert np.isnan(oracle.softmax(np.array([[0.0, np.inf]], np.float32))).all()
+
+
+def test_softmax_causal_prefix_closed_form():
+    x = normal((6, 8), 5) * 3
+    for off in (0, 2, 100):
+        y = oracle.softmax_causal(x, off)
+        for r in range(6):
+            lim = min(off + r + 1, 8)
+            # the kept prefix is the plain softmax of the prefix, bit for bit
+            assert (y[r, :lim] == oracle.softmax(x[r:r + 1, :lim])[0]).all()
+            assert (y[r, lim:] == 0.0).all()
+    ones = oracle.softmax_causal(np.ones((3, 4), np.float32))
+    assert np.allclose(ones, [[1, 0, 0, 0], [.5, .5, 0, 0], [1 / 3, 1 / 3, 1 / 3, 0]], atol=1e-7)
+
+
+def test_softmax_backward_reference_kat_and_finite_differences():
+    # cpu_fused_backward.rs:236-248: a uniform upstream gradient gives ~0
+    dx = oracle.softmax_backward(np.ones((1, 3)), np.array([[0.2, 0.3, 0.5]]))
+    assert np.abs(dx).max() < 1e-6
+    # central differences of L(x) = sum(dy * softmax(x)) in f64
+    x = normal((3, 7), 6).astype(np.float64)
+    dy = normal((3, 7), 7).astype(np.float64)
+    y = _softmax64(x)
+    num = np.zeros_like(x)
+    h = 1e-6
+    for i in range(x.shape[0]):
+        for j in range(x.shape[1]):
+            xp, xm = x.copy(), x.copy()
+            xp[i, j] += h
+            xm[i, j] -= h
+            num[i, j] = ((dy * _softmax64(xp)).sum() - (dy * _softmax64(xm)).sum()) / (2 * h)
+    got = oracle.softmax_backward(dy.astype(np.float32), y.astype(np.float32))
+    assert np.max(np.abs(got - num)) < 2e-6
+
+
+# -------------------------------------------------------- RMSNorm backward
+def test_rms_norm_backward_reference_kats():
+    # cpu_fused_backward.rs:195-234
+    dx, dg = oracle.rms_norm_backward(np.ones((2, 3)), np.arange(1, 7, dtype=np.float32).reshape(2, 3),
+                                      np.ones(3), 1e-5)
+    assert dx.shape == (2, 3) and dg.shape == (3,)
+    dx, dg = oracle.rms_norm_backward(np.array([[0.1, -0.2, 0.3], [-0.1, 0.4, -0.5]]),
+                                      np.array([[0.5, -0.3, 1.2], [-0.8, 0.1, 0.7]]), np.array([1.0, 0.5, 2.0]),
+                                      1e-5)
+    assert np.isfinite(dx).all() and np.isfinite(dg).all()
+    dx, dg = oracle.rms_norm_backward(np.zeros((1, 3)), np.array([[1.0, 2.0, 3.0]]), np.ones(3), 1e-5)
+    assert np.abs(dx).max() < 1e-6 and np.abs(dg).max() < 1e-6
+
+
+def test_rms_norm_backward_matches_torch_autograd_f64():
+    import torch
+
+    rows, cols, eps = 9, 37, 1e-5
+    x = normal((rows, cols), 8)
+    g = normal((cols,), 9, 1.0, 0.3)
+    dy = normal((rows, cols), 10)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    gt = torch.tensor(g, dtype=torch.float64, requires_grad=True)
+    y = xt * torch.rsqrt((xt * xt).mean(dim=-1, keepdim=True) + eps) * gt
+    y.backward(torch.tensor(dy, dtype=torch.float64))
+    dx, dg = oracle.rms_norm_backward(dy, x, g, eps)
+    assert np.allclose(dx, xt.grad.numpy(), rtol=1e-4, atol=2e-6)
+    assert np.allclose(dg, gt.grad.numpy(), rtol=1e-4, atol=2e-6)
