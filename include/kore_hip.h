@@ -184,6 +184,21 @@ int kore_hip_softmax_backward_f32(const float *grad_out, const float *out,
                                   float *grad_in, uint64_t rows, uint64_t cols,
                                   kore_stream_t stream);
 
+/* Cross-entropy backward from raw logits[batch, num_classes]:
+ * grad[b, :] = e * (inv_sum * inv_batch), e = exp(logits[b, :] - max),
+ * inv_sum = 1 / sum(e), inv_batch = 1 / batch; then
+ * grad[b, t] -= inv_batch for t = targets[b] converted like Rust's
+ * `f32 as usize` (truncation; NaN and negatives give 0).  A t >= num_classes
+ * (the reference panics on the index) subtracts nothing.  Twin of
+ * fused_cross_entropy_backward (crates/kore-kernels/src/cpu_fused_backward.rs:130-170,
+ * also reached through fused_softmax_cross_entropy_backward :179-184); the
+ * reference has no GPU version.  f32 tol.  grad_logits may equal logits. */
+int kore_hip_cross_entropy_backward_f32(const float *logits,
+                                        const float *targets,
+                                        float *grad_logits, uint64_t batch,
+                                        uint64_t num_classes,
+                                        kore_stream_t stream);
+
 /* --------------------------------------------------------- RMSNorm backward
  * For y = RMSNorm(x) * gamma (rows x cols), given grad_out = dL/dy:
  *   inv_r = 1 / sqrt(sum_i x^2 / cols + eps)

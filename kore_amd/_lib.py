@@ -43,6 +43,7 @@ SIGNATURES = {
     "kore_hip_softmax_f32": [_ptr, _ptr, _u64, _u64, _ptr],
     "kore_hip_softmax_causal_f32": [_ptr, _ptr, _u64, _u64, _u64, _ptr],
     "kore_hip_softmax_backward_f32": [_ptr, _ptr, _ptr, _u64, _u64, _ptr],
+    "kore_hip_cross_entropy_backward_f32": [_ptr, _ptr, _ptr, _u64, _u64, _ptr],
     "kore_hip_rms_norm_backward_f32": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _f32, _ptr],
 }
 

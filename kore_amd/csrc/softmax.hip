@@ -12,7 +12,12 @@
 //            (r counts over all rows of the call); the rest are -inf in the
 //            max and 0 in the output; inv = sum > 0 ? 1/sum : 0;
 //   backward crates/kore-kernels/src/cpu_fused_backward.rs:86-115
-//            (fused_softmax_backward): dx = y * (dy - sum(y * dy)).
+//            (fused_softmax_backward): dx = y * (dy - sum(y * dy));
+//   cross-entropy backward cpu_fused_backward.rs:130-170
+//            (fused_cross_entropy_backward): g = e * (inv_sum * inv_batch),
+//            inv_batch = 1 / rows, then g[t] -= inv_batch at t = targets[r]
+//            cast like Rust's `as usize` (truncation, NaN and negatives -> 0);
+//            a t >= cols (the reference panics) subtracts nothing.
 // The sums are tree reductions (lane partials, then a wave butterfly), so
 // results are within the f32 tolerance of the reference's left fold, as its
 // own CUDA kernel is.  exp is ocml's accurate expf.
@@ -28,11 +33,11 @@
 
 namespace kore {
 
-enum class SmKind : int { Fwd = 0, Causal = 1, Bwd = 2 };
+enum class SmKind : int { Fwd = 0, Causal = 1, Bwd = 2, CeBwd = 3 };
 
 struct SmArgs {
     const float* a;  // x (forward) or y (backward)
-    const float* b;  // dy (backward), unused otherwise
+    const float* b;  // dy (backward), targets[rows] (cross-entropy), unused otherwise
     float* out;
     uint64_t rows;
     uint64_t cols;
@@ -47,6 +52,15 @@ __device__ __forceinline__ float f4_get(const f32x4& v, int k) {
 }
 __device__ __forceinline__ void f4_set(f32x4& v, int k, float s) {
     if (k == 0) v.x = s; else if (k == 1) v.y = s; else if (k == 2) v.z = s; else v.w = s;
+}
+
+// Rust `f32 as usize`: NaN and negatives -> 0, truncation toward zero,
+// saturating; returned as a column index, or UINT64_MAX when >= cols.
+__device__ __forceinline__ uint64_t target_index(float t, uint64_t cols) {
+    if (!(t >= 1.0f)) return cols > 0 ? 0 : ~0ull;  // NaN, negative, [0, 1)
+    if (t >= 18446744073709551616.0f) return ~0ull;
+    const uint64_t i = (uint64_t)t;
+    return i < cols ? i : ~0ull;
 }
 
 // Number of leading columns of `row` that take part (causal mask).
@@ -144,6 +158,21 @@ __global__ __launch_bounds__(kSmBlock) void softmax_reg_kernel(SmArgs a) {
     s = wave_sum(s);
     if (Block) s = block_combine<false>(s, red);
     const float inv = (K == SmKind::Causal) ? (s > 0.0f ? 1.0f / s : 0.0f) : 1.0f / s;
+    if (K == SmKind::CeBwd) {
+        const float inv_batch = 1.0f / (float)a.rows;
+        const float scale = inv * inv_batch;
+        const uint64_t t = target_index(a.b[row], a.cols);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const uint32_t f = (uint32_t)(c * step + me);
+            f32x4 o = v[c] * scale;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if ((uint64_t)(4 * f + k) == t) f4_set(o, k, f4_get(o, k) - inv_batch);
+            if (f < cols4) st_stream(orow + f, o);
+        }
+        return;
+    }
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const uint32_t f = (uint32_t)(c * step + me);
@@ -211,14 +240,23 @@ __global__ __launch_bounds__(kSmBlock) void softmax_loop_kernel(SmArgs a) {
     }
     s = block_combine<false>(wave_sum(s), red);
     const float inv = (K == SmKind::Causal) ? (s > 0.0f ? 1.0f / s : 0.0f) : 1.0f / s;
+    const float inv_batch = 1.0f / (float)a.rows;
+    const float scale = (K == SmKind::CeBwd) ? inv * inv_batch : inv;
+    const uint64_t t = (K == SmKind::CeBwd) ? target_index(a.b[row], a.cols) : ~0ull;
     for (uint64_t i = threadIdx.x; i < n; i += kSmBlock) {
         if (Vec) {
             f32x4 v = reinterpret_cast<const f32x4*>(ar)[i];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) f4_set(v, k, 4 * i + k < lim ? expf(f4_get(v, k) - m) : 0.0f);
-            st_stream(reinterpret_cast<f32x4*>(orow) + i, v * inv);
+            for (int k = 0; k < 4; ++k) {
+                float o = (4 * i + k < lim ? expf(f4_get(v, k) - m) : 0.0f) * scale;
+                if (K == SmKind::CeBwd && 4 * i + k == t) o = o - inv_batch;
+                f4_set(v, k, o);
+            }
+            st_stream(reinterpret_cast<f32x4*>(orow) + i, v);
         } else {
-            orow[i] = (i < lim ? expf(ar[i] - m) : 0.0f) * inv;
+            float o = (i < lim ? expf(ar[i] - m) : 0.0f) * scale;
+            if (K == SmKind::CeBwd && i == t) o = o - inv_batch;
+            orow[i] = o;
         }
     }
 }
@@ -232,7 +270,7 @@ static void launch_wave(const SmArgs& a, hipStream_t s) {
 template <SmKind K>
 static int softmax_launch(const SmArgs& a, hipStream_t s) {
     if (a.rows == 0 || a.cols == 0) return KORE_HIP_OK;
-    if (!a.a || !a.out || (K == SmKind::Bwd && !a.b)) return KORE_HIP_ERR_NULL_PTR;
+    if (!a.a || !a.out || ((K == SmKind::Bwd || K == SmKind::CeBwd) && !a.b)) return KORE_HIP_ERR_NULL_PTR;
     uint64_t elems;
     if (!mul_ok(a.rows, a.cols, &elems) || elems > kMaxElements || a.rows > 0x7fffffffull)
         return KORE_HIP_ERR_OVERFLOW;
@@ -276,4 +314,10 @@ extern "C" int kore_hip_softmax_backward_f32(const float* grad_out, const float*
                                              uint64_t rows, uint64_t cols, kore_stream_t stream) {
     SmArgs a{out, grad_out, grad_in, rows, cols, 0};
     return softmax_launch<SmKind::Bwd>(a, (hipStream_t)stream);
+}
+
+extern "C" int kore_hip_cross_entropy_backward_f32(const float* logits, const float* targets, float* grad_logits,
+                                                   uint64_t batch, uint64_t num_classes, kore_stream_t stream) {
+    SmArgs a{logits, targets, grad_logits, batch, num_classes, 0};
+    return softmax_launch<SmKind::CeBwd>(a, (hipStream_t)stream);
 }

@@ -328,6 +328,20 @@ def rocm_softmax_backward_f32(device_idx: int, grad_output: HipBuffer, output: H
     return o
 
 
+def rocm_cross_entropy_backward_f32(device_idx: int, logits: HipBuffer, targets: HipBuffer, batch: int,
+                                    num_classes: int, out: Optional[HipBuffer] = None) -> HipBuffer:
+    """``fused_cross_entropy_backward`` (cpu_fused_backward.rs:130-170) on the
+    device: (softmax(logits) - one_hot(targets)) / batch; targets are f32."""
+    _require_device(device_idx)
+    n = batch * num_classes * 4
+    _need(logits, n, "cross_entropy_backward logits")
+    _need(targets, batch * 4, "cross_entropy_backward targets")
+    o = _out(device_idx, out, n, "cross_entropy_backward grad")
+    _check(_lib.load().kore_hip_cross_entropy_backward_f32(logits.ptr, targets.ptr, o.ptr, batch, num_classes,
+                                                           _stream(device_idx)), "cross_entropy_backward_f32")
+    return o
+
+
 # ------------------------------------------------------- RMSNorm backward
 def rocm_rms_norm_backward_workspace_bytes(rows: int, cols: int) -> int:
     """Device scratch ``rocm_rms_norm_backward_f32`` needs for (rows, cols)."""

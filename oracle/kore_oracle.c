@@ -326,3 +326,33 @@ void kore_oracle_rms_norm_backward_f32(const float *dy, const float *x,
         }
     }
 }
+
+/* Rust `f32 as usize`: NaN -> 0, negatives -> 0, truncation, saturating. */
+static size_t rust_f32_as_usize(float t) {
+    if (!(t >= 1.0f)) return 0;
+    if (t >= 18446744073709551616.0f) return (size_t)-1;
+    return (size_t)t;
+}
+
+/* cpu_fused_backward.rs:143-168. */
+void kore_oracle_cross_entropy_backward_f32(const float *logits,
+                                            const float *targets, float *grad,
+                                            size_t batch, size_t num_classes) {
+    float inv_batch = 1.0f / (float)batch;
+    for (size_t b = 0; b < batch; ++b) {
+        const float *row = logits + b * num_classes;
+        float *g = grad + b * num_classes;
+        size_t target_idx = rust_f32_as_usize(targets[b]);
+        float max_val = -INFINITY;
+        for (size_t i = 0; i < num_classes; ++i) max_val = rust_fmax(max_val, row[i]);
+        float sum = 0.0f;
+        for (size_t i = 0; i < num_classes; ++i) {
+            float e = expf(row[i] - max_val);
+            g[i] = e;
+            sum = sum + e;
+        }
+        float inv_sum = 1.0f / sum;
+        for (size_t i = 0; i < num_classes; ++i) g[i] = g[i] * (inv_sum * inv_batch);
+        if (target_idx < num_classes) g[target_idx] = g[target_idx] - inv_batch;
+    }
+}

@@ -116,6 +116,16 @@ void kore_oracle_softmax_causal_f32(const float *x, float *y, size_t rows,
 void kore_oracle_softmax_backward_f32(const float *dy, const float *y,
                                       float *dx, size_t rows, size_t cols);
 
+/* crates/kore-kernels/src/cpu_fused_backward.rs:130-170
+ * (fused_cross_entropy_backward): per row the softmax is formed as in
+ * fused_softmax, grad = e * (inv_sum * inv_batch), inv_batch = 1/batch (f32),
+ * then grad[t] -= inv_batch, t = targets[b] as usize (Rust's saturating
+ * float-to-int cast).  Where the reference would panic (t >= num_classes)
+ * this restatement, like the device op, subtracts nothing. */
+void kore_oracle_cross_entropy_backward_f32(const float *logits,
+                                            const float *targets, float *grad,
+                                            size_t batch, size_t num_classes);
+
 /* crates/kore-kernels/src/cpu_fused_backward.rs:20-81
  * (fused_rms_norm_backward): per row sum_sq, inv_rms = 1/sqrt(sum_sq/d + eps);
  * dgamma[i] += (go*x)*inv_rms (rows in order);

@@ -37,6 +37,7 @@ _SIGS = {
     "kore_oracle_softmax_f32": (None, [_p, _p, _sz, _sz]),
     "kore_oracle_softmax_causal_f32": (None, [_p, _p, _sz, _sz, _sz]),
     "kore_oracle_softmax_backward_f32": (None, [_p, _p, _p, _sz, _sz]),
+    "kore_oracle_cross_entropy_backward_f32": (None, [_p, _p, _p, _sz, _sz]),
     "kore_oracle_rms_norm_backward_f32": (None, [_p, _p, _p, _p, _p, _sz, _sz, _f]),
 }
 
@@ -184,7 +185,7 @@ def quant_code(xn: float, amax: float) -> int:
 
 __all__ = ["build", "lib", "rms_norm", "gelu", "silu", "mul", "swiglu", "rope_inv_freq", "rope", "embedding",
            "rms_norm_quant_i8", "rms_norm_silu_gate", "quant_code", "softmax", "softmax_causal",
-           "softmax_backward", "rms_norm_backward"]
+           "softmax_backward", "rms_norm_backward", "cross_entropy_backward"]
 
 
 def _rows_cols(x: np.ndarray):
@@ -227,3 +228,12 @@ def rms_norm_backward(dy, x, gamma, eps: float):
     dgamma = np.empty(cols, np.float32)
     lib().kore_oracle_rms_norm_backward_f32(_ptr(dy), _ptr(x), _ptr(gamma), _ptr(dx), _ptr(dgamma), rows, cols, eps)
     return dx, dgamma
+
+
+def cross_entropy_backward(logits, targets) -> np.ndarray:
+    """cpu_fused_backward.rs:130-170: (softmax(logits) - one_hot(targets)) / batch."""
+    l, t = _f32(logits), _f32(targets)
+    batch, classes = l.shape
+    g = np.empty_like(l)
+    lib().kore_oracle_cross_entropy_backward_f32(_ptr(l), _ptr(t), _ptr(g), batch, classes)
+    return g

@@ -510,3 +510,30 @@ def test_rms_norm_backward_deterministic_and_edge_cases():
     sdx, sdg = _rms_bwd_scales(dyu, xu, gu, 1e-5)
     assert_close_scaled(down(gx, np.float32, (7, 256)), dx_w, sdx, rtol=1e-5 + 256 * U32, what="unaligned dx")
     assert_close_scaled(down(gg, np.float32, (256,)), dg_w, sdg, rtol=1e-5 + 7 * U32, what="unaligned dgamma")
+
+
+# -------------------------------------------------- cross-entropy backward
+@pytest.mark.parametrize("batch,classes", [(1, 1), (3, 7), (2, 3), (64, 256), (17, 1000), (8, 4096), (4, 8192),
+                                           (3, 32000), (2, 128256), (5, 4099)])
+def test_cross_entropy_backward(batch, classes):
+    log(f"cross_entropy_backward batch={batch} classes={classes}")
+    x = normal((batch, classes), batch + classes) * 3
+    t = (np.arange(batch) * 7919 % classes).astype(np.float32)
+    got = down(rocm.rocm_cross_entropy_backward_f32(DEV, up(x), up(t), batch, classes), np.float32, (batch, classes))
+    want = oracle.cross_entropy_backward(x, t)
+    assert_close(got, want, rtol=1e-5 + classes * U32, what="cross_entropy_backward vs oracle")
+    e = np.exp(x.astype(np.float64) - x.max(axis=1, keepdims=True))
+    ref = e / e.sum(axis=1, keepdims=True)
+    ref[np.arange(batch), t.astype(int)] -= 1.0
+    assert_close(got, ref / batch, what="cross_entropy_backward vs f64")
+
+
+def test_cross_entropy_backward_target_cast_and_in_place():
+    log("cross_entropy_backward targets / in place")
+    for classes in (4, 256, 20000):  # register and looped paths
+        x = normal((6, classes), classes) * 2
+        t = np.array([2.7, -3.0, np.nan, 0.5, classes + 1.0, classes - 1], np.float32)
+        b = up(x)
+        rocm.rocm_cross_entropy_backward_f32(DEV, b, up(t), 6, classes, out=b)
+        assert_close(down(b, np.float32, (6, classes)), oracle.cross_entropy_backward(x, t),
+                     rtol=1e-5 + classes * U32, what=f"ce targets {classes}")

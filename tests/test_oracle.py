@@ -362,3 +362,35 @@ def test_rms_norm_backward_matches_torch_autograd_f64():
     dx, dg = oracle.rms_norm_backward(dy, x, g, eps)
     assert np.allclose(dx, xt.grad.numpy(), rtol=1e-4, atol=2e-6)
     assert np.allclose(dg, gt.grad.numpy(), rtol=1e-4, atol=2e-6)
+
+
+# -------------------------------------------------- cross-entropy backward
+def test_cross_entropy_backward_reference_kats_and_f64():
+    # cpu_fused_backward.rs:251-299
+    g = oracle.cross_entropy_backward(np.array([[1, 2, 3], [1, 2, 3]], np.float32), np.array([2, 0], np.float32))
+    assert g.shape == (2, 3)
+    g = oracle.cross_entropy_backward(np.array([[1, 2, 3], [0.5, -0.5, 1]], np.float32), np.array([1, 2], np.float32))
+    assert abs(g[0].sum()) < 1e-6 and abs(g[1].sum()) < 1e-6
+    g = oracle.cross_entropy_backward(np.array([[0, 0, 10]], np.float32), np.array([2], np.float32))
+    assert np.isfinite(g).all()
+    g = oracle.cross_entropy_backward(np.array([[10, 0, 0]], np.float32), np.array([2], np.float32))
+    assert g[0, 0] > 0 and g[0, 2] < 0
+    # (softmax - one_hot) / batch in f64
+    x = normal((5, 40), 12) * 3
+    t = np.array([0, 39, 7, 7, 20], np.float32)
+    e = np.exp(x.astype(np.float64) - x.max(axis=1, keepdims=True))
+    ref = e / e.sum(axis=1, keepdims=True)
+    ref[np.arange(5), t.astype(int)] -= 1.0
+    ref /= 5
+    assert np.allclose(oracle.cross_entropy_backward(x, t), ref, rtol=1e-5, atol=1e-7)
+
+
+def test_cross_entropy_backward_target_cast():
+    # `as usize`: truncation, NaN and negatives -> 0; out of range: no subtraction
+    x = np.zeros((5, 4), np.float32)
+    g = oracle.cross_entropy_backward(x, np.array([2.7, -3.0, np.nan, 0.5, 4.0], np.float32))
+    base = np.float32(0.25) * (np.float32(1.0) * np.float32(1 / 5))
+    for b, t in enumerate([2, 0, 0, 0, None]):
+        for i in range(4):
+            want = base - np.float32(0.2) if i == t else base
+            assert abs(g[b, i] - want) < 1e-7, (b, i)
