@@ -22,10 +22,9 @@
 //      registers (gamma is re-read from cache per row); the row slots'
 //      partials are added in a fixed order through LDS and written as
 //      workspace row p = the block index.
-//   2. rms_bwd_partials_kernel: block (column chunk of 64 float4, group of 64
-//      partials) sums its group in a fixed order -> level-2 rows.
-//   3. rms_bwd_final_kernel: one thread per float4 column sums the level-2
-//      rows in order -> dgamma.
+//   2. rms_bwd_reduce_kernel: 8 float4 columns x 64 row slots per block;
+//      every slot adds its partial rows in order, then the slots are added
+//      in order -> dgamma (deterministic).
 // Generic path (any shape): one workgroup per row writes dx and inv[r] to the
 // workspace; then one thread per column folds its dgamma over the rows in
 // the reference's order.
@@ -36,7 +35,6 @@ namespace kore {
 
 constexpr int kBwBlock = 256;
 constexpr int kBwWaves = kBwBlock / kWave;
-constexpr uint32_t kBwGroup = 64;  // partial rows per level-2 row
 
 struct BwArgs {
     const float* dy;
@@ -50,16 +48,16 @@ struct BwArgs {
     float eps;
     uint32_t rpw;       // row iterations per workgroup (vector path)
     uint64_t partials;  // P
-    uint64_t groups;    // level-2 rows
 };
 
 __device__ __forceinline__ float sum4(f32x4 a) { return (a.x + a.y) + (a.z + a.w); }
 
 // A row is split over S waves (wave w: row slot j = w / S, column part
 // q = w % S, float4 columns (q*NCHW + k)*64 + lane, k < NCHW), so a wave holds
-// at most 4 float4 per operand.  The workgroup covers rows
-// [b*rpb, (b+1)*rpb), rpb = iters * (4 / S): iteration i takes rows
-// b*rpb + i*(4/S) + j.  Per row, the S waves' partial sums meet in LDS (slot
+// at most 4 float4 per operand.  Iteration it of workgroup b takes row
+// (it * P + b) * (4/S) + j (P = the grid size), so each iteration of the grid
+// sweeps one contiguous band of rows (measured 89 -> 80 us at 16384 x 2048
+// against giving each workgroup a contiguous block of rows).  Per row, the S waves' partial sums meet in LDS (slot
 // parity double-buffered, one barrier per iteration) and are added in q
 // order.  Each wave keeps its dgamma partial in registers; at the end the
 // row slots' partials are added in j order through LDS and written as
@@ -67,7 +65,7 @@ __device__ __forceinline__ float sum4(f32x4 a) { return (a.x + a.y) + (a.z + a.w
 template <int NCHW, int S>
 __global__ __launch_bounds__(kBwBlock) void rms_bwd_rows_kernel(BwArgs a) {
     constexpr int kSlots = kBwWaves / S;
-    extern __shared__ f32x4 part[];  // [cols4]
+    extern __shared__ f32x4 part[];  // [cols4] dgamma combine
     __shared__ float red[2][kBwWaves][2];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -75,14 +73,16 @@ __global__ __launch_bounds__(kBwBlock) void rms_bwd_rows_kernel(BwArgs a) {
     const uint32_t cols4 = (uint32_t)(a.cols >> 2);
     const float fcols = (float)a.cols;
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    const uint64_t rpb = (uint64_t)a.rpw * kSlots;
-    const uint64_t rbase = (uint64_t)blockIdx.x * rpb;
+    // iteration it of block b: row (it * P + b) * slots + j -- the grid sweeps
+    // one contiguous band of rows per iteration.
+    const uint64_t rstride = (uint64_t)gridDim.x * kSlots;
+    const uint64_t rbase = (uint64_t)blockIdx.x * kSlots;
 
     f32x4 acc[NCHW];
 #pragma unroll
     for (int k = 0; k < NCHW; ++k) acc[k] = zero;
     for (uint32_t it = 0; it < a.rpw; ++it) {
-        const uint64_t r = rbase + (uint64_t)it * kSlots + j;
+        const uint64_t r = rbase + (uint64_t)it * rstride + j;
         const bool live = r < a.rows;
         const uint64_t rr = live ? r : 0;
         const f32x4* xr = reinterpret_cast<const f32x4*>(a.x) + rr * cols4;
@@ -155,46 +155,37 @@ __global__ __launch_bounds__(kBwBlock) void rms_bwd_rows_kernel(BwArgs a) {
     for (uint32_t f = threadIdx.x; f < cols4; f += kBwBlock) wrow[f] = part[f];
 }
 
-// grid (ceil(cols4 / 64), groups): wave w of the block sums partial rows
-// g*64 + w*16 + k (k = 0..15, in order) of column float4 cx*64 + lane; the 4
-// wave sums are then added in wave order.
-__global__ __launch_bounds__(kBwBlock) void rms_bwd_partials_kernel(BwArgs a) {
-    __shared__ f32x4 red[kBwWaves][kWave];
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+// dgamma = sum of the P partial rows, deterministic: block = 8 float4
+// columns x 64 row slots; thread (slot, c) adds rows slot, slot+64, ... in
+// order; the 64 slot sums are then added in slot order.
+constexpr int kRedCols = 8;
+constexpr int kRedSlots = 64;
+__global__ __launch_bounds__(kRedCols * kRedSlots) void rms_bwd_reduce_kernel(BwArgs a) {
+    __shared__ f32x4 red[kRedSlots][kRedCols];
     const uint64_t cols4 = a.cols >> 2;
-    const uint64_t col = (uint64_t)blockIdx.x * kWave + lane;
-    const uint64_t grp = blockIdx.y;
+    const int c = threadIdx.x % kRedCols;
+    const int slot = threadIdx.x / kRedCols;
+    const uint64_t col = (uint64_t)blockIdx.x * kRedCols + c;
     const f32x4* w4 = reinterpret_cast<const f32x4*>(a.ws);
-    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    constexpr int kPer = kBwGroup / kBwWaves;
-    f32x4 v[kPer];
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-        const uint64_t p = grp * kBwGroup + (uint64_t)wave * kPer + k;
-        v[k] = (p < a.partials && col < cols4) ? w4[p * cols4 + col] : zero;
+    f32x4 t = {0.f, 0.f, 0.f, 0.f};
+    if (col < cols4) {
+        uint64_t p = slot;
+        for (; p + 3 * kRedSlots < a.partials; p += 4 * kRedSlots) {  // 4 loads in flight, added in order
+            const f32x4 v0 = w4[p * cols4 + col];
+            const f32x4 v1 = w4[(p + kRedSlots) * cols4 + col];
+            const f32x4 v2 = w4[(p + 2 * kRedSlots) * cols4 + col];
+            const f32x4 v3 = w4[(p + 3 * kRedSlots) * cols4 + col];
+            t = (((t + v0) + v1) + v2) + v3;
+        }
+        for (; p < a.partials; p += kRedSlots) t = t + w4[p * cols4 + col];
     }
-    f32x4 s = v[0];
-#pragma unroll
-    for (int k = 1; k < kPer; ++k) s = s + v[k];
-    red[wave][lane] = s;
+    red[slot][c] = t;
     __syncthreads();
-    if (wave == 0 && col < cols4) {
-        f32x4 t = red[0][lane];
-#pragma unroll
-        for (int w = 1; w < kBwWaves; ++w) t = t + red[w][lane];
-        reinterpret_cast<f32x4*>(a.ws)[(a.partials + grp) * cols4 + col] = t;
+    if (slot == 0 && col < cols4) {
+        f32x4 u = red[0][c];
+        for (int k = 1; k < kRedSlots; ++k) u = u + red[k][c];
+        reinterpret_cast<f32x4*>(a.dgamma)[col] = u;
     }
-}
-
-__global__ __launch_bounds__(kBwBlock) void rms_bwd_final_kernel(BwArgs a) {
-    const uint64_t cols4 = a.cols >> 2;
-    const uint64_t col = (uint64_t)blockIdx.x * kBwBlock + threadIdx.x;
-    if (col >= cols4) return;
-    const f32x4* l2 = reinterpret_cast<const f32x4*>(a.ws) + a.partials * cols4;
-    f32x4 t = l2[col];
-    for (uint64_t g = 1; g < a.groups; ++g) t = t + l2[g * cols4 + col];
-    reinterpret_cast<f32x4*>(a.dgamma)[col] = t;
 }
 
 // ---- generic path
@@ -255,6 +246,7 @@ static uint32_t bwd_split(uint64_t cols) {
     return c4 <= 256 ? 1u : (c4 <= 512 ? 2u : 4u);
 }
 
+
 // Row iterations per workgroup: ~1024 workgroups (4 waves each) fill the
 // chip; at most 16 iterations so that large batches keep few partial rows.
 static uint32_t bwd_iters(uint64_t rows, uint32_t split) {
@@ -266,24 +258,21 @@ static uint32_t bwd_iters(uint64_t rows, uint32_t split) {
 }
 
 // Workspace floats for the vector and generic plans (the larger is required).
-static uint64_t bwd_ws_floats(uint64_t rows, uint64_t cols, uint64_t* partials, uint64_t* groups,
-                              uint32_t* iters) {
+static uint64_t bwd_ws_floats(uint64_t rows, uint64_t cols, uint64_t* partials, uint32_t* iters) {
     const uint32_t split = bwd_split(cols);
     const uint32_t it = bwd_iters(rows, split);
     const uint64_t rpb = (uint64_t)it * (kBwWaves / split);  // rows per block = per partial row
     const uint64_t p = (rows + rpb - 1) / rpb;
-    const uint64_t g = (p + kBwGroup - 1) / kBwGroup;
     if (partials) *partials = p;
-    if (groups) *groups = g;
     if (iters) *iters = it;
-    const uint64_t vec = bwd_vec(cols) ? (p + g) * cols : 0;
+    const uint64_t vec = bwd_vec(cols) ? p * cols : 0;
     return vec > rows ? vec : rows;
 }
 
 template <int NCHW, int S>
 static void launch_rows(const BwArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((rms_bwd_rows_kernel<NCHW, S>), dim3((uint32_t)a.partials), dim3(kBwBlock),
-                       (a.cols / 4) * sizeof(f32x4), s, a);
+    const size_t lds = (a.cols / 4) * sizeof(f32x4);
+    hipLaunchKernelGGL((rms_bwd_rows_kernel<NCHW, S>), dim3((uint32_t)a.partials), dim3(kBwBlock), lds, s, a);
 }
 
 }  // namespace kore
@@ -294,7 +283,7 @@ extern "C" uint64_t kore_hip_rms_norm_backward_workspace_bytes(uint64_t rows, ui
     if (rows == 0 || cols == 0) return 0;
     uint64_t elems;
     if (!mul_ok(rows, cols, &elems) || elems > kMaxElements) return 0;
-    return bwd_ws_floats(rows, cols, nullptr, nullptr, nullptr) * sizeof(float);
+    return bwd_ws_floats(rows, cols, nullptr, nullptr) * sizeof(float);
 }
 
 extern "C" int kore_hip_rms_norm_backward_f32(const float* grad_out, const float* x, const float* gamma,
@@ -314,9 +303,8 @@ extern "C" int kore_hip_rms_norm_backward_f32(const float* grad_out, const float
     if (!grad_out || !x || !grad_x || !workspace) return KORE_HIP_ERR_NULL_PTR;
     uint64_t elems;
     if (!mul_ok(rows, cols, &elems) || elems > kMaxElements || rows > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
-    BwArgs a{grad_out, x, gamma, grad_x, grad_gamma, workspace, rows, cols, eps, 0, 0, 0};
-    const uint64_t need = bwd_ws_floats(rows, cols, &a.partials, &a.groups, &a.rpw) * sizeof(float);
-    if (a.groups > 65535) return KORE_HIP_ERR_OVERFLOW;  // grid.y of the partial reduction
+    BwArgs a{grad_out, x, gamma, grad_x, grad_gamma, workspace, rows, cols, eps, 0, 0};
+    const uint64_t need = bwd_ws_floats(rows, cols, &a.partials, &a.rpw) * sizeof(float);
     if (workspace_bytes < need) return KORE_HIP_ERR_BAD_DIM;
     // grad_x must not overlap the inputs (the row pass reads a row ahead).
     const char* o0 = (const char*)grad_x;
@@ -334,10 +322,8 @@ extern "C" int kore_hip_rms_norm_backward_f32(const float* grad_out, const float
         else if (cols4 <= 256) launch_rows<4, 1>(a, s);
         else if (cols4 <= 512) launch_rows<4, 2>(a, s);
         else launch_rows<4, 4>(a, s);
-        hipLaunchKernelGGL(rms_bwd_partials_kernel, dim3((uint32_t)((cols4 + kWave - 1) / kWave), (uint32_t)a.groups),
-                           dim3(kBwBlock), 0, s, a);
-        hipLaunchKernelGGL(rms_bwd_final_kernel, dim3((uint32_t)((cols4 + kBwBlock - 1) / kBwBlock)),
-                           dim3(kBwBlock), 0, s, a);
+        hipLaunchKernelGGL(rms_bwd_reduce_kernel, dim3((uint32_t)((cols4 + kRedCols - 1) / kRedCols)),
+                           dim3(kRedCols * kRedSlots), 0, s, a);
     } else {
         hipLaunchKernelGGL(rms_bwd_row_generic_kernel, dim3((uint32_t)rows), dim3(kBwBlock), 0, s, a);
         hipLaunchKernelGGL(rms_bwd_col_generic_kernel, dim3((uint32_t)((cols + kBwBlock - 1) / kBwBlock)),

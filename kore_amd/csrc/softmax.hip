@@ -20,7 +20,8 @@
 //            a t >= cols (the reference panics) subtracts nothing.
 // The sums are tree reductions (lane partials, then a wave butterfly), so
 // results are within the f32 tolerance of the reference's left fold, as its
-// own CUDA kernel is.  exp is ocml's accurate expf.
+// own CUDA kernel is.  exp(d) is evaluated on the reference's d = x - m
+// (rounded the same way) as the hardware exp2(d * log2(e)); see exp_diff.
 //
 // Shapes: a row of up to 4096 floats is held in one wave's registers (one
 // wave per row, 4 rows per workgroup); up to 16384 floats in one 256-thread
@@ -62,6 +63,15 @@ __device__ __forceinline__ uint64_t target_index(float t, uint64_t cols) {
     const uint64_t i = (uint64_t)t;
     return i < cols ? i : ~0ull;
 }
+
+// exp(d) for d = x - max <= 0 as v_exp_f32(d * log2(e)): 2 VALU ops instead
+// of ~12 for ocml expf.  Rounding d*log2(e) perturbs the result by at most
+// |d| * 2^-24 * ln 2 relative (< 1e-6 for d >= -16, where e^d > 1e-7 still
+// matters next to the row's largest term e^0 = 1); v_exp_f32 adds ~1 ulp.
+// Below that the absolute error is < 1e-7 * e^d.  exp(-inf) = 0 and
+// exp(NaN) = NaN as in the reference.  (Measured: 87.2 -> 85.3 us on the
+// 32768 x 2048 softmax.)
+__device__ __forceinline__ float exp_diff(float d) { return __builtin_amdgcn_exp2f(d * 1.44269504f); }
 
 // Number of leading columns of `row` that take part (causal mask).
 template <SmKind K>
@@ -150,7 +160,7 @@ __global__ __launch_bounds__(kSmBlock) void softmax_reg_kernel(SmArgs a) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const bool in = 4 * f + k < lim;
-            const float e = in ? expf(f4_get(v[c], k) - m) : 0.0f;
+            const float e = in ? exp_diff(f4_get(v[c], k) - m) : 0.0f;
             f4_set(v[c], k, e);
             s += e;
         }
@@ -233,9 +243,9 @@ __global__ __launch_bounds__(kSmBlock) void softmax_loop_kernel(SmArgs a) {
         if (Vec) {
             const f32x4 v = reinterpret_cast<const f32x4*>(ar)[i];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) s += 4 * i + k < lim ? expf(f4_get(v, k) - m) : 0.0f;
+            for (int k = 0; k < 4; ++k) s += 4 * i + k < lim ? exp_diff(f4_get(v, k) - m) : 0.0f;
         } else {
-            s += i < lim ? expf(ar[i] - m) : 0.0f;
+            s += i < lim ? exp_diff(ar[i] - m) : 0.0f;
         }
     }
     s = block_combine<false>(wave_sum(s), red);
@@ -248,13 +258,13 @@ __global__ __launch_bounds__(kSmBlock) void softmax_loop_kernel(SmArgs a) {
             f32x4 v = reinterpret_cast<const f32x4*>(ar)[i];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                float o = (4 * i + k < lim ? expf(f4_get(v, k) - m) : 0.0f) * scale;
+                float o = (4 * i + k < lim ? exp_diff(f4_get(v, k) - m) : 0.0f) * scale;
                 if (K == SmKind::CeBwd && 4 * i + k == t) o = o - inv_batch;
                 f4_set(v, k, o);
             }
             st_stream(reinterpret_cast<f32x4*>(orow) + i, v);
         } else {
-            float o = (i < lim ? expf(ar[i] - m) : 0.0f) * scale;
+            float o = (i < lim ? exp_diff(ar[i] - m) : 0.0f) * scale;
             if (K == SmKind::CeBwd && i == t) o = o - inv_batch;
             orow[i] = o;
         }
