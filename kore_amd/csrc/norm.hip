@@ -33,21 +33,23 @@
 // checked against the plain fold on adversarial rows by the CPU test suite
 // (tests/csrc/check_segmented_fold.c restates this kernel in scalar C).
 //
-// Data movement per wave (R rows):
-//   * rows loaded with wave-wide global_load_dwordx4 (coalesced, 1 KiB per
-//     instruction), all in flight before first use, kept in VGPRs for the
-//     epilogue: one HBM read per byte;
-//   * per row, squares pass through a wave-private LDS tile once to put
-//     segment j into lane j (odd float4 pitch: conflict-free ds_read_b128);
-//   * each segment's (d_0, d_1, 2^E, 2^(E+1)) goes to an LDS table; the
-//     resolve runs lane-parallel over the wave's rows (lane r <-> row r);
-//   * segments predicted to fail (walk left the binade, or the estimate sits
-//     within 2^-10 of a binade edge) keep their squares in LDS slots so the
-//     fallback fold reads LDS; an unpredicted failure re-reads the segment
-//     from global memory (L2/MALL) -- rare, and still exact.
+// Data movement per wave (one row per wave, four waves per workgroup):
+//   * the row is loaded with wave-wide global_load_dwordx4 (coalesced, 1 KiB
+//     per instruction), all in flight before first use, and kept in VGPRs
+//     for the epilogue: one HBM read per byte;
+//   * its squares pass through a wave-private LDS tile (half a row at a time)
+//     to put segment j into lane 63 - j (odd float4 pitch: conflict-free
+//     ds_read_b128);
+//   * runs of segments in one binade are composed by a segmented DPP scan, so
+//     each lane holds its segment's run entry (d_0, d_1, window, next
+//     segment) and its squares in registers;
+//   * the resolve is wave-uniform: it reads entry j from lane 63 - j with
+//     v_readlane, jumps whole runs, and when a segment falls back the owning
+//     lane folds its own registers and broadcasts the sum.  No LDS, no
+//     re-read of global memory.
 // A wave's LDS traffic never crosses waves, so there are no barriers: LDS
 // operations from one wave complete in issue order.
-//
+
 // Epilogue (element-parallel over all 64 lanes, coalesced layout):
 //   inv  = 1 / sqrt(ss / cols + eps)   IEEE sqrt and division (cpu_fused.rs:181-182)
 //   xn   = (x * inv) * w                                      (cpu_fused.rs:185)
@@ -69,7 +71,6 @@ namespace kore {
 constexpr int kWavesPerBlock = 4;
 constexpr int kNormBlock = kWave * kWavesPerBlock;
 constexpr int kSegs = kWave;  // segments per row: one per lane
-constexpr int kSlots = 8;     // LDS fallback slots per row
 
 // F32: y = RMSNorm(x); I8: pre-quant codes + scales; SiluGate: y = RMSNorm(x)
 // * silu(z) (the Mamba input-path gate).
@@ -91,12 +92,9 @@ struct NormArgs {
 // segment starts j*pitch hit 16 distinct 16-byte bank groups per 16 lanes.
 __host__ __device__ constexpr uint32_t tile_pitch4(uint32_t sl4) { return sl4 + ((sl4 & 1u) ? 2u : 1u); }
 
-// Per-wave LDS: half-row transpose tile (32 segments), run table, fallback
-// slots, run-end bytes.
+// Per-wave LDS: the half-row transpose tile (32 segments).
 constexpr int kHalfSegs = kSegs / 2;
-__host__ __device__ constexpr uint32_t wave_lds_f4(uint32_t sl4, uint32_t rows) {
-    return kHalfSegs * tile_pitch4(sl4) + rows * kSegs + rows * kSlots * sl4 + (rows * kSegs + 15) / 16;
-}
+__host__ __device__ constexpr uint32_t wave_lds_f4(uint32_t sl4) { return kHalfSegs * tile_pitch4(sl4); }
 
 __device__ __forceinline__ int32_t cvt_i32_sat(float v) {
     // v_cvt_i32_f32: round toward zero, saturating, NaN -> 0.  Written as asm
@@ -236,8 +234,8 @@ __device__ __forceinline__ void run_scan(RunElem& e) {
 
 // Vector path: cols % 4 == 0, x/w/y 16-byte aligned, q 4-byte aligned,
 // ceil(cols/4 / 64) <= SL4.  Segment j covers float4 [j*SL4, (j+1)*SL4).
-// Grid: one block per kWavesPerBlock * R rows; dynamic LDS =
-// kWavesPerBlock * wave_lds_f4(SL4, R) float4.
+// Grid: one block per kWavesPerBlock rows (one row per wave); dynamic LDS =
+// kWavesPerBlock * wave_lds_f4(SL4) float4 (the transpose tiles).
 // silu(z) = z / (1 + e^-z) from the hardware exp2 and reciprocal (5 VALU
 // instead of ~25 for expf + IEEE division).  Error: v_exp_f32 and v_rcp_f32
 // are 1 ulp each; rounding z*log2(e) to f32 perturbs e^-z by |z|*2^-24*ln2
@@ -250,41 +248,30 @@ __device__ __forceinline__ float silu_fast(float z) {
     return z * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-template <NormOut Out, int SL4, int R>
+template <NormOut Out, int SL4>
 __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
     constexpr int NCH = SL4;  // 64*SL4 float4 cover the row: SL4 wave-wide chunks
     constexpr int TP4 = (int)tile_pitch4(SL4);
-    constexpr uint32_t kWaveF4 = wave_lds_f4(SL4, R);
+    constexpr uint32_t kWaveF4 = wave_lds_f4(SL4);
     extern __shared__ f32x4 lds4[];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const uint64_t row0 = ((uint64_t)blockIdx.x * kWavesPerBlock + wave) * R;
-    if (row0 >= args.rows) return;  // uniform per wave; no block barrier follows
-    const uint64_t left = args.rows - row0;
-    const int nrows = left < (uint64_t)R ? (int)left : R;
+    const uint64_t row = (uint64_t)blockIdx.x * kWavesPerBlock + wave;
+    if (row >= args.rows) return;  // uniform per wave; no block barrier follows
     const uint32_t cols4 = args.cols >> 2;
     const int nseg = (int)((cols4 + SL4 - 1) / SL4);
     f32x4* tile = lds4 + (size_t)wave * kWaveF4;
-    f32x4* table = tile + kHalfSegs * TP4;    // [R][64] (D0, D1, bot, top)
-    f32x4* slots = table + R * kSegs;         // [R][kSlots][SL4]
-    uint8_t* nexts = reinterpret_cast<uint8_t*>(slots + R * kSlots * SL4);  // [R][64]
-    const f32x4* x4 = reinterpret_cast<const f32x4*>(args.x);
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
     const float inf = __builtin_inff();
     const float qnan = __builtin_nanf("");
 
     // ---- HBM reads: coalesced, chunk-major, all in flight.
-    // Row-major issue order: row 0 lands first and its fold starts while the
-    // other rows are still streaming in.
-    f32x4 xv[R][NCH];
+    const f32x4* xr = reinterpret_cast<const f32x4*>(args.x) + row * cols4;
+    f32x4 xv[NCH];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const f32x4* xr = x4 + (row0 + r) * cols4;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const uint32_t f = (uint32_t)c * kWave + lane;
-            xv[r][c] = (f < cols4 && r < nrows) ? ld_stream(xr + f) : zero;
-        }
+    for (int c = 0; c < NCH; ++c) {
+        const uint32_t f = (uint32_t)c * kWave + lane;
+        xv[c] = (f < cols4) ? ld_stream(xr + f) : zero;
     }
 
     // Lane L holds segment j = 63 - L, so a forward (lane-increasing) scan
@@ -292,178 +279,116 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
     const int seg_id = kSegs - 1 - lane;
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
-    // ---- transpose every row through the wave's tile (sequentially: one
-    // tile), then run the per-row phases for all rows at once so their
-    // dependency chains interleave.  Rows past nrows compute on zeros and are
-    // never stored or resolved.
-    // The tile holds half a row (32 segments): pass h moves segments
-    // [32h, 32h + 32), which lanes 63 - seg read back.
-    f32x4 seg[R][SL4];
+    // ---- transpose the squares through the wave's tile.  The tile holds
+    // half a row (32 segments): pass h moves segments [32h, 32h + 32), which
+    // lanes 63 - seg read back.
+    f32x4 seg[SL4];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
+    for (int h = 0; h < 2; ++h) {
+        wave_lds_sync();  // previous tile reads precede these writes
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            wave_lds_sync();  // previous tile reads precede these writes
+        for (int c = 0; c < NCH; ++c) {
+            const int f = c * kWave + lane;  // float4 index in the row
+            const int sg = f / SL4 - h * kHalfSegs;
+            if (sg >= 0 && sg < kHalfSegs) tile[sg * TP4 + (f % SL4)] = xv[c] * xv[c];  // zero past the end
+        }
+        wave_lds_sync();
+        const int my = seg_id - h * kHalfSegs;
+        if (my >= 0 && my < kHalfSegs) {
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-                const int f = c * kWave + lane;  // float4 index in the row
-                const int sg = f / SL4 - h * kHalfSegs;
-                if (sg >= 0 && sg < kHalfSegs)
-                    tile[sg * TP4 + (f % SL4)] = xv[r][c] * xv[r][c];  // zero past the end
-            }
-            wave_lds_sync();
-            const int my = seg_id - h * kHalfSegs;
-            if (my >= 0 && my < kHalfSegs) {
-#pragma unroll
-                for (int k = 0; k < SL4; ++k) seg[r][k] = tile[my * TP4 + k];
-            }
+            for (int k = 0; k < SL4; ++k) seg[k] = tile[my * TP4 + k];
         }
     }
 
     const bool empty = seg_id >= nseg;
-    float ssum[R], est[R];
+    float ssum = 0.0f;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int k = 0; k < SL4; ++k) acc += sum4(seg[r][k]);
-        ssum[r] = acc;
-    }
+    for (int k = 0; k < SL4; ++k) ssum += sum4(seg[k]);
     // Estimate of the running sum at this segment's start = sum over the
     // segments before it = lanes above this one (any summation order).
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const float incl = wave_incl_scan(ssum[r]);
-        est[r] = read_lane(incl, kWave - 1) - incl;
-    }
+    const float incl = wave_incl_scan(ssum);
+    const float est = read_lane(incl, kWave - 1) - incl;
 
-    RunElem el[R];
-    float bot[R], top[R];
-    bool valid[R];
-    int key_me[R];
+    // Binade of the estimate (exponent field ef; ef <= 1 is the uniform grid
+    // [0, 2^-125) of step 2^-149), selected branch-free.  Segment 0 folds
+    // from its true start +0; an Inf/NaN estimate gets an empty window so the
+    // segment always falls back.
+    const uint32_t ef_raw = __float_as_uint(est) >> 23;  // est >= 0
+    const uint32_t ef = ef_raw < 1u ? 1u : ef_raw;
+    const bool sub = ef == 1u;
+    const bool first = seg_id == 0 || empty;
+    const bool bad = !first && ef >= 255u;
+    float sig0 = sub ? 0.0f : __uint_as_float(ef << 23);
+    float sig1 = sub ? __uint_as_float(1u) : __uint_as_float((ef << 23) | 1u);
+    float bot = sig0;
+    float top = __uint_as_float((ef + 1u) << 23);  // ef + 1 == 255 -> +Inf
+    sig0 = first ? 0.0f : sig0;
+    sig1 = first ? 0.0f : sig1;
+    bot = first ? 0.0f : (bad ? inf : bot);
+    top = first ? inf : (bad ? 0.0f : top);
+    float w0 = sig0, w1 = sig1;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        // Binade of the estimate (exponent field ef; ef <= 1 is the uniform
-        // grid [0, 2^-125) of step 2^-149), selected branch-free.  Segment 0
-        // folds from its true start +0; an Inf/NaN estimate gets an empty
-        // window so the segment always falls back.
-        const uint32_t ef_raw = __float_as_uint(est[r]) >> 23;  // est >= 0
-        const uint32_t ef = ef_raw < 1u ? 1u : ef_raw;
-        const bool sub = ef == 1u;
-        const bool first = seg_id == 0 || empty;
-        const bool bad = !first && ef >= 255u;
-        float sig0 = sub ? 0.0f : __uint_as_float(ef << 23);
-        float sig1 = sub ? __uint_as_float(1u) : __uint_as_float((ef << 23) | 1u);
-        float b = sig0;
-        float t = __uint_as_float((ef + 1u) << 23);  // ef + 1 == 255 -> +Inf
-        sig0 = first ? 0.0f : sig0;
-        sig1 = first ? 0.0f : sig1;
-        b = first ? 0.0f : (bad ? inf : b);
-        t = first ? inf : (bad ? 0.0f : t);
-        bot[r] = b;
-        top[r] = t;
-        float w0 = sig0, w1 = sig1;
-#pragma unroll
-        for (int k = 0; k < SL4; ++k) {
-            const f32x4 a = seg[r][k];
-            w0 = w0 + a.x; w1 = w1 + a.x;
-            w0 = w0 + a.y; w1 = w1 + a.y;
-            w0 = w0 + a.z; w1 = w1 + a.z;
-            w0 = w0 + a.w; w1 = w1 + a.w;
-        }
-        const bool ok0 = w0 < t;
-        const bool ok1 = first ? ok0 : (w1 < t);
-        // A segment whose estimated span touches a binade edge (within 2^-10;
-        // the estimate's own error is below cols * 2^-24 relative) will most
-        // likely cross it: keep it out of runs so that it is folded alone,
-        // from its LDS slot, instead of breaking a jump.
-        const bool edge = !first && (est[r] < b * 1.0009765625f || est[r] + ssum[r] >= t * 0.9990234375f);
-        valid[r] = ok0 && ok1 && !edge;
-        // Scan element of this single segment.
-        RunElem e;
-        e.d0 = ok0 ? w0 - sig0 : qnan;
-        e.d1 = (seg_id == 0) ? e.d0 : (ok1 ? w1 - sig1 : qnan);
-        e.bits = (int)(__float_as_uint(w0) & 1u) | (seg_id == 0 ? 0 : (int)((__float_as_uint(w1) & 1u) << 1));
-        if (empty) {
-            e.bits = kIdBits; e.d0 = 0.0f; e.d1 = 0.0f;
-        }
-        // Runs: maximal spans of valid segments with one binade key; an
-        // invalid segment is a run of its own.
-        key_me[r] = empty ? 1024 : (seg_id == 0 ? 1025 : (valid[r] ? (int)ef : 2048 + seg_id));
-        el[r] = e;
+    for (int k = 0; k < SL4; ++k) {
+        const f32x4 a = seg[k];
+        w0 = w0 + a.x; w1 = w1 + a.x;
+        w0 = w0 + a.y; w1 = w1 + a.y;
+        w0 = w0 + a.z; w1 = w1 + a.z;
+        w0 = w0 + a.w; w1 = w1 + a.w;
     }
-
-    uint64_t pmask[R];  // predicted-fallback segments, bit j = segment j
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        // This lane's span ends its run when the next segment (lane - 1) is
-        // in another run; wave_shr:1 moves lane - 1's key here.
-        const int key_next = __builtin_amdgcn_update_dpp(key_me[r], key_me[r], 0x138, 0xf, 0xf, false);
-        const bool ends_here = lane == 0 || key_next != key_me[r];
-        if (ends_here) el[r].bits |= 4;
-        const uint64_t ends = __ballot(ends_here);
-        run_scan(el[r]);
-        // The run of lane L ends at the highest lane <= L with its bit set.
-        const uint64_t below = ends & (lt_mask | (1ull << lane));
-        const int end_lane = 63 - __builtin_clzll(below);
-        f32x4 ent;
-        ent.x = el[r].d0; ent.y = el[r].d1; ent.z = bot[r]; ent.w = top[r];
-        // Predicted fallback: the segment cannot join a run.
-        const bool pred = !empty && !valid[r];
-        const uint64_t m = __builtin_bitreverse64(__ballot(pred));  // bit j = segment j
-        pmask[r] = m;
-        if (r < nrows) {
-            table[r * kSegs + seg_id] = ent;
-            nexts[r * kSegs + seg_id] = (uint8_t)(kSegs - end_lane);  // (63 - end_lane) + 1
-            const int slot = __popcll(m & ((1ull << seg_id) - 1ull));
-            if (pred && slot < kSlots) {
-                f32x4* dst = slots + (r * kSlots + slot) * SL4;
-#pragma unroll
-                for (int k = 0; k < SL4; ++k) dst[k] = seg[r][k];
-            }
-        }
+    const bool ok0 = w0 < top;
+    const bool ok1 = first ? ok0 : (w1 < top);
+    // A segment whose estimated span touches a binade edge (within 2^-10;
+    // the estimate's own error is below cols * 2^-24 relative) will most
+    // likely cross it: keep it out of runs so that it is folded alone
+    // instead of breaking a jump.
+    const bool edge = !first && (est < bot * 1.0009765625f || est + ssum >= top * 0.9990234375f);
+    const bool valid = ok0 && ok1 && !edge;
+    // Scan element of this single segment.
+    RunElem el;
+    el.d0 = ok0 ? w0 - sig0 : qnan;
+    el.d1 = (seg_id == 0) ? el.d0 : (ok1 ? w1 - sig1 : qnan);
+    el.bits = (int)(__float_as_uint(w0) & 1u) | (seg_id == 0 ? 0 : (int)((__float_as_uint(w1) & 1u) << 1));
+    if (empty) {
+        el.bits = kIdBits; el.d0 = 0.0f; el.d1 = 0.0f;
     }
+    // Runs: maximal spans of valid segments with one binade key; an invalid
+    // segment is a run of its own.  This lane's span ends its run when the
+    // next segment (lane - 1, moved here by wave_shr:1) is in another run.
+    const int key_me = empty ? 1024 : (seg_id == 0 ? 1025 : (valid ? (int)ef : 2048 + seg_id));
+    const int key_next = __builtin_amdgcn_update_dpp(key_me, key_me, 0x138, 0xf, 0xf, false);
+    const bool ends_here = lane == 0 || key_next != key_me;
+    if (ends_here) el.bits |= 4;
+    const uint64_t ends = __ballot(ends_here);
+    run_scan(el);
+    // The run of lane L ends at the highest lane <= L with its bit set; the
+    // segment after it is 64 - that lane.
+    const uint64_t below = ends & (lt_mask | (1ull << lane));
+    const int next_seg = kSegs - (63 - __builtin_clzll(below));
 
-    // ---- resolve: lane r owns row r; one step per run or fallback.
-    wave_lds_sync();  // table, run ends and slots were written by other lanes
-    uint64_t my_mask = pmask[0];
-#pragma unroll
-    for (int r = 1; r < R; ++r) my_mask = (lane == r) ? pmask[r] : my_mask;
+    // ---- resolve, wave-uniform: segment j's run entry lives in lane 63 - j
+    // and is read with v_readlane; a jump adds the run's exact increment when
+    // the running sum stays inside its binade window, else the owner lane
+    // folds its own segment in order and broadcasts the sum.  No LDS.
     float ss = 0.0f;
-    if (lane < nrows) {
-        const f32x4* trow = table + lane * kSegs;
-        const uint8_t* nrow = nexts + lane * kSegs;
-        const f32x4* xrow = x4 + (row0 + lane) * cols4;
-        int j = 0;
-        while (j < nseg) {
-            const f32x4 e = trow[j];
-            const int nj = nrow[j];
-            const float d = (__float_as_uint(ss) & 1u) ? e.y : e.x;
-            const float t = ss + d;
-            if (ss >= e.z && t < e.w) {
-                ss = t;
-                j = nj;
-            } else {
-                // Sequential fold of segment j from the exact start: the
-                // segment's data is fetched first, then folded in order.
-                f32x4 v[SL4];
-                const int slot = __popcll(my_mask & ((1ull << j) - 1ull));
-                if (((my_mask >> j) & 1ull) && slot < kSlots) {
-                    const f32x4* src = slots + (lane * kSlots + slot) * SL4;
+    int j = 0;
+    while (j < nseg) {
+        const int L = kSegs - 1 - j;
+        const float d0 = read_lane(el.d0, L), d1 = read_lane(el.d1, L);
+        const float b = read_lane(bot, L), t = read_lane(top, L);
+        const int nj = __builtin_amdgcn_readlane(next_seg, L);
+        const float d = (__float_as_uint(ss) & 1u) ? d1 : d0;
+        const float st = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ss + d)));
+        if (ss >= b && st < t) {
+            ss = st;
+            j = nj;
+        } else {
+            float acc = ss;
+            if (lane == L) {
 #pragma unroll
-                    for (int k = 0; k < SL4; ++k) v[k] = src[k];
-                } else {
-#pragma unroll
-                    for (int k = 0; k < SL4; ++k) {
-                        const uint32_t f = (uint32_t)(j * SL4 + k);
-                        const f32x4 xv1 = (f < cols4) ? xrow[f] : zero;
-                        v[k] = xv1 * xv1;
-                    }
-                }
-#pragma unroll
-                for (int k = 0; k < SL4; ++k) ss = fold4(ss, v[k]);
-                ++j;
+                for (int k = 0; k < SL4; ++k) acc = fold4(acc, seg[k]);
             }
+            ss = read_lane(acc, L);
+            ++j;
         }
     }
 
@@ -477,94 +402,59 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
         wv[c] = (f < cols4) ? ld_cached(w4 + f) : zero;
     }
 
-    // cpu_fused.rs:181-182 with IEEE sqrt and division.
-    float inv_lane = 0.0f;
-    if (lane < nrows) {
-        float rms = sqrtf(ss / (float)args.cols + args.eps);
-        inv_lane = 1.0f / rms;
-    }
-    float inv[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) inv[r] = read_lane(inv_lane, r);
+    // cpu_fused.rs:181-182 with IEEE sqrt and division (ss is uniform).
+    const float inv = 1.0f / sqrtf(ss / (float)args.cols + args.eps);
 
     if (Out == NormOut::F32) {
+        f32x4* yr = reinterpret_cast<f32x4*>(args.y) + row * cols4;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (r < nrows) {
-                f32x4* yr = reinterpret_cast<f32x4*>(args.y) + (row0 + r) * cols4;
-#pragma unroll
-                for (int c = 0; c < NCH; ++c) {
-                    const uint32_t f = (uint32_t)c * kWave + lane;
-                    if (f < cols4) st_stream(yr + f, (xv[r][c] * inv[r]) * wv[c]);
-                }
-            }
+        for (int c = 0; c < NCH; ++c) {
+            const uint32_t f = (uint32_t)c * kWave + lane;
+            if (f < cols4) st_stream(yr + f, (xv[c] * inv) * wv[c]);
         }
     } else if (Out == NormOut::SiluGate) {
         // cpu_fused.rs:466-471: x_hat = (x*inv)*g; y = x_hat * silu(z).
+        const f32x4* zr = reinterpret_cast<const f32x4*>(args.z) + row * cols4;
+        f32x4* yr = reinterpret_cast<f32x4*>(args.y) + row * cols4;
+        f32x4 zv[NCH];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (r < nrows) {
-                const f32x4* zr = reinterpret_cast<const f32x4*>(args.z) + (row0 + r) * cols4;
-                f32x4* yr = reinterpret_cast<f32x4*>(args.y) + (row0 + r) * cols4;
-                f32x4 zv[NCH];
+        for (int c = 0; c < NCH; ++c) {
+            const uint32_t f = (uint32_t)c * kWave + lane;
+            zv[c] = (f < cols4) ? ld_stream(zr + f) : zero;
+        }
 #pragma unroll
-                for (int c = 0; c < NCH; ++c) {
-                    const uint32_t f = (uint32_t)c * kWave + lane;
-                    zv[c] = (f < cols4) ? ld_stream(zr + f) : zero;
-                }
-#pragma unroll
-                for (int c = 0; c < NCH; ++c) {
-                    const uint32_t f = (uint32_t)c * kWave + lane;
-                    if (f < cols4) {
-                        const f32x4 xh = (xv[r][c] * inv[r]) * wv[c];
-                        f32x4 g;
-                        g.x = silu_fast(zv[c].x);
-                        g.y = silu_fast(zv[c].y);
-                        g.z = silu_fast(zv[c].z);
-                        g.w = silu_fast(zv[c].w);
-                        st_stream(yr + f, xh * g);
-                    }
-                }
+        for (int c = 0; c < NCH; ++c) {
+            const uint32_t f = (uint32_t)c * kWave + lane;
+            if (f < cols4) {
+                const f32x4 xh = (xv[c] * inv) * wv[c];
+                f32x4 g;
+                g.x = silu_fast(zv[c].x);
+                g.y = silu_fast(zv[c].y);
+                g.z = silu_fast(zv[c].z);
+                g.w = silu_fast(zv[c].w);
+                st_stream(yr + f, xh * g);
             }
         }
     } else {
-        float amax[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) amax[r] = 0.0f;
+        float amax = 0.0f;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                f32x4 xn = (xv[r][c] * inv[r]) * wv[c];
-                xv[r][c] = xn;
-                amax[r] = abs_max4(amax[r], xn);
-            }
+            f32x4 xn = (xv[c] * inv) * wv[c];
+            xv[c] = xn;
+            amax = abs_max4(amax, xn);
         }
-        float rcp[R];
+        amax = wave_max(amax);
+        amax = amax < 1e-8f ? 1.0f : amax;  // kore-btes/src/quantize.rs:10
+        const float rcp = 1.0f / amax;
+        if (lane == 0) args.scale[row] = amax / 127.0f;
+        uint32_t* qr = reinterpret_cast<uint32_t*>(args.q) + row * cols4;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float m = wave_max(amax[r]);
-            m = m < 1e-8f ? 1.0f : m;  // kore-btes/src/quantize.rs:10
-            amax[r] = m;
-            rcp[r] = 1.0f / m;
-        }
-        float my_amax = amax[0];
-#pragma unroll
-        for (int r = 1; r < R; ++r) my_amax = lane == r ? amax[r] : my_amax;
-        if (lane < nrows) args.scale[row0 + lane] = my_amax / 127.0f;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (r < nrows) {
-                uint32_t* qr = reinterpret_cast<uint32_t*>(args.q) + (row0 + r) * cols4;
-#pragma unroll
-                for (int c = 0; c < NCH; ++c) {
-                    const uint32_t f = (uint32_t)c * kWave + lane;
-                    if (f < cols4) {
-                        const f32x4 v = xv[r][c];
-                        qr[f] = pack4(quant_code(v.x, amax[r], rcp[r]), quant_code(v.y, amax[r], rcp[r]),
-                                      quant_code(v.z, amax[r], rcp[r]), quant_code(v.w, amax[r], rcp[r]));
-                    }
-                }
+        for (int c = 0; c < NCH; ++c) {
+            const uint32_t f = (uint32_t)c * kWave + lane;
+            if (f < cols4) {
+                const f32x4 v = xv[c];
+                qr[f] = pack4(quant_code(v.x, amax, rcp), quant_code(v.y, amax, rcp), quant_code(v.z, amax, rcp),
+                              quant_code(v.w, amax, rcp));
             }
         }
     }
@@ -604,28 +494,27 @@ __global__ __launch_bounds__(64) void row_norm_scalar_kernel(NormArgs args) {
     }
 }
 
-template <NormOut Out, int SL4, int R>
+template <NormOut Out, int SL4>
 static int launch_vec(NormArgs a, hipStream_t s) {
-    const size_t lds = (size_t)kWavesPerBlock * wave_lds_f4(SL4, R) * sizeof(f32x4);
-    const uint64_t rows_per_block = (uint64_t)kWavesPerBlock * R;
-    const uint64_t blocks = (a.rows + rows_per_block - 1) / rows_per_block;
+    const size_t lds = (size_t)kWavesPerBlock * wave_lds_f4(SL4) * sizeof(f32x4);
+    const uint64_t blocks = (a.rows + kWavesPerBlock - 1) / kWavesPerBlock;
     if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
-    hipLaunchKernelGGL((row_norm_kernel<Out, SL4, R>), dim3((uint32_t)blocks), dim3(kNormBlock), lds, s, a);
+    hipLaunchKernelGGL((row_norm_kernel<Out, SL4>), dim3((uint32_t)blocks), dim3(kNormBlock), lds, s, a);
     return launch_status();
 }
 
 template <NormOut Out>
 static int launch_sl4(NormArgs a, uint32_t nch, hipStream_t s) {
-    if (nch <= 1) return launch_vec<Out, 1, 1>(a, s);
-    if (nch <= 2) return launch_vec<Out, 2, 1>(a, s);
-    if (nch <= 4) return launch_vec<Out, 4, 1>(a, s);
-    if (nch <= 6) return launch_vec<Out, 6, 1>(a, s);
-    if (nch <= 8) return launch_vec<Out, 8, 1>(a, s);
-    if (nch <= 10) return launch_vec<Out, 10, 1>(a, s);
-    if (nch <= 12) return launch_vec<Out, 12, 1>(a, s);
-    if (nch <= 16) return launch_vec<Out, 16, 1>(a, s);
-    if (nch <= 24) return launch_vec<Out, 24, 1>(a, s);
-    return launch_vec<Out, 32, 1>(a, s);
+    if (nch <= 1) return launch_vec<Out, 1>(a, s);
+    if (nch <= 2) return launch_vec<Out, 2>(a, s);
+    if (nch <= 4) return launch_vec<Out, 4>(a, s);
+    if (nch <= 6) return launch_vec<Out, 6>(a, s);
+    if (nch <= 8) return launch_vec<Out, 8>(a, s);
+    if (nch <= 10) return launch_vec<Out, 10>(a, s);
+    if (nch <= 12) return launch_vec<Out, 12>(a, s);
+    if (nch <= 16) return launch_vec<Out, 16>(a, s);
+    if (nch <= 24) return launch_vec<Out, 24>(a, s);
+    return launch_vec<Out, 32>(a, s);
 }
 
 // One row per wave: with the half-row tile a wave needs ~8 KB of LDS and
