@@ -43,10 +43,13 @@
 //   * runs of segments in one binade are composed by a segmented DPP scan, so
 //     each lane holds its segment's run entry (d_0, d_1, window, next
 //     segment) and its squares in registers;
-//   * the resolve is wave-uniform: it reads entry j from lane 63 - j with
+//   * the resolve runs on the scalar unit in integers: inside one binade the
+//     float bits are linear in the value, so a run's exact increment is an
+//     integer added to the bits of the running sum, and the binade window
+//     checks are unsigned compares.  It reads entry j from lane 63 - j with
 //     v_readlane, jumps whole runs, and when a segment falls back the owning
-//     lane folds its own registers and broadcasts the sum.  No LDS, no
-//     re-read of global memory.
+//     lane's fold of its own registers is broadcast.  No LDS, no re-read of
+//     global memory.
 // A wave's LDS traffic never crosses waves, so there are no barriers: LDS
 // operations from one wave complete in issue order.
 
@@ -88,13 +91,14 @@ struct NormArgs {
     float eps;
 };
 
-// Odd pitch (in float4) of the transpose tile: 64 lanes reading 16 B at
-// segment starts j*pitch hit 16 distinct 16-byte bank groups per 16 lanes.
-__host__ __device__ constexpr uint32_t tile_pitch4(uint32_t sl4) { return sl4 + ((sl4 & 1u) ? 2u : 1u); }
-
-// Per-wave LDS: the half-row transpose tile (32 segments).
-constexpr int kHalfSegs = kSegs / 2;
-__host__ __device__ constexpr uint32_t wave_lds_f4(uint32_t sl4) { return kHalfSegs * tile_pitch4(sl4); }
+// Transpose tile geometry.  Segment j (SL4 consecutive float4 of the row)
+// starts at float4 j*P of the tile, with an odd pitch P: 16 lanes reading
+// float4 k of 16 consecutive segments then hit 16 distinct 16-byte bank
+// groups.  For even SL4 the tile holds half a row (32 segments = SL4/2 whole
+// load chunks) and is filled in two passes; SL4 = 1 takes one pass.
+__host__ __device__ constexpr int seg_pitch4(int sl4) { return (sl4 & 1) ? sl4 : sl4 + 1; }
+__host__ __device__ constexpr int tile_segs(int sl4) { return (sl4 & 1) ? kSegs : kSegs / 2; }
+__host__ __device__ constexpr uint32_t wave_lds_f4(int sl4) { return (uint32_t)(tile_segs(sl4) * seg_pitch4(sl4)); }
 
 __device__ __forceinline__ int32_t cvt_i32_sat(float v) {
     // v_cvt_i32_f32: round toward zero, saturating, NaN -> 0.  Written as asm
@@ -248,21 +252,68 @@ __device__ __forceinline__ float silu_fast(float z) {
     return z * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-template <NormOut Out, int SL4>
+// Inclusive wave64 max-scan in DPP (row_shr 1/2/4/8, then row_bcast 15/31);
+// lane 63 ends with the wave's max.  Lanes without a DPP source read 0, the
+// identity for the non-negative values it is used on; fmaxf drops NaN like
+// Rust's f32::max.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    v = fmaxf(v, dpp0<0x111, 0xf>(v));
+    v = fmaxf(v, dpp0<0x112, 0xf>(v));
+    v = fmaxf(v, dpp0<0x114, 0xf>(v));
+    v = fmaxf(v, dpp0<0x118, 0xf>(v));
+    v = fmaxf(v, dpp0<0x142, 0xa>(v));
+    v = fmaxf(v, dpp0<0x143, 0xc>(v));
+    return read_lane(v, kWave - 1);
+}
+
+// Integer form of a run entry for the scalar resolve.  Inside the binade
+// [bot, top) of grid g the float bits are linear in the value
+// (bits(bot + n*g) = bits(bot) + n, also for the merged [0, 2^-125) range
+// of grid 2^-149), so adding an exact increment d is adding d/g to the bits.
+// d/g = bits(bot + d) - bits(bot) when bot + d < top; otherwise (or for a
+// NaN d) no start in the binade can take the jump and the entry is
+// 0x7fffffff, which fails the resolve's window check.
+__device__ __forceinline__ uint32_t run_inc(float bot, float top, float d) {
+    const float e = bot + d;
+    return (e < top) ? __float_as_uint(e) - __float_as_uint(bot) : 0x7fffffffu;
+}
+
+// Run entry of the segment held by lane L, read into scalar registers.
+struct RunEntry {
+    uint32_t i0, i1, lo, wd;
+    int next;
+};
+__device__ __forceinline__ RunEntry read_entry(uint32_t inc0, uint32_t inc1, uint32_t lo, uint32_t wd,
+                                               uint32_t next, int L) {
+    RunEntry e;
+    e.i0 = (uint32_t)__builtin_amdgcn_readlane((int)inc0, L);
+    e.i1 = (uint32_t)__builtin_amdgcn_readlane((int)inc1, L);
+    e.lo = (uint32_t)__builtin_amdgcn_readlane((int)lo, L);
+    e.wd = (uint32_t)__builtin_amdgcn_readlane((int)wd, L);
+    e.next = __builtin_amdgcn_readlane((int)next, L);
+    return e;
+}
+
+// FULL: cols == 256*SL4 exactly (every chunk and segment complete, no bounds
+// checks).  Otherwise rows are ragged: loads past the end read 0, segments
+// past the end are empty.
+template <NormOut Out, int SL4, bool FULL>
 __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
     constexpr int NCH = SL4;  // 64*SL4 float4 cover the row: SL4 wave-wide chunks
-    constexpr int TP4 = (int)tile_pitch4(SL4);
+    constexpr int P = seg_pitch4(SL4);
+    constexpr int TS = tile_segs(SL4);
+    constexpr int NPASS = kSegs / TS;
+    constexpr int CPP = NCH / NPASS;  // load chunks per tile pass
     constexpr uint32_t kWaveF4 = wave_lds_f4(SL4);
     extern __shared__ f32x4 lds4[];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const uint64_t row = (uint64_t)blockIdx.x * kWavesPerBlock + wave;
     if (row >= args.rows) return;  // uniform per wave; no block barrier follows
-    const uint32_t cols4 = args.cols >> 2;
-    const int nseg = (int)((cols4 + SL4 - 1) / SL4);
+    const uint32_t cols4 = FULL ? (uint32_t)(kWave * SL4) : (args.cols >> 2);
+    const int nseg = FULL ? kSegs : (int)((cols4 + SL4 - 1) / SL4);
     f32x4* tile = lds4 + (size_t)wave * kWaveF4;
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    const float inf = __builtin_inff();
     const float qnan = __builtin_nanf("");
 
     // ---- HBM reads: coalesced, chunk-major, all in flight.
@@ -271,7 +322,7 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const uint32_t f = (uint32_t)c * kWave + lane;
-        xv[c] = (f < cols4) ? ld_stream(xr + f) : zero;
+        xv[c] = (FULL || f < cols4) ? ld_stream(xr + f) : zero;
     }
 
     // Lane L holds segment j = 63 - L, so a forward (lane-increasing) scan
@@ -279,28 +330,29 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
     const int seg_id = kSegs - 1 - lane;
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
-    // ---- transpose the squares through the wave's tile.  The tile holds
-    // half a row (32 segments): pass h moves segments [32h, 32h + 32), which
-    // lanes 63 - seg read back.
+    // ---- transpose the squares through the wave's tile: float4 f of the row
+    // (segment q = f / SL4, offset f % SL4) goes to q*P + f % SL4 = f + (P -
+    // SL4)*q, minus the pass's base; segment reads use constant offsets.
     f32x4 seg[SL4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        wave_lds_sync();  // previous tile reads precede these writes
+    for (int h = 0; h < NPASS; ++h) {
+        if (h) wave_lds_sync();  // previous tile reads precede these writes
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const int f = c * kWave + lane;  // float4 index in the row
-            const int sg = f / SL4 - h * kHalfSegs;
-            if (sg >= 0 && sg < kHalfSegs) tile[sg * TP4 + (f % SL4)] = xv[c] * xv[c];  // zero past the end
+        for (int cc = 0; cc < CPP; ++cc) {
+            const int c = h * CPP + cc;
+            const int f = c * kWave + lane;
+            const int q = f / SL4;
+            tile[f + (P - SL4) * q - h * TS * P] = xv[c] * xv[c];  // zero past the end
         }
         wave_lds_sync();
-        const int my = seg_id - h * kHalfSegs;
-        if (my >= 0 && my < kHalfSegs) {
+        const int my = seg_id - h * TS;
+        if (NPASS == 1 || (my >= 0 && my < TS)) {
 #pragma unroll
-            for (int k = 0; k < SL4; ++k) seg[k] = tile[my * TP4 + k];
+            for (int k = 0; k < SL4; ++k) seg[k] = tile[my * P + k];
         }
     }
 
-    const bool empty = seg_id >= nseg;
+    const bool empty = !FULL && seg_id >= nseg;
     float ssum = 0.0f;
 #pragma unroll
     for (int k = 0; k < SL4; ++k) ssum += sum4(seg[k]);
@@ -324,8 +376,6 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
     float top = __uint_as_float((ef + 1u) << 23);  // ef + 1 == 255 -> +Inf
     sig0 = first ? 0.0f : sig0;
     sig1 = first ? 0.0f : sig1;
-    bot = first ? 0.0f : (bad ? inf : bot);
-    top = first ? inf : (bad ? 0.0f : top);
     float w0 = sig0, w1 = sig1;
 #pragma unroll
     for (int k = 0; k < SL4; ++k) {
@@ -335,14 +385,14 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
         w0 = w0 + a.z; w1 = w1 + a.z;
         w0 = w0 + a.w; w1 = w1 + a.w;
     }
-    const bool ok0 = w0 < top;
-    const bool ok1 = first ? ok0 : (w1 < top);
+    const bool ok0 = first || w0 < top;
+    const bool ok1 = first || w1 < top;
     // A segment whose estimated span touches a binade edge (within 2^-10;
     // the estimate's own error is below cols * 2^-24 relative) will most
     // likely cross it: keep it out of runs so that it is folded alone
     // instead of breaking a jump.
     const bool edge = !first && (est < bot * 1.0009765625f || est + ssum >= top * 0.9990234375f);
-    const bool valid = ok0 && ok1 && !edge;
+    const bool valid = ok0 && ok1 && !edge && !bad;
     // Scan element of this single segment.
     RunElem el;
     el.d0 = ok0 ? w0 - sig0 : qnan;
@@ -363,34 +413,48 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
     // The run of lane L ends at the highest lane <= L with its bit set; the
     // segment after it is 64 - that lane.
     const uint64_t below = ends & (lt_mask | (1ull << lane));
-    const int next_seg = kSegs - (63 - __builtin_clzll(below));
+    const uint32_t next_seg = (uint32_t)(kSegs - (63 - __builtin_clzll(below)));
+    // Integer run entry: bit increments for entry parity 0/1, the binade
+    // window as lo = bits(bot) and width = bits(top) - lo (0 = never jump:
+    // Inf/NaN estimate), and the segment after the run.
+    const uint32_t inc0 = run_inc(bot, top, el.d0);
+    const uint32_t inc1 = run_inc(bot, top, el.d1);
+    const uint32_t lo_v = bad ? 0u : __float_as_uint(bot);
+    const uint32_t wd_v = bad ? 0u : __float_as_uint(top) - __float_as_uint(bot);
 
-    // ---- resolve, wave-uniform: segment j's run entry lives in lane 63 - j
-    // and is read with v_readlane; a jump adds the run's exact increment when
-    // the running sum stays inside its binade window, else the owner lane
-    // folds its own segment in order and broadcasts the sum.  No LDS.
-    float ss = 0.0f;
-    int j = 0;
+    // ---- resolve on the scalar unit.  s holds the bits of the exact running
+    // sum (non-negative, so unsigned order is float order and NaN/Inf sort
+    // above every window).  Segment 0 was folded from +0 and is exact.  For
+    // segment j the run entry lives in lane 63 - j: when s lies in the run's
+    // binade [lo, lo + width) and the jump lands inside it too, s moves by
+    // the entry for its parity (the lsb of s's bits is its parity on the
+    // binade grid); otherwise the owner lane folds segment j alone from s
+    // and broadcasts the sum.  With t = s + inc >= s, both window tests are
+    // max(s - lo, t - lo) < width in wrapping unsigned arithmetic (s < lo
+    // wraps to a huge value).  A step is five lane reads and about ten
+    // scalar instructions.
+    uint32_t s = __builtin_amdgcn_readlane(__float_as_uint(w0), kWave - 1);
+    int j = 1;
     while (j < nseg) {
         const int L = kSegs - 1 - j;
-        const float d0 = read_lane(el.d0, L), d1 = read_lane(el.d1, L);
-        const float b = read_lane(bot, L), t = read_lane(top, L);
-        const int nj = __builtin_amdgcn_readlane(next_seg, L);
-        const float d = (__float_as_uint(ss) & 1u) ? d1 : d0;
-        const float st = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ss + d)));
-        if (ss >= b && st < t) {
-            ss = st;
-            j = nj;
+        const RunEntry cur = read_entry(inc0, inc1, lo_v, wd_v, next_seg, L);
+        const uint32_t t = s + ((s & 1u) ? cur.i1 : cur.i0);
+        const uint32_t a = s - cur.lo, b = t - cur.lo;
+        if ((a > b ? a : b) < cur.wd) {
+            s = t;
+            j = cur.next;
         } else {
-            float acc = ss;
-            if (lane == L) {
+            // Every lane folds its own segment from s (same cost as one lane
+            // under an exec mask, without the mask changes); lane L's sum is
+            // the one kept.
+            float acc = __uint_as_float(s);
 #pragma unroll
-                for (int k = 0; k < SL4; ++k) acc = fold4(acc, seg[k]);
-            }
-            ss = read_lane(acc, L);
+            for (int k = 0; k < SL4; ++k) acc = fold4(acc, seg[k]);
+            s = (uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(acc), L);
             ++j;
         }
     }
+    const float ss = __uint_as_float(s);
 
     // Weights for the epilogue (L2 hits), loaded after the resolve so their
     // registers are free while it runs.
@@ -399,7 +463,7 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const uint32_t f = (uint32_t)c * kWave + lane;
-        wv[c] = (f < cols4) ? ld_cached(w4 + f) : zero;
+        wv[c] = (FULL || f < cols4) ? ld_cached(w4 + f) : zero;
     }
 
     // cpu_fused.rs:181-182 with IEEE sqrt and division (ss is uniform).
@@ -410,7 +474,7 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             const uint32_t f = (uint32_t)c * kWave + lane;
-            if (f < cols4) st_stream(yr + f, (xv[c] * inv) * wv[c]);
+            if (FULL || f < cols4) st_stream(yr + f, (xv[c] * inv) * wv[c]);
         }
     } else if (Out == NormOut::SiluGate) {
         // cpu_fused.rs:466-471: x_hat = (x*inv)*g; y = x_hat * silu(z).
@@ -420,12 +484,12 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             const uint32_t f = (uint32_t)c * kWave + lane;
-            zv[c] = (f < cols4) ? ld_stream(zr + f) : zero;
+            zv[c] = (FULL || f < cols4) ? ld_stream(zr + f) : zero;
         }
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             const uint32_t f = (uint32_t)c * kWave + lane;
-            if (f < cols4) {
+            if (FULL || f < cols4) {
                 const f32x4 xh = (xv[c] * inv) * wv[c];
                 f32x4 g;
                 g.x = silu_fast(zv[c].x);
@@ -443,7 +507,7 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
             xv[c] = xn;
             amax = abs_max4(amax, xn);
         }
-        amax = wave_max(amax);
+        amax = wave_max_nonneg(amax);
         amax = amax < 1e-8f ? 1.0f : amax;  // kore-btes/src/quantize.rs:10
         const float rcp = 1.0f / amax;
         if (lane == 0) args.scale[row] = amax / 127.0f;
@@ -451,7 +515,7 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             const uint32_t f = (uint32_t)c * kWave + lane;
-            if (f < cols4) {
+            if (FULL || f < cols4) {
                 const f32x4 v = xv[c];
                 qr[f] = pack4(quant_code(v.x, amax, rcp), quant_code(v.y, amax, rcp), quant_code(v.z, amax, rcp),
                               quant_code(v.w, amax, rcp));
@@ -499,7 +563,10 @@ static int launch_vec(NormArgs a, hipStream_t s) {
     const size_t lds = (size_t)kWavesPerBlock * wave_lds_f4(SL4) * sizeof(f32x4);
     const uint64_t blocks = (a.rows + kWavesPerBlock - 1) / kWavesPerBlock;
     if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
-    hipLaunchKernelGGL((row_norm_kernel<Out, SL4>), dim3((uint32_t)blocks), dim3(kNormBlock), lds, s, a);
+    if (a.cols == (uint32_t)(4 * kWave * SL4))
+        hipLaunchKernelGGL((row_norm_kernel<Out, SL4, true>), dim3((uint32_t)blocks), dim3(kNormBlock), lds, s, a);
+    else
+        hipLaunchKernelGGL((row_norm_kernel<Out, SL4, false>), dim3((uint32_t)blocks), dim3(kNormBlock), lds, s, a);
     return launch_status();
 }
 

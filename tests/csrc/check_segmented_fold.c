@@ -164,19 +164,32 @@ static float kernel_fold(const float *a, int n, long *fallbacks) {
     return s;
 }
 
+static long rfb = 0;
+
 /* Run-jumping resolve (row_norm_kernel's current form): consecutive valid
  * segments that share a binade form a run; for every segment j the exact
  * increment of [j, run end] is composed from the per-segment increments and
- * end parities (F_j(p) = lsb(w_p)), and the resolve jumps a whole span when
- * s >= 2^E and s + D < 2^(E+1); otherwise it folds segment j alone. */
+ * end parities (F_j(p) = lsb(w_p)).  The resolve runs on integers: inside a
+ * binade [bot, top) of grid g the float bits are linear in the value, so a
+ * run's increment D is stored as D/g = bits(bot + D) - bits(bot) (or
+ * 0x7fffffff when bot + D >= top), and a jump is taken when the bits s of the
+ * running sum satisfy max(s - lo, s + inc - lo) < width in wrapping unsigned
+ * arithmetic (lo = bits(bot), width = bits(top) - lo; both s and s + inc in
+ * [bot, top)); otherwise segment j is folded alone from s.  Segment 0 is folded from +0 exactly. */
+static uint32_t run_inc(float bot, float top, float d) {
+    float e = bot + d;
+    return (e < top) ? f2u(e) - f2u(bot) : 0x7fffffffu;
+}
+
 static float run_fold(const float *a, int n, long *steps) {
     const int n4 = n / 4;
     const int sl4 = (n4 + 63) / 64 ? (n4 + 63) / 64 : 1;
     const int nseg = (n4 + sl4 - 1) / sl4;
     const int sl = 4 * sl4;
-    float d0[64], d1[64], bot[64], top[64], ssum[64], est[64];
+    float d0[64], d1[64], bot[64], top[64], ssum[64], est[64], w0s[64];
     int f0[64], f1[64], key[64], valid[64];
-    const float inf = INFINITY, qnan = NAN;
+    uint32_t efs[64];
+    const float qnan = NAN;
     float total = 0.0f;
     for (int j = 0; j < 64; ++j) {
         ssum[j] = 0.0f;
@@ -185,25 +198,26 @@ static float run_fold(const float *a, int n, long *steps) {
     for (int j = 0; j < 64; ++j) { est[j] = total; total += ssum[j]; }
     for (int j = 0; j < 64; ++j) {
         float sig0, sig1;
-        if (j >= nseg) { d0[j] = d1[j] = 0; bot[j] = 0; top[j] = inf; f0[j] = 0; f1[j] = 1; key[j] = 1024; valid[j] = 1; continue; }
-        if (j == 0) { sig0 = 0; sig1 = 0; bot[j] = 0; top[j] = inf; key[j] = 1025; }
-        else {
-            uint32_t ef = f2u(est[j]) >> 23;
-            key[j] = (int)ef;
-            if (ef >= 255u) { sig0 = 0; sig1 = 0; bot[j] = inf; top[j] = 0; }
-            else if (ef <= 1u) { sig0 = 0; sig1 = u2f(1u); bot[j] = 0; top[j] = u2f(2u << 23); key[j] = 1; }
-            else { sig0 = u2f(ef << 23); sig1 = u2f((ef << 23) | 1u); bot[j] = sig0; top[j] = u2f((ef + 1u) << 23); }
-        }
+        if (j >= nseg) { d0[j] = d1[j] = 0; bot[j] = 0; top[j] = INFINITY; f0[j] = 0; f1[j] = 1; key[j] = 1024; valid[j] = 1; efs[j] = 0; continue; }
+        uint32_t ef = f2u(est[j]) >> 23;
+        if (ef < 1u) ef = 1u;
+        int bad = j != 0 && ef >= 255u;
+        efs[j] = bad ? 0u : ef;
+        if (ef == 1u) { sig0 = 0; sig1 = u2f(1u); } else { sig0 = u2f(ef << 23); sig1 = u2f((ef << 23) | 1u); }
+        bot[j] = sig0;
+        top[j] = u2f((ef + 1u) << 23);
+        if (j == 0) { sig0 = 0; sig1 = 0; key[j] = 1025; } else key[j] = (int)ef;
         float w0 = sig0, w1 = sig1;
         for (int i = j * sl; i < j * sl + sl; ++i) { float v = i < n ? a[i] : 0.0f; w0 = w0 + v; w1 = w1 + v; }
-        int ok0 = w0 < top[j], ok1 = (j == 0) ? ok0 : (w1 < top[j]);
+        w0s[j] = w0;
+        int ok0 = j == 0 || w0 < top[j], ok1 = j == 0 || w1 < top[j];
         int edge = j != 0 && (est[j] < bot[j] * 1.0009765625f || est[j] + ssum[j] >= top[j] * 0.9990234375f);
-        valid[j] = ok0 && ok1 && !edge;
+        valid[j] = ok0 && ok1 && !edge && !bad;
         d0[j] = ok0 ? w0 - sig0 : qnan;
         d1[j] = (j == 0) ? d0[j] : (ok1 ? w1 - sig1 : qnan);
         f0[j] = (int)(f2u(w0) & 1u);
         f1[j] = (j == 0) ? 0 : (int)(f2u(w1) & 1u);
-        if (!valid[j]) key[j] = 2048 + j;
+        if (!valid[j] && j != 0) key[j] = 2048 + j;
     }
     /* suffix composition within runs, built from the run end backwards */
     float D0[64], D1[64];
@@ -220,16 +234,24 @@ static float run_fold(const float *a, int n, long *steps) {
             next[j] = next[j + 1];
         }
     }
-    float s = 0.0f;
-    int j = 0;
+    uint32_t s = f2u(w0s[0]);
+    int j = 1;
     while (j < nseg) {
         ++*steps;
-        float d = (f2u(s) & 1u) ? D1[j] : D0[j];
-        float t = s + d;
-        if (s >= bot[j] && t < top[j]) { s = t; j = next[j]; }
-        else { for (int i = j * sl; i < j * sl + sl; ++i) s = s + (i < n ? a[i] : 0.0f); ++j; }
+        uint32_t i0 = run_inc(bot[j], top[j], D0[j]), i1 = run_inc(bot[j], top[j], D1[j]);
+        uint32_t lo = efs[j] ? f2u(bot[j]) : 0u, wd = efs[j] ? f2u(top[j]) - f2u(bot[j]) : 0u;
+        uint32_t t = s + ((s & 1u) ? i1 : i0);
+        uint32_t da = s - lo, db = t - lo;
+        if ((da > db ? da : db) < wd) { s = t; j = next[j]; }
+        else {
+            ++rfb;
+            float acc = u2f(s);
+            for (int i = j * sl; i < j * sl + sl; ++i) acc = acc + (i < n ? a[i] : 0.0f);
+            s = f2u(acc);
+            ++j;
+        }
     }
-    return s;
+    return u2f(s);
 }
 
 static uint64_t rs = 88172645463325252ull;
@@ -299,6 +321,6 @@ int main(int argc, char **argv) {
     }
     printf("ok: %ld rows, fallback segments %ld of %ld; kernel mirror: %ld rows, %.2f fallbacks/row\n", rows, fb,
            total_segs, krows, krows ? (double)kfb / krows : 0.0);
-    printf("run-jumping resolve: %.2f steps/row\n", krows ? (double)rsteps / krows : 0.0);
+    printf("run-jumping resolve: %.2f steps/row, %.2f fallbacks/row\n", krows ? (double)rsteps / krows : 0.0, krows ? (double)rfb / krows : 0.0);
     return 0;
 }
