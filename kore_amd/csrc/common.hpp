@@ -44,6 +44,24 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Wave64 sum through DPP (row_shr 1/2/4/8 within each row of 16 lanes, then
+// row_bcast 15/31 carry the row totals forward; lane 63 ends with the total,
+// which is read into every lane).  Lanes without a DPP source contribute 0.
+// A fixed-shape tree: the same inputs give the same bits on every call.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_zero_src(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, kRowMask, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_zero_src<0x111, 0xf>(v);  // row_shr:1
+    v += dpp_zero_src<0x112, 0xf>(v);  // row_shr:2
+    v += dpp_zero_src<0x114, 0xf>(v);  // row_shr:4
+    v += dpp_zero_src<0x118, 0xf>(v);  // row_shr:8
+    v += dpp_zero_src<0x142, 0xa>(v);  // row_bcast:15 -> rows 1, 3
+    v += dpp_zero_src<0x143, 0xc>(v);  // row_bcast:31 -> rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), kWave - 1));
+}
+
 // Read lane `src`'s value of v into every lane (v_readlane -> SGPR).
 __device__ __forceinline__ float read_lane(float v, int src) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));

@@ -278,7 +278,8 @@ __device__ __forceinline__ uint32_t run_inc(float bot, float top, float d) {
     return (e < top) ? __float_as_uint(e) - __float_as_uint(bot) : 0x7fffffffu;
 }
 
-// Run entry of the segment held by lane L, read into scalar registers.
+// Run entry of the segment held by lane L, read into scalar registers.  Lane
+// indices are taken modulo 64, so the read past the last segment is harmless.
 struct RunEntry {
     uint32_t i0, i1, lo, wd;
     int next;
@@ -415,12 +416,14 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
     const uint64_t below = ends & (lt_mask | (1ull << lane));
     const uint32_t next_seg = (uint32_t)(kSegs - (63 - __builtin_clzll(below)));
     // Integer run entry: bit increments for entry parity 0/1, the binade
-    // window as lo = bits(bot) and width = bits(top) - lo (0 = never jump:
-    // Inf/NaN estimate), and the segment after the run.
+    // window as lo = bits(bot) and width = bits(top) - lo, and the segment
+    // after the run.  Width 0 marks a segment outside every run (a predicted
+    // binade crossing, a walk that left its binade, an Inf/NaN estimate):
+    // the resolve folds it without trying a jump.
     const uint32_t inc0 = run_inc(bot, top, el.d0);
     const uint32_t inc1 = run_inc(bot, top, el.d1);
-    const uint32_t lo_v = bad ? 0u : __float_as_uint(bot);
-    const uint32_t wd_v = bad ? 0u : __float_as_uint(top) - __float_as_uint(bot);
+    const uint32_t lo_v = __float_as_uint(bot);
+    const uint32_t wd_v = valid ? __float_as_uint(top) - __float_as_uint(bot) : 0u;
 
     // ---- resolve on the scalar unit.  s holds the bits of the exact running
     // sum (non-negative, so unsigned order is float order and NaN/Inf sort
@@ -428,31 +431,36 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
     // segment j the run entry lives in lane 63 - j: when s lies in the run's
     // binade [lo, lo + width) and the jump lands inside it too, s moves by
     // the entry for its parity (the lsb of s's bits is its parity on the
-    // binade grid); otherwise the owner lane folds segment j alone from s
-    // and broadcasts the sum.  With t = s + inc >= s, both window tests are
+    // binade grid); otherwise (or for a width-0 entry) the owner lane folds
+    // segment j alone from s and broadcasts the sum.  With t = s + inc >= s, both window tests are
     // max(s - lo, t - lo) < width in wrapping unsigned arithmetic (s < lo
     // wraps to a huge value).  A step is five lane reads and about ten
     // scalar instructions.
     uint32_t s = __builtin_amdgcn_readlane(__float_as_uint(w0), kWave - 1);
     int j = 1;
+    RunEntry cur = read_entry(inc0, inc1, lo_v, wd_v, next_seg, kSegs - 2);
     while (j < nseg) {
         const int L = kSegs - 1 - j;
-        const RunEntry cur = read_entry(inc0, inc1, lo_v, wd_v, next_seg, L);
-        const uint32_t t = s + ((s & 1u) ? cur.i1 : cur.i0);
-        const uint32_t a = s - cur.lo, b = t - cur.lo;
-        if ((a > b ? a : b) < cur.wd) {
-            s = t;
-            j = cur.next;
-        } else {
-            // Every lane folds its own segment from s (same cost as one lane
-            // under an exec mask, without the mask changes); lane L's sum is
-            // the one kept.
-            float acc = __uint_as_float(s);
-#pragma unroll
-            for (int k = 0; k < SL4; ++k) acc = fold4(acc, seg[k]);
-            s = (uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(acc), L);
-            ++j;
+        if (cur.wd != 0u) {
+            const uint32_t t = s + ((s & 1u) ? cur.i1 : cur.i0);
+            const uint32_t a = s - cur.lo, b = t - cur.lo;
+            if ((a > b ? a : b) < cur.wd) {
+                s = t;
+                j = cur.next;
+                cur = read_entry(inc0, inc1, lo_v, wd_v, next_seg, (kSegs - 1 - j) & (kWave - 1));
+                continue;
+            }
         }
+        // Fold segment j alone.  The entry of segment j + 1 is read first so
+        // that its latency hides under the fold chain.  Every lane folds its
+        // own segment from s (same cost as one lane under an exec mask,
+        // without the mask changes); lane L's sum is the one kept.
+        cur = read_entry(inc0, inc1, lo_v, wd_v, next_seg, (L - 1) & (kWave - 1));
+        float acc = __uint_as_float(s);
+#pragma unroll
+        for (int k = 0; k < SL4; ++k) acc = fold4(acc, seg[k]);
+        s = (uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(acc), L);
+        ++j;
     }
     const float ss = __uint_as_float(s);
 

@@ -18,13 +18,13 @@
 // Vector path (cols % 4 == 0, 16-byte aligned, cols <= 4096):
 //   1. rms_bwd_rows_kernel: a row is split over S = 1, 2 or 4 waves (at
 //      most 4 float4 columns per wave and operand); a workgroup of 4 waves
-//      runs up to 16 row iterations; each wave's dgamma partial stays in
-//      registers (gamma is re-read from cache per row); the row slots'
-//      partials are added in a fixed order through LDS and written as
-//      workspace row p = the block index.
+//      runs up to 16 row iterations with the next row's loads in flight;
+//      gamma is staged in LDS; each wave's dgamma partial stays in
+//      registers; the row slots' partials are added in a fixed order through
+//      LDS and written as workspace row p = the block index.
 //   2. rms_bwd_reduce_kernel: 8 float4 columns x 64 row slots per block;
-//      every slot adds its partial rows in order, then the slots are added
-//      in order -> dgamma (deterministic).
+//      every slot adds its partial rows in order (16 loads in flight), then
+//      a fixed-shape tree adds the slots -> dgamma (deterministic).
 // Generic path (any shape): one workgroup per row writes dx and inv[r] to the
 // workspace; then one thread per column folds its dgamma over the rows in
 // the reference's order.
@@ -63,9 +63,10 @@ __device__ __forceinline__ float sum4(f32x4 a) { return (a.x + a.y) + (a.z + a.w
 // row slots' partials are added in j order through LDS and written as
 // workspace row b.
 template <int NCHW, int S>
-__global__ __launch_bounds__(kBwBlock) void rms_bwd_rows_kernel(BwArgs a) {
+__global__ __launch_bounds__(kBwBlock) __attribute__((amdgpu_waves_per_eu(4))) void rms_bwd_rows_kernel(BwArgs a) {
     constexpr int kSlots = kBwWaves / S;
-    extern __shared__ f32x4 part[];  // [cols4] dgamma combine
+    extern __shared__ f32x4 part[];  // [cols4] dgamma combine, then [cols4] gamma
+    f32x4* gam = part + (a.cols >> 2);
     __shared__ float red[2][kBwWaves][2];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -81,35 +82,42 @@ __global__ __launch_bounds__(kBwBlock) void rms_bwd_rows_kernel(BwArgs a) {
     f32x4 acc[NCHW];
 #pragma unroll
     for (int k = 0; k < NCHW; ++k) acc[k] = zero;
-    for (uint32_t it = 0; it < a.rpw; ++it) {
+    // Row loads are double-buffered: iteration it + 1's x and dy are in
+    // flight while iteration it reduces, synchronises and stores.
+    f32x4 xv[NCHW], dv[NCHW];
+    auto load_row = [&](uint32_t it, f32x4* xo, f32x4* dout) {
         const uint64_t r = rbase + (uint64_t)it * rstride + j;
-        const bool live = r < a.rows;
+        const bool live = it < a.rpw && r < a.rows;
         const uint64_t rr = live ? r : 0;
         const f32x4* xr = reinterpret_cast<const f32x4*>(a.x) + rr * cols4;
         const f32x4* dr = reinterpret_cast<const f32x4*>(a.dy) + rr * cols4;
-        // gamma is re-read per row (an L1/L2 hit) instead of held in
-        // registers: the empty asm makes its base opaque so the loads stay
-        // inside the loop.
-        uint64_t gaddr = reinterpret_cast<uint64_t>(a.g);
-        asm volatile("" : "+s"(gaddr));
-        const f32x4* g4 = reinterpret_cast<const f32x4*>(gaddr);
-        f32x4 xv[NCHW], dv[NCHW];
 #pragma unroll
         for (int k = 0; k < NCHW; ++k) {
             const uint32_t f = (uint32_t)(q * NCHW + k) * kWave + lane;
-            xv[k] = (live && f < cols4) ? ld_stream(xr + f) : zero;
-            dv[k] = (live && f < cols4) ? ld_stream(dr + f) : zero;
+            xo[k] = (live && f < cols4) ? ld_stream(xr + f) : zero;
+            dout[k] = (live && f < cols4) ? ld_stream(dr + f) : zero;
         }
+    };
+    load_row(0, xv, dv);
+    // gamma lives in LDS for the whole sweep: its reads are LDS operations,
+    // so they neither hold registers nor make a wait for them also wait for
+    // the prefetched row.
+    for (uint32_t f = threadIdx.x; f < cols4; f += kBwBlock) gam[f] = reinterpret_cast<const f32x4*>(a.g)[f];
+    __syncthreads();
+    for (uint32_t it = 0; it < a.rpw; ++it) {
+        const uint64_t r = rbase + (uint64_t)it * rstride + j;
+        const bool live = r < a.rows;
+        f32x4 xn[NCHW], dn[NCHW];
+        load_row(it + 1, xn, dn);
         float ss = 0.0f, dot = 0.0f;
 #pragma unroll
         for (int k = 0; k < NCHW; ++k) {
             const uint32_t f = (uint32_t)(q * NCHW + k) * kWave + lane;
-            const f32x4 gv = f < cols4 ? ld_cached(g4 + f) : zero;
             ss += sum4(xv[k] * xv[k]);
-            dot += sum4((xv[k] * dv[k]) * gv);
+            dot += sum4((xv[k] * dv[k]) * gam[f < cols4 ? f : 0]);
         }
-        ss = wave_sum(ss);
-        dot = wave_sum(dot);
+        ss = wave_sum_dpp(ss);
+        dot = wave_sum_dpp(dot);
         if (S > 1) {
             const int par = it & 1;
             if (lane == 0) {
@@ -129,14 +137,17 @@ __global__ __launch_bounds__(kBwBlock) void rms_bwd_rows_kernel(BwArgs a) {
         const float coeff = (dot * inv) / (ss + a.eps * fcols);
         if (live) {
             f32x4* orow = reinterpret_cast<f32x4*>(a.dx) + r * cols4;
-            asm volatile("" : "+s"(gaddr));
-            const f32x4* g4b = reinterpret_cast<const f32x4*>(gaddr);
 #pragma unroll
             for (int k = 0; k < NCHW; ++k) {
                 const uint32_t f = (uint32_t)(q * NCHW + k) * kWave + lane;
-                if (f < cols4) st_stream(orow + f, (ld_cached(g4b + f) * inv) * dv[k] - coeff * xv[k]);
+                if (f < cols4) st_stream(orow + f, (gam[f] * inv) * dv[k] - coeff * xv[k]);
                 acc[k] = acc[k] + (dv[k] * xv[k]) * inv;
             }
+        }
+#pragma unroll
+        for (int k = 0; k < NCHW; ++k) {
+            xv[k] = xn[k];
+            dv[k] = dn[k];
         }
     }
     // Row slots' partials added in j order through LDS, then one partial row.
@@ -156,10 +167,13 @@ __global__ __launch_bounds__(kBwBlock) void rms_bwd_rows_kernel(BwArgs a) {
 }
 
 // dgamma = sum of the P partial rows, deterministic: block = 8 float4
-// columns x 64 row slots; thread (slot, c) adds rows slot, slot+64, ... in
-// order; the 64 slot sums are then added in slot order.
+// columns (128 contiguous bytes of a partial row) x 64 row slots; thread
+// (slot, c) adds rows slot, slot+64, ... in order, with 16 loads in flight;
+// the 64 slot sums are then added by a fixed-shape tree in LDS.  The order
+// depends only on P, so repeated calls give identical bits.
 constexpr int kRedCols = 8;
 constexpr int kRedSlots = 64;
+constexpr int kRedBatch = 16;
 __global__ __launch_bounds__(kRedCols * kRedSlots) void rms_bwd_reduce_kernel(BwArgs a) {
     __shared__ f32x4 red[kRedSlots][kRedCols];
     const uint64_t cols4 = a.cols >> 2;
@@ -167,25 +181,30 @@ __global__ __launch_bounds__(kRedCols * kRedSlots) void rms_bwd_reduce_kernel(Bw
     const int slot = threadIdx.x / kRedCols;
     const uint64_t col = (uint64_t)blockIdx.x * kRedCols + c;
     const f32x4* w4 = reinterpret_cast<const f32x4*>(a.ws);
-    f32x4 t = {0.f, 0.f, 0.f, 0.f};
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 t = zero;
     if (col < cols4) {
-        uint64_t p = slot;
-        for (; p + 3 * kRedSlots < a.partials; p += 4 * kRedSlots) {  // 4 loads in flight, added in order
-            const f32x4 v0 = w4[p * cols4 + col];
-            const f32x4 v1 = w4[(p + kRedSlots) * cols4 + col];
-            const f32x4 v2 = w4[(p + 2 * kRedSlots) * cols4 + col];
-            const f32x4 v3 = w4[(p + 3 * kRedSlots) * cols4 + col];
-            t = (((t + v0) + v1) + v2) + v3;
+        for (uint64_t p0 = slot; p0 < a.partials; p0 += kRedBatch * kRedSlots) {
+            f32x4 v[kRedBatch];
+#pragma unroll
+            for (int u = 0; u < kRedBatch; ++u) {
+                const uint64_t p = p0 + (uint64_t)u * kRedSlots;
+                v[u] = p < a.partials ? w4[p * cols4 + col] : zero;
+            }
+#pragma unroll
+            for (int u = 0; u < kRedBatch; ++u) {
+                if (p0 + (uint64_t)u * kRedSlots < a.partials) t = t + v[u];
+            }
         }
-        for (; p < a.partials; p += kRedSlots) t = t + w4[p * cols4 + col];
     }
     red[slot][c] = t;
     __syncthreads();
-    if (slot == 0 && col < cols4) {
-        f32x4 u = red[0][c];
-        for (int k = 1; k < kRedSlots; ++k) u = u + red[k][c];
-        reinterpret_cast<f32x4*>(a.dgamma)[col] = u;
+#pragma unroll
+    for (int w = kRedSlots / 2; w >= 1; w >>= 1) {
+        if (slot < w) red[slot][c] = red[slot][c] + red[slot + w][c];
+        __syncthreads();
     }
+    if (slot == 0 && col < cols4) reinterpret_cast<f32x4*>(a.dgamma)[col] = red[0][c];
 }
 
 // ---- generic path
@@ -271,7 +290,7 @@ static uint64_t bwd_ws_floats(uint64_t rows, uint64_t cols, uint64_t* partials, 
 
 template <int NCHW, int S>
 static void launch_rows(const BwArgs& a, hipStream_t s) {
-    const size_t lds = (a.cols / 4) * sizeof(f32x4);
+    const size_t lds = 2 * (a.cols / 4) * sizeof(f32x4);
     hipLaunchKernelGGL((rms_bwd_rows_kernel<NCHW, S>), dim3((uint32_t)a.partials), dim3(kBwBlock), lds, s, a);
 }
 

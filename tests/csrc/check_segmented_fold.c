@@ -175,7 +175,8 @@ static long rfb = 0;
  * 0x7fffffff when bot + D >= top), and a jump is taken when the bits s of the
  * running sum satisfy max(s - lo, s + inc - lo) < width in wrapping unsigned
  * arithmetic (lo = bits(bot), width = bits(top) - lo; both s and s + inc in
- * [bot, top)); otherwise segment j is folded alone from s.  Segment 0 is folded from +0 exactly. */
+ * [bot, top)); otherwise, or when segment j is outside every run (width 0),
+ * segment j is folded alone from s.  Segment 0 is folded from +0 exactly. */
 static uint32_t run_inc(float bot, float top, float d) {
     float e = bot + d;
     return (e < top) ? f2u(e) - f2u(bot) : 0x7fffffffu;
@@ -239,10 +240,10 @@ static float run_fold(const float *a, int n, long *steps) {
     while (j < nseg) {
         ++*steps;
         uint32_t i0 = run_inc(bot[j], top[j], D0[j]), i1 = run_inc(bot[j], top[j], D1[j]);
-        uint32_t lo = efs[j] ? f2u(bot[j]) : 0u, wd = efs[j] ? f2u(top[j]) - f2u(bot[j]) : 0u;
+        uint32_t lo = f2u(bot[j]), wd = valid[j] ? f2u(top[j]) - f2u(bot[j]) : 0u;
         uint32_t t = s + ((s & 1u) ? i1 : i0);
         uint32_t da = s - lo, db = t - lo;
-        if ((da > db ? da : db) < wd) { s = t; j = next[j]; }
+        if (wd != 0u && (da > db ? da : db) < wd) { s = t; j = next[j]; }
         else {
             ++rfb;
             float acc = u2f(s);
