@@ -221,6 +221,27 @@ int kore_hip_rms_norm_backward_f32(const float *grad_out, const float *x,
                                    uint64_t cols, float eps,
                                    kore_stream_t stream);
 
+
+/* ------------------------------------------------------ ternary (BitLinear)
+ * Weights a_packed[m, ceil(k/5)] in the reference's base-243 format (five
+ * trits per byte, least significant base-3 digit first, digit 0/1/2 =
+ * -1/0/+1, bytes 243..255 = five zeros; crates/kore-btes/src/encoder.rs:50-95,
+ * as written by pack_weights_ternary, crates/kore-kernels/src/
+ * cpu_ternary_matmul.rs:198-240), per-row scales a_scales[m].
+ *
+ * BitLinear matmul on the pre-quant codes: q[n, k] int8 (one row per token,
+ * as kore_hip_rms_norm_quant_i8 writes them) with q_scales[n]:
+ *   c[m, n] = ((float)(sum_k trit[m, k] * q[n, k]) * a_scales[m]) * q_scales[n].
+ * The reference has no single function for this step: the dot product is
+ * the integer one of ternary_ternary_matmul and the epilogue its
+ * `int_acc as f32 * a_scale * b_scale` (cpu_ternary_matmul.rs:131-193, :188),
+ * which replaces ternary_matmul (cpu_ternary_matmul.rs:29-124) fed with
+ * dequantised activations.  Exact integer sum: bit-exact.  k <= 2^24. */
+int kore_hip_ternary_matmul_i8(const uint8_t *a_packed, const float *a_scales,
+                               const int8_t *q, const float *q_scales,
+                               float *c, uint64_t m, uint64_t n, uint64_t k,
+                               kore_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

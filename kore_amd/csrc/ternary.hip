@@ -1,0 +1,270 @@
+// ternary.hip -- BitLinear matmuls on base-243 packed ternary weights.
+//
+// Weights: a_packed[M, Kp] bytes, Kp = ceil(K/5); byte b holds trits
+// t_j = digit_j(b) - 1 (base 3, least significant digit first, j < 5) for
+// columns 5*i + j; bytes 243..255 decode to zeros (crates/kore-btes/src/
+// encoder.rs:50-95).  a_scales[M] per-row scales.
+//
+// kore_hip_ternary_matmul_i8: the matmul on the pre-quant codes,
+//   c[m, n] = ((float)(sum_k t[m, k] * q[n, k]) * a_scales[m]) * q_scales[n]
+// with q[N, K] int8 (one row per token, as kore_hip_rms_norm_quant_i8 writes
+// them) and c[M, N] f32; the dot product is exact in int32 and the epilogue
+// is the reference's ternary_ternary_matmul one
+// (crates/kore-kernels/src/cpu_ternary_matmul.rs:188), so the result is
+// bit-exact.
+//
+// Roofline: MFMA int8 (v_mfma_i32_32x32x32_i8, 5.0 POP/s dense): 2*M*N*K
+// operations; the f32 output (4*M*N bytes) is the largest HBM stream.
+//
+// Vector path (K % 16 == 0, q 16-byte aligned, c 4-byte aligned; packed rows
+// are read as 16-byte vectors when Kp % 16 == 0, else byte by byte):
+//   workgroup = 4 waves, 128 (m) x 128 (n) outputs, each wave 64 x 64 as
+//   2 x 2 MFMA tiles of 32 x 32; K advances 160 columns (32 packed bytes =
+//   five 32-deep MFMA steps) per iteration.  Per iteration every thread
+//   decodes 16 packed bytes into 80 trit bytes through a 256-entry LDS table
+//   (byte -> five int8 trits) and stages 5 x 16 bytes of q; both tiles sit
+//   in LDS at a 176-byte row pitch (44 dwords: 16 lanes reading 16 bytes at
+//   consecutive rows hit 16 distinct bank groups).  The next iteration's
+//   global loads are in flight while the current one computes.
+//   MFMA operands: lane l reads row l % 32 and 16 bytes at k = 16 * (l / 32)
+//   of a 32-deep step from both tiles (the k order inside an MFMA is the
+//   same for both operands, so any assignment gives the same sum);
+//   accumulator register r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
+//   column l % 32.
+// Generic path (any shape and alignment): one thread per output, the
+// reference loop order.
+#include "common.hpp"
+#include "kore_hip_internal.hpp"
+
+namespace kore {
+
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kTmBlock = 256;
+constexpr int kTmM = 128, kTmN = 128;  // workgroup tile; each wave 64 x 64
+constexpr int kTmK = 160;          // trit columns per iteration
+constexpr int kTmKp = kTmK / 5;    // packed bytes per iteration
+constexpr int kTmPitch = 176;      // LDS row pitch in bytes
+constexpr uint32_t kZeroByte = 121;  // encodes five zero trits
+constexpr uint32_t kXcds = 8;        // MI355X: 8 XCDs, one L2 each
+constexpr uint32_t kGroupM = 8;      // m-tiles per tile group
+
+struct TernArgs {
+    const uint8_t* a;   // packed [M, Kp]
+    const float* sa;    // [M]
+    const int8_t* q;    // [N, K]
+    const float* sq;    // [N]
+    float* c;           // [M, N]
+    uint32_t m, n, k, kp;
+};
+
+// Five trits of byte b as int8 in the low 40 bits (byte j = trit j).
+__device__ __forceinline__ uint64_t trit_lut_entry(uint32_t b) {
+    if (b >= 243u) return 0;
+    uint64_t v = 0;
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        const uint32_t d = b % 3u;
+        b /= 3u;
+        v |= (uint64_t)(uint8_t)(int8_t)((int)d - 1) << (8 * j);
+    }
+    return v;
+}
+
+// kAlignedA: packed rows are 16-byte aligned (Kp % 16 == 0) and read as
+// dwordx4; otherwise byte by byte.
+template <bool kAlignedA>
+__global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
+    __shared__ uint64_t lut[256];
+    __shared__ __attribute__((aligned(16))) uint8_t As[kTmM * kTmPitch];
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[kTmN * kTmPitch];
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = t / kWave;
+    const int wm = wave >> 1, wn = wave & 1;
+    // Tile order: workgroups are dispatched round-robin over the 8 XCDs
+    // (block b runs on XCD b % 8), each with its own L2.  XCD x takes the
+    // contiguous range [x * per, (x + 1) * per) of a grouped tile order
+    // (groups of kGroupM m-tiles, m fastest inside a group), so the tiles a
+    // CU's neighbours work on share weights and codes in that XCD's L2.
+    const uint32_t tm_n = (p.m + kTmM - 1) / kTmM, tn_n = (p.n + kTmN - 1) / kTmN;
+    const uint32_t ntiles = tm_n * tn_n;
+    const uint32_t per = (ntiles + kXcds - 1) / kXcds;
+    const uint32_t lin = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+    if (lin >= ntiles) return;  // whole workgroup: no barrier reached yet
+    const uint32_t grp = lin / (kGroupM * tn_n);
+    const uint32_t first_m = grp * kGroupM;
+    const uint32_t gsz = min(tm_n - first_m, (uint32_t)kGroupM);
+    const uint32_t in_grp = lin % (kGroupM * tn_n);
+    const uint32_t m0 = (first_m + in_grp % gsz) * kTmM, n0 = (in_grp / gsz) * kTmN;
+    lut[t] = trit_lut_entry((uint32_t)t);
+
+    // A staging: thread t decodes packed bytes [16h, 16h + 16) of tile row r.
+    const int ar = t >> 1, ah = t & 1;
+    const bool arow_ok = m0 + ar < p.m;
+    const uint8_t* arow8 = p.a + (uint64_t)(arow_ok ? m0 + ar : 0) * p.kp;
+    const u32x4* arow = reinterpret_cast<const u32x4*>(arow8);
+    // B staging: 16-byte pieces c = t + 256u (u < 5) of the 128 x 160 tile.
+    const uint32_t nkt = (p.k + kTmK - 1) / kTmK;
+    const u32x4 zero_bytes = {kZeroByte * 0x01010101u, kZeroByte * 0x01010101u, kZeroByte * 0x01010101u,
+                              kZeroByte * 0x01010101u};
+    const u32x4 zero4 = {0u, 0u, 0u, 0u};
+
+    auto load_tile = [&](uint32_t kt, u32x4& av, u32x4* bv) {
+        const uint32_t ab = kt * kTmKp + 16u * ah;  // packed byte offset
+        if (kAlignedA) {
+            av = (arow_ok && ab < p.kp) ? arow[ab >> 4] : zero_bytes;
+        } else {
+            uint32_t w[4];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                w[d] = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t o = ab + 4 * d + e;
+                    const uint32_t b = (arow_ok && o < p.kp) ? arow8[o] : kZeroByte;
+                    w[d] |= b << (8 * e);
+                }
+            }
+            av = u32x4{w[0], w[1], w[2], w[3]};
+        }
+#pragma unroll
+        for (int u = 0; u < 5; ++u) {
+            const int c = t + kTmBlock * u;
+            const int row = c / 10, piece = c % 10;
+            const uint32_t kb = kt * kTmK + 16u * piece;
+            const bool ok = n0 + row < p.n && kb < p.k;
+            bv[u] = ok ? *reinterpret_cast<const u32x4*>(p.q + (uint64_t)(n0 + row) * p.k + kb) : zero4;
+        }
+    };
+
+    i32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    u32x4 av, bv[5];
+    load_tile(0, av, bv);
+    for (uint32_t kt = 0; kt < nkt; ++kt) {
+        __syncthreads();  // previous tile's MFMA reads (and the LUT fill) are done
+        // decode 16 packed bytes -> 80 trit bytes, little-endian in 20 dwords
+        uint32_t out[20];
+#pragma unroll
+        for (int d = 0; d < 20; ++d) out[d] = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t b = (av[i >> 2] >> (8 * (i & 3))) & 0xffu;
+            const uint64_t v = lut[b];
+            const int off = 5 * i, d = off >> 2, sh = (off & 3) * 8;
+            out[d] |= (uint32_t)(v << sh);
+            out[d + 1] |= (uint32_t)(v >> (32 - sh));
+        }
+        u32x4* adst = reinterpret_cast<u32x4*>(As + ar * kTmPitch + ah * 80);
+#pragma unroll
+        for (int w = 0; w < 5; ++w) {
+            const u32x4 o = {out[4 * w], out[4 * w + 1], out[4 * w + 2], out[4 * w + 3]};
+            adst[w] = o;
+        }
+#pragma unroll
+        for (int u = 0; u < 5; ++u) {
+            const int c = t + kTmBlock * u;
+            const int row = c / 10, piece = c % 10;
+            *reinterpret_cast<u32x4*>(Bs + row * kTmPitch + 16 * piece) = bv[u];
+        }
+        __syncthreads();
+        if (kt + 1 < nkt) load_tile(kt + 1, av, bv);
+#pragma unroll
+        for (int s = 0; s < 5; ++s) {
+            const int koff = 32 * s + 16 * (lane >> 5);
+            i32x4 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                a[i] = *reinterpret_cast<const i32x4*>(As + (wm * 64 + i * 32 + (lane & 31)) * kTmPitch + koff);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                b[j] = *reinterpret_cast<const i32x4*>(Bs + (wn * 64 + j * 32 + (lane & 31)) * kTmPitch + koff);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    }
+
+    // epilogue: ((float)acc * sa[m]) * sq[n]
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t n = n0 + wn * 64 + j * 32 + (lane & 31);
+        const bool n_ok = n < p.n;
+        const float sqn = n_ok ? p.sq[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (n_ok && m < p.m) {
+                    const float v = ((float)acc[i][j][r] * p.sa[m]) * sqn;
+                    __builtin_nontemporal_store(v, p.c + (uint64_t)m * p.n + n);
+                }
+            }
+        }
+    }
+}
+
+// Generic path: one thread per output, integer accumulation in k order.
+__global__ __launch_bounds__(kTmBlock) void ternary_i8_generic_kernel(TernArgs p) {
+    __shared__ uint64_t lut[256];
+    lut[threadIdx.x] = trit_lut_entry(threadIdx.x);
+    __syncthreads();
+    const uint64_t idx = (uint64_t)blockIdx.x * kTmBlock + threadIdx.x;
+    if (idx >= (uint64_t)p.m * p.n) return;
+    const uint32_t m = (uint32_t)(idx / p.n), n = (uint32_t)(idx % p.n);
+    const uint8_t* ar = p.a + (uint64_t)m * p.kp;
+    const int8_t* qr = p.q + (uint64_t)n * p.k;
+    int32_t acc = 0;
+    for (uint32_t k = 0; k < p.k; ++k) {
+        const uint64_t v = lut[ar[k / 5]];
+        const int8_t tr = (int8_t)(uint8_t)(v >> (8 * (k % 5)));
+        acc += (int32_t)tr * (int32_t)qr[k];
+    }
+    p.c[idx] = ((float)acc * p.sa[m]) * p.sq[n];
+}
+
+}  // namespace kore
+
+using namespace kore;
+
+extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* a_scales, const int8_t* q,
+                                          const float* q_scales, float* c, uint64_t m, uint64_t n, uint64_t k,
+                                          kore_stream_t stream) {
+    if (m == 0 || n == 0) return KORE_HIP_OK;
+    if (!c || !a_scales || !q_scales) return KORE_HIP_ERR_NULL_PTR;
+    if (k > 0 && (!a_packed || !q)) return KORE_HIP_ERR_NULL_PTR;
+    // |sum| <= 127 * k must stay exact in int32 and every index in 32 bits.
+    if (m > 0x7fffffffull || n > 0x7fffffffull || k > (1ull << 24)) return KORE_HIP_ERR_OVERFLOW;
+    uint64_t mn, nk;
+    if (!mul_ok(m, n, &mn) || mn > kMaxElements || !mul_ok(n, k, &nk) || nk > kMaxElements)
+        return KORE_HIP_ERR_OVERFLOW;
+    const uint64_t kp = (k + 4) / 5;
+    TernArgs p{a_packed, a_scales, q, q_scales, c, (uint32_t)m, (uint32_t)n, (uint32_t)k, (uint32_t)kp};
+    hipStream_t s = (hipStream_t)stream;
+    const bool vec = k > 0 && k % 16 == 0 && aligned16(q) && (reinterpret_cast<uintptr_t>(c) & 3u) == 0;
+    if (vec) {
+        const uint64_t tiles = ((m + kTmM - 1) / kTmM) * ((n + kTmN - 1) / kTmN);
+        const uint64_t per = (tiles + kXcds - 1) / kXcds;
+        if (per * kXcds > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
+        const dim3 grid((uint32_t)(per * kXcds));
+        if (kp % 16 == 0 && aligned16(a_packed))
+            hipLaunchKernelGGL(ternary_i8_mfma_kernel<true>, grid, dim3(kTmBlock), 0, s, p);
+        else
+            hipLaunchKernelGGL(ternary_i8_mfma_kernel<false>, grid, dim3(kTmBlock), 0, s, p);
+    } else {
+        const uint64_t blocks = (mn + kTmBlock - 1) / kTmBlock;
+        if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
+        hipLaunchKernelGGL(ternary_i8_generic_kernel, dim3((uint32_t)blocks), dim3(kTmBlock), 0, s, p);
+    }
+    return launch_status();
+}

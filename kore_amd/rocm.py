@@ -366,3 +366,25 @@ def rocm_rms_norm_backward_f32(device_idx: int, grad_output: HipBuffer, input: H
                                                       ws.nbytes, rows, cols, eps, _stream(device_idx)),
            "rms_norm_backward_f32")
     return gx, gg
+
+
+# ------------------------------------------------------- ternary (BitLinear)
+def rocm_ternary_matmul_i8(device_idx: int, a_packed: HipBuffer, a_scales: HipBuffer, q: HipBuffer,
+                           q_scales: HipBuffer, m: int, n: int, k: int,
+                           out: Optional[HipBuffer] = None) -> HipBuffer:
+    """BitLinear matmul on pre-quant codes: c[m, n] = ((float)(sum_k trit[m, k]
+    * q[n, k]) * a_scales[m]) * q_scales[n], with the base-243 weights of
+    ``pack_weights_ternary`` (cpu_ternary_matmul.rs:198-240) and the epilogue
+    of ``ternary_ternary_matmul`` (cpu_ternary_matmul.rs:188)."""
+    _require_device(device_idx)
+    _need(a_packed, m * ((k + 4) // 5), "ternary weights")
+    _need(a_scales, m * 4, "ternary scales")
+    _need(q, n * k, "ternary codes")
+    _need(q_scales, n * 4, "ternary code scales")
+    c = _out(device_idx, out, m * n * 4, "ternary out")
+    _check(_lib.load().kore_hip_ternary_matmul_i8(a_packed.ptr, a_scales.ptr, q.ptr, q_scales.ptr, c.ptr, m, n, k,
+                                                  _stream(device_idx)), "ternary_matmul_i8")
+    return c
+
+
+__all__ += ["rocm_ternary_matmul_i8"]

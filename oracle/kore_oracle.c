@@ -356,3 +356,108 @@ void kore_oracle_cross_entropy_backward_f32(const float *logits,
         if (target_idx < num_classes) g[target_idx] = g[target_idx] - inv_batch;
     }
 }
+
+/* ------------------------------------------------------------ ternary */
+
+void kore_oracle_decode_trits(uint8_t byte, int8_t out[5]) {
+    /* crates/kore-btes/src/encoder.rs:50-70 (TERNARY_DECODE_LUT) and :89-95
+     * (decode_trits): base-3 digits, least significant first, digit 0 ->
+     * Neg, 1 -> Zero, 2 -> Pos; bytes 243..255 decode to five zeros. */
+    if (byte >= 243) {
+        for (int j = 0; j < 5; ++j) out[j] = 0;
+        return;
+    }
+    unsigned v = byte;
+    for (int j = 0; j < 5; ++j) {
+        out[j] = (int8_t)((int)(v % 3u) - 1);
+        v /= 3u;
+    }
+}
+
+uint8_t kore_oracle_encode_trits(const int8_t t[5]) {
+    /* crates/kore-btes/src/encoder.rs:73-86: digit (t + 1) times 3^j, with
+     * the reference's u8 arithmetic (the sum of 5 digits <= 2*121 fits). */
+    unsigned val = 0, mul = 1;
+    for (int j = 0; j < 5; ++j) {
+        val += (unsigned)(t[j] + 1) * mul;
+        mul *= 3u;
+    }
+    return (uint8_t)val;
+}
+
+static float rust_fmax_t(float a, float b) {
+    if (a != a) return b;
+    if (b != b) return a;
+    return a > b ? a : b;
+}
+
+void kore_oracle_pack_weights_ternary(const float *w, size_t m, size_t k,
+                                      float threshold, uint8_t *packed,
+                                      float *scales) {
+    /* crates/kore-kernels/src/cpu_ternary_matmul.rs:198-240 */
+    const size_t kp = (k + 4) / 5;
+    for (size_t row = 0; row < m; ++row) {
+        const float *rd = w + row * k;
+        float abs_max = 0.0f;
+        for (size_t i = 0; i < k; ++i) abs_max = rust_fmax_t(abs_max, fabsf(rd[i]));
+        const float scale = abs_max < 1e-8f ? 1.0f : abs_max;
+        scales[row] = scale;
+        for (size_t b = 0; b < kp; ++b) {
+            int8_t block[5] = {0, 0, 0, 0, 0};
+            for (size_t j = 0; j < 5 && b * 5 + j < k; ++j) {
+                const float nv = rd[b * 5 + j] / scale;
+                block[j] = nv > threshold ? 1 : (nv < -threshold ? -1 : 0);
+            }
+            packed[row * kp + b] = kore_oracle_encode_trits(block);
+        }
+    }
+}
+
+void kore_oracle_ternary_matmul_f32(const uint8_t *a_packed,
+                                    const float *a_scales, const float *b,
+                                    float *c, size_t m, size_t n, size_t k) {
+    /* crates/kore-kernels/src/cpu_ternary_matmul.rs:29-124 (ternary_matmul:
+     * unpack_row_trits :91-101, compute_row :105-124); the same loop is
+     * crates/kore-edge/src/ops/matmul.rs:49-93.  Per output row: c = 0; for
+     * each k in order, skip zero trits, c[col] += t * b[k, col]; then
+     * c[col] *= scale. */
+    const size_t kp = (k + 4) / 5;
+    int8_t t5[5];
+    for (size_t row = 0; row < m; ++row) {
+        float *cr = c + row * n;
+        for (size_t col = 0; col < n; ++col) cr[col] = 0.0f;
+        for (size_t ki = 0; ki < k; ++ki) {
+            kore_oracle_decode_trits(a_packed[row * kp + ki / 5], t5);
+            const int8_t t = t5[ki % 5];
+            if (t == 0) continue;
+            const float tf = (float)t;
+            const float *br = b + ki * n;
+            for (size_t col = 0; col < n; ++col) cr[col] = cr[col] + tf * br[col];
+        }
+        const float s = a_scales[row];
+        for (size_t col = 0; col < n; ++col) cr[col] = cr[col] * s;
+    }
+}
+
+void kore_oracle_ternary_matmul_i8(const uint8_t *a_packed,
+                                   const float *a_scales, const int8_t *q,
+                                   const float *q_scales, float *c, size_t m,
+                                   size_t n, size_t k) {
+    /* The BitLinear matmul on pre-quant codes: integer dot products of the
+     * decoded trits with the int8 codes q[n, :] (exact in 64-bit), then the
+     * ternary-ternary epilogue of crates/kore-kernels/src/cpu_ternary_matmul.rs
+     * (ternary_ternary_matmul, `int_acc as f32 * a_scale * b_scale`) with the
+     * code row's scale in place of b_scale. */
+    const size_t kp = (k + 4) / 5;
+    int8_t t5[5];
+    for (size_t row = 0; row < m; ++row) {
+        for (size_t col = 0; col < n; ++col) {
+            long long acc = 0;
+            for (size_t ki = 0; ki < k; ++ki) {
+                kore_oracle_decode_trits(a_packed[row * kp + ki / 5], t5);
+                acc += (long long)t5[ki % 5] * (long long)q[col * k + ki];
+            }
+            c[row * n + col] = ((float)acc * a_scales[row]) * q_scales[col];
+        }
+    }
+}

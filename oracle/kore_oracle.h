@@ -136,6 +136,41 @@ void kore_oracle_rms_norm_backward_f32(const float *dy, const float *x,
                                        float *dgamma, size_t rows, size_t cols,
                                        float eps);
 
+
+/* ---------------------------------------------------------------- ternary
+ * Base-243 packed ternary weights: 5 trits per byte, least significant
+ * base-3 digit first, digit 0/1/2 = -1/0/+1 (crates/kore-btes/src/encoder.rs). */
+
+/* crates/kore-btes/src/encoder.rs:89-95 (decode_trits; LUT :50-70). */
+void kore_oracle_decode_trits(uint8_t byte, int8_t out[5]);
+
+/* crates/kore-btes/src/encoder.rs:73-86 (encode_trits). */
+uint8_t kore_oracle_encode_trits(const int8_t t[5]);
+
+/* crates/kore-kernels/src/cpu_ternary_matmul.rs:198-240
+ * (pack_weights_ternary): per-row absmax scale (1.0 below 1e-8), trit =
+ * sign(w/scale) where |w/scale| > threshold.  packed[m, ceil(k/5)]. */
+void kore_oracle_pack_weights_ternary(const float *w, size_t m, size_t k,
+                                      float threshold, uint8_t *packed,
+                                      float *scales);
+
+/* crates/kore-kernels/src/cpu_ternary_matmul.rs:29-124 (ternary_matmul) ==
+ * crates/kore-edge/src/ops/matmul.rs:49-93 (matmul_ternary):
+ * c[m, n] = scale[m] * sum_k trit[m, k] * b[k, n], b row-major [k, n],
+ * summed in k order, zero trits skipped. */
+void kore_oracle_ternary_matmul_f32(const uint8_t *a_packed,
+                                    const float *a_scales, const float *b,
+                                    float *c, size_t m, size_t n, size_t k);
+
+/* BitLinear matmul on the pre-quant codes (no single reference function):
+ * c[m, n] = ((float)(sum_k trit[m, k] * q[n, k]) * a_scales[m]) * q_scales[n],
+ * the integer dot product exact, the epilogue of
+ * crates/kore-kernels/src/cpu_ternary_matmul.rs:188 (ternary_ternary_matmul). */
+void kore_oracle_ternary_matmul_i8(const uint8_t *a_packed,
+                                   const float *a_scales, const int8_t *q,
+                                   const float *q_scales, float *c, size_t m,
+                                   size_t n, size_t k);
+
 #ifdef __cplusplus
 }
 #endif

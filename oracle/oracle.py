@@ -39,6 +39,11 @@ _SIGS = {
     "kore_oracle_softmax_backward_f32": (None, [_p, _p, _p, _sz, _sz]),
     "kore_oracle_cross_entropy_backward_f32": (None, [_p, _p, _p, _sz, _sz]),
     "kore_oracle_rms_norm_backward_f32": (None, [_p, _p, _p, _p, _p, _sz, _sz, _f]),
+    "kore_oracle_decode_trits": (None, [_c.c_uint8, _p]),
+    "kore_oracle_encode_trits": (_c.c_uint8, [_p]),
+    "kore_oracle_pack_weights_ternary": (None, [_p, _sz, _sz, _f, _p, _p]),
+    "kore_oracle_ternary_matmul_f32": (None, [_p, _p, _p, _p, _sz, _sz, _sz]),
+    "kore_oracle_ternary_matmul_i8": (None, [_p, _p, _p, _p, _p, _sz, _sz, _sz]),
 }
 
 _lib = None
@@ -185,7 +190,8 @@ def quant_code(xn: float, amax: float) -> int:
 
 __all__ = ["build", "lib", "rms_norm", "gelu", "silu", "mul", "swiglu", "rope_inv_freq", "rope", "embedding",
            "rms_norm_quant_i8", "rms_norm_silu_gate", "quant_code", "softmax", "softmax_causal",
-           "softmax_backward", "rms_norm_backward", "cross_entropy_backward"]
+           "softmax_backward", "rms_norm_backward", "cross_entropy_backward", "decode_trits", "encode_trits",
+           "pack_weights_ternary", "ternary_matmul", "ternary_matmul_i8", "unpack_trits"]
 
 
 def _rows_cols(x: np.ndarray):
@@ -237,3 +243,54 @@ def cross_entropy_backward(logits, targets) -> np.ndarray:
     g = np.empty_like(l)
     lib().kore_oracle_cross_entropy_backward_f32(_ptr(l), _ptr(t), _ptr(g), batch, classes)
     return g
+
+
+# ------------------------------------------------------------------ ternary
+def decode_trits(byte: int) -> np.ndarray:
+    """encoder.rs:89-95: base-243 byte -> 5 trits in {-1, 0, 1}."""
+    out = np.zeros(5, np.int8)
+    lib().kore_oracle_decode_trits(int(byte), _ptr(out))
+    return out
+
+
+def encode_trits(trits) -> int:
+    """encoder.rs:73-86: 5 trits -> base-243 byte."""
+    t = np.ascontiguousarray(trits, dtype=np.int8)
+    return int(lib().kore_oracle_encode_trits(_ptr(t)))
+
+
+def pack_weights_ternary(w, threshold: float):
+    """cpu_ternary_matmul.rs:198-240 -> (packed uint8[m, ceil(k/5)], scales f32[m])."""
+    w = _f32(w)
+    m, k = w.shape
+    packed = np.empty((m, (k + 4) // 5), np.uint8)
+    scales = np.empty(m, np.float32)
+    lib().kore_oracle_pack_weights_ternary(_ptr(w), m, k, threshold, _ptr(packed), _ptr(scales))
+    return packed, scales
+
+
+def ternary_matmul(packed, scales, b, m: int, n: int, k: int) -> np.ndarray:
+    """cpu_ternary_matmul.rs:29-124: c[m, n] = scale[m] * sum_k trit[m, k] * b[k, n]."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    scales, b = _f32(scales), _f32(b)
+    c = np.empty((m, n), np.float32)
+    lib().kore_oracle_ternary_matmul_f32(_ptr(packed), _ptr(scales), _ptr(b), _ptr(c), m, n, k)
+    return c
+
+
+def ternary_matmul_i8(packed, scales, q, q_scales, m: int, n: int, k: int) -> np.ndarray:
+    """c[m, n] = ((float)(sum_k trit[m, k] * q[n, k]) * scales[m]) * q_scales[n]
+    (integer dot exact; epilogue of cpu_ternary_matmul.rs:188)."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    scales, q_scales = _f32(scales), _f32(q_scales)
+    c = np.empty((m, n), np.float32)
+    lib().kore_oracle_ternary_matmul_i8(_ptr(packed), _ptr(scales), _ptr(q), _ptr(q_scales), _ptr(c), m, n, k)
+    return c
+
+
+def unpack_trits(packed, k: int) -> np.ndarray:
+    """All rows of a packed matrix as int8 trits [m, k] (decode_trits per byte, truncated to k)."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    lut = np.stack([decode_trits(b) for b in range(256)])
+    return lut[packed].reshape(packed.shape[0], -1)[:, :k]

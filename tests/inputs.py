@@ -130,3 +130,24 @@ def assert_close_scaled(got, ref, scale, rtol: float = 1e-5, atol: float = 1e-6,
         i = tuple(bad[0])
         raise AssertionError(f"{what}: {len(bad)} of {ok.size} elements outside tol (rtol={rtol} of scale, "
                              f"atol={atol}); first at {i}: got {got[i]!r} ref {ref[i]!r} scale {scale[i]!r}")
+
+
+def ternary_weights(m: int, k: int, seed: int = 0, threshold: float = 0.3):
+    """BitLinear weights: w ~ U(-1, 1) (the reference's BitLinear::random,
+    crates/kore-nn/src/bit_linear.rs:93-108) packed by the oracle's
+    pack_weights_ternary; returns (packed uint8[m, ceil(k/5)], scales f32[m])."""
+    import oracle
+
+    w = rng(seed).uniform(-1.0, 1.0, size=(m, k)).astype(np.float32)
+    return oracle.pack_weights_ternary(w, threshold)
+
+
+def raw_packed(m: int, k: int, seed: int = 0) -> np.ndarray:
+    """Arbitrary packed bytes 0..255: includes bytes >= 243 (decode to zeros)
+    and nonzero padding trits past column k (ignored by the reference's
+    truncate(k))."""
+    return rng(seed).integers(0, 256, size=(m, (k + 4) // 5), dtype=np.int64).astype(np.uint8)
+
+
+def int8_codes(n: int, k: int, seed: int = 0) -> np.ndarray:
+    return rng(seed).integers(-128, 128, size=(n, k), dtype=np.int64).astype(np.int8)

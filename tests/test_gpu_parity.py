@@ -537,3 +537,77 @@ def test_cross_entropy_backward_target_cast_and_in_place():
         rocm.rocm_cross_entropy_backward_f32(DEV, b, up(t), 6, classes, out=b)
         assert_close(down(b, np.float32, (6, classes)), oracle.cross_entropy_backward(x, t),
                      rtol=1e-5 + classes * U32, what=f"ce targets {classes}")
+
+
+# ---------------------------------------------------- ternary (BitLinear i8)
+TERN_SHAPES = [(1, 1, 16), (3, 5, 16), (128, 128, 160), (129, 130, 320), (200, 77, 2560), (64, 33, 6912),
+               (5, 7, 13), (33, 65, 1000), (6912, 1, 2560), (300, 64, 2560), (17, 300, 2576)]
+
+
+@pytest.mark.parametrize("m,n,k", TERN_SHAPES)
+def test_ternary_matmul_i8(m, n, k):
+    """Bit-exact against the oracle (integer dot product, the ternary_ternary
+    epilogue), on arbitrary packed bytes: bytes >= 243 and nonzero padding
+    trits past k included."""
+    from inputs import int8_codes, raw_packed
+
+    log(f"ternary_matmul_i8 m={m} n={n} k={k}")
+    p = raw_packed(m, k, m + k)
+    q = int8_codes(n, k, n + 1)
+    sa = normal((m,), 3, 1.0, 0.1)
+    sq = np.abs(normal((n,), 4, 0.02, 0.005))
+    got = down(rocm.rocm_ternary_matmul_i8(DEV, up(p), up(sa), up(q), up(sq), m, n, k), np.float32, (m, n))
+    assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), "ternary_matmul_i8")
+
+
+def test_ternary_matmul_i8_full_size_and_pipeline():
+    """BitLinear 2560 -> 6912 on 4096 tokens (the pre-quant config's
+    activations): bit-exact against an f64 GEMM of the decoded trits (exact
+    for these integer sums) with the same f32 epilogue; then the end-to-end
+    chain pre-quant codes -> ternary matmul against the oracle on a slice."""
+    from inputs import ternary_weights
+
+    m, n, k = 6912, 4096, 2560
+    log(f"ternary_matmul_i8 full size m={m} n={n} k={k}")
+    p, sa = ternary_weights(m, k, 21)
+    x, g = prequant_inputs(n, k, 0)
+    qb, sb = rocm.rocm_rms_norm_quant_i8(DEV, up(x), up(g), n, k, 1e-6)
+    c = rocm.rocm_ternary_matmul_i8(DEV, up(p), up(sa), qb, sb, m, n, k)
+    got = torch.from_numpy(down(c, np.float32, (m, n))).cuda()
+    t = torch.from_numpy(oracle.unpack_trits(p, k)).cuda().double()
+    qd = torch.from_numpy(down(qb, np.int8, (n, k))).cuda().double()
+    acc = (t @ qd.T).float()
+    want = (acc * torch.from_numpy(sa).cuda()[:, None]) * torch.from_numpy(down(sb, np.float32, (n,))).cuda()[None, :]
+    assert torch.equal(got, want), "ternary_matmul_i8 full size vs f64 GEMM"
+    # the chain on a slice of tokens, against the oracle end to end
+    rows = 8
+    wq, ws = oracle.rms_norm_quant_i8(x[:rows], g, 1e-6)
+    ref = oracle.ternary_matmul_i8(p[:96], sa[:96], wq, ws, 96, rows, k)
+    assert_bitexact(got[:96, :rows].cpu().numpy(), ref, "prequant -> ternary chain")
+
+
+def test_ternary_matmul_i8_edges():
+    log("ternary_matmul_i8 edges")
+    lib = __import__("kore_amd._lib", fromlist=["load"]).load()
+    # empty work: nothing launched, status 0
+    assert lib.kore_hip_ternary_matmul_i8(None, None, None, None, None, 0, 5, 16, None) == 0
+    assert lib.kore_hip_ternary_matmul_i8(None, None, None, None, None, 5, 0, 16, None) == 0
+    # k = 0: every dot product is 0
+    sa, sq = np.ones(3, np.float32), np.ones(4, np.float32)
+    c = rocm.rocm_ternary_matmul_i8(DEV, up(np.zeros(1, np.uint8)), up(sa), up(np.zeros(1, np.int8)), up(sq),
+                                    3, 4, 0)
+    assert (down(c, np.float32, (3, 4)) == 0).all()
+    # argument errors
+    assert lib.kore_hip_ternary_matmul_i8(None, None, None, None, None, 2, 2, 16, None) == -1
+    assert lib.kore_hip_ternary_matmul_i8(1, 1, 1, 1, 1, 2, 2, (1 << 24) + 1, None) == -3
+    # unaligned codes take the generic path with identical results
+    m, n, k = 40, 9, 320
+    from inputs import int8_codes, raw_packed
+
+    p, q = raw_packed(m, k, 1), int8_codes(n, k, 2)
+    sa, sq = normal((m,), 5), normal((n,), 6)
+    t = torch.empty(n * k + 1, dtype=torch.int8, device="cuda")
+    t[1:].copy_(torch.from_numpy(q.ravel()))
+    got = down(rocm.rocm_ternary_matmul_i8(DEV, up(p), up(sa), HipBuffer.from_tensor(t[1:]), up(sq), m, n, k),
+               np.float32, (m, n))
+    assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), "ternary unaligned q")

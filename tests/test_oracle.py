@@ -394,3 +394,95 @@ def test_cross_entropy_backward_target_cast():
         for i in range(4):
             want = base - np.float32(0.2) if i == t else base
             assert abs(g[b, i] - want) < 1e-7, (b, i)
+
+
+# ------------------------------------------------------------------ ternary
+def _base3_digits(b: int) -> list:
+    return [(b // 3 ** j) % 3 - 1 for j in range(5)]
+
+
+def test_trit_codec_reference_kats():
+    # encoder.rs tests: every byte 0..242 round-trips; five zeros encode to
+    # 121 = 1+3+9+27+81; the (Pos, Neg, Zero, Pos, Neg) example round-trips.
+    for b in range(243):
+        t = oracle.decode_trits(b)
+        assert list(t) == _base3_digits(b), b  # closed form: base-3 digits, lsd first
+        assert oracle.encode_trits(t) == b
+    assert oracle.encode_trits([0, 0, 0, 0, 0]) == 121
+    assert list(oracle.decode_trits(121)) == [0] * 5
+    assert oracle.decode_trits(oracle.encode_trits([1, -1, 0, 1, -1])).tolist() == [1, -1, 0, 1, -1]
+    for b in range(243, 256):  # decode_trits: bytes past the table decode to zeros
+        assert list(oracle.decode_trits(b)) == [0] * 5
+
+
+def test_pack_weights_ternary_kats_and_brute_force():
+    # cpu_ternary_matmul.rs test_pack_ternary: 2 rows x 4 -> one byte per row, scales > 0.
+    p, s = oracle.pack_weights_ternary(np.array([1.0, -1.0, 0.0, 0.5, -0.5, 1.0, -1.0, 0.0], np.float32)
+                                       .reshape(2, 4), 0.3)
+    assert p.shape == (2, 1) and (s > 0).all()
+    assert list(oracle.unpack_trits(p, 4)[0]) == [1, -1, 0, 1]
+    # brute force: scale = row absmax (1.0 below 1e-8), trit = sign where |w/scale| > threshold,
+    # padding trits are zeros
+    w = np.random.default_rng(3).uniform(-1, 1, size=(7, 23)).astype(np.float32)
+    w[2] = 0.0
+    p, s = oracle.pack_weights_ternary(w, 0.3)
+    amax = np.abs(w).max(axis=1)
+    assert (s == np.where(amax < 1e-8, 1.0, amax).astype(np.float32)).all()
+    nv = w / s[:, None]
+    want = np.where(nv > 0.3, 1, np.where(nv < -0.3, -1, 0))
+    assert (oracle.unpack_trits(p, 23) == want).all()
+    assert (oracle.unpack_trits(p, 25)[:, 23:] == 0).all()
+
+
+def test_ternary_matmul_reference_kats():
+    # cpu_ternary_matmul.rs test_ternary_matmul_identity and
+    # kore-edge ops/matmul.rs test_matmul_ternary_identity: C = I @ [[2,0],[0,3]]
+    p, s = oracle.pack_weights_ternary(np.array([[1.0, 0.0], [0.0, 1.0]], np.float32), 0.3)
+    c = oracle.ternary_matmul(p, s, np.array([[2.0, 0.0], [0.0, 3.0]], np.float32), 2, 2, 2)
+    assert (c == np.array([[2.0, 0.0], [0.0, 3.0]], np.float32)).all()
+    # kore-edge test_matmul_ternary_with_scale: [[+1, -1]] * 2 @ [[3], [1]] = 4
+    row = oracle.encode_trits([1, -1, 0, 0, 0])
+    c = oracle.ternary_matmul(np.array([[row]], np.uint8), np.array([2.0], np.float32),
+                              np.array([[3.0], [1.0]], np.float32), 1, 1, 2)
+    assert c[0, 0] == 4.0
+    # test_ternary_matmul_larger: 8 x 20 x 4, weights (i % 3) - 1, b = (i % 5) * 0.2 -> finite
+    w = (np.arange(160) % 3 - 1).astype(np.float32).reshape(8, 20)
+    b = ((np.arange(80) % 5) * np.float32(0.2)).astype(np.float32).reshape(20, 4)
+    p, s = oracle.pack_weights_ternary(w, 0.3)
+    c = oracle.ternary_matmul(p, s, b, 8, 4, 20)
+    assert c.shape == (8, 4) and np.isfinite(c).all()
+    assert (oracle.unpack_trits(p, 20) == w).all()  # (i % 3) - 1 is already ternary, scale 1
+
+
+def test_ternary_matmul_exact_and_f64():
+    m, n, k = 9, 6, 47
+    p = np.random.default_rng(5).integers(0, 256, size=(m, (k + 4) // 5)).astype(np.uint8)
+    s = np.random.default_rng(6).uniform(0.5, 2.0, size=m).astype(np.float32)
+    t = oracle.unpack_trits(p, k).astype(np.float64)
+    # small-integer activations: every partial sum is exact, so c is the exact product times scale
+    bi = np.random.default_rng(7).integers(-50, 50, size=(k, n)).astype(np.float32)
+    c = oracle.ternary_matmul(p, s, bi, m, n, k)
+    assert (c == ((t @ bi).astype(np.float32) * s[:, None])).all()
+    # general activations: within the sequential-sum bound of the f64 product
+    b = np.random.default_rng(8).standard_normal((k, n)).astype(np.float32)
+    c = oracle.ternary_matmul(p, s, b, m, n, k).astype(np.float64)
+    ref = (t @ b.astype(np.float64)) * s[:, None]
+    bound = (k + 2) * 2.0 ** -24 * (np.abs(t) @ np.abs(b.astype(np.float64))) * s[:, None]
+    assert (np.abs(c - ref) <= bound + 1e-30).all()
+
+
+def test_ternary_matmul_i8_exact():
+    m, n, k = 11, 7, 93
+    p = np.random.default_rng(9).integers(0, 256, size=(m, (k + 4) // 5)).astype(np.uint8)
+    q = np.random.default_rng(10).integers(-128, 128, size=(n, k)).astype(np.int8)
+    sa = np.random.default_rng(11).uniform(0.1, 2.0, size=m).astype(np.float32)
+    sq = np.random.default_rng(12).uniform(0.001, 0.1, size=n).astype(np.float32)
+    c = oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k)
+    acc = oracle.unpack_trits(p, k).astype(np.int64) @ q.astype(np.int64).T
+    want = (acc.astype(np.float32) * sa[:, None]).astype(np.float32) * sq[None, :]
+    assert c.tobytes() == want.astype(np.float32).tobytes()
+    # equals ternary_matmul on the dequantised codes up to its sequential-sum rounding
+    b = (q.astype(np.float32) * sq[:, None]).T.copy()
+    ref = oracle.ternary_matmul(p, sa, b, m, n, k)
+    bound = (k + 3) * 2.0 ** -24 * (np.abs(oracle.unpack_trits(p, k)) @ np.abs(b.astype(np.float64))) * sa[:, None]
+    assert (np.abs(c.astype(np.float64) - ref) <= bound + 1e-30).all()
