@@ -39,6 +39,7 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 PEAK_GBS = 8000.0
+MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
 MALL_BYTES = 256 << 20
 
 
@@ -61,6 +62,8 @@ class Workload:
     bytes = 0
     kernel = ""       # device kernel symbol prefix (for rocprof cross-checks)
     dtype = "f32"
+    bound = "hbm"     # roofline of the dominant kernel: "hbm" or "mfma"
+    ops = 0           # arithmetic operations per launch (MFMA-bound workloads)
 
     def setup(self, torch, lib):  # allocate inputs, return None
         raise NotImplementedError
@@ -447,6 +450,55 @@ class RmsNormBackward(Workload):
             f"{rows} rows, single thread"
 
 
+class TernaryI8(Workload):
+    """BitLinear int8 x ternary matmul (kore_hip_ternary_matmul_i8) on the
+    pre-quant config's activations: 4096 tokens of 2560 codes against a
+    2560 -> 6912 base-243 ternary weight matrix (BitNet-2B4T FFN shape).
+    MFMA-bound: reported as int8 TOPS against MI355X's 5.0 POP/s dense."""
+    kernel = "ternary_i8_mfma_kernel"
+    bound = "mfma"
+
+    def __init__(self, m=6912, n=4096, k=2560):
+        self.m, self.n, self.k = m, n, k
+        self.kp = (k + 4) // 5
+        self.name = f"ternary_i8_{m}x{n}x{k}"
+        self.tokens = n
+        self.ops = 2 * m * n * k
+        self.bytes = m * self.kp + n * k + 4 * m * n + 4 * (m + n)
+        self.desc = (f"BitLinear int8 x ternary matmul c[{m},{n}] = ((float)(trits[{m},{k}] . q[{n},{k}]) * "
+                     f"a_scale) * q_scale, base-243 weights, int8 codes (bit-exact)")
+
+    def setup(self, torch, lib):
+        self.lib = lib
+        self.k_sets = 4
+        g = torch.Generator(device="cuda")
+        g.manual_seed(0)
+        self._da = [torch.randint(0, 243, (self.m * self.kp,), generator=g, dtype=torch.uint8, device="cuda")
+                    for _ in range(self.k_sets)]
+        self._dq = [torch.randint(-128, 128, (self.n * self.k,), generator=g, dtype=torch.int8, device="cuda")
+                    for _ in range(self.k_sets)]
+        self._dsa = torch.rand(self.m, generator=g, device="cuda")
+        self._dsq = torch.rand(self.n, generator=g, device="cuda")
+        self._dc = [torch.empty(self.m * self.n, device="cuda") for _ in range(self.k_sets)]
+
+    def launch(self, i, stream):
+        j = i % self.k_sets
+        return self.lib.kore_hip_ternary_matmul_i8(self._da[j].data_ptr(), self._dsa.data_ptr(),
+                                                   self._dq[j].data_ptr(), self._dsq.data_ptr(),
+                                                   self._dc[j].data_ptr(), self.m, self.n, self.k, stream)
+
+    def cpu_sample(self):
+        import oracle
+        from inputs import int8_codes, raw_packed
+
+        m, n = 16, 256
+        p, q = raw_packed(m, self.k, 1), int8_codes(n, self.k, 2)
+        sa, sq = np.ones(m, np.float32), np.ones(n, np.float32)
+        return (lambda: oracle.ternary_matmul_i8(p, sa, q, sq, m, n, self.k)), \
+            m * self.kp + n * self.k + 4 * m * n, n * m / self.m, 1, \
+            f"{m} weight rows x {n} tokens, single thread", 2 * m * n * self.k
+
+
 class Copy(Workload):
     """A plain 1 GiB device copy through the gather kernel with ids = 0..N-1;
     used to calibrate rocprof's FETCH_SIZE / WRITE_SIZE counters."""
@@ -476,7 +528,7 @@ class Copy(Workload):
 def all_workloads():
     return [RopeQK(False), RopeQK(True), RMSNorm(32, 2048), RMSNorm(16384, 2048), Swiglu(), Gelu(), Embedding(),
             Prequant(4096), Prequant(64), Prequant(1), RmsNormSiluGate(), Softmax(), SoftmaxBackward(),
-            RmsNormBackward(), Copy()]
+            RmsNormBackward(), TernaryI8(), Copy()]
 
 
 # ------------------------------------------------------------------ measure
@@ -507,7 +559,8 @@ def time_cpu(w: Workload, budget_s: float):
     s = w.cpu_sample()
     if s is None:
         return None
-    run, nbytes, ntok, threads, desc = s
+    run, nbytes, ntok, threads, desc = s[:5]
+    ops = s[5] if len(s) > 5 else 0
     run()  # warm (page-in, libm init)
     reps, t = 0, 0.0
     t0 = time.perf_counter()
@@ -518,9 +571,13 @@ def time_cpu(w: Workload, budget_s: float):
         if t >= budget_s or reps >= 1000:
             break
     per = t / reps
-    return {"value": round(nbytes / per / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-            "ns_per_token": round(per / ntok * 1e9, 1), "seconds": round(t, 2), "reps": reps,
-            "sample": desc, "host_cores": os.cpu_count()}
+    out = {"value": round(nbytes / per / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+           "ns_per_token": round(per / ntok * 1e9, 1), "seconds": round(t, 2), "reps": reps,
+           "sample": desc, "host_cores": os.cpu_count()}
+    if ops:
+        out.update({"value": round(ops / per / 1e9, 4), "unit": "GOP/s (int8 multiply-adds x 2)",
+                    "gbs": round(nbytes / per / 1e9, 4)})
+    return out
 
 
 def load_traffic():
@@ -573,6 +630,10 @@ def main():
             "ns_per_token": round(ms * 1e6 / w.tokens, 3), "steps": steps, "wall_s": round(wall, 4),
             "wall_gbs": round(w.bytes * steps / wall / 1e9, 1),
         }
+        if w.ops:
+            tops = w.ops / (ms * 1e-3) / 1e12
+            r.update({"bound": w.bound, "ops_per_launch": w.ops, "achieved_tops": round(tops, 1),
+                      "frac_of_mfma_peak": round(tops / MFMA_I8_PEAK_TOPS, 4)})
         if w.name in traffic:
             r["hbm_traffic_bytes"] = traffic[w.name]
         w.free()
@@ -581,8 +642,10 @@ def main():
             print(f"[bench] {w.name}: cpu baseline", file=sys.stderr, flush=True)
             r["cpu_baseline"] = time_cpu(w, args.cpu_seconds if w.name == "rope_qk" else args.cpu_seconds / 3)
         results[w.name] = r
+        extra = (f", {r['achieved_tops']} TOPS ({100 * r['frac_of_mfma_peak']:.1f}% of the int8 MFMA peak)"
+                 if w.ops else "")
         print(f"[bench] {w.name}: {r['kernel_us']} us, {r['achieved_gbs']} GB/s ({100 * r['frac_of_peak']:.1f}% "
-              f"of peak), {r['ns_per_token']} ns/token", file=sys.stderr, flush=True)
+              f"of peak), {r['ns_per_token']} ns/token{extra}", file=sys.stderr, flush=True)
 
     head_name = "rope_qk" if "rope_qk" in results else next(iter(results))
     h = results[head_name]

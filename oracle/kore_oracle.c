@@ -10,6 +10,7 @@
 #include "kore_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <pthread.h>
 #include <string.h>
 
@@ -413,6 +414,16 @@ void kore_oracle_pack_weights_ternary(const float *w, size_t m, size_t k,
     }
 }
 
+/* unpack_row_trits (cpu_ternary_matmul.rs:91-101): decode every byte of
+ * the packed row and keep the first k trits. */
+static void unpack_row_trits(const uint8_t *row, size_t k, int8_t *out) {
+    int8_t t5[5];
+    for (size_t b = 0; b * 5 < k; ++b) {
+        kore_oracle_decode_trits(row[b], t5);
+        for (size_t j = 0; j < 5 && b * 5 + j < k; ++j) out[b * 5 + j] = t5[j];
+    }
+}
+
 void kore_oracle_ternary_matmul_f32(const uint8_t *a_packed,
                                     const float *a_scales, const float *b,
                                     float *c, size_t m, size_t n, size_t k) {
@@ -422,13 +433,13 @@ void kore_oracle_ternary_matmul_f32(const uint8_t *a_packed,
      * each k in order, skip zero trits, c[col] += t * b[k, col]; then
      * c[col] *= scale. */
     const size_t kp = (k + 4) / 5;
-    int8_t t5[5];
+    int8_t *tr = (int8_t *)malloc(k ? k : 1);
     for (size_t row = 0; row < m; ++row) {
+        unpack_row_trits(a_packed + row * kp, k, tr);
         float *cr = c + row * n;
         for (size_t col = 0; col < n; ++col) cr[col] = 0.0f;
         for (size_t ki = 0; ki < k; ++ki) {
-            kore_oracle_decode_trits(a_packed[row * kp + ki / 5], t5);
-            const int8_t t = t5[ki % 5];
+            const int8_t t = tr[ki];
             if (t == 0) continue;
             const float tf = (float)t;
             const float *br = b + ki * n;
@@ -437,6 +448,7 @@ void kore_oracle_ternary_matmul_f32(const uint8_t *a_packed,
         const float s = a_scales[row];
         for (size_t col = 0; col < n; ++col) cr[col] = cr[col] * s;
     }
+    free(tr);
 }
 
 void kore_oracle_ternary_matmul_i8(const uint8_t *a_packed,
@@ -444,20 +456,21 @@ void kore_oracle_ternary_matmul_i8(const uint8_t *a_packed,
                                    const float *q_scales, float *c, size_t m,
                                    size_t n, size_t k) {
     /* The BitLinear matmul on pre-quant codes: integer dot products of the
-     * decoded trits with the int8 codes q[n, :] (exact in 64-bit), then the
-     * ternary-ternary epilogue of crates/kore-kernels/src/cpu_ternary_matmul.rs
+     * decoded trits (unpacked once per row, cpu_ternary_matmul.rs:91-101)
+     * with the int8 codes q[n, :] (exact in 64-bit), then the ternary-ternary
+     * epilogue of crates/kore-kernels/src/cpu_ternary_matmul.rs:188
      * (ternary_ternary_matmul, `int_acc as f32 * a_scale * b_scale`) with the
      * code row's scale in place of b_scale. */
     const size_t kp = (k + 4) / 5;
-    int8_t t5[5];
+    int8_t *tr = (int8_t *)malloc(k ? k : 1);
     for (size_t row = 0; row < m; ++row) {
+        unpack_row_trits(a_packed + row * kp, k, tr);
         for (size_t col = 0; col < n; ++col) {
+            const int8_t *qr = q + col * k;
             long long acc = 0;
-            for (size_t ki = 0; ki < k; ++ki) {
-                kore_oracle_decode_trits(a_packed[row * kp + ki / 5], t5);
-                acc += (long long)t5[ki % 5] * (long long)q[col * k + ki];
-            }
+            for (size_t ki = 0; ki < k; ++ki) acc += (long long)tr[ki] * (long long)qr[ki];
             c[row * n + col] = ((float)acc * a_scales[row]) * q_scales[col];
         }
     }
+    free(tr);
 }
