@@ -487,6 +487,25 @@ class TernaryI8(Workload):
                                                    self._dq[j].data_ptr(), self._dsq.data_ptr(),
                                                    self._dc[j].data_ptr(), self.m, self.n, self.k, stream)
 
+    def library_reference(self, torch):
+        """The vendor library's plain int8 GEMM on the same shape for context
+        (torch._int_mm: hipBLASLt, int8 x int8 -> int32 [m, n], no trit
+        decode, no scales): average of 20 launches after 3 warmups."""
+        a = torch.randint(-128, 128, (self.m, self.k), dtype=torch.int8, device="cuda")
+        b = torch.randint(-128, 128, (self.k, self.n), dtype=torch.int8, device="cuda")
+        for _ in range(3):
+            torch._int_mm(a, b)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(20):
+            torch._int_mm(a, b)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / 20
+        return {"op": "torch._int_mm int8 x int8 -> int32 (hipBLASLt)", "us": round(us, 3),
+                "tops": round(self.ops / (us * 1e-6) / 1e12, 1)}
+
     def cpu_sample(self):
         import oracle
         from inputs import int8_codes, raw_packed
@@ -636,6 +655,11 @@ def main():
                       "frac_of_mfma_peak": round(tops / MFMA_I8_PEAK_TOPS, 4)})
         if w.name in traffic:
             r["hbm_traffic_bytes"] = traffic[w.name]
+        if hasattr(w, "library_reference"):
+            try:
+                r["library_reference"] = w.library_reference(torch)
+            except Exception as ex:  # the reference is context only
+                r["library_reference"] = {"error": str(ex)[:200]}
         w.free()
         torch.cuda.empty_cache()
         if not args.no_cpu:
