@@ -12,8 +12,8 @@
 //
 // Roofline: HBM.  Algorithmic bytes: x and dy read once, dx written once
 // (12 * rows * cols), plus gamma and dgamma.  The dgamma partials add
-// 2 * P * cols * 4 bytes (P = the workgroup count, ~1024 for large batches:
-// 4% of the traffic at 16384 x 2048).
+// 2 * P * cols * 4 bytes (P = the workgroup count, ~512 for large batches:
+// 2% of the traffic at 16384 x 2048).
 //
 // Vector path (cols % 4 == 0, 16-byte aligned, cols <= 4096):
 //   1. rms_bwd_rows_kernel: a row is split over S = 1, 2 or 4 waves (at
@@ -266,11 +266,14 @@ static uint32_t bwd_split(uint64_t cols) {
 }
 
 
-// Row iterations per workgroup: ~1024 workgroups (4 waves each) fill the
-// chip; at most 16 iterations so that large batches keep few partial rows.
+// Row iterations per workgroup: ~512 workgroups (4 waves each, two per SIMD,
+// with the next row's loads in flight) -- measured against 256, 384, 768 and
+// 1024 at 16384 x 2048: fewer partial rows to reduce, and enough waves to keep
+// HBM busy (70.0 vs 72.7 us at 1024); at most 16 iterations so that large
+// batches keep few partial rows.
 static uint32_t bwd_iters(uint64_t rows, uint32_t split) {
     const uint64_t per_iter = kBwWaves / split;
-    uint64_t it = (rows + 1024 * per_iter - 1) / (1024 * per_iter);
+    uint64_t it = (rows + 512 * per_iter - 1) / (512 * per_iter);
     if (it < 1) it = 1;
     if (it > 16) it = 16;
     return (uint32_t)it;
