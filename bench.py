@@ -452,9 +452,11 @@ class RmsNormBackward(Workload):
 
 class TernaryI8(Workload):
     """BitLinear int8 x ternary matmul (kore_hip_ternary_matmul_i8) on the
-    pre-quant config's activations: 4096 tokens of 2560 codes against a
-    2560 -> 6912 base-243 ternary weight matrix (BitNet-2B4T FFN shape).
-    MFMA-bound: reported as int8 TOPS against MI355X's 5.0 POP/s dense."""
+    pre-quant config's activations: 4096 tokens (also the decode batches of 64
+    and 1) of 2560 codes against a 2560 -> 6912 base-243 ternary weight matrix
+    (BitNet-2B4T FFN shape).  At 4096 tokens MFMA-bound, reported as int8 TOPS
+    against MI355X's 5.0 POP/s dense; at 1 token bound by the packed weights'
+    HBM bytes."""
     kernel = "ternary_i8_mfma_kernel"
     bound = "mfma"
 
@@ -547,7 +549,7 @@ class Copy(Workload):
 def all_workloads():
     return [RopeQK(False), RopeQK(True), RMSNorm(32, 2048), RMSNorm(16384, 2048), Swiglu(), Gelu(), Embedding(),
             Prequant(4096), Prequant(64), Prequant(1), RmsNormSiluGate(), Softmax(), SoftmaxBackward(),
-            RmsNormBackward(), TernaryI8(), Copy()]
+            RmsNormBackward(), TernaryI8(), TernaryI8(6912, 64, 2560), TernaryI8(6912, 1, 2560), Copy()]
 
 
 # ------------------------------------------------------------------ measure

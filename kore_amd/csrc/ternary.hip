@@ -214,6 +214,108 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
     }
 }
 
+// Small-n path (n <= 16, k % 8 == 0, 8-byte aligned codes): a wave owns 4
+// weight rows and every lane a 40-column window of them (8 packed bytes per
+// row), decoded through the LDS table and reused for every code row:
+// 10 v_dot4_i32_i8 per row and code row, then exact integer wave sums (DPP)
+// and the same epilogue.  K is walked in chunks of 2560 columns (512 packed
+// bytes), past-the-end codes read as 0.  Memory-bound on the packed weights
+// (m * ceil(k/5) bytes) where the MFMA tiles would waste 127/128 of their
+// columns.
+constexpr int kGvRows = 4;     // weight rows per wave
+constexpr int kGvChunk = 2560; // columns per lane-window sweep (64 lanes x 40)
+// Largest n the small-n path takes: measured faster than the MFMA tiles for
+// every n <= 16 (6912 x 16 x 2560: 20.9 vs 24.6 us; 2560 x 16 x 6912: 31.9 vs
+// 125.8 us) and slower beyond (6912 x 64 x 2560: 77.7 vs 27.7 us).
+constexpr uint64_t kGvMaxN = 16;
+
+__device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return __builtin_amdgcn_readlane(v, kWave - 1);
+}
+
+template <int NT>
+__global__ __launch_bounds__(kTmBlock) void ternary_i8_gemv_kernel(TernArgs p) {
+    __shared__ uint64_t lut[256];
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    lut[t] = trit_lut_entry((uint32_t)t);
+    __syncthreads();
+    const uint32_t mrow0 = (blockIdx.x * (kTmBlock / kWave) + t / kWave) * kGvRows;
+    if (mrow0 >= p.m) return;  // uniform per wave; no barrier follows
+    // code rows in groups of NT (the last one partial); each group re-walks K
+    for (uint32_t n0 = 0; n0 < p.n; n0 += NT) {
+    int32_t acc[kGvRows][NT];
+#pragma unroll
+    for (int r = 0; r < kGvRows; ++r)
+#pragma unroll
+        for (int n = 0; n < NT; ++n) acc[r][n] = 0;
+    for (uint32_t k0 = 0; k0 < p.k; k0 += kGvChunk) {
+        const uint32_t kw = k0 + 40u * lane;  // this lane's first column
+        const uint32_t pb = kw / 5u;          // its first packed byte
+        // decode 8 packed bytes of each row -> 40 trits in 10 dwords
+        uint32_t td[kGvRows][10];
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) {
+            const uint32_t m = mrow0 + r;
+            const uint8_t* ar = p.a + (uint64_t)(m < p.m ? m : 0) * p.kp;
+            uint32_t out[10];
+#pragma unroll
+            for (int d = 0; d < 10; ++d) out[d] = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t o = pb + i;
+                const uint32_t b = (m < p.m && o < p.kp) ? ar[o] : kZeroByte;
+                const uint64_t v = lut[b];
+                const int off = 5 * i, d = off >> 2, sh = (off & 3) * 8;
+                out[d] |= (uint32_t)(v << sh);
+                if (d + 1 < 10) out[d + 1] |= (uint32_t)(v >> (32 - sh));
+            }
+#pragma unroll
+            for (int d = 0; d < 10; ++d) td[r][d] = out[d];
+        }
+        // dot with every code row's 40-column window (past k: zeros)
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            if (n0 + n >= p.n) continue;  // (not break: keeps the loop unrolled)
+            const int8_t* qr = p.q + (uint64_t)(n0 + n) * p.k;
+            uint32_t qw[10];
+#pragma unroll
+            for (int h = 0; h < 5; ++h) {
+                const uint32_t c = kw + 8u * h;
+                uint2 v = make_uint2(0u, 0u);
+                if (c < p.k) v = *reinterpret_cast<const uint2*>(qr + c);
+                qw[2 * h] = v.x;
+                qw[2 * h + 1] = v.y;
+            }
+#pragma unroll
+            for (int r = 0; r < kGvRows; ++r) {
+                int32_t a = acc[r][n];
+#pragma unroll
+                for (int d = 0; d < 10; ++d) a = __builtin_amdgcn_sdot4((int)td[r][d], (int)qw[d], a, false);
+                acc[r][n] = a;
+            }
+        }
+    }
+    // exact integer sums over the wave, then ((float)acc * sa[m]) * sq[n]
+#pragma unroll
+    for (int r = 0; r < kGvRows; ++r) {
+        const uint32_t m = mrow0 + r;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            if (n0 + n >= p.n) continue;
+            const int32_t tot = wave_sum_i32(acc[r][n]);
+            if (lane == 0 && m < p.m) p.c[(uint64_t)m * p.n + n0 + n] = ((float)tot * p.sa[m]) * p.sq[n0 + n];
+        }
+    }
+    }
+}
+
 // Generic path: one thread per output, integer accumulation in k order.
 __global__ __launch_bounds__(kTmBlock) void ternary_i8_generic_kernel(TernArgs p) {
     __shared__ uint64_t lut[256];
@@ -251,7 +353,20 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
     const uint64_t kp = (k + 4) / 5;
     TernArgs p{a_packed, a_scales, q, q_scales, c, (uint32_t)m, (uint32_t)n, (uint32_t)k, (uint32_t)kp};
     hipStream_t s = (hipStream_t)stream;
-    const bool vec = k > 0 && k % 16 == 0 && aligned16(q) && (reinterpret_cast<uintptr_t>(c) & 3u) == 0;
+    const bool c_ok = (reinterpret_cast<uintptr_t>(c) & 3u) == 0;
+    if (n <= kGvMaxN && k > 0 && k % 8 == 0 && (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && c_ok) {
+        const uint64_t rows_per_block = (uint64_t)(kTmBlock / kWave) * kGvRows;
+        const uint64_t blocks = (m + rows_per_block - 1) / rows_per_block;
+        if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
+        const dim3 g((uint32_t)blocks), b(kTmBlock);
+        if (n <= 1) hipLaunchKernelGGL(ternary_i8_gemv_kernel<1>, g, b, 0, s, p);
+        else if (n <= 2) hipLaunchKernelGGL(ternary_i8_gemv_kernel<2>, g, b, 0, s, p);
+        else if (n <= 4) hipLaunchKernelGGL(ternary_i8_gemv_kernel<4>, g, b, 0, s, p);
+        else if (n <= 8) hipLaunchKernelGGL(ternary_i8_gemv_kernel<8>, g, b, 0, s, p);
+        else hipLaunchKernelGGL(ternary_i8_gemv_kernel<16>, g, b, 0, s, p);
+        return launch_status();
+    }
+    const bool vec = k > 0 && k % 16 == 0 && aligned16(q) && c_ok;
     if (vec) {
         const uint64_t tiles = ((m + kTmM - 1) / kTmM) * ((n + kTmN - 1) / kTmN);
         const uint64_t per = (tiles + kXcds - 1) / kXcds;

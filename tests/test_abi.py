@@ -87,10 +87,10 @@ def test_rms_norm_backward_workspace_size():
     ws = _lib.load().kore_hip_rms_norm_backward_workspace_bytes
     assert ws(0, 128) == 0 and ws(128, 0) == 0 and ws(2**40, 2**40) == 0
     # vector plan: a row split over S = 1/2/4 waves (cols <= 1024/2048/4096),
-    # 4/S rows per iteration, iters = clamp(ceil(rows / (1024 * 4/S)), 1, 16),
+    # 4/S rows per iteration, iters = clamp(ceil(rows / (512 * 4/S)), 1, 16),
     # P = ceil(rows / (iters * 4/S)) partial rows of cols floats;
     # generic plan: one float per row.
-    assert ws(16384, 2048) == 1024 * 2048 * 4
+    assert ws(16384, 2048) == 512 * 2048 * 4
     assert ws(100, 256) == 25 * 256 * 4
     assert ws(1 << 20, 4096) == 65536 * 4096 * 4
     assert ws(16384, 2050) == 16384 * 4       # cols % 4 != 0 -> generic

@@ -560,6 +560,25 @@ def test_ternary_matmul_i8(m, n, k):
     assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), "ternary_matmul_i8")
 
 
+@pytest.mark.parametrize("m,n,k", [(7, 1, 2560), (6912, 1, 2560), (130, 2, 1000), (257, 3, 6912), (64, 4, 8),
+                                   (33, 8, 2568), (100, 9, 5128), (6912, 16, 2560), (5, 16, 40), (1, 12, 7688),
+                                   (129, 17, 2560), (6912, 64, 2560), (70, 40, 6920)])
+def test_ternary_matmul_i8_small_n(m, n, k):
+    """The small-n path (n <= 16: one wave per 4 weight rows, dot4 over
+    40-column lane windows, K in 2560-column chunks) and the first n past it
+    (MFMA tiles): bit-exact against the oracle on arbitrary packed bytes,
+    ragged m, odd packed-row lengths and k % 16 != 0."""
+    from inputs import int8_codes, raw_packed
+
+    log(f"ternary_matmul_i8 small n m={m} n={n} k={k}")
+    p = raw_packed(m, k, 3 * m + k)
+    q = int8_codes(n, k, n + 7)
+    sa = normal((m,), 8, 1.0, 0.1)
+    sq = np.abs(normal((n,), 9, 0.02, 0.005))
+    got = down(rocm.rocm_ternary_matmul_i8(DEV, up(p), up(sa), up(q), up(sq), m, n, k), np.float32, (m, n))
+    assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), "ternary_matmul_i8 small n")
+
+
 def test_ternary_matmul_i8_full_size_and_pipeline():
     """BitLinear 2560 -> 6912 on 4096 tokens (the pre-quant config's
     activations): bit-exact against an f64 GEMM of the decoded trits (exact
