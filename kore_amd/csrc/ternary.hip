@@ -33,6 +33,8 @@
 //   column l % 32.
 // Generic path (any shape and alignment): one thread per output, the
 // reference loop order.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kore_hip_internal.hpp"
 
@@ -56,6 +58,7 @@ struct TernArgs {
     const float* sq;    // [N]
     float* c;           // [M, N]
     uint32_t m, n, k, kp;
+    uint32_t splits, kt_per;  // split-K: K-tile ranges of kt_per per workgroup
 };
 
 // Five trits of byte b as int8 in the low 40 bits (byte j = trit j).
@@ -73,7 +76,11 @@ __device__ __forceinline__ uint64_t trit_lut_entry(uint32_t b) {
 
 // kAlignedA: packed rows are 16-byte aligned (Kp % 16 == 0) and read as
 // dwordx4; otherwise byte by byte.
-template <bool kAlignedA>
+// kSplit: the workgroup covers K-tiles [split * kt_per, (split + 1) * kt_per)
+// of its output tile and adds its int32 sums into c (zeroed, read as int32)
+// with integer atomics -- exact and order-free, so the result is the same on
+// every run; ternary_i8_finish_kernel then applies the epilogue in place.
+template <bool kAlignedA, bool kSplit>
 __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
     __shared__ uint64_t lut[256];
     __shared__ __attribute__((aligned(16))) uint8_t As[kTmM * kTmPitch];
@@ -89,9 +96,12 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
     // CU's neighbours work on share weights and codes in that XCD's L2.
     const uint32_t tm_n = (p.m + kTmM - 1) / kTmM, tn_n = (p.n + kTmN - 1) / kTmN;
     const uint32_t ntiles = tm_n * tn_n;
-    const uint32_t per = (ntiles + kXcds - 1) / kXcds;
-    const uint32_t lin = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
-    if (lin >= ntiles) return;  // whole workgroup: no barrier reached yet
+    const uint32_t nwork = ntiles * (kSplit ? p.splits : 1u);
+    const uint32_t per = (nwork + kXcds - 1) / kXcds;
+    const uint32_t work = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+    if (work >= nwork) return;  // whole workgroup: no barrier reached yet
+    const uint32_t lin = kSplit ? work / p.splits : work;
+    const uint32_t kt_lo = kSplit ? (work % p.splits) * p.kt_per : 0u;
     const uint32_t grp = lin / (kGroupM * tn_n);
     const uint32_t first_m = grp * kGroupM;
     const uint32_t gsz = min(tm_n - first_m, (uint32_t)kGroupM);
@@ -105,7 +115,8 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
     const uint8_t* arow8 = p.a + (uint64_t)(arow_ok ? m0 + ar : 0) * p.kp;
     const u32x4* arow = reinterpret_cast<const u32x4*>(arow8);
     // B staging: 16-byte pieces c = t + 256u (u < 5) of the 128 x 160 tile.
-    const uint32_t nkt = (p.k + kTmK - 1) / kTmK;
+    const uint32_t nkt_all = (p.k + kTmK - 1) / kTmK;
+    const uint32_t nkt = kSplit ? min(nkt_all, kt_lo + p.kt_per) : nkt_all;
     const u32x4 zero_bytes = {kZeroByte * 0x01010101u, kZeroByte * 0x01010101u, kZeroByte * 0x01010101u,
                               kZeroByte * 0x01010101u};
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
@@ -147,8 +158,8 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
     u32x4 av, bv[5];
-    load_tile(0, av, bv);
-    for (uint32_t kt = 0; kt < nkt; ++kt) {
+    load_tile(kt_lo, av, bv);
+    for (uint32_t kt = kt_lo; kt < nkt; ++kt) {
         __syncthreads();  // previous tile's MFMA reads (and the LUT fill) are done
         // decode 16 packed bytes -> 80 trit bytes, little-endian in 20 dwords
         uint32_t out[20];
@@ -206,15 +217,35 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
             for (int r = 0; r < 16; ++r) {
                 const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (n_ok && m < p.m) {
-                    const float v = ((float)acc[i][j][r] * p.sa[m]) * sqn;
-                    __builtin_nontemporal_store(v, p.c + (uint64_t)m * p.n + n);
+                    if (kSplit) {
+                        atomicAdd(reinterpret_cast<int*>(p.c) + (uint64_t)m * p.n + n, acc[i][j][r]);
+                    } else {
+                        const float v = ((float)acc[i][j][r] * p.sa[m]) * sqn;
+                        __builtin_nontemporal_store(v, p.c + (uint64_t)m * p.n + n);
+                    }
                 }
             }
         }
     }
 }
 
-// Small-n path (n <= 16, k % 8 == 0, 8-byte aligned codes): a wave owns 4
+// Split-K helpers: zero c as int32 (a kernel, not hipMemsetAsync, so the
+// call can be captured in a graph), then turn the int32 sums into
+// ((float)acc * a_scale) * q_scale in place.
+__global__ __launch_bounds__(kTmBlock) void ternary_i8_zero_kernel(int32_t* c, uint64_t total) {
+    const uint64_t i = (uint64_t)blockIdx.x * kTmBlock + threadIdx.x;
+    if (i < total) c[i] = 0;
+}
+
+__global__ __launch_bounds__(kTmBlock) void ternary_i8_finish_kernel(TernArgs p) {
+    const uint64_t i = (uint64_t)blockIdx.x * kTmBlock + threadIdx.x;
+    if (i >= (uint64_t)p.m * p.n) return;
+    const uint32_t m = (uint32_t)(i / p.n), n = (uint32_t)(i % p.n);
+    const int32_t acc = reinterpret_cast<const int32_t*>(p.c)[i];
+    p.c[i] = ((float)acc * p.sa[m]) * p.sq[n];
+}
+
+// Small-n path (n <= 4, k % 8 == 0, 8-byte aligned codes): a wave owns 4
 // weight rows and every lane a 40-column window of them (8 packed bytes per
 // row), decoded through the LDS table and reused for every code row:
 // 10 v_dot4_i32_i8 per row and code row, then exact integer wave sums (DPP)
@@ -224,10 +255,10 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
 // columns.
 constexpr int kGvRows = 4;     // weight rows per wave
 constexpr int kGvChunk = 2560; // columns per lane-window sweep (64 lanes x 40)
-// Largest n the small-n path takes: measured faster than the MFMA tiles for
-// every n <= 16 (6912 x 16 x 2560: 20.9 vs 24.6 us; 2560 x 16 x 6912: 31.9 vs
-// 125.8 us) and slower beyond (6912 x 64 x 2560: 77.7 vs 27.7 us).
-constexpr uint64_t kGvMaxN = 16;
+// Largest n the small-n path takes: against the split-K MFMA tiles it is
+// faster up to n = 4 (6912 x 4 x 2560: 8.7 vs 11.5 us; n = 1: 5.6 vs 11.3 us)
+// and slower from n = 8 (12.6 vs 11.2 us; 2560 x 16 x 6912: 32.8 vs 15.0 us).
+constexpr uint64_t kGvMaxN = 4;
 
 __device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
     v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
@@ -351,7 +382,7 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
     if (!mul_ok(m, n, &mn) || mn > kMaxElements || !mul_ok(n, k, &nk) || nk > kMaxElements)
         return KORE_HIP_ERR_OVERFLOW;
     const uint64_t kp = (k + 4) / 5;
-    TernArgs p{a_packed, a_scales, q, q_scales, c, (uint32_t)m, (uint32_t)n, (uint32_t)k, (uint32_t)kp};
+    TernArgs p{a_packed, a_scales, q, q_scales, c, (uint32_t)m, (uint32_t)n, (uint32_t)k, (uint32_t)kp, 1u, 0u};
     hipStream_t s = (hipStream_t)stream;
     const bool c_ok = (reinterpret_cast<uintptr_t>(c) & 3u) == 0;
     if (n <= kGvMaxN && k > 0 && k % 8 == 0 && (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && c_ok) {
@@ -361,21 +392,41 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
         const dim3 g((uint32_t)blocks), b(kTmBlock);
         if (n <= 1) hipLaunchKernelGGL(ternary_i8_gemv_kernel<1>, g, b, 0, s, p);
         else if (n <= 2) hipLaunchKernelGGL(ternary_i8_gemv_kernel<2>, g, b, 0, s, p);
-        else if (n <= 4) hipLaunchKernelGGL(ternary_i8_gemv_kernel<4>, g, b, 0, s, p);
-        else if (n <= 8) hipLaunchKernelGGL(ternary_i8_gemv_kernel<8>, g, b, 0, s, p);
-        else hipLaunchKernelGGL(ternary_i8_gemv_kernel<16>, g, b, 0, s, p);
+        else hipLaunchKernelGGL(ternary_i8_gemv_kernel<4>, g, b, 0, s, p);
         return launch_status();
     }
     const bool vec = k > 0 && k % 16 == 0 && aligned16(q) && c_ok;
     if (vec) {
         const uint64_t tiles = ((m + kTmM - 1) / kTmM) * ((n + kTmN - 1) / kTmN);
-        const uint64_t per = (tiles + kXcds - 1) / kXcds;
+        const uint64_t nkt = (k + kTmK - 1) / kTmK;
+        // Few output tiles (small m * n): split K so that ~512 workgroups run,
+        // each over at least two K-tiles.
+        uint64_t splits = 1;
+        if (tiles < 128 && nkt >= 4) {
+            splits = std::min<uint64_t>(nkt / 2, (512 + tiles - 1) / tiles);
+            const uint64_t kt_per = (nkt + splits - 1) / splits;
+            splits = (nkt + kt_per - 1) / kt_per;
+            p.splits = (uint32_t)splits;
+            p.kt_per = (uint32_t)kt_per;
+        }
+        const uint64_t work = tiles * splits;
+        const uint64_t per = (work + kXcds - 1) / kXcds;
         if (per * kXcds > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
         const dim3 grid((uint32_t)(per * kXcds));
-        if (kp % 16 == 0 && aligned16(a_packed))
-            hipLaunchKernelGGL(ternary_i8_mfma_kernel<true>, grid, dim3(kTmBlock), 0, s, p);
-        else
-            hipLaunchKernelGGL(ternary_i8_mfma_kernel<false>, grid, dim3(kTmBlock), 0, s, p);
+        const bool al = kp % 16 == 0 && aligned16(a_packed);
+        if (splits > 1) {
+            const dim3 eg((uint32_t)((mn + kTmBlock - 1) / kTmBlock));
+            hipLaunchKernelGGL(ternary_i8_zero_kernel, eg, dim3(kTmBlock), 0, s, reinterpret_cast<int32_t*>(c), mn);
+            if (al)
+                hipLaunchKernelGGL((ternary_i8_mfma_kernel<true, true>), grid, dim3(kTmBlock), 0, s, p);
+            else
+                hipLaunchKernelGGL((ternary_i8_mfma_kernel<false, true>), grid, dim3(kTmBlock), 0, s, p);
+            hipLaunchKernelGGL(ternary_i8_finish_kernel, eg, dim3(kTmBlock), 0, s, p);
+        } else if (al) {
+            hipLaunchKernelGGL((ternary_i8_mfma_kernel<true, false>), grid, dim3(kTmBlock), 0, s, p);
+        } else {
+            hipLaunchKernelGGL((ternary_i8_mfma_kernel<false, false>), grid, dim3(kTmBlock), 0, s, p);
+        }
     } else {
         const uint64_t blocks = (mn + kTmBlock - 1) / kTmBlock;
         if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;

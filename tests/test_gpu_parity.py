@@ -564,10 +564,10 @@ def test_ternary_matmul_i8(m, n, k):
                                    (33, 8, 2568), (100, 9, 5128), (6912, 16, 2560), (5, 16, 40), (1, 12, 7688),
                                    (129, 17, 2560), (6912, 64, 2560), (70, 40, 6920)])
 def test_ternary_matmul_i8_small_n(m, n, k):
-    """The small-n path (n <= 16: one wave per 4 weight rows, dot4 over
-    40-column lane windows, K in 2560-column chunks) and the first n past it
-    (MFMA tiles): bit-exact against the oracle on arbitrary packed bytes,
-    ragged m, odd packed-row lengths and k % 16 != 0."""
+    """The small-n path (n <= 4: one wave per 4 weight rows, dot4 over
+    40-column lane windows, K in 2560-column chunks) and the n past it
+    (split-K MFMA tiles with integer atomics): bit-exact against the oracle on
+    arbitrary packed bytes, ragged m, odd packed-row lengths and k % 16 != 0."""
     from inputs import int8_codes, raw_packed
 
     log(f"ternary_matmul_i8 small n m={m} n={n} k={k}")
