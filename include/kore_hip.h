@@ -236,7 +236,8 @@ int kore_hip_rms_norm_backward_f32(const float *grad_out, const float *x,
  * the integer one of ternary_ternary_matmul and the epilogue its
  * `int_acc as f32 * a_scale * b_scale` (cpu_ternary_matmul.rs:131-193, :188),
  * which replaces ternary_matmul (cpu_ternary_matmul.rs:29-124) fed with
- * dequantised activations.  Exact integer sum: bit-exact.  k <= 2^24. */
+ * dequantised activations.  Exact integer sum: bit-exact.  k <= 2^24.
+ * c must not overlap an input (KORE_HIP_ERR_ALIAS). */
 int kore_hip_ternary_matmul_i8(const uint8_t *a_packed, const float *a_scales,
                                const int8_t *q, const float *q_scales,
                                float *c, uint64_t m, uint64_t n, uint64_t k,

@@ -382,6 +382,18 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
     if (!mul_ok(m, n, &mn) || mn > kMaxElements || !mul_ok(n, k, &nk) || nk > kMaxElements)
         return KORE_HIP_ERR_OVERFLOW;
     const uint64_t kp = (k + 4) / 5;
+    // c is written (and, with split-K, zeroed first) while the inputs are
+    // read: it must not overlap any of them.
+    {
+        const char* c0 = reinterpret_cast<const char*>(c);
+        const char* c1 = c0 + mn * sizeof(float);
+        const struct { const void* p; uint64_t bytes; } ins[] = {
+            {a_packed, m * kp}, {q, nk}, {a_scales, m * sizeof(float)}, {q_scales, n * sizeof(float)}};
+        for (const auto& in : ins) {
+            const char* i0 = reinterpret_cast<const char*>(in.p);
+            if (in.p && in.bytes && i0 < c1 && c0 < i0 + in.bytes) return KORE_HIP_ERR_ALIAS;
+        }
+    }
     TernArgs p{a_packed, a_scales, q, q_scales, c, (uint32_t)m, (uint32_t)n, (uint32_t)k, (uint32_t)kp, 1u, 0u};
     hipStream_t s = (hipStream_t)stream;
     const bool c_ok = (reinterpret_cast<uintptr_t>(c) & 3u) == 0;

@@ -619,6 +619,9 @@ def test_ternary_matmul_i8_edges():
     # argument errors
     assert lib.kore_hip_ternary_matmul_i8(None, None, None, None, None, 2, 2, 16, None) == -1
     assert lib.kore_hip_ternary_matmul_i8(1, 1, 1, 1, 1, 2, 2, (1 << 24) + 1, None) == -3
+    # the output may not overlap an input
+    cb = up(np.zeros(64 * 64 + 64 * 16, np.float32))
+    assert lib.kore_hip_ternary_matmul_i8(1 << 40, 1 << 41, cb.ptr, 1 << 42, cb.ptr, 4, 4, 16, None) == -4
     # unaligned codes take the generic path with identical results
     m, n, k = 40, 9, 320
     from inputs import int8_codes, raw_packed
