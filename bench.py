@@ -657,7 +657,9 @@ def main():
                       "frac_of_mfma_peak": round(tops / MFMA_I8_PEAK_TOPS, 4)})
         if w.name in traffic:
             r["hbm_traffic_bytes"] = traffic[w.name]
-        if hasattr(w, "library_reference"):
+        if hasattr(w, "library_reference") and getattr(w, "n", 8) % 8 != 0:
+            r["library_reference"] = {"skipped": "torch._int_mm needs n % 8 == 0"}
+        elif hasattr(w, "library_reference"):
             try:
                 r["library_reference"] = w.library_reference(torch)
             except Exception as ex:  # the reference is context only
