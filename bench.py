@@ -14,7 +14,7 @@ Per workload:
     launched on give the average kernel duration;
   * algorithmic bytes = every input read once + every output written once;
     achieved GB/s = bytes / average duration; frac = achieved / 8000 GB/s;
-  * inputs are rotated over enough buffer sets to exceed the 256 MB MALL, so
+  * inputs are rotated over enough buffer sets to exceed four times the 256 MB MALL, so
     HBM is measured, not cache;
   * cpu_baseline: the oracle (a C restatement of the reference's CPU
     functions) timed on this host on a bounded sample of the same workload.
@@ -82,8 +82,10 @@ class Workload:
                 delattr(self, k)
 
 
-def n_sets(bytes_per_set: int, cap: int = 8) -> int:
-    return max(1, min(cap, math.ceil(2 * MALL_BYTES / max(bytes_per_set, 1))))
+def n_sets(bytes_per_set: int, cap: int = 16) -> int:
+    # four MALLs' worth: a buffer set is reused only after enough other
+    # traffic to evict it even where some of that traffic bypasses the MALL
+    return max(1, min(cap, math.ceil(4 * MALL_BYTES / max(bytes_per_set, 1))))
 
 
 def randn(torch, shape, seed, mean=0.0, std=1.0):
@@ -116,12 +118,14 @@ class RopeQK(Workload):
         from kore_amd import rocm
 
         self.lib = lib
-        self._dq = randn(torch, (self.B, self.S, self.HQ, self.D), 0)
-        self._dk = randn(torch, (self.B, self.S, self.HK, self.D), 1)
+        self.k = n_sets(self.bytes // 2)
+        self._dq = [randn(torch, (self.B, self.S, self.HQ, self.D), 2 * s) for s in range(self.k)]
+        self._dk = [randn(torch, (self.B, self.S, self.HK, self.D), 2 * s + 1) for s in range(self.k)]
         self._dinv = torch.from_numpy(rocm.rope_inv_freq_host(self.D, 10000.0)).cuda()
 
     def launch(self, i, stream):
-        return self.lib.kore_hip_rope_qk_f32(self._dq.data_ptr(), self._dk.data_ptr(), self._dinv.data_ptr(),
+        j = i % self.k
+        return self.lib.kore_hip_rope_qk_f32(self._dq[j].data_ptr(), self._dk[j].data_ptr(), self._dinv.data_ptr(),
                                              self.B, self.S, self.HQ, self.HK, self.D, 0, int(self.interleaved),
                                              stream)
 
@@ -246,7 +250,7 @@ class Embedding(Workload):
 
         self.lib = lib
         self._dt = randn(torch, (self.V, self.D), 0, 0.0, 0.02)
-        self.k = 4
+        self.k = n_sets(self.bytes)
         self._dids = [torch.from_numpy(embedding_ids(self.N, self.V, seed=s)).cuda() for s in range(self.k)]
         self._do = [torch.empty((self.N, self.D), device="cuda") for _ in range(self.k)]
 
