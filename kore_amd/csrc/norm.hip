@@ -488,6 +488,10 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
         // cpu_fused.rs:466-471: x_hat = (x*inv)*g; y = x_hat * silu(z).
         const f32x4* zr = reinterpret_cast<const f32x4*>(args.z) + row * cols4;
         f32x4* yr = reinterpret_cast<f32x4*>(args.y) + row * cols4;
+        // x_hat first, so that the weights are dead before z is loaded
+        // (keeps the 2560-column kernel within 128 VGPRs: four waves a SIMD)
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) xv[c] = (xv[c] * inv) * wv[c];
         f32x4 zv[NCH];
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
@@ -498,7 +502,7 @@ __global__ __launch_bounds__(kNormBlock) void row_norm_kernel(NormArgs args) {
         for (int c = 0; c < NCH; ++c) {
             const uint32_t f = (uint32_t)c * kWave + lane;
             if (FULL || f < cols4) {
-                const f32x4 xh = (xv[c] * inv) * wv[c];
+                const f32x4 xh = xv[c];
                 f32x4 g;
                 g.x = silu_fast(zv[c].x);
                 g.y = silu_fast(zv[c].y);
