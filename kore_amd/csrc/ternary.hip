@@ -270,7 +270,9 @@ __device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
     return __builtin_amdgcn_readlane(v, kWave - 1);
 }
 
-template <int NT>
+// kAligned8: packed rows start 8-byte aligned (a and Kp), so a lane's window
+// (8 bytes at a multiple of 8) is one load.
+template <int NT, bool kAligned8>
 __global__ __launch_bounds__(kTmBlock) void ternary_i8_gemv_kernel(TernArgs p) {
     __shared__ uint64_t lut[256];
     const int t = threadIdx.x;
@@ -286,22 +288,57 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_gemv_kernel(TernArgs p) {
     for (int r = 0; r < kGvRows; ++r)
 #pragma unroll
         for (int n = 0; n < NT; ++n) acc[r][n] = 0;
+    // bounds of the packed matrix for the unaligned path's dword reads
+    const uintptr_t a_lo = reinterpret_cast<uintptr_t>(p.a);
+    const uintptr_t a_hi = a_lo + (uintptr_t)p.m * p.kp;
     for (uint32_t k0 = 0; k0 < p.k; k0 += kGvChunk) {
         const uint32_t kw = k0 + 40u * lane;  // this lane's first column
         const uint32_t pb = kw / 5u;          // its first packed byte
-        // decode 8 packed bytes of each row -> 40 trits in 10 dwords
-        uint32_t td[kGvRows][10];
+        // the 8 packed bytes of each row (one 8-byte load when the row and
+        // the window allow it; bytes past the row read as five zero trits),
+        // all rows in flight before any is decoded
+        uint32_t pk[kGvRows][2];
 #pragma unroll
         for (int r = 0; r < kGvRows; ++r) {
             const uint32_t m = mrow0 + r;
             const uint8_t* ar = p.a + (uint64_t)(m < p.m ? m : 0) * p.kp;
+            const uintptr_t wa = reinterpret_cast<uintptr_t>(ar + pb);  // window address
+            const uintptr_t w0 = wa & ~(uintptr_t)3;
+            if (kAligned8 && m < p.m && pb + 8u <= p.kp) {
+                const uint2 v = *reinterpret_cast<const uint2*>(ar + pb);
+                pk[r][0] = v.x;
+                pk[r][1] = v.y;
+            } else if (!kAligned8 && m < p.m && pb + 8u <= p.kp && w0 >= a_lo && w0 + 12u <= a_hi) {
+                // unaligned row: the three dwords around the window, shifted
+                const uint3 v = *reinterpret_cast<const uint3*>(w0);
+                const uint32_t sh = (uint32_t)(wa & 3u);
+                pk[r][0] = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+                pk[r][1] = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+            } else if (m >= p.m || pb >= p.kp) {
+                pk[r][0] = pk[r][1] = kZeroByte * 0x01010101u;  // window past the row
+            } else {
+                // byte by byte; out-of-row bytes load byte 0 of the row (always
+                // valid) and are replaced, so every load issues unconditionally
+                pk[r][0] = pk[r][1] = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t o = pb + i;
+                    const bool ok = m < p.m && o < p.kp;
+                    const uint32_t b = ar[ok ? o : 0u];
+                    pk[r][i >> 2] |= (ok ? b : kZeroByte) << (8 * (i & 3));
+                }
+            }
+        }
+        // decode -> 40 trits in 10 dwords per row
+        uint32_t td[kGvRows][10];
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) {
             uint32_t out[10];
 #pragma unroll
             for (int d = 0; d < 10; ++d) out[d] = 0;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const uint32_t o = pb + i;
-                const uint32_t b = (m < p.m && o < p.kp) ? ar[o] : kZeroByte;
+                const uint32_t b = (pk[r][i >> 2] >> (8 * (i & 3))) & 0xffu;
                 const uint64_t v = lut[b];
                 const int off = 5 * i, d = off >> 2, sh = (off & 3) * 8;
                 out[d] |= (uint32_t)(v << sh);
@@ -402,9 +439,16 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
         const uint64_t blocks = (m + rows_per_block - 1) / rows_per_block;
         if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
         const dim3 g((uint32_t)blocks), b(kTmBlock);
-        if (n <= 1) hipLaunchKernelGGL(ternary_i8_gemv_kernel<1>, g, b, 0, s, p);
-        else if (n <= 2) hipLaunchKernelGGL(ternary_i8_gemv_kernel<2>, g, b, 0, s, p);
-        else hipLaunchKernelGGL(ternary_i8_gemv_kernel<4>, g, b, 0, s, p);
+        const bool al8 = kp % 8 == 0 && (reinterpret_cast<uintptr_t>(a_packed) & 7u) == 0;
+        if (al8) {
+            if (n <= 1) hipLaunchKernelGGL((ternary_i8_gemv_kernel<1, true>), g, b, 0, s, p);
+            else if (n <= 2) hipLaunchKernelGGL((ternary_i8_gemv_kernel<2, true>), g, b, 0, s, p);
+            else hipLaunchKernelGGL((ternary_i8_gemv_kernel<4, true>), g, b, 0, s, p);
+        } else {
+            if (n <= 1) hipLaunchKernelGGL((ternary_i8_gemv_kernel<1, false>), g, b, 0, s, p);
+            else if (n <= 2) hipLaunchKernelGGL((ternary_i8_gemv_kernel<2, false>), g, b, 0, s, p);
+            else hipLaunchKernelGGL((ternary_i8_gemv_kernel<4, false>), g, b, 0, s, p);
+        }
         return launch_status();
     }
     const bool vec = k > 0 && k % 16 == 0 && aligned16(q) && c_ok;
