@@ -272,15 +272,26 @@ __device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
 
 // kAligned8: packed rows start 8-byte aligned (a and Kp), so a lane's window
 // (8 bytes at a multiple of 8) is one load.
-template <int NT, bool kAligned8>
+// W: waves per group of kGvRows weight rows.  With K longer than one chunk
+// the W waves of a group take chunks ks, ks + W, ... (ks = wave % W) so that
+// their loads are in flight together; their exact int32 sums meet in LDS and
+// the group's first wave adds them (fixed order) and applies the epilogue.
+template <int NT, bool kAligned8, int W>
 __global__ __launch_bounds__(kTmBlock) void ternary_i8_gemv_kernel(TernArgs p) {
+    constexpr int kWaves = kTmBlock / kWave;
     __shared__ uint64_t lut[256];
+    __shared__ int32_t part[kWaves][kGvRows][NT];
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
+    const int wave = t / kWave;
+    const int ks = wave % W;
     lut[t] = trit_lut_entry((uint32_t)t);
     __syncthreads();
-    const uint32_t mrow0 = (blockIdx.x * (kTmBlock / kWave) + t / kWave) * kGvRows;
-    if (mrow0 >= p.m) return;  // uniform per wave; no barrier follows
+    const uint32_t mrow0 = (blockIdx.x * (kWaves / W) + wave / W) * kGvRows;
+    const bool live = mrow0 < p.m;  // uniform per wave; every wave reaches the barriers
+    // bounds of the packed matrix for the unaligned path's dword reads
+    const uintptr_t a_lo = reinterpret_cast<uintptr_t>(p.a);
+    const uintptr_t a_hi = a_lo + (uintptr_t)p.m * p.kp;
     // code rows in groups of NT (the last one partial); each group re-walks K
     for (uint32_t n0 = 0; n0 < p.n; n0 += NT) {
     int32_t acc[kGvRows][NT];
@@ -288,10 +299,7 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_gemv_kernel(TernArgs p) {
     for (int r = 0; r < kGvRows; ++r)
 #pragma unroll
         for (int n = 0; n < NT; ++n) acc[r][n] = 0;
-    // bounds of the packed matrix for the unaligned path's dword reads
-    const uintptr_t a_lo = reinterpret_cast<uintptr_t>(p.a);
-    const uintptr_t a_hi = a_lo + (uintptr_t)p.m * p.kp;
-    for (uint32_t k0 = 0; k0 < p.k; k0 += kGvChunk) {
+    for (uint32_t k0 = (uint32_t)ks * kGvChunk; live && k0 < p.k; k0 += (uint32_t)W * kGvChunk) {
         const uint32_t kw = k0 + 40u * lane;  // this lane's first column
         const uint32_t pb = kw / 5u;          // its first packed byte
         // the 8 packed bytes of each row (one 8-byte load when the row and
@@ -329,8 +337,29 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_gemv_kernel(TernArgs p) {
                 }
             }
         }
-        // decode -> 40 trits in 10 dwords per row
-        uint32_t td[kGvRows][10];
+        // every code row's 40-column window, also in flight; 8-column pieces
+        // past k read the row's first 8 codes instead (in bounds), which meet
+        // the zeroed trits below
+        uint32_t qw[NT][10];
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            const uint32_t nn = n0 + n < p.n ? n0 + n : 0u;
+            const int8_t* qr = p.q + (uint64_t)nn * p.k;
+#pragma unroll
+            for (int h = 0; h < 5; ++h) {
+                const uint32_t c = kw + 8u * h;
+                const uint2 v = *reinterpret_cast<const uint2*>(qr + (c < p.k ? c : 0u));
+                qw[n][2 * h] = v.x;
+                qw[n][2 * h + 1] = v.y;
+            }
+        }
+        // decode -> 40 trits in 10 dwords per row (all table reads issued
+        // first), dot with the code windows
+        uint64_t lv[kGvRows][8];
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) lv[r][i] = lut[(pk[r][i >> 2] >> (8 * (i & 3))) & 0xffu];
 #pragma unroll
         for (int r = 0; r < kGvRows; ++r) {
             uint32_t out[10];
@@ -338,50 +367,75 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_gemv_kernel(TernArgs p) {
             for (int d = 0; d < 10; ++d) out[d] = 0;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const uint32_t b = (pk[r][i >> 2] >> (8 * (i & 3))) & 0xffu;
-                const uint64_t v = lut[b];
+                const uint64_t v = lv[r][i];
                 const int off = 5 * i, d = off >> 2, sh = (off & 3) * 8;
                 out[d] |= (uint32_t)(v << sh);
                 if (d + 1 < 10) out[d + 1] |= (uint32_t)(v >> (32 - sh));
             }
+            // trits of columns >= k (a last byte's padding) are not in the
+            // sum (k % 4 == 0: whole dwords)
 #pragma unroll
-            for (int d = 0; d < 10; ++d) td[r][d] = out[d];
-        }
-        // dot with every code row's 40-column window (past k: zeros)
+            for (int d = 0; d < 10; ++d) out[d] = kw + 4u * d < p.k ? out[d] : 0u;
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            if (n0 + n >= p.n) continue;  // (not break: keeps the loop unrolled)
-            const int8_t* qr = p.q + (uint64_t)(n0 + n) * p.k;
-            uint32_t qw[10];
-#pragma unroll
-            for (int h = 0; h < 5; ++h) {
-                const uint32_t c = kw + 8u * h;
-                uint2 v = make_uint2(0u, 0u);
-                if (c < p.k) v = *reinterpret_cast<const uint2*>(qr + c);
-                qw[2 * h] = v.x;
-                qw[2 * h + 1] = v.y;
-            }
-#pragma unroll
-            for (int r = 0; r < kGvRows; ++r) {
+            for (int n = 0; n < NT; ++n) {
                 int32_t a = acc[r][n];
 #pragma unroll
-                for (int d = 0; d < 10; ++d) a = __builtin_amdgcn_sdot4((int)td[r][d], (int)qw[d], a, false);
+                for (int d = 0; d < 10; ++d) a = __builtin_amdgcn_sdot4((int)out[d], (int)qw[n][d], a, false);
                 acc[r][n] = a;
             }
         }
     }
-    // exact integer sums over the wave, then ((float)acc * sa[m]) * sq[n]
+    // exact integer sums over the wave (and the group's W waves), then
+    // ((float)acc * sa[m]) * sq[n]
+    int32_t tot[kGvRows][NT];
 #pragma unroll
-    for (int r = 0; r < kGvRows; ++r) {
-        const uint32_t m = mrow0 + r;
+    for (int r = 0; r < kGvRows; ++r)
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            if (n0 + n >= p.n) continue;
-            const int32_t tot = wave_sum_i32(acc[r][n]);
-            if (lane == 0 && m < p.m) p.c[(uint64_t)m * p.n + n0 + n] = ((float)tot * p.sa[m]) * p.sq[n0 + n];
+        for (int n = 0; n < NT; ++n) tot[r][n] = wave_sum_i32(acc[r][n]);
+    if (W > 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < kGvRows; ++r)
+#pragma unroll
+                for (int n = 0; n < NT; ++n) part[wave][r][n] = tot[r][n];
+        }
+        __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int r = 0; r < kGvRows; ++r)
+#pragma unroll
+                for (int n = 0; n < NT; ++n) {
+                    int32_t v = 0;
+#pragma unroll
+                    for (int j = 0; j < W; ++j) v += part[wave + j][r][n];
+                    tot[r][n] = v;
+                }
+        }
+        __syncthreads();  // part is rewritten by the next code-row group
+    }
+    if (ks == 0 && live && lane == 0) {
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) {
+            const uint32_t m = mrow0 + r;
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                if (n0 + n >= p.n || m >= p.m) continue;
+                p.c[(uint64_t)m * p.n + n0 + n] = ((float)tot[r][n] * p.sa[m]) * p.sq[n0 + n];
+            }
         }
     }
     }
+}
+
+template <int NT, bool kAligned8>
+static void launch_gemv(const TernArgs& p, uint64_t m, uint64_t k, hipStream_t s) {
+    const uint64_t chunks = (k + kGvChunk - 1) / kGvChunk;
+    const int w = chunks >= 3 ? 4 : (chunks == 2 ? 2 : 1);
+    const uint64_t rows_per_block = (uint64_t)(kTmBlock / kWave / w) * kGvRows;
+    const dim3 g((uint32_t)((m + rows_per_block - 1) / rows_per_block)), b(kTmBlock);
+    if (w == 4) hipLaunchKernelGGL((ternary_i8_gemv_kernel<NT, kAligned8, 4>), g, b, 0, s, p);
+    else if (w == 2) hipLaunchKernelGGL((ternary_i8_gemv_kernel<NT, kAligned8, 2>), g, b, 0, s, p);
+    else hipLaunchKernelGGL((ternary_i8_gemv_kernel<NT, kAligned8, 1>), g, b, 0, s, p);
 }
 
 // Generic path: one thread per output, integer accumulation in k order.
@@ -435,19 +489,16 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
     hipStream_t s = (hipStream_t)stream;
     const bool c_ok = (reinterpret_cast<uintptr_t>(c) & 3u) == 0;
     if (n <= kGvMaxN && k > 0 && k % 8 == 0 && (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && c_ok) {
-        const uint64_t rows_per_block = (uint64_t)(kTmBlock / kWave) * kGvRows;
-        const uint64_t blocks = (m + rows_per_block - 1) / rows_per_block;
-        if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
-        const dim3 g((uint32_t)blocks), b(kTmBlock);
+        // grid: at most m / 4 blocks of one wave group (m < 2^31)
         const bool al8 = kp % 8 == 0 && (reinterpret_cast<uintptr_t>(a_packed) & 7u) == 0;
         if (al8) {
-            if (n <= 1) hipLaunchKernelGGL((ternary_i8_gemv_kernel<1, true>), g, b, 0, s, p);
-            else if (n <= 2) hipLaunchKernelGGL((ternary_i8_gemv_kernel<2, true>), g, b, 0, s, p);
-            else hipLaunchKernelGGL((ternary_i8_gemv_kernel<4, true>), g, b, 0, s, p);
+            if (n <= 1) launch_gemv<1, true>(p, m, k, s);
+            else if (n <= 2) launch_gemv<2, true>(p, m, k, s);
+            else launch_gemv<4, true>(p, m, k, s);
         } else {
-            if (n <= 1) hipLaunchKernelGGL((ternary_i8_gemv_kernel<1, false>), g, b, 0, s, p);
-            else if (n <= 2) hipLaunchKernelGGL((ternary_i8_gemv_kernel<2, false>), g, b, 0, s, p);
-            else hipLaunchKernelGGL((ternary_i8_gemv_kernel<4, false>), g, b, 0, s, p);
+            if (n <= 1) launch_gemv<1, false>(p, m, k, s);
+            else if (n <= 2) launch_gemv<2, false>(p, m, k, s);
+            else launch_gemv<4, false>(p, m, k, s);
         }
         return launch_status();
     }
