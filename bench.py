@@ -40,6 +40,9 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 PEAK_GBS = 8000.0
 MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
+# MI355X vector fp32 FMA without packed math: 256 CUs x 4 SIMDs x 16 lanes x
+# 2 flops x 2.4 GHz
+VALU_F32_PEAK_TFLOPS = 78.6
 MALL_BYTES = 256 << 20
 
 
@@ -524,6 +527,55 @@ class TernaryI8(Workload):
             f"{m} weight rows x {n} tokens, single thread", 2 * m * n * self.k
 
 
+class TernaryF32(Workload):
+    """BitLinear matmul on f32 activations (kore_hip_ternary_matmul_f32, the
+    reference's ternary_matmul as BitLinear::forward calls it): the same
+    2560 -> 6912 weights on a decode batch.  Every output is the reference's
+    sequential f32 fold over K (bit-exact), one fma per term and lane, so the
+    kernel is bound by vector issue along the K chain; reported as fp32 FMA
+    throughput (2 flops per term) next to the bytes."""
+    kernel = "ternary_f32_seq_kernel"
+    bound = "valu"
+
+    def __init__(self, m=6912, n=1, k=2560):
+        self.m, self.n, self.k = m, n, k
+        self.kp = (k + 4) // 5
+        self.name = f"ternary_f32_{m}x{n}x{k}"
+        self.tokens = n
+        self.ops = 2 * m * n * k
+        self.bytes = m * self.kp + 4 * k * n + 4 * m * n + 4 * m
+        self.desc = (f"BitLinear f32 x ternary matmul c[{m},{n}] = (sum_k trits[{m},{k}] * b[{k},{n}]) * a_scale, "
+                     "sequential f32 fold in k order (bit-exact)")
+
+    def setup(self, torch, lib):
+        self.lib = lib
+        self.k_sets = 4
+        g = torch.Generator(device="cuda")
+        g.manual_seed(0)
+        self._da = [torch.randint(0, 243, (self.m * self.kp,), generator=g, dtype=torch.uint8, device="cuda")
+                    for _ in range(self.k_sets)]
+        self._db = [torch.randn((self.k * self.n,), generator=g, device="cuda") for _ in range(self.k_sets)]
+        self._dsa = torch.rand(self.m, generator=g, device="cuda")
+        self._dc = [torch.empty(self.m * self.n, device="cuda") for _ in range(self.k_sets)]
+
+    def launch(self, i, stream):
+        j = i % self.k_sets
+        return self.lib.kore_hip_ternary_matmul_f32(self._da[j].data_ptr(), self._dsa.data_ptr(),
+                                                    self._db[j].data_ptr(), self._dc[j].data_ptr(), self.m, self.n,
+                                                    self.k, stream)
+
+    def cpu_sample(self):
+        import oracle
+        from inputs import normal, raw_packed
+
+        m = 512
+        p, b = raw_packed(m, self.k, 1), normal((self.k, self.n), 2)
+        sa = np.ones(m, np.float32)
+        return (lambda: oracle.ternary_matmul(p, sa, b, m, self.n, self.k)), \
+            m * self.kp + 4 * self.k * self.n + 4 * m * self.n, self.n * m / self.m, 1, \
+            f"{m} weight rows x {self.n} tokens, single thread", 2 * m * self.n * self.k
+
+
 class Copy(Workload):
     """A plain 1 GiB device copy through the gather kernel with ids = 0..N-1;
     used to calibrate rocprof's FETCH_SIZE / WRITE_SIZE counters."""
@@ -553,7 +605,8 @@ class Copy(Workload):
 def all_workloads():
     return [RopeQK(False), RopeQK(True), RMSNorm(32, 2048), RMSNorm(16384, 2048), Swiglu(), Gelu(), Embedding(),
             Prequant(4096), Prequant(64), Prequant(1), RmsNormSiluGate(), Softmax(), SoftmaxBackward(),
-            RmsNormBackward(), TernaryI8(), TernaryI8(6912, 64, 2560), TernaryI8(6912, 1, 2560), Copy()]
+            RmsNormBackward(), TernaryI8(), TernaryI8(6912, 64, 2560), TernaryI8(6912, 1, 2560), TernaryF32(),
+            TernaryF32(6912, 64, 2560), Copy()]
 
 
 # ------------------------------------------------------------------ measure
@@ -600,8 +653,8 @@ def time_cpu(w: Workload, budget_s: float):
            "ns_per_token": round(per / ntok * 1e9, 1), "seconds": round(t, 2), "reps": reps,
            "sample": desc, "host_cores": os.cpu_count()}
     if ops:
-        out.update({"value": round(ops / per / 1e9, 4), "unit": "GOP/s (int8 multiply-adds x 2)",
-                    "gbs": round(nbytes / per / 1e9, 4)})
+        unit = "GOP/s (int8 multiply-adds x 2)" if w.bound == "mfma" else "GFLOP/s (f32 fold, 2 per term)"
+        out.update({"value": round(ops / per / 1e9, 4), "unit": unit, "gbs": round(nbytes / per / 1e9, 4)})
     return out
 
 
@@ -657,8 +710,11 @@ def main():
         }
         if w.ops:
             tops = w.ops / (ms * 1e-3) / 1e12
-            r.update({"bound": w.bound, "ops_per_launch": w.ops, "achieved_tops": round(tops, 1),
-                      "frac_of_mfma_peak": round(tops / MFMA_I8_PEAK_TOPS, 4)})
+            r.update({"bound": w.bound, "ops_per_launch": w.ops, "achieved_tops": round(tops, 3)})
+            if w.bound == "mfma":
+                r["frac_of_mfma_peak"] = round(tops / MFMA_I8_PEAK_TOPS, 4)
+            else:
+                r["frac_of_valu_f32_peak"] = round(tops / VALU_F32_PEAK_TFLOPS, 4)
         if w.name in traffic:
             r["hbm_traffic_bytes"] = traffic[w.name]
         if hasattr(w, "library_reference") and getattr(w, "n", 8) % 8 != 0:
@@ -674,8 +730,11 @@ def main():
             print(f"[bench] {w.name}: cpu baseline", file=sys.stderr, flush=True)
             r["cpu_baseline"] = time_cpu(w, args.cpu_seconds if w.name == "rope_qk" else args.cpu_seconds / 3)
         results[w.name] = r
-        extra = (f", {r['achieved_tops']} TOPS ({100 * r['frac_of_mfma_peak']:.1f}% of the int8 MFMA peak)"
-                 if w.ops else "")
+        extra = ""
+        if w.ops and w.bound == "mfma":
+            extra = f", {r['achieved_tops']} TOPS ({100 * r['frac_of_mfma_peak']:.1f}% of the int8 MFMA peak)"
+        elif w.ops:
+            extra = f", {r['achieved_tops']} TFLOP/s ({100 * r['frac_of_valu_f32_peak']:.1f}% of the fp32 FMA peak)"
         print(f"[bench] {w.name}: {r['kernel_us']} us, {r['achieved_gbs']} GB/s ({100 * r['frac_of_peak']:.1f}% "
               f"of peak), {r['ns_per_token']} ns/token{extra}", file=sys.stderr, flush=True)
 

@@ -243,6 +243,17 @@ int kore_hip_ternary_matmul_i8(const uint8_t *a_packed, const float *a_scales,
                                float *c, uint64_t m, uint64_t n, uint64_t k,
                                kore_stream_t stream);
 
+/* c[M,N] = (sum over k, in order, of t[m,k] * b[k,n]) * a_scales[m] with f32
+ * activations b[K,N] row-major: replaces ternary_matmul
+ * (crates/kore-kernels/src/cpu_ternary_matmul.rs:29-124; unpack_row_trits
+ * :91-101, compute_row :105-124), which BitLinear::forward
+ * (crates/kore-nn/src/bit_linear.rs:175-237) calls with the transposed input.
+ * The sum is the reference's sequential f32 fold that skips zero trits, so c
+ * is bit-exact.  c must not overlap the inputs (KORE_HIP_ERR_ALIAS). */
+int kore_hip_ternary_matmul_f32(const uint8_t *a_packed, const float *a_scales,
+                                const float *b, float *c, uint64_t m,
+                                uint64_t n, uint64_t k, kore_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

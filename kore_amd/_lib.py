@@ -46,6 +46,7 @@ SIGNATURES = {
     "kore_hip_cross_entropy_backward_f32": [_ptr, _ptr, _ptr, _u64, _u64, _ptr],
     "kore_hip_rms_norm_backward_f32": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _f32, _ptr],
     "kore_hip_ternary_matmul_i8": [_ptr, _ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _ptr],
+    "kore_hip_ternary_matmul_f32": [_ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _ptr],
 }
 
 # Entry points whose return type is not int.

@@ -457,6 +457,212 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_generic_kernel(TernArgs p
     p.c[idx] = ((float)acc * p.sa[m]) * p.sq[n];
 }
 
+// ---------------------------------------------------------------------------
+// f32 activations (the reference's ternary_matmul, cpu_ternary_matmul.rs:29-124,
+// which BitLinear::forward calls): c[m, col] = (sum over ki in order of
+// t[m, ki] * b[ki, col]) * a_scales[m] with b[K, N] f32 and the sum a
+// sequential f32 fold that skips zero trits (compute_row :105-124).  Every
+// lane owns one output and folds its K terms in the reference's order, so the
+// result is bit-exact: acc = fma(t, b, acc) is fl(acc + t*b) (t*b = +-b is
+// exact), and a zero trit adds +-0, which leaves acc unchanged (acc is never
+// -0: it starts at +0 and an exact-zero sum rounds to +0) -- except when b is
+// Inf or NaN (0 * Inf = NaN), so chunks holding such a b skip zero trits
+// explicitly.  Issue-bound: one fma, one LDS read of b and a fifth of a table
+// read per term and lane.
+//
+// Block: 4 waves; a wave's 64 lanes are CT columns x 64/CT rows.  Per chunk
+// of kF32Kc columns of K the block stages b[kc.., col0..col0+CT) in LDS
+// ([ki][c]: lanes of one row read consecutive banks, lanes of one column
+// broadcast) and every lane loads its row's packed bytes of the chunk.
+constexpr int kF32Kc = 160;           // K columns per chunk (32 packed bytes)
+constexpr int kF32Bytes = kF32Kc / 5;
+
+struct TernF32Args {
+    const uint8_t* a;   // packed [M, Kp]
+    const float* sa;    // [M]
+    const float* b;     // [K, N]
+    float* c;           // [M, N]
+    uint32_t m, n, k, kp;
+};
+
+template <int CT, int R, bool kAligned16>
+__global__ __launch_bounds__(kTmBlock) void ternary_f32_seq_kernel(TernF32Args p) {
+    constexpr int kSlots = (kTmBlock / kWave) * (kWave / CT);  // row slots per block
+    constexpr int RB = kSlots * R;                               // rows per block
+    constexpr int kSub = 8 / R;  // packed bytes whose operands are read ahead of their fmas
+    __shared__ __attribute__((aligned(16))) float flut[256 * 8];  // byte -> 5 trits as floats
+    // b of the chunk, per column c: 32 groups of 8 floats (the 5 columns of K
+    // one packed byte covers, padded), so a lane reads its 5 terms as one
+    // 16-byte and one 4-byte read; odd pitch in 16-byte units
+    constexpr int kPitch = kF32Bytes * 8 + 4;
+    __shared__ __attribute__((aligned(16))) float bs[CT * kPitch];
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = t / kWave;
+    {
+        uint32_t v = (uint32_t)t;
+        const bool pad = v >= 243u;
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            flut[t * 8 + j] = pad ? 0.0f : (float)((int)(v % 3u) - 1);
+            v /= 3u;
+        }
+    }
+    const uint32_t col0 = blockIdx.y * CT;
+    const int cl = lane % CT;
+    const uint32_t col = col0 + cl;
+    const uint32_t slot = (uint32_t)(wave * (kWave / CT) + lane / CT);
+    // this lane's R rows (independent folds, interleaved so that each hides
+    // the others' latency)
+    uint32_t rows[R];
+    const uint8_t* arow[R];
+    bool live[R];
+    bool any_live = false;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        rows[i] = blockIdx.x * RB + slot + (uint32_t)i * kSlots;
+        live[i] = rows[i] < p.m && col < p.n;
+        any_live |= live[i];
+        arow[i] = p.a + (uint64_t)(rows[i] < p.m ? rows[i] : 0) * p.kp;
+    }
+    const uintptr_t a_hi = reinterpret_cast<uintptr_t>(p.a) + (uintptr_t)p.m * p.kp;
+    // A chunk's operands are loaded one chunk ahead into registers (every
+    // load unconditional, at a clamped in-bounds index, so none waits for
+    // another), then b goes to LDS for the chunk's folds.
+    constexpr int kStage = (kF32Kc * CT + kTmBlock - 1) / kTmBlock;  // b elements per thread
+    uint32_t pbn[R][kF32Bytes / 4];  // packed bytes, 4 per register
+    float bvn[kStage];
+    auto load_chunk = [&](uint32_t kc) {
+        const uint32_t kn = min((uint32_t)kF32Kc, p.k - kc);
+        const uint32_t pb0 = kc / 5u;
+        // each row's 32 packed bytes of the chunk: two 16-byte loads (aligned
+        // rows), nine dwords shifted into place (unaligned rows), or bytes
+        // (the row's end)
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const uintptr_t wa = reinterpret_cast<uintptr_t>(arow[i] + pb0);
+            const uintptr_t w0 = wa & ~(uintptr_t)3;
+            if (kAligned16 && pb0 + kF32Bytes <= p.kp) {
+                const u32x4 x0 = *reinterpret_cast<const u32x4*>(arow[i] + pb0);
+                const u32x4 x1 = *reinterpret_cast<const u32x4*>(arow[i] + pb0 + 16);
+                pbn[i][0] = x0[0]; pbn[i][1] = x0[1]; pbn[i][2] = x0[2]; pbn[i][3] = x0[3];
+                pbn[i][4] = x1[0]; pbn[i][5] = x1[1]; pbn[i][6] = x1[2]; pbn[i][7] = x1[3];
+            } else if (!kAligned16 && pb0 + kF32Bytes <= p.kp && w0 + 36u <= a_hi) {
+                uint32_t d[9];
+#pragma unroll
+                for (int q = 0; q < 9; ++q) d[q] = reinterpret_cast<const uint32_t*>(w0)[q];
+                const uint32_t sh = (uint32_t)(wa & 3u);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) pbn[i][q] = __builtin_amdgcn_alignbyte(d[q + 1], d[q], sh);
+            } else {
+#pragma unroll
+                for (int q = 0; q < kF32Bytes / 4; ++q) pbn[i][q] = 0;
+#pragma unroll
+                for (int j = 0; j < kF32Bytes; ++j) {
+                    const uint32_t o = pb0 + j;
+                    pbn[i][j >> 2] |= (uint32_t)arow[i][o < p.kp ? o : 0u] << (8 * (j & 3));
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const uint32_t e = (uint32_t)t + kTmBlock * u;
+            const uint32_t ki = e / CT, c = e % CT;
+            const bool ok = e < kn * CT && col0 + c < p.n;
+            const float v = p.b[ok ? (uint64_t)(kc + ki) * p.n + col0 + c : 0u];
+            bvn[u] = ok ? v : 0.0f;
+        }
+    };
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = 0.0f;
+    if (p.k > 0) load_chunk(0);
+    for (uint32_t kc = 0; kc < p.k; kc += kF32Kc) {
+        const uint32_t kn = min((uint32_t)kF32Kc, p.k - kc);
+        __syncthreads();  // the previous chunk's b reads are done (and the table is filled)
+        bool bad = false;
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const uint32_t e = (uint32_t)t + kTmBlock * u;
+            const uint32_t ki = e / CT, c = e % CT;
+            if (e < (uint32_t)(kF32Kc * CT)) bs[c * kPitch + (ki / 5u) * 8u + ki % 5u] = bvn[u];
+            bad |= !__builtin_isfinite(bvn[u]);
+        }
+        uint32_t pb[R][kF32Bytes / 4];
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int q = 0; q < kF32Bytes / 4; ++q) pb[i][q] = pbn[i][q];
+        const uint32_t pb0 = kc / 5u;
+        const bool skip_zero = __syncthreads_or(bad);
+        if (kc + kF32Kc < p.k) load_chunk(kc + kF32Kc);
+        if (!any_live) continue;
+        const float* bc = bs + cl * kPitch;
+        if (kn == (uint32_t)kF32Kc && !skip_zero) {
+#pragma unroll
+            for (int j0 = 0; j0 < kF32Bytes; j0 += kSub) {
+                f32x4 b4[kSub], t4[R][kSub];
+                float b5[kSub], t5[R][kSub];
+#pragma unroll
+                for (int jj = 0; jj < kSub; ++jj) {
+                    const int j = j0 + jj;
+                    b4[jj] = *reinterpret_cast<const f32x4*>(bc + 8 * j);
+                    b5[jj] = bc[8 * j + 4];
+#pragma unroll
+                    for (int i = 0; i < R; ++i) {
+                        const uint32_t byte = (pb[i][j >> 2] >> (8 * (j & 3))) & 0xffu;
+                        t4[i][jj] = *reinterpret_cast<const f32x4*>(flut + byte * 8);
+                        t5[i][jj] = flut[byte * 8 + 4];
+                    }
+                }
+#pragma unroll
+                for (int jj = 0; jj < kSub; ++jj)
+#pragma unroll
+                    for (int i = 0; i < R; ++i) {
+                        acc[i] = __builtin_fmaf(t4[i][jj].x, b4[jj].x, acc[i]);
+                        acc[i] = __builtin_fmaf(t4[i][jj].y, b4[jj].y, acc[i]);
+                        acc[i] = __builtin_fmaf(t4[i][jj].z, b4[jj].z, acc[i]);
+                        acc[i] = __builtin_fmaf(t4[i][jj].w, b4[jj].w, acc[i]);
+                        acc[i] = __builtin_fmaf(t5[i][jj], b5[jj], acc[i]);
+                    }
+            }
+        } else {
+            // last partial chunk, or Inf/NaN in b: bounds and zero trits checked
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                for (uint32_t ki = 0; ki < kn; ++ki) {
+                    const uint32_t o = pb0 + ki / 5u;
+                    const float tr = flut[(uint32_t)arow[i][o < p.kp ? o : 0u] * 8 + ki % 5u];
+                    if (tr != 0.0f) acc[i] = __builtin_fmaf(tr, bc[(ki / 5u) * 8u + ki % 5u], acc[i]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+        if (live[i]) p.c[(uint64_t)rows[i] * p.n + col] = acc[i] * p.sa[rows[i]];
+}
+
+// rows per lane: 1 for narrow column tiles (many waves, one fold each), more
+// for wide ones (b staged once for more rows, folds interleaved)
+template <int CT>
+constexpr int f32_rows_per_lane() { return CT >= 16 ? 4 : 1; }
+
+template <bool kAligned16>
+static void launch_f32_seq(int ct, dim3 g, dim3 blk, hipStream_t s, const TernF32Args& p) {
+    switch (ct) {
+        case 1: hipLaunchKernelGGL((ternary_f32_seq_kernel<1, f32_rows_per_lane<1>(), kAligned16>), g, blk, 0, s, p); break;
+        case 2: hipLaunchKernelGGL((ternary_f32_seq_kernel<2, f32_rows_per_lane<2>(), kAligned16>), g, blk, 0, s, p); break;
+        case 4: hipLaunchKernelGGL((ternary_f32_seq_kernel<4, f32_rows_per_lane<4>(), kAligned16>), g, blk, 0, s, p); break;
+        case 8: hipLaunchKernelGGL((ternary_f32_seq_kernel<8, f32_rows_per_lane<8>(), kAligned16>), g, blk, 0, s, p); break;
+        case 16: hipLaunchKernelGGL((ternary_f32_seq_kernel<16, f32_rows_per_lane<16>(), kAligned16>), g, blk, 0, s, p); break;
+        case 32: hipLaunchKernelGGL((ternary_f32_seq_kernel<32, f32_rows_per_lane<32>(), kAligned16>), g, blk, 0, s, p); break;
+        default: hipLaunchKernelGGL((ternary_f32_seq_kernel<64, f32_rows_per_lane<64>(), kAligned16>), g, blk, 0, s, p); break;
+    }
+}
+
+static int f32_rows_per_lane_rt(int ct) { return ct >= 16 ? 4 : 1; }
+
 }  // namespace kore
 
 using namespace kore;
@@ -539,5 +745,40 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
         if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
         hipLaunchKernelGGL(ternary_i8_generic_kernel, dim3((uint32_t)blocks), dim3(kTmBlock), 0, s, p);
     }
+    return launch_status();
+}
+
+extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float* a_scales, const float* b, float* c,
+                                           uint64_t m, uint64_t n, uint64_t k, kore_stream_t stream) {
+    if (m == 0 || n == 0) return KORE_HIP_OK;
+    if (!c || !a_scales) return KORE_HIP_ERR_NULL_PTR;
+    if (k > 0 && (!a_packed || !b)) return KORE_HIP_ERR_NULL_PTR;
+    if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
+    uint64_t mn, kn;
+    if (!mul_ok(m, n, &mn) || mn > kMaxElements || !mul_ok(k, n, &kn) || kn > kMaxElements)
+        return KORE_HIP_ERR_OVERFLOW;
+    const uint64_t kp = (k + 4) / 5;
+    uint64_t mkp;
+    if (!mul_ok(m, kp, &mkp) || mkp > kMaxElements) return KORE_HIP_ERR_OVERFLOW;
+    {
+        const char* c0 = reinterpret_cast<const char*>(c);
+        const char* c1 = c0 + mn * sizeof(float);
+        const struct { const void* p; uint64_t bytes; } ins[] = {
+            {a_packed, mkp}, {b, kn * sizeof(float)}, {a_scales, m * sizeof(float)}};
+        for (const auto& in : ins) {
+            const char* i0 = reinterpret_cast<const char*>(in.p);
+            if (in.p && in.bytes && i0 < c1 && c0 < i0 + in.bytes) return KORE_HIP_ERR_ALIAS;
+        }
+    }
+    TernF32Args p{a_packed, a_scales, b, c, (uint32_t)m, (uint32_t)n, (uint32_t)k, (uint32_t)kp};
+    hipStream_t s = (hipStream_t)stream;
+    int ct = 64;
+    while (ct > 1 && (uint64_t)(ct / 2) >= n) ct /= 2;  // smallest power of two >= n (<= 64)
+    const uint64_t rb = (uint64_t)(kTmBlock / kWave) * (kWave / ct) * f32_rows_per_lane_rt(ct);
+    const uint64_t gx = (m + rb - 1) / rb, gy = (n + ct - 1) / ct;
+    if (gx > 0x7fffffffull || gy > 65535) return KORE_HIP_ERR_OVERFLOW;
+    const dim3 g((uint32_t)gx, (uint32_t)gy), blk(kTmBlock);
+    if (kp % 16 == 0 && aligned16(a_packed)) launch_f32_seq<true>(ct, g, blk, s, p);
+    else launch_f32_seq<false>(ct, g, blk, s, p);
     return launch_status();
 }

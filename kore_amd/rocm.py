@@ -387,4 +387,20 @@ def rocm_ternary_matmul_i8(device_idx: int, a_packed: HipBuffer, a_scales: HipBu
     return c
 
 
-__all__ += ["rocm_ternary_matmul_i8"]
+def rocm_ternary_matmul_f32(device_idx: int, a_packed: HipBuffer, a_scales: HipBuffer, b: HipBuffer, m: int,
+                            n: int, k: int, out: Optional[HipBuffer] = None) -> HipBuffer:
+    """``ternary_matmul`` (cpu_ternary_matmul.rs:29-124, as ``BitLinear::forward``
+    calls it): c[m, n] = (sum over k in order of trit[m, k] * b[k, n]) *
+    a_scales[m] with f32 activations b[K, N], the sum the reference's
+    sequential f32 fold (bit-exact)."""
+    _require_device(device_idx)
+    _need(a_packed, m * ((k + 4) // 5), "ternary weights")
+    _need(a_scales, m * 4, "ternary scales")
+    _need(b, k * n * 4, "ternary activations")
+    c = _out(device_idx, out, m * n * 4, "ternary out")
+    _check(_lib.load().kore_hip_ternary_matmul_f32(a_packed.ptr, a_scales.ptr, b.ptr, c.ptr, m, n, k,
+                                                   _stream(device_idx)), "ternary_matmul_f32")
+    return c
+
+
+__all__ += ["rocm_ternary_matmul_i8", "rocm_ternary_matmul_f32"]

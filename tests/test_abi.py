@@ -83,6 +83,19 @@ def test_argument_errors_are_reported_on_host():
         _lib.KORE_HIP_ERR_ALIAS
 
 
+def test_ternary_argument_errors_are_reported_on_host():
+    lib = _lib.load()
+    for f in (lambda *a: lib.kore_hip_ternary_matmul_f32(a[0], a[1], a[2], a[3], *a[4:]),):
+        assert f(None, None, None, None, 0, 4, 16, None) == 0
+        assert f(None, None, None, None, 4, 0, 16, None) == 0
+        assert f(P, None, P, P + 4096, 4, 4, 16, None) == _lib.KORE_HIP_ERR_NULL_PTR
+        assert f(None, P, None, P + 4096, 4, 4, 16, None) == _lib.KORE_HIP_ERR_NULL_PTR
+        assert f(P, P, P, P, 2**32, 2**32, 16, None) == _lib.KORE_HIP_ERR_OVERFLOW
+        # the output may not overlap the weights, scales or activations
+        assert f(P, P + 2**20, P + 2**21, P + 2**21 + 64, 4, 4, 16, None) == _lib.KORE_HIP_ERR_ALIAS
+    assert lib.kore_hip_ternary_matmul_i8(P, None, P, P, P + 4096, 4, 4, 16, None) == _lib.KORE_HIP_ERR_NULL_PTR
+
+
 def test_rms_norm_backward_workspace_size():
     ws = _lib.load().kore_hip_rms_norm_backward_workspace_bytes
     assert ws(0, 128) == 0 and ws(128, 0) == 0 and ws(2**40, 2**40) == 0

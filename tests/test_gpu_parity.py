@@ -635,3 +635,63 @@ def test_ternary_matmul_i8_edges():
     got = down(rocm.rocm_ternary_matmul_i8(DEV, up(p), up(sa), HipBuffer.from_tensor(t[1:]), up(sq), m, n, k),
                np.float32, (m, n))
     assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), "ternary unaligned q")
+
+
+TERN_F32_SHAPES = [(1, 1, 5), (7, 1, 2560), (6912, 1, 2560), (33, 3, 161), (64, 5, 1000), (130, 17, 320),
+                   (65, 64, 2560), (9, 65, 2563), (257, 130, 799), (2, 200, 6920), (40, 33, 0)]
+
+
+@pytest.mark.parametrize("m,n,k", TERN_F32_SHAPES)
+def test_ternary_matmul_f32(m, n, k):
+    """The f32-activation ternary_matmul (BitLinear::forward's matmul):
+    bit-exact against the oracle's sequential fold, on arbitrary packed bytes
+    (bytes >= 243, nonzero padding trits past k), every column-tile width and
+    K with a partial last chunk."""
+    from inputs import raw_packed
+
+    log(f"ternary_matmul_f32 m={m} n={n} k={k}")
+    p = raw_packed(m, k, 5 * m + k) if k else np.zeros((m, 1), np.uint8)
+    sa = normal((m,), 11, 1.0, 0.1)
+    b = normal((k, n), 12) if k else np.zeros(1, np.float32)
+    got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
+    assert_bitexact(got, oracle.ternary_matmul(p, sa, b, m, n, k), "ternary_matmul_f32")
+
+
+def test_ternary_matmul_f32_order_and_nonfinite():
+    """Cancellation that only the reference's k order produces, and Inf/NaN
+    activations at zero-trit positions (skipped by the reference) next to
+    ones at nonzero trits (propagated)."""
+    log("ternary_matmul_f32 order and non-finite")
+    m, n, k = 3, 2, 400
+    w = np.zeros((m, k), np.float32)
+    w[0, :3] = 1.0              # row 0: b0 + b1 + b2 in order
+    w[1, 0] = 1.0; w[1, 5] = -1.0  # row 1: zero trits over the Inf/NaN positions
+    w[2, 7] = 1.0               # row 2: picks up the Inf
+    p, sa = oracle.pack_weights_ternary(w, 0.3)
+    b = np.zeros((k, n), np.float32)
+    b[0, :] = 1e8; b[1, :] = 1.0; b[2, :] = -1e8  # sequential: (1e8 + 1) - 1e8 = 0, not 1
+    b[3, 0] = np.inf; b[4, 1] = np.nan; b[5, :] = 2.0; b[7, 0] = np.inf
+    want = oracle.ternary_matmul(p, sa, b, m, n, k)
+    assert want[0, 0] == 0.0 and np.isfinite(want[1]).all() and np.isinf(want[2, 0])
+    got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
+    assert_bitexact(got, want, "ternary_matmul_f32 order/non-finite")
+
+
+def test_ternary_matmul_f32_edges():
+    log("ternary_matmul_f32 edges")
+    lib = __import__("kore_amd._lib", fromlist=["load"]).load()
+    assert lib.kore_hip_ternary_matmul_f32(None, None, None, None, 0, 5, 16, None) == 0
+    assert lib.kore_hip_ternary_matmul_f32(None, None, None, None, 5, 0, 16, None) == 0
+    assert lib.kore_hip_ternary_matmul_f32(None, None, None, None, 2, 2, 16, None) == -1
+    cb = up(np.zeros(64, np.float32))
+    assert lib.kore_hip_ternary_matmul_f32(1 << 40, 1 << 41, cb.ptr, cb.ptr, 4, 4, 16, None) == -4
+    # unaligned activations and an odd packed-row length: same results
+    from inputs import raw_packed
+
+    m, n, k = 50, 3, 333
+    p, sa, b = raw_packed(m, k, 3), normal((m,), 4), normal((k, n), 5)
+    t = torch.empty(k * n + 1, dtype=torch.float32, device="cuda")
+    t[1:].copy_(torch.from_numpy(b.ravel()))
+    got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), HipBuffer.from_tensor(t[1:]), m, n, k),
+               np.float32, (m, n))
+    assert_bitexact(got, oracle.ternary_matmul(p, sa, b, m, n, k), "ternary_matmul_f32 unaligned b")

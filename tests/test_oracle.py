@@ -471,6 +471,28 @@ def test_ternary_matmul_exact_and_f64():
     assert (np.abs(c - ref) <= bound + 1e-30).all()
 
 
+def test_ternary_matmul_sequential_order_and_zero_skip():
+    # The fold runs in k order: (1e8 + 1) - 1e8 is 0 in f32 (ulp(1e8) = 8),
+    # any other order or a wider accumulator gives 1.  Zero trits are skipped
+    # (compute_row `if t == 0 { continue; }`): an Inf at a zero-trit position
+    # leaves the output finite, at a nonzero trit it propagates.
+    k = 10
+    w = np.zeros((2, k), np.float32)
+    w[0, :3] = 1.0
+    w[1, 4] = -1.0
+    p, s = oracle.pack_weights_ternary(w, 0.3)
+    t = oracle.unpack_trits(p, k)
+    assert list(t[0, :4]) == [1, 1, 1, 0] and t[1, 4] == -1 and t[1, 3] == 0
+    b = np.zeros((k, 1), np.float32)
+    b[:3, 0] = [1e8, 1.0, -1e8]
+    b[3, 0] = np.inf
+    c = oracle.ternary_matmul(p, s, b, 2, 1, k)
+    assert c[0, 0] == 0.0 and c[1, 0] == 0.0
+    b[4, 0] = np.inf
+    c = oracle.ternary_matmul(p, s, b, 2, 1, k)
+    assert c[0, 0] == 0.0 and c[1, 0] == -np.inf
+
+
 def test_ternary_matmul_i8_exact():
     m, n, k = 11, 7, 93
     p = np.random.default_rng(9).integers(0, 256, size=(m, (k + 4) // 5)).astype(np.uint8)
