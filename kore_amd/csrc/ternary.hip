@@ -467,15 +467,15 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_generic_kernel(TernArgs p
 // exact), and a zero trit adds +-0, which leaves acc unchanged (acc is never
 // -0: it starts at +0 and an exact-zero sum rounds to +0) -- except when b is
 // Inf or NaN (0 * Inf = NaN), so chunks holding such a b skip zero trits
-// explicitly.  Issue-bound: one fma, one LDS read of b and a fifth of a table
-// read per term and lane.
+// explicitly.  Bound by the K chain: per term one fma, and per 5 terms two
+// LDS reads of b and two of the trit table; with one column (decode) the
+// table reads of 64 different rows' bytes dominate.
 //
-// Block: 4 waves; a wave's 64 lanes are CT columns x 64/CT rows.  Per chunk
-// of kF32Kc columns of K the block stages b[kc.., col0..col0+CT) in LDS
-// ([ki][c]: lanes of one row read consecutive banks, lanes of one column
-// broadcast) and every lane loads its row's packed bytes of the chunk.
-constexpr int kF32Kc = 160;           // K columns per chunk (32 packed bytes)
-constexpr int kF32Bytes = kF32Kc / 5;
+// Block: 4 waves; a wave's 64 lanes are CT columns x 64/CT row slots, each
+// lane R rows of its column.  Per chunk of KC columns of K (640, 320 or 160
+// as CT is 1, 2 or wider) the block stages b[kc.., col0..col0+CT) in LDS,
+// per column as groups of 8 floats (the 5 terms of one packed byte), and
+// every lane loads its rows' packed bytes of the chunk.
 
 struct TernF32Args {
     const uint8_t* a;   // packed [M, Kp]
@@ -489,12 +489,16 @@ template <int CT, int R, bool kAligned16>
 __global__ __launch_bounds__(kTmBlock) void ternary_f32_seq_kernel(TernF32Args p) {
     constexpr int kSlots = (kTmBlock / kWave) * (kWave / CT);  // row slots per block
     constexpr int RB = kSlots * R;                               // rows per block
-    constexpr int kSub = 8 / R;  // packed bytes whose operands are read ahead of their fmas
+    constexpr int kSub = 8 / R;
+    // K columns per chunk: longer for narrow column tiles (few b values per
+    // chunk), so that a chunk's folds outlast the next chunk's loads
+    constexpr int KC = CT == 1 ? 640 : (CT == 2 ? 320 : 160);
+    constexpr int NB = KC / 5;  // packed bytes per chunk  // packed bytes whose operands are read ahead of their fmas
     __shared__ __attribute__((aligned(16))) float flut[256 * 8];  // byte -> 5 trits as floats
     // b of the chunk, per column c: 32 groups of 8 floats (the 5 columns of K
     // one packed byte covers, padded), so a lane reads its 5 terms as one
     // 16-byte and one 4-byte read; odd pitch in 16-byte units
-    constexpr int kPitch = kF32Bytes * 8 + 4;
+    constexpr int kPitch = NB * 8 + 4;
     __shared__ __attribute__((aligned(16))) float bs[CT * kPitch];
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
@@ -529,11 +533,11 @@ __global__ __launch_bounds__(kTmBlock) void ternary_f32_seq_kernel(TernF32Args p
     // A chunk's operands are loaded one chunk ahead into registers (every
     // load unconditional, at a clamped in-bounds index, so none waits for
     // another), then b goes to LDS for the chunk's folds.
-    constexpr int kStage = (kF32Kc * CT + kTmBlock - 1) / kTmBlock;  // b elements per thread
-    uint32_t pbn[R][kF32Bytes / 4];  // packed bytes, 4 per register
+    constexpr int kStage = (KC * CT + kTmBlock - 1) / kTmBlock;  // b elements per thread
+    uint32_t pbn[R][NB / 4];  // packed bytes, 4 per register
     float bvn[kStage];
     auto load_chunk = [&](uint32_t kc) {
-        const uint32_t kn = min((uint32_t)kF32Kc, p.k - kc);
+        const uint32_t kn = min((uint32_t)KC, p.k - kc);
         const uint32_t pb0 = kc / 5u;
         // each row's 32 packed bytes of the chunk: two 16-byte loads (aligned
         // rows), nine dwords shifted into place (unaligned rows), or bytes
@@ -542,23 +546,24 @@ __global__ __launch_bounds__(kTmBlock) void ternary_f32_seq_kernel(TernF32Args p
         for (int i = 0; i < R; ++i) {
             const uintptr_t wa = reinterpret_cast<uintptr_t>(arow[i] + pb0);
             const uintptr_t w0 = wa & ~(uintptr_t)3;
-            if (kAligned16 && pb0 + kF32Bytes <= p.kp) {
-                const u32x4 x0 = *reinterpret_cast<const u32x4*>(arow[i] + pb0);
-                const u32x4 x1 = *reinterpret_cast<const u32x4*>(arow[i] + pb0 + 16);
-                pbn[i][0] = x0[0]; pbn[i][1] = x0[1]; pbn[i][2] = x0[2]; pbn[i][3] = x0[3];
-                pbn[i][4] = x1[0]; pbn[i][5] = x1[1]; pbn[i][6] = x1[2]; pbn[i][7] = x1[3];
-            } else if (!kAligned16 && pb0 + kF32Bytes <= p.kp && w0 + 36u <= a_hi) {
-                uint32_t d[9];
+            if (kAligned16 && pb0 + NB <= p.kp) {
 #pragma unroll
-                for (int q = 0; q < 9; ++q) d[q] = reinterpret_cast<const uint32_t*>(w0)[q];
+                for (int q = 0; q < NB / 16; ++q) {
+                    const u32x4 x = *reinterpret_cast<const u32x4*>(arow[i] + pb0 + 16 * q);
+                    pbn[i][4 * q] = x[0]; pbn[i][4 * q + 1] = x[1]; pbn[i][4 * q + 2] = x[2]; pbn[i][4 * q + 3] = x[3];
+                }
+            } else if (!kAligned16 && pb0 + NB <= p.kp && w0 + NB + 4u <= a_hi) {
+                uint32_t d[NB / 4 + 1];
+#pragma unroll
+                for (int q = 0; q <= NB / 4; ++q) d[q] = reinterpret_cast<const uint32_t*>(w0)[q];
                 const uint32_t sh = (uint32_t)(wa & 3u);
 #pragma unroll
-                for (int q = 0; q < 8; ++q) pbn[i][q] = __builtin_amdgcn_alignbyte(d[q + 1], d[q], sh);
+                for (int q = 0; q < NB / 4; ++q) pbn[i][q] = __builtin_amdgcn_alignbyte(d[q + 1], d[q], sh);
             } else {
 #pragma unroll
-                for (int q = 0; q < kF32Bytes / 4; ++q) pbn[i][q] = 0;
+                for (int q = 0; q < NB / 4; ++q) pbn[i][q] = 0;
 #pragma unroll
-                for (int j = 0; j < kF32Bytes; ++j) {
+                for (int j = 0; j < NB; ++j) {
                     const uint32_t o = pb0 + j;
                     pbn[i][j >> 2] |= (uint32_t)arow[i][o < p.kp ? o : 0u] << (8 * (j & 3));
                 }
@@ -577,30 +582,30 @@ __global__ __launch_bounds__(kTmBlock) void ternary_f32_seq_kernel(TernF32Args p
 #pragma unroll
     for (int i = 0; i < R; ++i) acc[i] = 0.0f;
     if (p.k > 0) load_chunk(0);
-    for (uint32_t kc = 0; kc < p.k; kc += kF32Kc) {
-        const uint32_t kn = min((uint32_t)kF32Kc, p.k - kc);
+    for (uint32_t kc = 0; kc < p.k; kc += KC) {
+        const uint32_t kn = min((uint32_t)KC, p.k - kc);
         __syncthreads();  // the previous chunk's b reads are done (and the table is filled)
         bool bad = false;
 #pragma unroll
         for (int u = 0; u < kStage; ++u) {
             const uint32_t e = (uint32_t)t + kTmBlock * u;
             const uint32_t ki = e / CT, c = e % CT;
-            if (e < (uint32_t)(kF32Kc * CT)) bs[c * kPitch + (ki / 5u) * 8u + ki % 5u] = bvn[u];
+            if (e < (uint32_t)(KC * CT)) bs[c * kPitch + (ki / 5u) * 8u + ki % 5u] = bvn[u];
             bad |= !__builtin_isfinite(bvn[u]);
         }
-        uint32_t pb[R][kF32Bytes / 4];
+        uint32_t pb[R][NB / 4];
 #pragma unroll
         for (int i = 0; i < R; ++i)
 #pragma unroll
-            for (int q = 0; q < kF32Bytes / 4; ++q) pb[i][q] = pbn[i][q];
+            for (int q = 0; q < NB / 4; ++q) pb[i][q] = pbn[i][q];
         const uint32_t pb0 = kc / 5u;
         const bool skip_zero = __syncthreads_or(bad);
-        if (kc + kF32Kc < p.k) load_chunk(kc + kF32Kc);
+        if (kc + KC < p.k) load_chunk(kc + KC);
         if (!any_live) continue;
         const float* bc = bs + cl * kPitch;
-        if (kn == (uint32_t)kF32Kc && !skip_zero) {
+        if (kn == (uint32_t)KC && !skip_zero) {
 #pragma unroll
-            for (int j0 = 0; j0 < kF32Bytes; j0 += kSub) {
+            for (int j0 = 0; j0 < NB; j0 += kSub) {
                 f32x4 b4[kSub], t4[R][kSub];
                 float b5[kSub], t5[R][kSub];
 #pragma unroll
