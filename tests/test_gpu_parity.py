@@ -695,3 +695,78 @@ def test_ternary_matmul_f32_edges():
     got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), HipBuffer.from_tensor(t[1:]), m, n, k),
                np.float32, (m, n))
     assert_bitexact(got, oracle.ternary_matmul(p, sa, b, m, n, k), "ternary_matmul_f32 unaligned b")
+
+
+def test_decode_chain_graph_replays_match_eager():
+    """A decode step's launches (pre-quant, the BitLinear matmul on its codes
+    -- the split-K path's zero/finish kernels included at 64 tokens -- the
+    RMSNorm+SiLU gate, RoPE, softmax and the f32 matmul) captured in one HIP
+    graph on a side stream: no entry point allocates, synchronises or records
+    a memset, so every replay, with eager work between replays, reproduces the
+    eager outputs bit for bit."""
+    from inputs import raw_packed
+
+    lib = __import__("kore_amd._lib", fromlist=["load"]).load()
+    dev = torch.device("cuda", DEV)
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    k, m, vocab = 2560, 6912, 4096
+    out = {}
+
+    def make(tokens):
+        t = {"x": torch.randn(tokens, k, generator=g, device=dev),
+             "w": torch.randn(k, generator=g, device=dev),
+             "z": torch.randn(tokens, k, generator=g, device=dev),
+             "a": torch.from_numpy(raw_packed(m, k, 3).ravel()).to(dev),
+             "sa": torch.rand(m, generator=g, device=dev),
+             "q": torch.randn(tokens, 4, 128, generator=g, device=dev),
+             "kk": torch.randn(tokens, 2, 128, generator=g, device=dev),
+             "inv": torch.from_numpy(oracle.rope_inv_freq(128, 10000.0)).to(dev),
+             "logits": torch.randn(tokens, vocab, generator=g, device=dev)}
+        t["codes"] = torch.empty(tokens, k, dtype=torch.int8, device=dev)
+        t["scales"] = torch.empty(tokens, device=dev)
+        t["c"] = torch.empty(m, tokens, device=dev)
+        t["gate"] = torch.empty(tokens, k, device=dev)
+        t["probs"] = torch.empty(tokens, vocab, device=dev)
+        t["cf"] = torch.empty(m, tokens, device=dev)
+        t["xt"] = t["x"].t().contiguous()
+        return t
+
+    def step(t, tokens, s):
+        P = lambda name: t[name].data_ptr()  # noqa: E731
+        rc = [lib.kore_hip_rms_norm_quant_i8(P("x"), P("w"), P("codes"), P("scales"), tokens, k, 1e-6, s),
+              lib.kore_hip_ternary_matmul_i8(P("a"), P("sa"), P("codes"), P("scales"), P("c"), m, tokens, k, s),
+              lib.kore_hip_rms_norm_silu_gate_f32(P("x"), P("w"), P("z"), P("gate"), tokens, k, 1e-6, s),
+              lib.kore_hip_rope_qk_f32(P("q"), P("kk"), P("inv"), 1, tokens, 4, 2, 128, 5, 0, s),
+              lib.kore_hip_softmax_f32(P("logits"), P("probs"), tokens, vocab, s),
+              lib.kore_hip_ternary_matmul_f32(P("a"), P("sa"), P("xt"), P("cf"), m, tokens, k, s)]
+        assert rc == [0] * len(rc), rc
+
+    for tokens in (1, 64):
+        log(f"decode chain graph tokens={tokens}")
+        t = make(tokens)
+        q0, k0 = t["q"].clone(), t["kk"].clone()
+        step(t, tokens, torch.cuda.current_stream(dev).cuda_stream)
+        torch.cuda.synchronize(dev)
+        want = {n: t[n].clone() for n in ("codes", "scales", "c", "gate", "q", "kk", "probs", "cf")}
+        side = torch.cuda.Stream(device=dev)
+        graph = torch.cuda.CUDAGraph()
+        t["q"].copy_(q0)
+        t["kk"].copy_(k0)
+        torch.cuda.synchronize(dev)
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                step(t, tokens, side.cuda_stream)
+        torch.cuda.synchronize(dev)
+        for rep in range(3):
+            for n in ("codes", "scales", "c", "gate", "probs", "cf"):
+                t[n].fill_(float("nan") if t[n].is_floating_point() else 0)
+            t["q"].copy_(q0)
+            t["kk"].copy_(k0)
+            torch.cuda.synchronize(dev)
+            graph.replay()
+            torch.cuda.synchronize(dev)
+            for n, v in want.items():
+                assert torch.equal(t[n], v), (tokens, rep, n)
+        out[tokens] = True
+    assert out == {1: True, 64: True}
