@@ -31,8 +31,14 @@
 //   same for both operands, so any assignment gives the same sum);
 //   accumulator register r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
 //   column l % 32.
+// Few output tiles (e.g. 64 tokens): the same kernel over K ranges, summed
+// with exact int32 atomics into the output (zeroed first, finished in place).
+// n <= 8: the small-n path below (dot4 on decoded windows, no MFMA).
 // Generic path (any shape and alignment): one thread per output, the
 // reference loop order.
+//
+// kore_hip_ternary_matmul_f32: the reference's f32-activation ternary_matmul,
+// a sequential fold per output (ternary_f32_seq_kernel, at the end).
 #include <algorithm>
 
 #include "common.hpp"
@@ -245,20 +251,22 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_finish_kernel(TernArgs p)
     p.c[i] = ((float)acc * p.sa[m]) * p.sq[n];
 }
 
-// Small-n path (n <= 4, k % 8 == 0, 8-byte aligned codes): a wave owns 4
-// weight rows and every lane a 40-column window of them (8 packed bytes per
-// row), decoded through the LDS table and reused for every code row:
-// 10 v_dot4_i32_i8 per row and code row, then exact integer wave sums (DPP)
-// and the same epilogue.  K is walked in chunks of 2560 columns (512 packed
-// bytes), past-the-end codes read as 0.  Memory-bound on the packed weights
-// (m * ceil(k/5) bytes) where the MFMA tiles would waste 127/128 of their
-// columns.
-constexpr int kGvRows = 4;     // weight rows per wave
+// Small-n path (n <= 8, k % 8 == 0, 8-byte aligned codes): a group of waves
+// owns 4 weight rows and every lane a 40-column window of them (8 packed
+// bytes per row), decoded through the LDS table and reused for up to 4 code
+// rows at a time: 10 v_dot4_i32_i8 per row and code row, then exact integer
+// wave sums (DPP) and the same epilogue.  K is walked in chunks of 2560
+// columns (512 packed bytes) shared by the group's waves.  Bound by the
+// packed weights' bytes (m * ceil(k/5)) and latency where the MFMA tiles
+// would waste most of their columns.
+constexpr int kGvRows = 4;     // weight rows per wave group
 constexpr int kGvChunk = 2560; // columns per lane-window sweep (64 lanes x 40)
-// Largest n the small-n path takes: against the split-K MFMA tiles it is
-// faster up to n = 4 (6912 x 4 x 2560: 8.7 vs 11.5 us; n = 1: 5.6 vs 11.3 us)
-// and slower from n = 8 (12.6 vs 11.2 us; 2560 x 16 x 6912: 32.8 vs 15.0 us).
-constexpr uint64_t kGvMaxN = 4;
+// Largest n the small-n path takes, by measured crossover against the
+// split-K MFMA tiles: n = 8 is faster here (6912 x 8 x 2560: 10.4 vs 10.7 us;
+// 2560 x 8 x 6912: 13.6 vs 15.9 us), n = 16 is not (6912 x 16 x 2560: 18.5
+// vs 10.4 us).  It also spares k % 16 == 8 shapes the one-thread-per-output
+// kernel (2560 x 8 x 6920: 12.5 vs 334 us).
+constexpr uint64_t kGvMaxN = 8;
 
 __device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
     v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
