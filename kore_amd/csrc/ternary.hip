@@ -503,6 +503,8 @@ __global__ __launch_bounds__(kTmBlock) void ternary_f32_seq_kernel(TernF32Args p
     constexpr int KC = CT == 1 ? 640 : (CT == 2 ? 320 : 160);
     constexpr int NB = KC / 5;  // packed bytes per chunk  // packed bytes whose operands are read ahead of their fmas
     __shared__ __attribute__((aligned(16))) float flut[256 * 8];  // byte -> 5 trits as floats
+    __shared__ __attribute__((aligned(16))) float lut9[9 * 2];      // b % 9  -> trits 0, 1
+    __shared__ __attribute__((aligned(16))) float lut27[27 * 4];    // b / 9 -> trits 2, 3, 4
     // b of the chunk, per column c: 32 groups of 8 floats (the 5 columns of K
     // one packed byte covers, padded), so a lane reads its 5 terms as one
     // 16-byte and one 4-byte read; odd pitch in 16-byte units
@@ -518,6 +520,16 @@ __global__ __launch_bounds__(kTmBlock) void ternary_f32_seq_kernel(TernF32Args p
         for (int j = 0; j < 5; ++j) {
             flut[t * 8 + j] = pad ? 0.0f : (float)((int)(v % 3u) - 1);
             v /= 3u;
+        }
+        if (t < 9) {
+            lut9[2 * t] = (float)((int)(t % 3) - 1);
+            lut9[2 * t + 1] = (float)((int)(t / 3) - 1);
+        }
+        if (t < 27) {
+            lut27[4 * t] = (float)((int)(t % 3) - 1);
+            lut27[4 * t + 1] = (float)((int)(t / 3 % 3) - 1);
+            lut27[4 * t + 2] = (float)((int)(t / 9) - 1);
+            lut27[4 * t + 3] = 0.0f;
         }
     }
     const uint32_t col0 = blockIdx.y * CT;
@@ -611,7 +623,33 @@ __global__ __launch_bounds__(kTmBlock) void ternary_f32_seq_kernel(TernF32Args p
         if (kc + KC < p.k) load_chunk(kc + KC);
         if (!any_live) continue;
         const float* bc = bs + cl * kPitch;
-        if (kn == (uint32_t)KC && !skip_zero) {
+        if (CT == 1 && kn == (uint32_t)KC && !skip_zero) {
+            // One column: the 64 lanes hold 64 different rows, whose reads of
+            // the 256-entry table would conflict.  A byte b < 243 is instead
+            // split as b = 9 h + l: trits 0-1 from a 9-entry table indexed by
+            // l, trits 2-4 from a 27-entry one indexed by h (both small enough
+            // that the reads are broadcasts or distinct banks); bytes >= 243
+            // decode as 121 (five zero trits).  b is read uniformly from LDS.
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const f32x4 b4 = *reinterpret_cast<const f32x4*>(bc + 8 * j);
+                const float b5 = bc[8 * j + 4];
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    uint32_t byte = (pb[i][j >> 2] >> (8 * (j & 3))) & 0xffu;
+                    byte = byte >= 243u ? 121u : byte;
+                    const uint32_t h = (byte * 57u) >> 9;  // byte / 9 for byte < 256
+                    const uint32_t l = byte - 9u * h;
+                    const float2 tl = *reinterpret_cast<const float2*>(lut9 + 2 * l);
+                    const f32x4 th = *reinterpret_cast<const f32x4*>(lut27 + 4 * h);
+                    acc[i] = __builtin_fmaf(tl.x, b4.x, acc[i]);
+                    acc[i] = __builtin_fmaf(tl.y, b4.y, acc[i]);
+                    acc[i] = __builtin_fmaf(th.x, b4.z, acc[i]);
+                    acc[i] = __builtin_fmaf(th.y, b4.w, acc[i]);
+                    acc[i] = __builtin_fmaf(th.z, b5, acc[i]);
+                }
+            }
+        } else if (kn == (uint32_t)KC && !skip_zero) {
 #pragma unroll
             for (int j0 = 0; j0 < NB; j0 += kSub) {
                 f32x4 b4[kSub], t4[R][kSub];
