@@ -471,8 +471,10 @@ class TernaryI8(Workload):
         self.m, self.n, self.k = m, n, k
         self.kp = (k + 4) // 5
         self.name = f"ternary_i8_{m}x{n}x{k}"
-        if n <= 4:
+        if n <= 8:
             self.kernel = "ternary_i8_gemv_kernel"
+        elif n <= 64:
+            self.kernel = "ternary_i8_skinny_kernel"
         self.tokens = n
         self.ops = 2 * m * n * k
         self.bytes = m * self.kp + n * k + 4 * m * n + 4 * (m + n)

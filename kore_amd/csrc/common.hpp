@@ -73,4 +73,14 @@ __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x));
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Orders this wave's LDS accesses across lanes.  A lane reading what another
+// lane of the same wave wrote (or overwriting what another lane read) needs
+// it: the compiler reasons per thread, sees different addresses, and would
+// otherwise move the load above the store.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 }  // namespace kore

@@ -147,16 +147,6 @@ __device__ __forceinline__ float fold4(float s, f32x4 a) {
 
 __device__ __forceinline__ float sum4(f32x4 a) { return (a.x + a.y) + (a.z + a.w); }
 
-// Orders this wave's LDS accesses across lanes.  A lane reading what another
-// lane of the same wave wrote (or overwriting what another lane read) needs
-// it: the compiler reasons per thread, sees different addresses, and would
-// otherwise move the load above the store.
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // DPP move of v with lanes that have no source reading 0 (bound_ctrl off,
 // old = 0).  ctrl/row_mask follow the gfx9 DPP encoding.
 template <int kCtrl, int kRowMask>

@@ -235,6 +235,165 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
     }
 }
 
+// Skinny path (8 < n <= 64, the vector path's alignment): a decode batch
+// against a tall weight matrix.  A workgroup owns 32 weight rows and every
+// code row (NT tiles of 32); its kWaves waves split K (160-column blocks kb =
+// w, w + kWaves, ...), and their exact int32 partials meet in LDS, each wave
+// adding one slice of the accumulators over all waves in wave order -- no
+// atomics, no zero / finish launches.  A lane decodes its own weight row's
+// 16 packed bytes per block straight into MFMA operands: the k order inside a
+// block is permuted the same way for both operands (step s, lane half h ->
+// columns 80 h + 16 s .. + 16), which leaves each 32-deep MFMA's sum
+// unchanged.  The block's codes are read coalesced (10 lanes per 160-byte row
+// piece) into the wave's LDS tile, then read back as operands with that
+// mapping.  The next block's loads are in flight during the current block's
+// MFMAs.
+constexpr int kSkRows = 32;
+constexpr uint64_t kSkMaxN = 64;
+constexpr int kSkPitch = 176;  // LDS bytes per code row of a block (160 + 16)
+
+template <int NT, bool kAlignedA, int kWaves>
+__global__ __launch_bounds__(kWaves * kWave) void ternary_i8_skinny_kernel(TernArgs p) {
+    constexpr int kRowsB = 32 * NT;                   // code rows of the workgroup
+    constexpr int kPieces = kRowsB * 10 / kWave;     // 16-byte code pieces per lane and block
+    constexpr int kTileB = kRowsB * kSkPitch;        // bytes of one wave's code tile
+    constexpr int kPart = NT * kWave * 64;           // bytes of one wave's partial sums
+    constexpr int kRegion = kTileB > kPart ? kTileB : kPart;
+    __shared__ uint64_t lut[256];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kWaves * kRegion];
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = t / kWave;
+    const int r = lane & 31, h = lane >> 5;
+    uint8_t* region = smem + wave * kRegion;
+    if (t < 256) lut[t] = trit_lut_entry((uint32_t)t);
+    const uint32_t m0 = blockIdx.x * kSkRows;
+    const bool row_ok = m0 + r < p.m;
+    const uint8_t* arow8 = p.a + (uint64_t)(row_ok ? m0 + r : 0) * p.kp;
+    const uintptr_t a_hi = reinterpret_cast<uintptr_t>(p.a) + (uintptr_t)p.m * p.kp;
+    const uint32_t nkb = (p.k + kTmK - 1) / kTmK;
+    const u32x4 zero_bytes = {kZeroByte * 0x01010101u, kZeroByte * 0x01010101u, kZeroByte * 0x01010101u,
+                              kZeroByte * 0x01010101u};
+    const u32x4 zero4 = {0u, 0u, 0u, 0u};
+    auto load_a = [&](uint32_t kb) -> u32x4 {
+        const uint32_t ab = kb * kTmKp + 16u * h;
+        if (kAlignedA) return (row_ok && ab < p.kp) ? *reinterpret_cast<const u32x4*>(arow8 + ab) : zero_bytes;
+        // unaligned rows: the five dwords around the 16 bytes, shifted
+        const uintptr_t wa = reinterpret_cast<uintptr_t>(arow8 + ab);
+        const uintptr_t w0 = wa & ~(uintptr_t)3;
+        if (row_ok && ab + 16u <= p.kp && w0 + 20u <= a_hi) {
+            const uint32_t* d = reinterpret_cast<const uint32_t*>(w0);
+            const uint32_t d0 = d[0], d1 = d[1], d2 = d[2], d3 = d[3], d4 = d[4];
+            const uint32_t sh = (uint32_t)(wa & 3u);
+            return u32x4{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
+                         __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh)};
+        }
+        uint32_t w[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            w[d] = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t o = ab + 4 * d + e;
+                const bool ok = row_ok && o < p.kp;
+                const uint32_t b = arow8[ok ? o : 0u];
+                w[d] |= (ok ? b : kZeroByte) << (8 * e);
+            }
+        }
+        return u32x4{w[0], w[1], w[2], w[3]};
+    };
+    // piece u of this lane: row (u * 64 + lane) / 10, 16-byte piece % 10
+    auto load_b = [&](uint32_t kb, u32x4 (&bv)[kPieces]) {
+#pragma unroll
+        for (int u = 0; u < kPieces; ++u) {
+            const uint32_t pc = (uint32_t)(u * kWave + lane);
+            const uint32_t n = pc / 10u, c = kb * kTmK + 16u * (pc % 10u);
+            const bool ok = n < p.n && c < p.k;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(p.q + (ok ? (uint64_t)n * p.k + c : 0u));
+            bv[u] = ok ? v : zero4;
+        }
+    };
+
+    i32x16 acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[j][q] = 0;
+    __syncthreads();  // table filled
+    uint32_t kb = (uint32_t)wave;
+    u32x4 av = zero_bytes;
+    u32x4 bv[kPieces];
+    if (kb < nkb) {
+        av = load_a(kb);
+        load_b(kb, bv);
+    }
+    for (; kb < nkb; kb += kWaves) {
+        // this block's codes into the wave's tile (after the last block's reads)
+        wave_lds_sync();
+#pragma unroll
+        for (int u = 0; u < kPieces; ++u) {
+            const uint32_t pc = (uint32_t)(u * kWave + lane);
+            *reinterpret_cast<u32x4*>(region + (pc / 10u) * kSkPitch + 16u * (pc % 10u)) = bv[u];
+        }
+        // decode this block's 16 packed bytes into 80 trits (20 dwords)
+        uint32_t out[20];
+#pragma unroll
+        for (int d = 0; d < 20; ++d) out[d] = 0;
+        uint64_t lv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) lv[i] = lut[(av[i >> 2] >> (8 * (i & 3))) & 0xffu];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int off = 5 * i, d = off >> 2, sh = (off & 3) * 8;
+            out[d] |= (uint32_t)(lv[i] << sh);
+            out[d + 1] |= (uint32_t)(lv[i] >> (32 - sh));
+        }
+        const uint32_t kn = kb + kWaves;
+        if (kn < nkb) {
+            av = load_a(kn);
+            load_b(kn, bv);
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int s = 0; s < 5; ++s) {
+            const i32x4 a = {(int)out[4 * s], (int)out[4 * s + 1], (int)out[4 * s + 2], (int)out[4 * s + 3]};
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const i32x4 b = *reinterpret_cast<const i32x4*>(region + (32 * j + r) * kSkPitch + 80 * h + 16 * s);
+                acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[j], 0, 0, 0);
+            }
+        }
+    }
+    // every wave stores its partial sums; wave w then adds accumulator
+    // registers [w * kSlice, (w + 1) * kSlice) over all waves, in wave order
+    // (exact), and applies the epilogue to them
+    __syncthreads();  // all waves are done with their code tiles
+    i32x4* mypart = reinterpret_cast<i32x4*>(region);
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+            mypart[(j * 4 + q4) * kWave + lane] = i32x4{acc[j][4 * q4], acc[j][4 * q4 + 1], acc[j][4 * q4 + 2],
+                                                        acc[j][4 * q4 + 3]};
+    __syncthreads();
+    constexpr int kQuads = NT * 4;  // 4-register groups per lane
+    for (int g = wave; g < kQuads; g += kWaves) {
+        i32x4 sum = {0, 0, 0, 0};
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) sum += reinterpret_cast<const i32x4*>(smem + w * kRegion)[g * kWave + lane];
+        const int j = g / 4, q4 = g % 4;
+        const uint32_t n = (uint32_t)j * 32u + (uint32_t)r;
+        if (n < p.n) {
+            const float sqn = p.sq[n];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t m = m0 + 8 * q4 + 4 * h + e;  // register 4 q4 + e
+                if (m < p.m) p.c[(uint64_t)m * p.n + n] = ((float)sum[e] * p.sa[m]) * sqn;
+            }
+        }
+    }
+}
+
 // Split-K helpers: zero c as int32 (a kernel, not hipMemsetAsync, so the
 // call can be captured in a graph), then turn the int32 sums into
 // ((float)acc * a_scale) * q_scale in place.
@@ -760,6 +919,21 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
         return launch_status();
     }
     const bool vec = k > 0 && k % 16 == 0 && aligned16(q) && c_ok;
+    if (vec && n <= kSkMaxN) {
+        const uint64_t blocks = (m + kSkRows - 1) / kSkRows;
+        if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
+        const bool al = kp % 16 == 0 && aligned16(a_packed);
+        const dim3 g((uint32_t)blocks);
+        const int nt = (int)((n + 31) / 32);
+        if (al) {
+            if (nt == 1) hipLaunchKernelGGL((ternary_i8_skinny_kernel<1, true, 8>), g, dim3(8 * kWave), 0, s, p);
+            else hipLaunchKernelGGL((ternary_i8_skinny_kernel<2, true, 8>), g, dim3(8 * kWave), 0, s, p);
+        } else {
+            if (nt == 1) hipLaunchKernelGGL((ternary_i8_skinny_kernel<1, false, 8>), g, dim3(8 * kWave), 0, s, p);
+            else hipLaunchKernelGGL((ternary_i8_skinny_kernel<2, false, 8>), g, dim3(8 * kWave), 0, s, p);
+        }
+        return launch_status();
+    }
     if (vec) {
         const uint64_t tiles = ((m + kTmM - 1) / kTmM) * ((n + kTmN - 1) / kTmN);
         const uint64_t nkt = (k + kTmK - 1) / kTmK;

@@ -563,12 +563,15 @@ def test_ternary_matmul_i8(m, n, k):
 @pytest.mark.parametrize("m,n,k", [(7, 1, 2560), (6912, 1, 2560), (130, 2, 1000), (257, 3, 6912), (64, 4, 8),
                                    (2560, 1, 6920), (300, 2, 5000), (61, 4, 4096), (9, 1, 12800), (3, 3, 2568),
                                    (2560, 8, 6920), (130, 6, 2560), (77, 5, 336),
+                                   (2560, 64, 6912), (1000, 33, 2576), (7, 40, 6912), (300, 9, 160), (600, 100, 2560),
                                    (33, 8, 2568), (100, 9, 5128), (6912, 16, 2560), (5, 16, 40), (1, 12, 7688),
                                    (129, 17, 2560), (6912, 64, 2560), (70, 40, 6920)])
 def test_ternary_matmul_i8_small_n(m, n, k):
     """The small-n path (n <= 8: 1, 2 or 4 waves per 4 weight rows, dot4 over
     40-column lane windows, K in 2560-column chunks shared by the waves;
-    8-byte-aligned and unaligned packed rows) and the n past it
+    8-byte-aligned and unaligned packed rows), the skinny MFMA path (n <= 64:
+    32 weight rows per workgroup, K split over 8 waves, aligned and unaligned
+    packed rows) and the n past it
     (split-K MFMA tiles with integer atomics): bit-exact against the oracle on
     arbitrary packed bytes, ragged m, odd packed-row lengths and k % 16 != 0."""
     from inputs import int8_codes, raw_packed
