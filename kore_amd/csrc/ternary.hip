@@ -31,9 +31,11 @@
 //   same for both operands, so any assignment gives the same sum);
 //   accumulator register r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
 //   column l % 32.
-// Few output tiles (e.g. 64 tokens): the same kernel over K ranges, summed
-// with exact int32 atomics into the output (zeroed first, finished in place).
-// n <= 8: the small-n path below (dot4 on decoded windows, no MFMA).
+// n <= 8: the small-n path (dot4 on decoded windows, no MFMA); 8 < n <= 64:
+// the skinny path (32 weight rows per workgroup, K split over its waves and
+// summed exactly in LDS); few output tiles beyond that: the tile kernel over
+// K ranges, summed with exact int32 atomics into the output (zeroed first,
+// finished in place).
 // Generic path (any shape and alignment): one thread per output, the
 // reference loop order.
 //
