@@ -654,9 +654,10 @@ struct TernF32Args {
     uint32_t m, n, k, kp;
 };
 
-template <int CT, int R, bool kAligned16>
-__global__ __launch_bounds__(kTmBlock) void ternary_f32_seq_kernel(TernF32Args p) {
-    constexpr int kSlots = (kTmBlock / kWave) * (kWave / CT);  // row slots per block
+template <int CT, int R, int kW, bool kAligned16>
+__global__ __launch_bounds__(kW * kWave) void ternary_f32_seq_kernel(TernF32Args p) {
+    constexpr int kThreads = kW * kWave;
+    constexpr int kSlots = kW * (kWave / CT);  // row slots per block
     constexpr int RB = kSlots * R;                               // rows per block
     constexpr int kSub = 8 / R;
     // K columns per chunk: longer for narrow column tiles (few b values per
@@ -714,11 +715,10 @@ __global__ __launch_bounds__(kTmBlock) void ternary_f32_seq_kernel(TernF32Args p
     // A chunk's operands are loaded one chunk ahead into registers (every
     // load unconditional, at a clamped in-bounds index, so none waits for
     // another), then b goes to LDS for the chunk's folds.
-    constexpr int kStage = (KC * CT + kTmBlock - 1) / kTmBlock;  // b elements per thread
+    constexpr int kStage = (KC * CT + kThreads - 1) / kThreads;  // b elements per thread
     uint32_t pbn[R][NB / 4];  // packed bytes, 4 per register
     float bvn[kStage];
-    auto load_chunk = [&](uint32_t kc) {
-        const uint32_t kn = min((uint32_t)KC, p.k - kc);
+    auto load_pb = [&](uint32_t kc) {
         const uint32_t pb0 = kc / 5u;
         // each row's 32 packed bytes of the chunk: two 16-byte loads (aligned
         // rows), nine dwords shifted into place (unaligned rows), or bytes
@@ -750,9 +750,12 @@ __global__ __launch_bounds__(kTmBlock) void ternary_f32_seq_kernel(TernF32Args p
                 }
             }
         }
+    };
+    auto load_b = [&](uint32_t kc) {
+        const uint32_t kn = min((uint32_t)KC, p.k - kc);
 #pragma unroll
         for (int u = 0; u < kStage; ++u) {
-            const uint32_t e = (uint32_t)t + kTmBlock * u;
+            const uint32_t e = (uint32_t)t + kThreads * u;
             const uint32_t ki = e / CT, c = e % CT;
             const bool ok = e < kn * CT && col0 + c < p.n;
             const float v = p.b[ok ? (uint64_t)(kc + ki) * p.n + col0 + c : 0u];
@@ -762,26 +765,23 @@ __global__ __launch_bounds__(kTmBlock) void ternary_f32_seq_kernel(TernF32Args p
     float acc[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) acc[i] = 0.0f;
-    if (p.k > 0) load_chunk(0);
+    if (p.k > 0) load_b(0);
     for (uint32_t kc = 0; kc < p.k; kc += KC) {
         const uint32_t kn = min((uint32_t)KC, p.k - kc);
+        load_pb(kc);  // small; its latency overlaps the barrier and the staging
         __syncthreads();  // the previous chunk's b reads are done (and the table is filled)
         bool bad = false;
 #pragma unroll
         for (int u = 0; u < kStage; ++u) {
-            const uint32_t e = (uint32_t)t + kTmBlock * u;
+            const uint32_t e = (uint32_t)t + kThreads * u;
             const uint32_t ki = e / CT, c = e % CT;
             if (e < (uint32_t)(KC * CT)) bs[c * kPitch + (ki / 5u) * 8u + ki % 5u] = bvn[u];
             bad |= !__builtin_isfinite(bvn[u]);
         }
-        uint32_t pb[R][NB / 4];
-#pragma unroll
-        for (int i = 0; i < R; ++i)
-#pragma unroll
-            for (int q = 0; q < NB / 4; ++q) pb[i][q] = pbn[i][q];
         const uint32_t pb0 = kc / 5u;
         const bool skip_zero = __syncthreads_or(bad);
-        if (kc + KC < p.k) load_chunk(kc + KC);
+        if (kc + KC < p.k) load_b(kc + KC);
+        auto& pb = pbn;
         if (!any_live) continue;
         const float* bc = bs + cl * kPitch;
         if (CT == 1 && kn == (uint32_t)KC && !skip_zero) {
@@ -855,25 +855,34 @@ __global__ __launch_bounds__(kTmBlock) void ternary_f32_seq_kernel(TernF32Args p
         if (live[i]) p.c[(uint64_t)rows[i] * p.n + col] = acc[i] * p.sa[rows[i]];
 }
 
-// rows per lane: 1 for narrow column tiles (many waves, one fold each), more
-// for wide ones (b staged once for more rows, folds interleaved)
-template <int CT>
-constexpr int f32_rows_per_lane() { return CT >= 16 ? 4 : 1; }
-
+// Rows per lane (R) and waves per block (W): narrow column tiles take one
+// fold per lane and 4 waves (many waves in flight); 16-32 columns 2 rows per
+// lane; 64 columns 8 waves with 4 rows per lane when m gives >= 200 blocks of
+// 32 rows (b staged once for more rows), else 2 (more blocks).
 template <bool kAligned16>
-static void launch_f32_seq(int ct, dim3 g, dim3 blk, hipStream_t s, const TernF32Args& p) {
+static void launch_f32_seq(int ct, uint64_t m, dim3 g, hipStream_t s, const TernF32Args& p) {
+#define KORE_F32_SEQ(C, R, W) \
+    hipLaunchKernelGGL((ternary_f32_seq_kernel<C, R, W, kAligned16>), g, dim3((W) * kWave), 0, s, p)
     switch (ct) {
-        case 1: hipLaunchKernelGGL((ternary_f32_seq_kernel<1, f32_rows_per_lane<1>(), kAligned16>), g, blk, 0, s, p); break;
-        case 2: hipLaunchKernelGGL((ternary_f32_seq_kernel<2, f32_rows_per_lane<2>(), kAligned16>), g, blk, 0, s, p); break;
-        case 4: hipLaunchKernelGGL((ternary_f32_seq_kernel<4, f32_rows_per_lane<4>(), kAligned16>), g, blk, 0, s, p); break;
-        case 8: hipLaunchKernelGGL((ternary_f32_seq_kernel<8, f32_rows_per_lane<8>(), kAligned16>), g, blk, 0, s, p); break;
-        case 16: hipLaunchKernelGGL((ternary_f32_seq_kernel<16, f32_rows_per_lane<16>(), kAligned16>), g, blk, 0, s, p); break;
-        case 32: hipLaunchKernelGGL((ternary_f32_seq_kernel<32, f32_rows_per_lane<32>(), kAligned16>), g, blk, 0, s, p); break;
-        default: hipLaunchKernelGGL((ternary_f32_seq_kernel<64, f32_rows_per_lane<64>(), kAligned16>), g, blk, 0, s, p); break;
+        case 1: KORE_F32_SEQ(1, 1, 4); break;
+        case 2: KORE_F32_SEQ(2, 1, 4); break;
+        case 4: KORE_F32_SEQ(4, 1, 4); break;
+        case 8: KORE_F32_SEQ(8, 1, 4); break;
+        case 16: KORE_F32_SEQ(16, 2, 4); break;
+        case 32: KORE_F32_SEQ(32, 2, 4); break;
+        default:
+            if (m >= 32 * 200) KORE_F32_SEQ(64, 4, 8);
+            else KORE_F32_SEQ(64, 2, 8);
+            break;
     }
+#undef KORE_F32_SEQ
 }
 
-static int f32_rows_per_lane_rt(int ct) { return ct >= 16 ? 4 : 1; }
+static uint64_t f32_rows_per_block(int ct, uint64_t m) {
+    if (ct <= 8) return 4 * (kWave / ct);
+    if (ct <= 32) return 4 * (kWave / ct) * 2;
+    return m >= 32 * 200 ? 8 * 4 : 8 * 2;
+}
 
 }  // namespace kore
 
@@ -1001,11 +1010,11 @@ extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float*
     hipStream_t s = (hipStream_t)stream;
     int ct = 64;
     while (ct > 1 && (uint64_t)(ct / 2) >= n) ct /= 2;  // smallest power of two >= n (<= 64)
-    const uint64_t rb = (uint64_t)(kTmBlock / kWave) * (kWave / ct) * f32_rows_per_lane_rt(ct);
+    const uint64_t rb = f32_rows_per_block(ct, m);
     const uint64_t gx = (m + rb - 1) / rb, gy = (n + ct - 1) / ct;
     if (gx > 0x7fffffffull || gy > 65535) return KORE_HIP_ERR_OVERFLOW;
-    const dim3 g((uint32_t)gx, (uint32_t)gy), blk(kTmBlock);
-    if (kp % 16 == 0 && aligned16(a_packed)) launch_f32_seq<true>(ct, g, blk, s, p);
-    else launch_f32_seq<false>(ct, g, blk, s, p);
+    const dim3 g((uint32_t)gx, (uint32_t)gy);
+    if (kp % 16 == 0 && aligned16(a_packed)) launch_f32_seq<true>(ct, m, g, s, p);
+    else launch_f32_seq<false>(ct, m, g, s, p);
     return launch_status();
 }

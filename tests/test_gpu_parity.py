@@ -642,7 +642,8 @@ def test_ternary_matmul_i8_edges():
 
 
 TERN_F32_SHAPES = [(1, 1, 5), (7, 1, 2560), (6912, 1, 2560), (33, 3, 161), (64, 5, 1000), (130, 17, 320),
-                   (65, 64, 2560), (9, 65, 2563), (257, 130, 799), (2, 200, 6920), (40, 33, 0)]
+                   (65, 64, 2560), (9, 65, 2563), (257, 130, 799), (2, 200, 6920), (40, 33, 0), (6500, 64, 320),
+                   (301, 24, 640)]
 
 
 @pytest.mark.parametrize("m,n,k", TERN_F32_SHAPES)
@@ -650,7 +651,7 @@ def test_ternary_matmul_f32(m, n, k):
     """The f32-activation ternary_matmul (BitLinear::forward's matmul):
     bit-exact against the oracle's sequential fold, on arbitrary packed bytes
     (bytes >= 243, nonzero padding trits past k), every column-tile width and
-    K with a partial last chunk."""
+    rows-per-lane choice, and K with a partial last chunk."""
     from inputs import raw_packed
 
     log(f"ternary_matmul_f32 m={m} n={n} k={k}")
