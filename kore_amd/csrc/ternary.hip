@@ -658,12 +658,12 @@ template <int CT, int R, int kW, bool kAligned16>
 __global__ __launch_bounds__(kW * kWave) void ternary_f32_seq_kernel(TernF32Args p) {
     constexpr int kThreads = kW * kWave;
     constexpr int kSlots = kW * (kWave / CT);  // row slots per block
-    constexpr int RB = kSlots * R;                               // rows per block
-    constexpr int kSub = 8 / R;
+    constexpr int RB = kSlots * R;             // rows per block
+    constexpr int kSub = 8 / R;  // packed bytes whose operands are read ahead of their fmas
     // K columns per chunk: longer for narrow column tiles (few b values per
     // chunk), so that a chunk's folds outlast the next chunk's loads
     constexpr int KC = CT == 1 ? 640 : (CT == 2 ? 320 : 160);
-    constexpr int NB = KC / 5;  // packed bytes per chunk  // packed bytes whose operands are read ahead of their fmas
+    constexpr int NB = KC / 5;  // packed bytes per chunk
     __shared__ __attribute__((aligned(16))) float flut[256 * 8];  // byte -> 5 trits as floats
     __shared__ __attribute__((aligned(16))) float lut9[9 * 2];      // b % 9  -> trits 0, 1
     __shared__ __attribute__((aligned(16))) float lut27[27 * 4];    // b / 9 -> trits 2, 3, 4
@@ -712,17 +712,19 @@ __global__ __launch_bounds__(kW * kWave) void ternary_f32_seq_kernel(TernF32Args
         arow[i] = p.a + (uint64_t)(rows[i] < p.m ? rows[i] : 0) * p.kp;
     }
     const uintptr_t a_hi = reinterpret_cast<uintptr_t>(p.a) + (uintptr_t)p.m * p.kp;
-    // A chunk's operands are loaded one chunk ahead into registers (every
-    // load unconditional, at a clamped in-bounds index, so none waits for
-    // another), then b goes to LDS for the chunk's folds.
+    // b is loaded one chunk ahead into registers, then staged in LDS for the
+    // chunk's folds; the rows' packed bytes are loaded at the chunk's start
+    // (small, their latency overlaps the barrier and the staging).  Every load
+    // is unconditional, at a clamped in-bounds index, so none waits for
+    // another.
     constexpr int kStage = (KC * CT + kThreads - 1) / kThreads;  // b elements per thread
     uint32_t pbn[R][NB / 4];  // packed bytes, 4 per register
     float bvn[kStage];
     auto load_pb = [&](uint32_t kc) {
         const uint32_t pb0 = kc / 5u;
-        // each row's 32 packed bytes of the chunk: two 16-byte loads (aligned
-        // rows), nine dwords shifted into place (unaligned rows), or bytes
-        // (the row's end)
+        // each row's NB packed bytes of the chunk: 16-byte loads (aligned
+        // rows), NB/4 + 1 dwords shifted into place (unaligned rows), or
+        // bytes (the row's end)
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             const uintptr_t wa = reinterpret_cast<uintptr_t>(arow[i] + pb0);
