@@ -775,3 +775,41 @@ def test_decode_chain_graph_replays_match_eager():
                 assert torch.equal(t[n], v), (tokens, rep, n)
         out[tokens] = True
     assert out == {1: True, 64: True}
+
+
+def _adversarial_rows(rows: int, cols: int, seed: int) -> np.ndarray:
+    """Rows whose running sum of squares crosses many binades in awkward
+    places: wide per-row scales, exponential ramps (every segment in a new
+    binade), a few huge entries among tiny ones (late crossings), sums that
+    sit just below powers of two, and subnormal-heavy rows."""
+    g = np.random.default_rng(seed)
+    x = g.standard_normal((rows, cols)).astype(np.float32)
+    kind = np.arange(rows) % 6
+    scale = (10.0 ** g.uniform(-18, 18, size=rows)).astype(np.float32)
+    x[kind == 0] *= scale[kind == 0, None]
+    ramp = (2.0 ** np.linspace(-20, 20, cols)).astype(np.float32)
+    x[kind == 1] = (x[kind == 1] * ramp[None, :]).astype(np.float32)
+    spikes = g.random((rows, cols)) < 0.002
+    x[(kind == 2)[:, None] & spikes] *= np.float32(1e6)
+    x[kind == 2] *= np.float32(1e-3)
+    # constant rows whose sum of squares lands next to 2^k
+    x[kind == 3] = np.float32(np.sqrt(2.0 ** 11 / cols)) * (1 + g.uniform(-1e-6, 1e-6, size=(int((kind == 3).sum()), cols))).astype(np.float32)
+    x[kind == 4] *= np.float32(1e-22)
+    x[kind == 5] = (x[kind == 5] * (g.random((int((kind == 5).sum()), cols)) < 0.5)).astype(np.float32)  # half zeros
+    return x
+
+
+@pytest.mark.parametrize("cols", [2048, 2560, 4096, 1000])
+def test_norm_family_adversarial_rows_bit_exact(cols):
+    """The exact segmented fold under stress: 6144 rows of the kinds above,
+    RMSNorm and pre-quant bit-exact against the oracle's sequential fold."""
+    rows = 6144
+    log(f"adversarial rows cols={cols}")
+    x = _adversarial_rows(rows, cols, cols)
+    g = (1.0 + 0.02 * np.random.default_rng(cols + 1).standard_normal(cols)).astype(np.float32)
+    got = down(rocm.rocm_rms_norm_f32(DEV, up(x), up(g), rows, cols, 1e-6), np.float32, (rows, cols))
+    assert_bitexact(got, oracle.rms_norm(x, g, 1e-6), f"rms_norm adversarial {cols}")
+    q, s = rocm.rocm_rms_norm_quant_i8(DEV, up(x), up(g), rows, cols, 1e-6)
+    wq, ws = oracle.rms_norm_quant_i8(x, g, 1e-6)
+    assert down(q, np.int8, (rows, cols)).tobytes() == wq.tobytes(), f"prequant codes adversarial {cols}"
+    assert down(s, np.float32, (rows,)).tobytes() == ws.tobytes(), f"prequant scales adversarial {cols}"
