@@ -40,7 +40,8 @@
 // reference loop order.
 //
 // kore_hip_ternary_matmul_f32: the reference's f32-activation ternary_matmul,
-// a sequential fold per output (ternary_f32_seq_kernel, at the end).
+// a sequential fold per output (ternary_f32_seq_kernel, and for one column
+// ternary_f32_pipe_kernel, at the end).
 #include <algorithm>
 
 #include "common.hpp"
@@ -880,6 +881,242 @@ static void launch_f32_seq(int ct, uint64_t m, dim3 g, hipStream_t s, const Tern
 #undef KORE_F32_SEQ
 }
 
+// One column (a decode step, n == 1), any row alignment.  The
+// fold is a chain of k dependent f32 operations per output, so its floor is k
+// times the latency of one dependent vector operation (about 8 cycles for a
+// single wave); the per-lane kernel above also puts the decode, the table and
+// the b reads into that chain's wave.  Here a workgroup of seven waves owns 64
+// rows: six waves decode and form the terms t * b in LDS, one wave folds them
+// with plain dependent adds, nothing else in its instruction stream but the
+// 16-byte LDS reads of the terms.
+//
+// A term is fl(t * b) = +-b exactly for a nonzero trit and +-0 for a zero
+// one, and acc + (+-0) = acc (acc is never -0): acc + term is the
+// reference's acc + t * b with zero trits skipped, bit for bit.  Where b is
+// Inf or NaN, 0 * b would be NaN: in such a step the terms are selected
+// instead (+0 for a zero trit).  The decode is f32 arithmetic, no tables: with
+// c the f32 just above 1/3^i, floor(byte * c) is byte / 3^i for every byte <
+// 243 (exhaustively true), and the base-3 digits u follow exactly as
+// q_i - 3 q_(i+1); the term is fma(u, b, -b) = (u - 1) * b, exact.
+//
+// K advances in steps of 240 columns (48 packed bytes per row; decoder d
+// takes bytes [8 d, 8 d + 8) = columns [40 d, 40 d + 40)), double-buffered:
+// in iteration s the decoders write the terms of step s (and stage b of step
+// s + 1) while the fold wave reads the terms of step s - 1; one barrier per
+// iteration separates them.  The decoders keep the packed bytes and b of the
+// next kPfDepth steps in flight.
+constexpr int kPfStep = 240;               // K columns per step
+constexpr int kPfDec = 6;                  // decoding waves
+constexpr int kDecB = kPfStep / 5 / kPfDec;  // packed bytes per decoder and step
+constexpr int kDecQ = kDecB * 5 / 4;         // ... as groups of 4 terms
+constexpr int kStageN = (kPfStep + kPfDec * kWave - 1) / (kPfDec * kWave);  // b elements per decoder lane
+static_assert(kDecB * kPfDec * 5 == kPfStep && kDecB % 4 == 0, "decoder split");
+constexpr int kPfQuads = kPfStep / 4;      // 16-byte groups of 4 terms per step
+constexpr int kPfDepth = 2;                // steps of loads in flight
+
+// One workgroup per CU (its LDS): the compiler may use registers for
+// instruction-level parallelism rather than occupancy.
+__global__ __launch_bounds__((kPfDec + 1) * kWave) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void ternary_f32_pipe_kernel(TernF32Args p) {
+    // terms of the step per group of 4 columns, lane-major (a lane reads and
+    // writes 16 consecutive bytes: conflict-free); 120 KB
+    __shared__ f32x4 tb[2][kPfQuads][kWave];
+    __shared__ f32x4 bb[2][kPfQuads];  // b of a step, zero past k
+    __shared__ uint32_t bflag[2][kPfDec];
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = t / kWave;
+    const uint32_t row = blockIdx.x * kWave + lane;
+    const uint32_t steps = (p.k + kPfStep - 1) / kPfStep;
+    // the decoders run whole rounds of kPfDepth steps (the ones past K decode
+    // zeros), so that every round issues and waits for its loads alike
+    const uint32_t steps_p = (steps + kPfDepth - 1) / kPfDepth * kPfDepth;
+    // b staging: decoder lane e takes elements e + h * (decoder lanes) < 240
+    const int e = (wave - 1) * kWave + lane;
+    constexpr int kSL = kPfDec * kWave;
+    auto b_ok = [&](uint32_t s, int h) {
+        return (e + kSL * h) < kPfStep && s * kPfStep + (uint32_t)(e + kSL * h) < p.k;
+    };
+    float bv[kPfDepth][kStageN];
+    // stage b of step s into bb[buf]; bflag[buf][d]: decoder d staged an Inf
+    // or NaN
+    auto stage_b = [&](uint32_t s, int buf, const float (&v)[kStageN]) {
+        bool bad = false;
+#pragma unroll
+        for (int h = 0; h < kStageN; ++h)
+            if (e + kSL * h < kPfStep) {
+                const float x = b_ok(s, h) ? v[h] : 0.0f;
+                reinterpret_cast<float*>(bb[buf])[e + kSL * h] = x;
+                bad |= !__builtin_isfinite(x);
+            }
+        const bool any_bad = __any(bad);
+        if (lane == 0) bflag[buf][wave - 1] = any_bad ? 1u : 0u;
+    };
+    if (wave > 0) {
+        float v[kStageN];
+#pragma unroll
+        for (int h = 0; h < kStageN; ++h) v[h] = p.b[b_ok(0, h) ? (uint32_t)(e + kSL * h) : 0u];
+        stage_b(0, 0, v);
+    }
+    __syncthreads();  // b of step 0
+    if (wave == 0) {
+        float acc = 0.0f;
+        for (uint32_t s = 0; s <= steps_p; ++s) {
+            if (s > 0 && s <= steps) {
+                const int buf = (s - 1) & 1;
+                // batches of kFb groups, the next batch's reads in flight
+                // during a batch's adds
+                constexpr int kFb = 6;
+                f32x4 tq[2][kFb];
+#pragma unroll
+                for (int i = 0; i < kFb; ++i) tq[0][i] = tb[buf][i][lane];
+#pragma unroll
+                for (int bt = 0; bt < kPfQuads / kFb; ++bt) {
+                    const int cur = bt & 1;
+                    if (bt + 1 < kPfQuads / kFb) {
+#pragma unroll
+                        for (int i = 0; i < kFb; ++i) tq[cur ^ 1][i] = tb[buf][(bt + 1) * kFb + i][lane];
+                    }
+#pragma unroll
+                    for (int i = 0; i < kFb; ++i) {
+                        acc += tq[cur][i].x;
+                        acc += tq[cur][i].y;
+                        acc += tq[cur][i].z;
+                        acc += tq[cur][i].w;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        if (row < p.m) p.c[row] = acc * p.sa[row];
+        return;
+    }
+    const int d = wave - 1;
+    const uint8_t* arow = p.a + (uint64_t)(row < p.m ? row : 0u) * p.kp;
+    // Loads are unconditional, at clamped in-bounds addresses; what lies
+    // past the row or past k is replaced when the step is used (a select
+    // right after a load would wait for it).  A decoder's 8 bytes of a step
+    // come from the three dwords around them (any row alignment), the first
+    // at floor4(address), clamped so that the three end at ceil4 of the
+    // matrix's end (the host launches this kernel for m * kp >= 12 only); the
+    // bytes are then at offset o = address - first dword (o < 4 unless
+    // clamped, and up to 11 for the matrix's last bytes).
+    static_assert(kDecB == 8, "three-dword window");
+    const uintptr_t a_end4 =
+        (reinterpret_cast<uintptr_t>(p.a) + (uintptr_t)p.m * p.kp + 3u) & ~(uintptr_t)3;
+    auto pb_of = [&](uint32_t s) { return s * (kPfStep / 5) + (uint32_t)(kDecB * d); };
+    auto addr_of = [&](uint32_t s) {
+        return reinterpret_cast<uintptr_t>(arow) + (pb_of(s) < p.kp ? pb_of(s) : 0u);
+    };
+    auto first_of = [&](uintptr_t a) { return min(a & ~(uintptr_t)3, a_end4 - 12u); };
+    uint32_t pk[kPfDepth][3];
+    auto load = [&](uint32_t s, int r) {
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(first_of(addr_of(s)));
+#pragma unroll
+        for (int i = 0; i < 3; ++i) pk[r][i] = w[i];
+#pragma unroll
+        for (int h = 0; h < kStageN; ++h)
+            bv[r][h] = p.b[b_ok(s + 1, h) ? (s + 1) * kPfStep + (uint32_t)(e + kSL * h) : 0u];
+        // keep every step's loads in one order (prologue and loop alike), so
+        // that each step waits only for its own
+        __builtin_amdgcn_sched_barrier(0);
+    };
+#pragma unroll
+    for (int r = 0; r < kPfDepth; ++r) load((uint32_t)r, r);
+    for (uint32_t s0 = 0; s0 < steps_p; s0 += kPfDepth) {
+#pragma unroll
+        for (int r = 0; r < kPfDepth; ++r) {
+            const uint32_t s = s0 + r;
+            const int buf = s & 1;
+            const f32x4* bq = bb[buf] + kDecQ * d;
+            uint32_t any_bad = 0;
+#pragma unroll
+            for (int i = 0; i < kPfDec; ++i) any_bad |= bflag[buf][i];
+            const bool safe = any_bad == 0u;
+            // b of step s + 1 into the other buffer (read after the barrier)
+            stage_b(s + 1, buf ^ 1, bv[r]);
+            // the slice's b first, then the digits, the terms and the stores
+            f32x4 bx[kDecQ];
+#pragma unroll
+            for (int q = 0; q < kDecQ; ++q) bx[q] = bq[q];
+            // the step's 8 bytes (bytes past the row: 121, five zero trits)
+            uint32_t wd[2];
+            {
+                const uintptr_t a = addr_of(s);
+                const uint32_t o = (uint32_t)(a - first_of(a));
+                const uint32_t o4 = o >> 2, sh = o & 3u;
+                const uint32_t e0 = o4 == 0 ? pk[r][0] : (o4 == 1 ? pk[r][1] : pk[r][2]);
+                const uint32_t e1 = o4 == 0 ? pk[r][1] : (o4 == 1 ? pk[r][2] : 0u);
+                const uint32_t e2 = o4 == 0 ? pk[r][2] : 0u;
+                wd[0] = __builtin_amdgcn_alignbyte(e1, e0, sh);
+                wd[1] = __builtin_amdgcn_alignbyte(e2, e1, sh);
+                const uint32_t pb = pb_of(s);
+                const uint32_t nvalid = pb < p.kp ? min(p.kp - pb, (uint32_t)kDecB) : 0u;  // step-uniform
+                if (nvalid < (uint32_t)kDecB) {
+#pragma unroll
+                    for (int j = 0; j < kDecB; ++j)
+                        if ((uint32_t)j >= nvalid)
+                            wd[j / 4] = (wd[j / 4] & ~(0xffu << (8 * (j % 4)))) | (kZeroByte << (8 * (j % 4)));
+                }
+            }
+            // base-3 digits u = t + 1 of each byte; bytes >= 243 decode as
+            // 121 (all zero trits).  Each stage runs over all the bytes
+            // before the next, so that no operation waits on the one just
+            // issued.
+            float x[kDecB], q[4][kDecB], u[kDecB * 5];
+#pragma unroll
+            for (int j = 0; j < kDecB; ++j) {
+                const uint32_t w = wd[j / 4];
+                x[j] = (float)((w >> (8 * (j % 4))) & 0xffu);
+            }
+#pragma unroll
+            for (int j = 0; j < kDecB; ++j) x[j] = x[j] >= 243.0f ? 121.0f : x[j];
+            constexpr float kInv3[4] = {0x1.555558p-2f, 0x1.c71c74p-4f, 0x1.2f684ep-5f, 0x1.948b12p-7f};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < kDecB; ++j) q[i][j] = x[j] * kInv3[i];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < kDecB; ++j) q[i][j] = __builtin_floorf(q[i][j]);
+#pragma unroll
+            for (int j = 0; j < kDecB; ++j) {
+                u[5 * j] = __builtin_fmaf(q[0][j], -3.0f, x[j]);
+                u[5 * j + 1] = __builtin_fmaf(q[1][j], -3.0f, q[0][j]);
+                u[5 * j + 2] = __builtin_fmaf(q[2][j], -3.0f, q[1][j]);
+                u[5 * j + 3] = __builtin_fmaf(q[3][j], -3.0f, q[2][j]);
+                u[5 * j + 4] = q[3][j];
+            }
+            // term = (u - 1) * b: fma(u, b, -b) is exact (-b, +0 or b) for
+            // finite b; otherwise selected, +0 for a zero trit
+            if (safe) {
+#pragma unroll
+                for (int q = 0; q < kDecQ; ++q) {
+                    f32x4 v;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) v[c] = __builtin_fmaf(u[4 * q + c], bx[q][c], -bx[q][c]);
+                    tb[buf][kDecQ * d + q][lane] = v;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < kDecQ; ++q) {
+                    f32x4 v;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        v[c] = u[4 * q + c] == 1.0f ? 0.0f : (u[4 * q + c] == 0.0f ? -bx[q][c] : bx[q][c]);
+                    tb[buf][kDecQ * d + q][lane] = v;
+                }
+            }
+            // unconditional (in bounds past the last step too), so that the
+            // wait for each step's loads is a fixed count
+            load(s + kPfDepth, r);
+            __syncthreads();
+        }
+    }
+    __syncthreads();  // the fold of the last step
+}
+
 static uint64_t f32_rows_per_block(int ct, uint64_t m) {
     if (ct <= 8) return 4 * (kWave / ct);
     if (ct <= 32) return 4 * (kWave / ct) * 2;
@@ -1016,6 +1253,10 @@ extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float*
     const uint64_t gx = (m + rb - 1) / rb, gy = (n + ct - 1) / ct;
     if (gx > 0x7fffffffull || gy > 65535) return KORE_HIP_ERR_OVERFLOW;
     const dim3 g((uint32_t)gx, (uint32_t)gy);
+    if (n == 1 && k > 0 && mkp >= 12) {
+        hipLaunchKernelGGL(ternary_f32_pipe_kernel, dim3((uint32_t)((m + kWave - 1) / kWave)), dim3((kPfDec + 1) * kWave), 0, s, p);
+        return launch_status();
+    }
     if (kp % 16 == 0 && aligned16(a_packed)) launch_f32_seq<true>(ct, m, g, s, p);
     else launch_f32_seq<false>(ct, m, g, s, p);
     return launch_status();

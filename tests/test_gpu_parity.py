@@ -643,7 +643,12 @@ def test_ternary_matmul_i8_edges():
 
 TERN_F32_SHAPES = [(1, 1, 5), (7, 1, 2560), (6912, 1, 2560), (33, 3, 161), (64, 5, 1000), (130, 17, 320),
                    (65, 64, 2560), (9, 65, 2563), (257, 130, 799), (2, 200, 6920), (40, 33, 0), (6500, 64, 320),
-                   (301, 24, 640)]
+                   (301, 24, 640),
+                   # one column (the decode-step kernel): any packed-row alignment, partial
+                   # last steps, more workgroups than CUs, and matrices whose last bytes
+                   # sit at the end of the allocation (m * kp as small as 12)
+                   (1, 1, 60), (3, 1, 21), (2, 1, 30), (37, 1, 333), (65, 1, 245), (300, 1, 1203),
+                   (2560, 1, 6912), (20000, 1, 480), (129, 1, 241)]
 
 
 @pytest.mark.parametrize("m,n,k", TERN_F32_SHAPES)
@@ -662,12 +667,14 @@ def test_ternary_matmul_f32(m, n, k):
     assert_bitexact(got, oracle.ternary_matmul(p, sa, b, m, n, k), "ternary_matmul_f32")
 
 
-def test_ternary_matmul_f32_order_and_nonfinite():
+@pytest.mark.parametrize("n", [1, 2])
+def test_ternary_matmul_f32_order_and_nonfinite(n):
     """Cancellation that only the reference's k order produces, and Inf/NaN
     activations at zero-trit positions (skipped by the reference) next to
-    ones at nonzero trits (propagated)."""
-    log("ternary_matmul_f32 order and non-finite")
-    m, n, k = 3, 2, 400
+    ones at nonzero trits (propagated); one column runs the decode-step
+    kernel."""
+    log(f"ternary_matmul_f32 order and non-finite n={n}")
+    m, k = 3, 400
     w = np.zeros((m, k), np.float32)
     w[0, :3] = 1.0              # row 0: b0 + b1 + b2 in order
     w[1, 0] = 1.0; w[1, 5] = -1.0  # row 1: zero trits over the Inf/NaN positions
@@ -675,11 +682,29 @@ def test_ternary_matmul_f32_order_and_nonfinite():
     p, sa = oracle.pack_weights_ternary(w, 0.3)
     b = np.zeros((k, n), np.float32)
     b[0, :] = 1e8; b[1, :] = 1.0; b[2, :] = -1e8  # sequential: (1e8 + 1) - 1e8 = 0, not 1
-    b[3, 0] = np.inf; b[4, 1] = np.nan; b[5, :] = 2.0; b[7, 0] = np.inf
+    b[3, 0] = np.inf; b[5, :] = 2.0; b[7, 0] = np.inf
+    if n > 1:
+        b[4, 1] = np.nan
     want = oracle.ternary_matmul(p, sa, b, m, n, k)
     assert want[0, 0] == 0.0 and np.isfinite(want[1]).all() and np.isinf(want[2, 0])
     got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
     assert_bitexact(got, want, "ternary_matmul_f32 order/non-finite")
+
+
+def test_ternary_matmul_f32_decode_nonfinite_steps():
+    """One column over several K steps and workgroups, Inf/NaN activations
+    in some steps only (those steps select their terms, the others take the
+    product path): bit-exact against the oracle, non-finite rows included."""
+    from inputs import raw_packed
+
+    m, k = 130, 1203
+    log(f"ternary_matmul_f32 decode non-finite m={m} k={k}")
+    p, sa, b = raw_packed(m, k, 21), normal((m,), 22, 1.0, 0.1), normal((k, 1), 23)
+    b[5, 0] = np.inf; b[250, 0] = -np.inf; b[777, 0] = np.nan; b[1200, 0] = np.inf
+    want = oracle.ternary_matmul(p, sa, b, m, 1, k)
+    assert np.isfinite(want).any() and not np.isfinite(want).all()
+    got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, 1, k), np.float32, (m, 1))
+    assert_bitexact(got, want, "ternary_matmul_f32 decode non-finite")
 
 
 def test_ternary_matmul_f32_edges():
@@ -693,13 +718,13 @@ def test_ternary_matmul_f32_edges():
     # unaligned activations and an odd packed-row length: same results
     from inputs import raw_packed
 
-    m, n, k = 50, 3, 333
-    p, sa, b = raw_packed(m, k, 3), normal((m,), 4), normal((k, n), 5)
-    t = torch.empty(k * n + 1, dtype=torch.float32, device="cuda")
-    t[1:].copy_(torch.from_numpy(b.ravel()))
-    got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), HipBuffer.from_tensor(t[1:]), m, n, k),
-               np.float32, (m, n))
-    assert_bitexact(got, oracle.ternary_matmul(p, sa, b, m, n, k), "ternary_matmul_f32 unaligned b")
+    for m, n, k in ((50, 3, 333), (50, 1, 333)):
+        p, sa, b = raw_packed(m, k, 3), normal((m,), 4), normal((k, n), 5)
+        t = torch.empty(k * n + 1, dtype=torch.float32, device="cuda")
+        t[1:].copy_(torch.from_numpy(b.ravel()))
+        got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), HipBuffer.from_tensor(t[1:]), m, n, k),
+                   np.float32, (m, n))
+        assert_bitexact(got, oracle.ternary_matmul(p, sa, b, m, n, k), f"ternary_matmul_f32 unaligned b n={n}")
 
 
 def test_decode_chain_graph_replays_match_eager():
