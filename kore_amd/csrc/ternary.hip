@@ -40,8 +40,8 @@
 // reference loop order.
 //
 // kore_hip_ternary_matmul_f32: the reference's f32-activation ternary_matmul,
-// a sequential fold per output (ternary_f32_seq_kernel, and for one column
-// ternary_f32_pipe_kernel, at the end).
+// a sequential fold per output (ternary_f32_seq_kernel, and for up to four
+// columns ternary_f32_pipe_kernel, at the end).
 #include <algorithm>
 
 #include "common.hpp"
@@ -881,14 +881,15 @@ static void launch_f32_seq(int ct, uint64_t m, dim3 g, hipStream_t s, const Tern
 #undef KORE_F32_SEQ
 }
 
-// One column (a decode step, n == 1), any row alignment.  The
+// One to four columns (decode steps), any row alignment.  The
 // fold is a chain of k dependent f32 operations per output, so its floor is k
 // times the latency of one dependent vector operation (about 8 cycles for a
 // single wave); the per-lane kernel above also puts the decode, the table and
-// the b reads into that chain's wave.  Here a workgroup of seven waves owns 64
-// rows: six waves decode and form the terms t * b in LDS, one wave folds them
-// with plain dependent adds, nothing else in its instruction stream but the
-// 16-byte LDS reads of the terms.
+// the b reads into that chain's wave.  Here a workgroup owns 64 rows: six
+// waves decode, and one fold wave per column runs the chain.  With one
+// column the decoders form the terms t * b in LDS and the fold wave adds
+// them, nothing else in its instruction stream but the 16-byte LDS reads of
+// the terms (with more columns, see the kernel).
 //
 // A term is fl(t * b) = +-b exactly for a nonzero trit and +-0 for a zero
 // one, and acc + (+-0) = acc (acc is never -0): acc + term is the
@@ -909,89 +910,130 @@ constexpr int kPfStep = 240;               // K columns per step
 constexpr int kPfDec = 6;                  // decoding waves
 constexpr int kDecB = kPfStep / 5 / kPfDec;  // packed bytes per decoder and step
 constexpr int kDecQ = kDecB * 5 / 4;         // ... as groups of 4 terms
-constexpr int kStageN = (kPfStep + kPfDec * kWave - 1) / (kPfDec * kWave);  // b elements per decoder lane
 static_assert(kDecB * kPfDec * 5 == kPfStep && kDecB % 4 == 0, "decoder split");
 constexpr int kPfQuads = kPfStep / 4;      // 16-byte groups of 4 terms per step
 constexpr int kPfDepth = 2;                // steps of loads in flight
 
 // One workgroup per CU (its LDS): the compiler may use registers for
 // instruction-level parallelism rather than occupancy.
-__global__ __launch_bounds__((kPfDec + 1) * kWave) __attribute__((amdgpu_waves_per_eu(1, 1)))
+//
+// CT = 1: the decoders write the terms t * b and the fold wave adds them.
+// CT = 2 or 4 columns (decode batches of 2-4 tokens): the decoders write the
+// trits once (as floats) and fold wave c of the CT computes
+// acc = fma(t, b[., c], acc), b read from LDS (the same address in every
+// lane); a step whose column-c b holds an Inf or NaN skips zero trits
+// explicitly.
+template <int CT>
+__global__ __launch_bounds__((kPfDec + CT) * kWave) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void ternary_f32_pipe_kernel(TernF32Args p) {
-    // terms of the step per group of 4 columns, lane-major (a lane reads and
-    // writes 16 consecutive bytes: conflict-free); 120 KB
+    constexpr int kStageN = (CT * kPfStep + kPfDec * kWave - 1) / (kPfDec * kWave);  // b elements per decoder lane
+    // terms (CT = 1) or trits of the step per group of 4 K columns,
+    // lane-major (a lane reads and writes 16 consecutive bytes:
+    // conflict-free); 120 KB
     __shared__ f32x4 tb[2][kPfQuads][kWave];
-    __shared__ f32x4 bb[2][kPfQuads];  // b of a step, zero past k
-    __shared__ uint32_t bflag[2][kPfDec];
+    // b of a step per column, zero past k and n; three buffers: in iteration
+    // s the decoders write step s + 1 while the fold waves read step s - 1
+    // (and the decoders, for one column, step s)
+    __shared__ f32x4 bb[3][CT][kPfQuads];
+    __shared__ uint32_t bflag[2][kPfDec];   // per decoder: columns whose staged b holds an Inf or NaN
+    __shared__ uint32_t tmask[2];           // the same for the step whose trits are in tb[buf]
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
     const int wave = t / kWave;
     const uint32_t row = blockIdx.x * kWave + lane;
+    const uint32_t col0 = blockIdx.y * CT;
     const uint32_t steps = (p.k + kPfStep - 1) / kPfStep;
     // the decoders run whole rounds of kPfDepth steps (the ones past K decode
     // zeros), so that every round issues and waits for its loads alike
     const uint32_t steps_p = (steps + kPfDepth - 1) / kPfDepth * kPfDepth;
-    // b staging: decoder lane e takes elements e + h * (decoder lanes) < 240
-    const int e = (wave - 1) * kWave + lane;
+    // b staging: decoder lane e takes elements e + h * (decoder lanes) of the
+    // step's CT x 240 (K-major, as b[K, N] is stored)
+    const int e = (wave - CT) * kWave + lane;
     constexpr int kSL = kPfDec * kWave;
     auto b_ok = [&](uint32_t s, int h) {
-        return (e + kSL * h) < kPfStep && s * kPfStep + (uint32_t)(e + kSL * h) < p.k;
+        const int i = e + kSL * h;
+        return i < CT * kPfStep && s * kPfStep + (uint32_t)(i / CT) < p.k && col0 + (uint32_t)(i % CT) < p.n;
+    };
+    auto b_idx = [&](uint32_t s, int h) {
+        const int i = e + kSL * h;
+        return b_ok(s, h) ? (uint64_t)(s * kPfStep + (uint32_t)(i / CT)) * p.n + col0 + (uint32_t)(i % CT) : 0u;
     };
     float bv[kPfDepth][kStageN];
-    // stage b of step s into bb[buf]; bflag[buf][d]: decoder d staged an Inf
-    // or NaN
+    // stage b of step s into bb[s % 3]; bflag[buf][d]: the columns in which
+    // decoder d staged an Inf or NaN
     auto stage_b = [&](uint32_t s, int buf, const float (&v)[kStageN]) {
-        bool bad = false;
+        const uint32_t bbuf = s % 3u;
+        uint32_t bad = 0;
 #pragma unroll
-        for (int h = 0; h < kStageN; ++h)
-            if (e + kSL * h < kPfStep) {
+        for (int h = 0; h < kStageN; ++h) {
+            const int i = e + kSL * h;
+            if (i < CT * kPfStep) {
                 const float x = b_ok(s, h) ? v[h] : 0.0f;
-                reinterpret_cast<float*>(bb[buf])[e + kSL * h] = x;
-                bad |= !__builtin_isfinite(x);
+                reinterpret_cast<float*>(bb[bbuf][i % CT])[i / CT] = x;
+                bad |= __builtin_isfinite(x) ? 0u : 1u << (i % CT);
             }
-        const bool any_bad = __any(bad);
-        if (lane == 0) bflag[buf][wave - 1] = any_bad ? 1u : 0u;
+        }
+        uint32_t mask = 0;
+#pragma unroll
+        for (int c = 0; c < CT; ++c) mask |= __any((bad >> c) & 1u) ? 1u << c : 0u;
+        if (lane == 0) bflag[buf][wave - CT] = mask;
     };
-    if (wave > 0) {
+    if (wave >= CT) {
         float v[kStageN];
 #pragma unroll
-        for (int h = 0; h < kStageN; ++h) v[h] = p.b[b_ok(0, h) ? (uint32_t)(e + kSL * h) : 0u];
+        for (int h = 0; h < kStageN; ++h) v[h] = p.b[b_idx(0, h)];
         stage_b(0, 0, v);
     }
     __syncthreads();  // b of step 0
-    if (wave == 0) {
+    if (wave < CT) {
+        // fold wave of column col0 + wave
+        const int c = wave;
         float acc = 0.0f;
         for (uint32_t s = 0; s <= steps_p; ++s) {
             if (s > 0 && s <= steps) {
                 const int buf = (s - 1) & 1;
+                const uint32_t bbuf = (s - 1) % 3u;
                 // batches of kFb groups, the next batch's reads in flight
-                // during a batch's adds
-                constexpr int kFb = 6;
-                f32x4 tq[2][kFb];
+                // during a batch's operations
+                constexpr int kFb = CT == 1 ? 6 : 4;
+                if (CT == 1 || ((tmask[buf] >> c) & 1u) == 0u) {
+                    f32x4 tq[2][kFb], bq[2][kFb];
+                    auto rd = [&](int slot, int g0) {
 #pragma unroll
-                for (int i = 0; i < kFb; ++i) tq[0][i] = tb[buf][i][lane];
+                        for (int i = 0; i < kFb; ++i) {
+                            tq[slot][i] = tb[buf][g0 + i][lane];
+                            if (CT > 1) bq[slot][i] = bb[bbuf][c][g0 + i];
+                        }
+                    };
+                    rd(0, 0);
 #pragma unroll
-                for (int bt = 0; bt < kPfQuads / kFb; ++bt) {
-                    const int cur = bt & 1;
-                    if (bt + 1 < kPfQuads / kFb) {
+                    for (int bt = 0; bt < kPfQuads / kFb; ++bt) {
+                        const int cur = bt & 1;
+                        if (bt + 1 < kPfQuads / kFb) rd(cur ^ 1, (bt + 1) * kFb);
 #pragma unroll
-                        for (int i = 0; i < kFb; ++i) tq[cur ^ 1][i] = tb[buf][(bt + 1) * kFb + i][lane];
+                        for (int i = 0; i < kFb; ++i)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) {
+                                if (CT == 1) acc += tq[cur][i][j];
+                                else acc = __builtin_fmaf(tq[cur][i][j], bq[cur][i][j], acc);
+                            }
                     }
+                } else {
+                    for (int g = 0; g < kPfQuads; ++g) {
+                        const f32x4 t4 = tb[buf][g][lane];
+                        const f32x4 b4 = bb[bbuf][c][g];
 #pragma unroll
-                    for (int i = 0; i < kFb; ++i) {
-                        acc += tq[cur][i].x;
-                        acc += tq[cur][i].y;
-                        acc += tq[cur][i].z;
-                        acc += tq[cur][i].w;
+                        for (int j = 0; j < 4; ++j)
+                            if (t4[j] != 0.0f) acc = __builtin_fmaf(t4[j], b4[j], acc);
                     }
                 }
             }
             __syncthreads();
         }
-        if (row < p.m) p.c[row] = acc * p.sa[row];
+        if (row < p.m && col0 + c < p.n) p.c[(uint64_t)row * p.n + col0 + c] = acc * p.sa[row];
         return;
     }
-    const int d = wave - 1;
+    const int d = wave - CT;
     const uint8_t* arow = p.a + (uint64_t)(row < p.m ? row : 0u) * p.kp;
     // Loads are unconditional, at clamped in-bounds addresses; what lies
     // past the row or past k is replaced when the step is used (a select
@@ -1015,8 +1057,7 @@ void ternary_f32_pipe_kernel(TernF32Args p) {
 #pragma unroll
         for (int i = 0; i < 3; ++i) pk[r][i] = w[i];
 #pragma unroll
-        for (int h = 0; h < kStageN; ++h)
-            bv[r][h] = p.b[b_ok(s + 1, h) ? (s + 1) * kPfStep + (uint32_t)(e + kSL * h) : 0u];
+        for (int h = 0; h < kStageN; ++h) bv[r][h] = p.b[b_idx(s + 1, h)];
         // keep every step's loads in one order (prologue and loop alike), so
         // that each step waits only for its own
         __builtin_amdgcn_sched_barrier(0);
@@ -1028,17 +1069,21 @@ void ternary_f32_pipe_kernel(TernF32Args p) {
         for (int r = 0; r < kPfDepth; ++r) {
             const uint32_t s = s0 + r;
             const int buf = s & 1;
-            const f32x4* bq = bb[buf] + kDecQ * d;
+            const f32x4* bq = bb[s % 3u][0] + kDecQ * d;
             uint32_t any_bad = 0;
 #pragma unroll
             for (int i = 0; i < kPfDec; ++i) any_bad |= bflag[buf][i];
+            if (CT > 1 && d == 0 && lane == 0) tmask[buf] = any_bad;
             const bool safe = any_bad == 0u;
             // b of step s + 1 into the other buffer (read after the barrier)
             stage_b(s + 1, buf ^ 1, bv[r]);
-            // the slice's b first, then the digits, the terms and the stores
+            // the slice's b first (one column), then the digits, the terms
+            // and the stores
             f32x4 bx[kDecQ];
+            if (CT == 1) {
 #pragma unroll
-            for (int q = 0; q < kDecQ; ++q) bx[q] = bq[q];
+                for (int q = 0; q < kDecQ; ++q) bx[q] = bq[q];
+            }
             // the step's 8 bytes (bytes past the row: 121, five zero trits)
             uint32_t wd[2];
             {
@@ -1088,9 +1133,15 @@ void ternary_f32_pipe_kernel(TernF32Args p) {
                 u[5 * j + 3] = __builtin_fmaf(q[3][j], -3.0f, q[2][j]);
                 u[5 * j + 4] = q[3][j];
             }
-            // term = (u - 1) * b: fma(u, b, -b) is exact (-b, +0 or b) for
-            // finite b; otherwise selected, +0 for a zero trit
-            if (safe) {
+            if (CT > 1) {
+                // the trits t = u - 1
+#pragma unroll
+                for (int q = 0; q < kDecQ; ++q)
+                    tb[buf][kDecQ * d + q][lane] =
+                        f32x4{u[4 * q] - 1.0f, u[4 * q + 1] - 1.0f, u[4 * q + 2] - 1.0f, u[4 * q + 3] - 1.0f};
+            } else if (safe) {
+                // term = (u - 1) * b: fma(u, b, -b) is exact (-b, +0 or b)
+                // for finite b; otherwise selected, +0 for a zero trit
 #pragma unroll
                 for (int q = 0; q < kDecQ; ++q) {
                     f32x4 v;
@@ -1253,8 +1304,11 @@ extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float*
     const uint64_t gx = (m + rb - 1) / rb, gy = (n + ct - 1) / ct;
     if (gx > 0x7fffffffull || gy > 65535) return KORE_HIP_ERR_OVERFLOW;
     const dim3 g((uint32_t)gx, (uint32_t)gy);
-    if (n == 1 && k > 0 && mkp >= 12) {
-        hipLaunchKernelGGL(ternary_f32_pipe_kernel, dim3((uint32_t)((m + kWave - 1) / kWave)), dim3((kPfDec + 1) * kWave), 0, s, p);
+    if (n <= 4 && k > 0 && mkp >= 12) {
+        const dim3 gp((uint32_t)((m + kWave - 1) / kWave));
+        if (n == 1) hipLaunchKernelGGL(ternary_f32_pipe_kernel<1>, gp, dim3((kPfDec + 1) * kWave), 0, s, p);
+        else if (n == 2) hipLaunchKernelGGL(ternary_f32_pipe_kernel<2>, gp, dim3((kPfDec + 2) * kWave), 0, s, p);
+        else hipLaunchKernelGGL(ternary_f32_pipe_kernel<4>, gp, dim3((kPfDec + 4) * kWave), 0, s, p);
         return launch_status();
     }
     if (kp % 16 == 0 && aligned16(a_packed)) launch_f32_seq<true>(ct, m, g, s, p);

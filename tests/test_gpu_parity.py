@@ -648,7 +648,9 @@ TERN_F32_SHAPES = [(1, 1, 5), (7, 1, 2560), (6912, 1, 2560), (33, 3, 161), (64, 
                    # last steps, more workgroups than CUs, and matrices whose last bytes
                    # sit at the end of the allocation (m * kp as small as 12)
                    (1, 1, 60), (3, 1, 21), (2, 1, 30), (37, 1, 333), (65, 1, 245), (300, 1, 1203),
-                   (2560, 1, 6912), (20000, 1, 480), (129, 1, 241)]
+                   (2560, 1, 6912), (20000, 1, 480), (129, 1, 241),
+                   # two to four columns (the same kernel with one fold wave per column)
+                   (6912, 2, 2560), (301, 4, 1203), (1, 2, 60), (129, 3, 241), (5, 4, 24), (2560, 3, 6912)]
 
 
 @pytest.mark.parametrize("m,n,k", TERN_F32_SHAPES)
@@ -691,20 +693,22 @@ def test_ternary_matmul_f32_order_and_nonfinite(n):
     assert_bitexact(got, want, "ternary_matmul_f32 order/non-finite")
 
 
-def test_ternary_matmul_f32_decode_nonfinite_steps():
-    """One column over several K steps and workgroups, Inf/NaN activations
-    in some steps only (those steps select their terms, the others take the
-    product path): bit-exact against the oracle, non-finite rows included."""
+@pytest.mark.parametrize("n", [1, 2, 3, 4])
+def test_ternary_matmul_f32_decode_nonfinite_steps(n):
+    """One to four columns over several K steps and workgroups, Inf/NaN
+    activations in some steps and columns only (those take the explicit
+    zero-trit skip, the others the fast path): bit-exact against the oracle,
+    non-finite outputs included."""
     from inputs import raw_packed
 
     m, k = 130, 1203
-    log(f"ternary_matmul_f32 decode non-finite m={m} k={k}")
-    p, sa, b = raw_packed(m, k, 21), normal((m,), 22, 1.0, 0.1), normal((k, 1), 23)
-    b[5, 0] = np.inf; b[250, 0] = -np.inf; b[777, 0] = np.nan; b[1200, 0] = np.inf
-    want = oracle.ternary_matmul(p, sa, b, m, 1, k)
+    log(f"ternary_matmul_f32 decode non-finite m={m} n={n} k={k}")
+    p, sa, b = raw_packed(m, k, 21), normal((m,), 22, 1.0, 0.1), normal((k, n), 23)
+    b[5, 0] = np.inf; b[250, n - 1] = -np.inf; b[777, 0] = np.nan; b[1200, n // 2] = np.inf
+    want = oracle.ternary_matmul(p, sa, b, m, n, k)
     assert np.isfinite(want).any() and not np.isfinite(want).all()
-    got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, 1, k), np.float32, (m, 1))
-    assert_bitexact(got, want, "ternary_matmul_f32 decode non-finite")
+    got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
+    assert_bitexact(got, want, f"ternary_matmul_f32 decode non-finite n={n}")
 
 
 def test_ternary_matmul_f32_edges():
