@@ -1042,7 +1042,9 @@ void ternary_f32_pipe_kernel(TernF32Args p) {
     // at floor4(address), clamped so that the three end at ceil4 of the
     // matrix's end (the host launches this kernel for m * kp >= 12 only); the
     // bytes are then at offset o = address - first dword (o < 4 unless
-    // clamped, and up to 11 for the matrix's last bytes).
+    // clamped, and up to 11 for the matrix's last bytes).  Only the dwords
+    // holding the matrix's first and last bytes can reach past it, by at most
+    // 3 bytes that are never used; a dword never spans two pages.
     static_assert(kDecB == 8, "three-dword window");
     const uintptr_t a_end4 =
         (reinterpret_cast<uintptr_t>(p.a) + (uintptr_t)p.m * p.kp + 3u) & ~(uintptr_t)3;
