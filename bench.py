@@ -538,11 +538,11 @@ class TernaryF32(Workload):
     sequential f32 fold over K (bit-exact), one fma per term and lane, so the
     kernel is bound by vector issue along the K chain; reported as fp32 FMA
     throughput (2 flops per term) next to the bytes."""
-    kernel = "ternary_f32_seq_kernel"
     bound = "valu"
 
     def __init__(self, m=6912, n=1, k=2560):
         self.m, self.n, self.k = m, n, k
+        self.kernel = "ternary_f32_pipe_kernel" if n <= 4 else "ternary_f32_seq_kernel"
         self.kp = (k + 4) // 5
         self.name = f"ternary_f32_{m}x{n}x{k}"
         self.tokens = n
@@ -580,6 +580,45 @@ class TernaryF32(Workload):
             f"{m} weight rows x {self.n} tokens, single thread", 2 * m * self.n * self.k
 
 
+class PackTernary(Workload):
+    """Weight packing (kore_hip_pack_weights_ternary, the reference's
+    pack_weights_ternary): f32 weights of the 2560 -> 6912 BitLinear to
+    base-243 bytes and per-row scales, bit-exact.  Reads 4 m k bytes, writes
+    m ceil(k/5) + 4 m: HBM-bound."""
+    kernel = "ternary_pack_kernel"
+
+    def __init__(self, m=6912, k=2560):
+        self.m, self.k = m, k
+        self.kp = (k + 4) // 5
+        self.name = f"pack_weights_ternary_{m}x{k}"
+        self.tokens = m  # weight rows
+        self.bytes = 4 * m * k + m * self.kp + 4 * m
+        self.desc = f"ternary weight packing w[{m},{k}] f32 -> base-243 bytes [{m},{self.kp}] + scales, threshold 0.3"
+
+    def setup(self, torch, lib):
+        self.lib = lib
+        self.k_sets = n_sets(self.bytes)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(0)
+        self._dw = [torch.randn((self.m * self.k,), generator=g, device="cuda") for _ in range(self.k_sets)]
+        self._dp = [torch.empty(self.m * self.kp, dtype=torch.uint8, device="cuda") for _ in range(self.k_sets)]
+        self._ds = [torch.empty(self.m, device="cuda") for _ in range(self.k_sets)]
+
+    def launch(self, i, stream):
+        j = i % self.k_sets
+        return self.lib.kore_hip_pack_weights_ternary(self._dw[j].data_ptr(), self.m, self.k, 0.3,
+                                                      self._dp[j].data_ptr(), self._ds[j].data_ptr(), stream)
+
+    def cpu_sample(self):
+        import oracle
+        from inputs import normal
+
+        m = 1024
+        w = normal((m, self.k), 3)
+        return (lambda: oracle.pack_weights_ternary(w, 0.3)), 4 * m * self.k + m * self.kp + 4 * m, m, 1, \
+            f"{m} weight rows, single thread"
+
+
 class Copy(Workload):
     """A plain 1 GiB device copy through the gather kernel with ids = 0..N-1;
     used to calibrate rocprof's FETCH_SIZE / WRITE_SIZE counters."""
@@ -610,7 +649,7 @@ def all_workloads():
     return [RopeQK(False), RopeQK(True), RMSNorm(32, 2048), RMSNorm(16384, 2048), Swiglu(), Gelu(), Embedding(),
             Prequant(4096), Prequant(64), Prequant(1), RmsNormSiluGate(), Softmax(), SoftmaxBackward(),
             RmsNormBackward(), TernaryI8(), TernaryI8(6912, 64, 2560), TernaryI8(6912, 1, 2560), TernaryF32(),
-            TernaryF32(6912, 64, 2560), Copy()]
+            TernaryF32(6912, 64, 2560), PackTernary(), Copy()]
 
 
 # ------------------------------------------------------------------ measure

@@ -254,6 +254,19 @@ int kore_hip_ternary_matmul_f32(const uint8_t *a_packed, const float *a_scales,
                                 const float *b, float *c, uint64_t m,
                                 uint64_t n, uint64_t k, kore_stream_t stream);
 
+/* Quantise f32 weights w[m, k] (row-major) to ternary with a per-row scale
+ * and pack them base-243, the weight format both matmuls read: replaces
+ * pack_weights_ternary (crates/kore-kernels/src/cpu_ternary_matmul.rs:198-240;
+ * encode_trits crates/kore-btes/src/encoder.rs:72-86).  scales[row] =
+ * max |w| of the row (NaN dropped; 1.0 below 1e-8); a weight's trit is +1 /
+ * -1 / 0 as w / scale (IEEE quotient) is > threshold / < -threshold /
+ * otherwise; packed[row, j] = sum over i < 5 of (trit[5 j + i] + 1) * 3^i,
+ * zero trits past k.  Bit-exact.  packed [m, ceil(k/5)] and scales [m] must
+ * not overlap w (KORE_HIP_ERR_ALIAS). */
+int kore_hip_pack_weights_ternary(const float *w, uint64_t m, uint64_t k,
+                                  float threshold, uint8_t *packed,
+                                  float *scales, kore_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

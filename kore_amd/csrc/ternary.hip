@@ -1176,6 +1176,103 @@ static uint64_t f32_rows_per_block(int ct, uint64_t m) {
     return m >= 32 * 200 ? 8 * 4 : 8 * 2;
 }
 
+// ---------------------------------------------------------------------------
+// Weight packing, the weight-side format of the matmuls above
+// (pack_weights_ternary, cpu_ternary_matmul.rs:198-240; encode_trits,
+// kore-btes/src/encoder.rs:72-86): per row, scale = max |w| (f32::max drops
+// NaN; 1.0 below 1e-8), trit = +1 / -1 / 0 for w / scale (the IEEE quotient)
+// > threshold / < -threshold / otherwise (NaN: 0), and byte j = sum over i of
+// (trit[5 j + i] + 1) * 3^i, zero trits past k.  HBM-bound: 4 m k bytes
+// read, m ceil(k/5) + 4 m written.
+//
+// One wave per row.  Vector path (k % 20 == 0, 16-byte aligned rows,
+// k <= 64 * 20 * NC): lane l owns the 20-float chunks l, l + 64, ... (NC of
+// them, held in registers), so the row is read once; a chunk packs into 4
+// bytes, one dword store.  Otherwise the generic path reads the row twice
+// (max, then one byte per lane and step).
+constexpr int kPackWaves = 4;
+
+__device__ __forceinline__ uint32_t trit_digit(float x, float scale, float threshold) {
+    const float nv = x / scale;
+    return nv > threshold ? 2u : (nv < -threshold ? 0u : 1u);
+}
+
+template <int NC>
+__global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_vec_kernel(const float* __restrict__ w, uint64_t m,
+                                                                              uint32_t k, float threshold,
+                                                                              uint8_t* __restrict__ packed,
+                                                                              float* __restrict__ scales) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint64_t row = (uint64_t)blockIdx.x * kPackWaves + threadIdx.x / kWave;
+    if (row >= m) return;  // whole waves; no barriers below
+    const uint32_t chunks = k / 20;
+    const f32x4* rd = reinterpret_cast<const f32x4*>(w + row * k);
+    f32x4 v[NC][5];
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const uint32_t ch = (uint32_t)lane + kWave * c;
+        const uint32_t src = ch < chunks ? ch : 0u;  // clamped, in-bounds
+#pragma unroll
+        for (int q = 0; q < 5; ++q) v[c][q] = ld_stream(rd + 5 * src + q);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+        if ((uint32_t)lane + kWave * c < chunks)
+#pragma unroll
+            for (int q = 0; q < 5; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(v[c][q][e]));
+    amax = wave_max(amax);
+    const float scale = amax < 1e-8f ? 1.0f : amax;
+    if (lane == 0) scales[row] = scale;
+    uint32_t* pr = reinterpret_cast<uint32_t*>(packed + row * (k / 5));
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const uint32_t ch = (uint32_t)lane + kWave * c;
+        if (ch >= chunks) break;
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            uint32_t val = 0, mul = 1;
+#pragma unroll
+            for (int j = 0; j < 5; ++j) {
+                const int f = 5 * b + j;
+                val += trit_digit(v[c][f / 4][f % 4], scale, threshold) * mul;
+                mul *= 3u;
+            }
+            word |= val << (8 * b);
+        }
+        pr[ch] = word;
+    }
+}
+
+__global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_kernel(const float* __restrict__ w, uint64_t m,
+                                                                          uint32_t k, uint32_t kp, float threshold,
+                                                                          uint8_t* __restrict__ packed,
+                                                                          float* __restrict__ scales) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint64_t row = (uint64_t)blockIdx.x * kPackWaves + threadIdx.x / kWave;
+    if (row >= m) return;  // whole waves; no barriers below
+    const float* rd = w + row * k;
+    float amax = 0.0f;
+    for (uint32_t i = (uint32_t)lane; i < k; i += kWave) amax = fmaxf(amax, fabsf(rd[i]));
+    amax = wave_max(amax);
+    const float scale = amax < 1e-8f ? 1.0f : amax;
+    if (lane == 0) scales[row] = scale;
+    uint8_t* pr = packed + row * kp;
+    for (uint32_t b = (uint32_t)lane; b < kp; b += kWave) {
+        uint32_t val = 0, mul = 1;
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            const uint32_t i = 5u * b + (uint32_t)j;
+            val += (i < k ? trit_digit(rd[i], scale, threshold) : 1u) * mul;  // zero trits past k
+            mul *= 3u;
+        }
+        pr[b] = (uint8_t)val;
+    }
+}
+
 }  // namespace kore
 
 using namespace kore;
@@ -1315,5 +1412,39 @@ extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float*
     }
     if (kp % 16 == 0 && aligned16(a_packed)) launch_f32_seq<true>(ct, m, g, s, p);
     else launch_f32_seq<false>(ct, m, g, s, p);
+    return launch_status();
+}
+
+extern "C" int kore_hip_pack_weights_ternary(const float* w, uint64_t m, uint64_t k, float threshold,
+                                             uint8_t* packed, float* scales, kore_stream_t stream) {
+    if (m == 0) return KORE_HIP_OK;
+    if (!scales || (k > 0 && (!w || !packed))) return KORE_HIP_ERR_NULL_PTR;
+    uint64_t mk;
+    if (k > 0xffffffffull - 4 || !mul_ok(m, k, &mk) || mk > kMaxElements) return KORE_HIP_ERR_OVERFLOW;
+    const uint64_t kp = (k + 4) / 5;
+    // the outputs are written while w is read: no overlap
+    {
+        const char* w0 = reinterpret_cast<const char*>(w);
+        const char* w1 = w0 + mk * sizeof(float);
+        const struct { const void* p; uint64_t bytes; } outs[] = {{packed, m * kp}, {scales, m * sizeof(float)}};
+        for (const auto& o : outs) {
+            const char* o0 = reinterpret_cast<const char*>(o.p);
+            if (w && mk && o.p && o.bytes && o0 < w1 && w0 < o0 + o.bytes) return KORE_HIP_ERR_ALIAS;
+        }
+    }
+    const uint64_t blocks = (m + kPackWaves - 1) / kPackWaves;
+    if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
+    const dim3 g((uint32_t)blocks), blk(kPackWaves * kWave);
+    hipStream_t s = (hipStream_t)stream;
+    const uint64_t nc = (k / 20 + kWave - 1) / kWave;  // 20-float chunks per lane
+    if (k > 0 && k % 20 == 0 && aligned16(w) && (reinterpret_cast<uintptr_t>(packed) & 3u) == 0 && nc <= 8) {
+        if (nc <= 1) hipLaunchKernelGGL(ternary_pack_vec_kernel<1>, g, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
+        else if (nc <= 2) hipLaunchKernelGGL(ternary_pack_vec_kernel<2>, g, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
+        else if (nc <= 4) hipLaunchKernelGGL(ternary_pack_vec_kernel<4>, g, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
+        else hipLaunchKernelGGL(ternary_pack_vec_kernel<8>, g, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
+    } else {
+        hipLaunchKernelGGL(ternary_pack_kernel, g, blk, 0, s, w, m, (uint32_t)k, (uint32_t)kp, threshold, packed,
+                           scales);
+    }
     return launch_status();
 }

@@ -403,4 +403,20 @@ def rocm_ternary_matmul_f32(device_idx: int, a_packed: HipBuffer, a_scales: HipB
     return c
 
 
-__all__ += ["rocm_ternary_matmul_i8", "rocm_ternary_matmul_f32"]
+def rocm_pack_weights_ternary(device_idx: int, w: HipBuffer, m: int, k: int, threshold: float,
+                              packed: Optional[HipBuffer] = None,
+                              scales: Optional[HipBuffer] = None) -> Tuple[HipBuffer, HipBuffer]:
+    """``pack_weights_ternary`` (cpu_ternary_matmul.rs:198-240): f32 weights
+    w[m, k] -> (base-243 packed bytes [m, ceil(k/5)], per-row scales [m]),
+    bit-exact."""
+    _require_device(device_idx)
+    _need(w, m * k * 4, "weights")
+    kp = (k + 4) // 5
+    p = _out(device_idx, packed, m * kp, "packed weights")
+    sc = _out(device_idx, scales, m * 4, "weight scales")
+    _check(_lib.load().kore_hip_pack_weights_ternary(w.ptr, m, k, threshold, p.ptr, sc.ptr, _stream(device_idx)),
+           "pack_weights_ternary")
+    return p, sc
+
+
+__all__ += ["rocm_ternary_matmul_i8", "rocm_ternary_matmul_f32", "rocm_pack_weights_ternary"]

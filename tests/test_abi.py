@@ -94,6 +94,14 @@ def test_ternary_argument_errors_are_reported_on_host():
         # the output may not overlap the weights, scales or activations
         assert f(P, P + 2**20, P + 2**21, P + 2**21 + 64, 4, 4, 16, None) == _lib.KORE_HIP_ERR_ALIAS
     assert lib.kore_hip_ternary_matmul_i8(P, None, P, P, P + 4096, 4, 4, 16, None) == _lib.KORE_HIP_ERR_NULL_PTR
+    pack = lib.kore_hip_pack_weights_ternary
+    assert pack(None, 0, 16, 0.3, None, None, None) == 0
+    assert pack(P, 4, 16, 0.3, P + 4096, None, None) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert pack(None, 4, 16, 0.3, P + 4096, P + 8192, None) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert pack(P, 2**32, 2**32, 0.3, P, P, None) == _lib.KORE_HIP_ERR_OVERFLOW
+    # packed bytes or scales inside the weights
+    assert pack(P, 4, 16, 0.3, P + 64, P + 4096, None) == _lib.KORE_HIP_ERR_ALIAS
+    assert pack(P, 4, 16, 0.3, P + 4096, P + 60, None) == _lib.KORE_HIP_ERR_ALIAS
 
 
 def test_rms_norm_backward_workspace_size():

@@ -711,6 +711,39 @@ def test_ternary_matmul_f32_decode_nonfinite_steps(n):
     assert_bitexact(got, want, f"ternary_matmul_f32 decode non-finite n={n}")
 
 
+@pytest.mark.parametrize("m,k,threshold", [(2, 4, 0.3), (1, 1, 0.3), (7, 5, 0.0), (64, 2560, 0.3), (257, 6912, 0.5),
+                                         (33, 333, 0.3), (6912, 2560, 0.3), (3, 64 * 5 + 3, 0.3),
+                                         # K % 20 == 0 (the register-resident path, 1 to 8 chunks a lane)
+                                         (9, 20, 0.3), (100, 1280, 0.3), (8, 2580, 0.3), (40, 6920, 0.5),
+                                         (7, 10240, 0.3)])
+def test_pack_weights_ternary(m, k, threshold):
+    """pack_weights_ternary on the GPU: bytes and scales bit-exact against the
+    oracle (the reference's KAT shape included), with a zero row (scale 1),
+    a row below 1e-8, NaN and Inf weights, weights exactly at +-threshold *
+    scale, and K not a multiple of 5; the packed result feeds the f32 matmul
+    like the oracle's."""
+    log(f"pack_weights_ternary m={m} k={k} threshold={threshold}")
+    w = normal((m, k), 31 + m)
+    if m >= 7:
+        w[1] = 0.0
+        w[2] *= 1e-9
+        w[3, ::7] = np.nan
+        w[4, 0] = np.inf
+        w[5, :] = np.float32(1.0)
+        w[5, ::3] = np.float32(threshold)   # w / scale == threshold: not > threshold
+        w[6, ::2] = -w[6, ::2]
+    if (m, k) == (2, 4):
+        w = np.array([[1.0, -1.0, 0.0, 0.5], [-0.5, 1.0, -1.0, 0.0]], np.float32)  # cpu_ternary_matmul.rs:247-253
+    want_p, want_s = oracle.pack_weights_ternary(w, threshold)
+    gp, gs = rocm.rocm_pack_weights_ternary(DEV, up(w), m, k, threshold)
+    assert_bitexact(down(gs, np.float32, (m,)), want_s, "pack scales")
+    assert_bitexact(down(gp, np.uint8, want_p.shape), want_p, "pack bytes")
+    if k >= 5 and m <= 300:
+        b = normal((k, 2), 32)
+        got = down(rocm.rocm_ternary_matmul_f32(DEV, gp, gs, up(b), m, 2, k), np.float32, (m, 2))
+        assert_bitexact(got, oracle.ternary_matmul(want_p, want_s, b, m, 2, k), "pack -> ternary_matmul_f32")
+
+
 def test_ternary_matmul_f32_edges():
     log("ternary_matmul_f32 edges")
     lib = __import__("kore_amd._lib", fromlist=["load"]).load()
