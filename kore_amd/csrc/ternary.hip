@@ -1202,48 +1202,76 @@ __global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_vec_kernel(co
                                                                               uint32_t k, float threshold,
                                                                               uint8_t* __restrict__ packed,
                                                                               float* __restrict__ scales) {
+    // per wave: 64 chunks of 20 floats, staged to turn coalesced loads into
+    // each lane's own chunk
+    __shared__ f32x4 stage[kPackWaves][5 * kWave];
     const int lane = threadIdx.x & (kWave - 1);
-    const uint64_t row = (uint64_t)blockIdx.x * kPackWaves + threadIdx.x / kWave;
-    if (row >= m) return;  // whole waves; no barriers below
-    const uint32_t chunks = k / 20;
+    const int wv = threadIdx.x / kWave;
+    const uint64_t row = (uint64_t)blockIdx.x * kPackWaves + wv;
+    if (row >= m) return;  // whole waves; only wave-local LDS sync below
+    const uint32_t n4 = k / 4;  // float4s in the row
     const f32x4* rd = reinterpret_cast<const f32x4*>(w + row * k);
-    f32x4 v[NC][5];
-    float amax = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        const uint32_t ch = (uint32_t)lane + kWave * c;
-        const uint32_t src = ch < chunks ? ch : 0u;  // clamped, in-bounds
-#pragma unroll
-        for (int q = 0; q < 5; ++q) v[c][q] = ld_stream(rd + 5 * src + q);
-    }
+    // coalesced loads: iteration c, step q -> float4 320 c + 64 q + lane
+    f32x4 g[NC][5];
 #pragma unroll
     for (int c = 0; c < NC; ++c)
-        if ((uint32_t)lane + kWave * c < chunks)
 #pragma unroll
-            for (int q = 0; q < 5; ++q)
+        for (int q = 0; q < 5; ++q) {
+            const uint32_t i = (uint32_t)(320 * c + 64 * q + lane);
+            g[c][q] = ld_stream(rd + (i < n4 ? i : 0u));  // clamped, in-bounds
+        }
+    float amax = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(v[c][q][e]));
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < 5; ++q)
+            if ((uint32_t)(320 * c + 64 * q + lane) < n4)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(g[c][q][e]));
     amax = wave_max(amax);
     const float scale = amax < 1e-8f ? 1.0f : amax;
     if (lane == 0) scales[row] = scale;
+    // w / scale as w * (1 / scale), exact where it decides nothing: that
+    // product is within 3 ulp of the IEEE quotient, so only values within
+    // 2^-20 (relative) of +-threshold -- or tiny ones when the threshold is
+    // 0 -- take the IEEE division (NaN stays NaN either way)
+    const float rcp = 1.0f / scale;
+    const float tt = fabsf(threshold);
+    const float tol = fmaxf(tt * 0x1p-20f, 0x1p-100f);
+    auto digit = [&](float x) -> uint32_t {
+        float nv = x * rcp;
+        if (fabsf(fabsf(nv) - tt) <= tol) nv = x / scale;
+        return nv > threshold ? 2u : (nv < -threshold ? 0u : 1u);
+    };
+    const uint32_t chunks = k / 20;
     uint32_t* pr = reinterpret_cast<uint32_t*>(packed + row * (k / 5));
+    f32x4* st = stage[wv];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
+        if ((uint32_t)(kWave * c) >= chunks) break;  // wave-uniform
+#pragma unroll
+        for (int q = 0; q < 5; ++q) st[64 * q + lane] = g[c][q];
+        wave_lds_sync();
+        f32x4 v[5];
+#pragma unroll
+        for (int q = 0; q < 5; ++q) v[q] = st[5 * lane + q];  // chunk 64 c + lane
+        wave_lds_sync();
         const uint32_t ch = (uint32_t)lane + kWave * c;
-        if (ch >= chunks) break;
-        uint32_t word = 0;
+        if (ch < chunks) {
+            uint32_t word = 0;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            uint32_t val = 0, mul = 1;
+            for (int bq = 0; bq < 4; ++bq) {
+                uint32_t val = 0, mul = 1;
 #pragma unroll
-            for (int j = 0; j < 5; ++j) {
-                const int f = 5 * b + j;
-                val += trit_digit(v[c][f / 4][f % 4], scale, threshold) * mul;
-                mul *= 3u;
+                for (int j = 0; j < 5; ++j) {
+                    const int f = 5 * bq + j;
+                    val += digit(v[f / 4][f % 4]) * mul;
+                    mul *= 3u;
+                }
+                word |= val << (8 * bq);
             }
-            word |= val << (8 * b);
+            pr[ch] = word;
         }
-        pr[ch] = word;
     }
 }
 

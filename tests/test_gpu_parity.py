@@ -732,6 +732,14 @@ def test_pack_weights_ternary(m, k, threshold):
         w[5, :] = np.float32(1.0)
         w[5, ::3] = np.float32(threshold)   # w / scale == threshold: not > threshold
         w[6, ::2] = -w[6, ::2]
+    if m >= 8:
+        # quotients within a few ulps of +-threshold under a scale that is not
+        # a power of two (where w * (1 / scale) and w / scale can differ)
+        sc = np.float32(3.7)
+        near = (np.float32(threshold) * sc) * (1 + np.arange(-6, 7, dtype=np.float32) * np.float32(2.0**-23))
+        row = np.resize(np.concatenate([near, -near]), k).astype(np.float32)
+        row[0] = sc
+        w[7] = row
     if (m, k) == (2, 4):
         w = np.array([[1.0, -1.0, 0.0, 0.5], [-0.5, 1.0, -1.0, 0.0]], np.float32)  # cpu_ternary_matmul.rs:247-253
     want_p, want_s = oracle.pack_weights_ternary(w, threshold)
