@@ -914,8 +914,8 @@ static_assert(kDecB * kPfDec * 5 == kPfStep && kDecB % 4 == 0, "decoder split");
 constexpr int kPfQuads = kPfStep / 4;      // 16-byte groups of 4 terms per step
 constexpr int kPfDepth = 2;                // steps of loads in flight
 
-// One workgroup per CU (its LDS): the compiler may use registers for
-// instruction-level parallelism rather than occupancy.
+// One workgroup per CU (its LDS); the launch bound (7 to 10 waves, 2 or 3
+// per SIMD) caps the registers.
 //
 // CT = 1: the decoders write the terms t * b and the fold wave adds them.
 // CT = 2 or 4 columns (decode batches of 2-4 tokens): the decoders write the
@@ -924,7 +924,7 @@ constexpr int kPfDepth = 2;                // steps of loads in flight
 // lane); a step whose column-c b holds an Inf or NaN skips zero trits
 // explicitly.
 template <int CT>
-__global__ __launch_bounds__((kPfDec + CT) * kWave) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__((kPfDec + CT) * kWave)
 void ternary_f32_pipe_kernel(TernF32Args p) {
     constexpr int kStageN = (CT * kPfStep + kPfDec * kWave - 1) / (kPfDec * kWave);  // b elements per decoder lane
     // terms (CT = 1) or trits of the step per group of 4 K columns,
