@@ -1192,6 +1192,13 @@ static uint64_t f32_rows_per_block(int ct, uint64_t m) {
 // (max, then one byte per lane and step).
 constexpr int kPackWaves = 4;
 
+// The next float above (up) or below x, for finite x.
+__device__ __forceinline__ float float_next(float x, bool up) {
+    if (x == 0.0f) return up ? 0x1p-149f : -0x1p-149f;
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    return __builtin_bit_cast(float, (x > 0.0f) == up ? b + 1u : b - 1u);
+}
+
 __device__ __forceinline__ uint32_t trit_digit(float x, float scale, float threshold) {
     const float nv = x / scale;
     return nv > threshold ? 2u : (nv < -threshold ? 0u : 1u);
@@ -1231,14 +1238,28 @@ __global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_vec_kernel(co
     amax = wave_max(amax);
     const float scale = amax < 1e-8f ? 1.0f : amax;
     if (lane == 0) scales[row] = scale;
-    // w / scale as w * (1 / scale), exact where it decides nothing: that
-    // product is within 3 ulp of the IEEE quotient, so only values within
-    // 2^-20 (relative) of +-threshold -- or tiny ones when the threshold is
-    // 0 -- take the IEEE division (NaN stays NaN either way)
+    // The comparisons as bounds on w: fl(w / scale) is monotone in w and odd,
+    // so with xh the largest float whose quotient is <= threshold,
+    // quotient > threshold <=> w > xh and quotient < -threshold <=> w < -xh
+    // (NaN: neither).  xh is found from fl(threshold * scale), within a few
+    // ulps, by stepping with IEEE divisions (the same for every lane).  If
+    // that fails (an infinite scale or threshold, a NaN threshold), each
+    // weight is divided instead, as w * (1 / scale) -- within 3 ulp of the
+    // quotient -- with the IEEE division for values within 2^-20 (relative)
+    // of +-threshold (below 2^-100 for a zero threshold).
+    float xh = threshold * scale;
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+        if (xh / scale > threshold) xh = float_next(xh, false);
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+        if (float_next(xh, true) / scale <= threshold) xh = float_next(xh, true);
+    const bool bounds = __builtin_isfinite(xh) && xh / scale <= threshold && !(float_next(xh, true) / scale <= threshold);
     const float rcp = 1.0f / scale;
     const float tt = fabsf(threshold);
     const float tol = fmaxf(tt * 0x1p-20f, 0x1p-100f);
     auto digit = [&](float x) -> uint32_t {
+        if (bounds) return x > xh ? 2u : (x < -xh ? 0u : 1u);
         float nv = x * rcp;
         if (fabsf(fabsf(nv) - tt) <= tol) nv = x / scale;
         return nv > threshold ? 2u : (nv < -threshold ? 0u : 1u);

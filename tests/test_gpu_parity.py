@@ -715,7 +715,9 @@ def test_ternary_matmul_f32_decode_nonfinite_steps(n):
                                          (33, 333, 0.3), (6912, 2560, 0.3), (3, 64 * 5 + 3, 0.3),
                                          # K % 20 == 0 (the register-resident path, 1 to 8 chunks a lane)
                                          (9, 20, 0.3), (100, 1280, 0.3), (8, 2580, 0.3), (40, 6920, 0.5),
-                                         (7, 10240, 0.3)])
+                                         (7, 10240, 0.3),
+                                         # a negative and an infinite threshold (the per-weight fallback)
+                                         (16, 100, -0.2), (8, 40, float("inf"))])
 def test_pack_weights_ternary(m, k, threshold):
     """pack_weights_ternary on the GPU: bytes and scales bit-exact against the
     oracle (the reference's KAT shape included), with a zero row (scale 1),
