@@ -649,7 +649,7 @@ def all_workloads():
     return [RopeQK(False), RopeQK(True), RMSNorm(32, 2048), RMSNorm(16384, 2048), Swiglu(), Gelu(), Embedding(),
             Prequant(4096), Prequant(64), Prequant(1), RmsNormSiluGate(), Softmax(), SoftmaxBackward(),
             RmsNormBackward(), TernaryI8(), TernaryI8(6912, 64, 2560), TernaryI8(6912, 1, 2560), TernaryF32(),
-            TernaryF32(6912, 64, 2560), PackTernary(), Copy()]
+            TernaryF32(6912, 64, 2560), PackTernary(), PackTernary(2560, 6912), Copy()]
 
 
 # ------------------------------------------------------------------ measure

@@ -1185,10 +1185,10 @@ static uint64_t f32_rows_per_block(int ct, uint64_t m) {
 // (trit[5 j + i] + 1) * 3^i, zero trits past k.  HBM-bound: 4 m k bytes
 // read, m ceil(k/5) + 4 m written.
 //
-// One wave per row.  Vector path (k % 20 == 0, 16-byte aligned rows,
+// One wave per row.  Vector path (k % 4 == 0, 16-byte aligned rows,
 // k <= 64 * 20 * NC): lane l owns the 20-float chunks l, l + 64, ... (NC of
 // them, held in registers), so the row is read once; a chunk packs into 4
-// bytes, one dword store.  Otherwise the generic path reads the row twice
+// bytes (one dword store where the packed rows are dword-aligned).  Otherwise the generic path reads the row twice
 // (max, then one byte per lane and step).
 constexpr int kPackWaves = 4;
 
@@ -1264,8 +1264,10 @@ __global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_vec_kernel(co
         if (fabsf(fabsf(nv) - tt) <= tol) nv = x / scale;
         return nv > threshold ? 2u : (nv < -threshold ? 0u : 1u);
     };
-    const uint32_t chunks = k / 20;
-    uint32_t* pr = reinterpret_cast<uint32_t*>(packed + row * (k / 5));
+    const uint32_t chunks = (k + 19) / 20;  // the last one partial when k % 20 != 0
+    const uint32_t kp = (k + 4) / 5;
+    uint8_t* pr = packed + row * kp;
+    const bool word_stores = kp % 4 == 0 && (reinterpret_cast<uintptr_t>(packed) & 3u) == 0;
     f32x4* st = stage[wv];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -1286,12 +1288,18 @@ __global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_vec_kernel(co
 #pragma unroll
                 for (int j = 0; j < 5; ++j) {
                     const int f = 5 * bq + j;
-                    val += digit(v[f / 4][f % 4]) * mul;
+                    val += (20u * ch + (uint32_t)f < k ? digit(v[f / 4][f % 4]) : 1u) * mul;  // zero trits past k
                     mul *= 3u;
                 }
                 word |= val << (8 * bq);
             }
-            pr[ch] = word;
+            if (word_stores && 4u * ch + 4u <= kp) {
+                reinterpret_cast<uint32_t*>(pr)[ch] = word;
+            } else {
+#pragma unroll
+                for (int bq = 0; bq < 4; ++bq)
+                    if (4u * ch + (uint32_t)bq < kp) pr[4u * ch + bq] = (uint8_t)(word >> (8 * bq));
+            }
         }
     }
 }
@@ -1485,8 +1493,8 @@ extern "C" int kore_hip_pack_weights_ternary(const float* w, uint64_t m, uint64_
     if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
     const dim3 g((uint32_t)blocks), blk(kPackWaves * kWave);
     hipStream_t s = (hipStream_t)stream;
-    const uint64_t nc = (k / 20 + kWave - 1) / kWave;  // 20-float chunks per lane
-    if (k > 0 && k % 20 == 0 && aligned16(w) && (reinterpret_cast<uintptr_t>(packed) & 3u) == 0 && nc <= 8) {
+    const uint64_t nc = ((k + 19) / 20 + kWave - 1) / kWave;  // 20-float chunks per lane
+    if (k > 0 && k % 4 == 0 && aligned16(w) && nc <= 8) {
         if (nc <= 1) hipLaunchKernelGGL(ternary_pack_vec_kernel<1>, g, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
         else if (nc <= 2) hipLaunchKernelGGL(ternary_pack_vec_kernel<2>, g, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
         else if (nc <= 4) hipLaunchKernelGGL(ternary_pack_vec_kernel<4>, g, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
