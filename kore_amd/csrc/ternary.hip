@@ -1185,11 +1185,11 @@ static uint64_t f32_rows_per_block(int ct, uint64_t m) {
 // (trit[5 j + i] + 1) * 3^i, zero trits past k.  HBM-bound: 4 m k bytes
 // read, m ceil(k/5) + 4 m written.
 //
-// One wave per row.  Vector path (k % 4 == 0, 16-byte aligned rows,
-// k <= 64 * 20 * NC): lane l owns the 20-float chunks l, l + 64, ... (NC of
-// them, held in registers), so the row is read once; a chunk packs into 4
-// bytes (one dword store where the packed rows are dword-aligned).  Otherwise the generic path reads the row twice
-// (max, then one byte per lane and step).
+// Vector path (k % 4 == 0, 16-byte aligned rows): one wave per row for
+// k <= 2560, else a workgroup per row (k <= 40960); a lane holds its 20-float
+// chunks in registers, so the row is read once; a chunk packs into 4 bytes
+// (one dword store where the packed rows are dword-aligned).  Otherwise the
+// generic path reads the row twice (max, then one byte per lane and step).
 constexpr int kPackWaves = 4;
 
 // The next float above (up) or below x, for finite x.
@@ -1204,7 +1204,9 @@ __device__ __forceinline__ uint32_t trit_digit(float x, float scale, float thres
     return nv > threshold ? 2u : (nv < -threshold ? 0u : 1u);
 }
 
-template <int NC>
+// RB: a workgroup per row (long rows): wave w takes the 64-chunk slices w,
+// w + 4, ..., and the row max meets in LDS.
+template <int NC, bool RB>
 __global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_vec_kernel(const float* __restrict__ w, uint64_t m,
                                                                               uint32_t k, float threshold,
                                                                               uint8_t* __restrict__ packed,
@@ -1212,10 +1214,12 @@ __global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_vec_kernel(co
     // per wave: 64 chunks of 20 floats, staged to turn coalesced loads into
     // each lane's own chunk
     __shared__ f32x4 stage[kPackWaves][5 * kWave];
+    __shared__ float red[kPackWaves];
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x / kWave;
-    const uint64_t row = (uint64_t)blockIdx.x * kPackWaves + wv;
-    if (row >= m) return;  // whole waves; only wave-local LDS sync below
+    const uint64_t row = RB ? (uint64_t)blockIdx.x : (uint64_t)blockIdx.x * kPackWaves + wv;
+    if (!RB && row >= m) return;  // whole waves; only wave-local LDS sync below
+    auto slice = [&](int c) { return RB ? wv + kPackWaves * c : c; };  // this wave's c-th 64-chunk slice
     const uint32_t n4 = k / 4;  // float4s in the row
     const f32x4* rd = reinterpret_cast<const f32x4*>(w + row * k);
     // coalesced loads: iteration c, step q -> float4 320 c + 64 q + lane
@@ -1224,7 +1228,7 @@ __global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_vec_kernel(co
     for (int c = 0; c < NC; ++c)
 #pragma unroll
         for (int q = 0; q < 5; ++q) {
-            const uint32_t i = (uint32_t)(320 * c + 64 * q + lane);
+            const uint32_t i = (uint32_t)(320 * slice(c) + 64 * q + lane);
             g[c][q] = ld_stream(rd + (i < n4 ? i : 0u));  // clamped, in-bounds
         }
     float amax = 0.0f;
@@ -1232,12 +1236,18 @@ __global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_vec_kernel(co
     for (int c = 0; c < NC; ++c)
 #pragma unroll
         for (int q = 0; q < 5; ++q)
-            if ((uint32_t)(320 * c + 64 * q + lane) < n4)
+            if ((uint32_t)(320 * slice(c) + 64 * q + lane) < n4)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(g[c][q][e]));
     amax = wave_max(amax);
+    if (RB) {
+        if (lane == 0) red[wv] = amax;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kPackWaves; ++i) amax = fmaxf(amax, red[i]);
+    }
     const float scale = amax < 1e-8f ? 1.0f : amax;
-    if (lane == 0) scales[row] = scale;
+    if (lane == 0 && (!RB || wv == 0)) scales[row] = scale;
     // The comparisons as bounds on w: fl(w / scale) is monotone in w and odd,
     // so with xh the largest float whose quotient is <= threshold,
     // quotient > threshold <=> w > xh and quotient < -threshold <=> w < -xh
@@ -1271,7 +1281,7 @@ __global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_vec_kernel(co
     f32x4* st = stage[wv];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        if ((uint32_t)(kWave * c) >= chunks) break;  // wave-uniform
+        if ((uint32_t)(kWave * slice(c)) >= chunks) break;  // wave-uniform
 #pragma unroll
         for (int q = 0; q < 5; ++q) st[64 * q + lane] = g[c][q];
         wave_lds_sync();
@@ -1279,7 +1289,7 @@ __global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_vec_kernel(co
 #pragma unroll
         for (int q = 0; q < 5; ++q) v[q] = st[5 * lane + q];  // chunk 64 c + lane
         wave_lds_sync();
-        const uint32_t ch = (uint32_t)lane + kWave * c;
+        const uint32_t ch = (uint32_t)lane + kWave * slice(c);
         if (ch < chunks) {
             uint32_t word = 0;
 #pragma unroll
@@ -1493,12 +1503,19 @@ extern "C" int kore_hip_pack_weights_ternary(const float* w, uint64_t m, uint64_
     if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
     const dim3 g((uint32_t)blocks), blk(kPackWaves * kWave);
     hipStream_t s = (hipStream_t)stream;
-    const uint64_t nc = ((k + 19) / 20 + kWave - 1) / kWave;  // 20-float chunks per lane
-    if (k > 0 && k % 4 == 0 && aligned16(w) && nc <= 8) {
-        if (nc <= 1) hipLaunchKernelGGL(ternary_pack_vec_kernel<1>, g, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
-        else if (nc <= 2) hipLaunchKernelGGL(ternary_pack_vec_kernel<2>, g, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
-        else if (nc <= 4) hipLaunchKernelGGL(ternary_pack_vec_kernel<4>, g, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
-        else hipLaunchKernelGGL(ternary_pack_vec_kernel<8>, g, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
+    const uint64_t slices = ((k + 19) / 20 + kWave - 1) / kWave;  // 64-chunk slices of 20 floats per row
+    if (k > 0 && k % 4 == 0 && aligned16(w) && slices <= 2) {
+        if (slices <= 1) hipLaunchKernelGGL((ternary_pack_vec_kernel<1, false>), g, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
+        else hipLaunchKernelGGL((ternary_pack_vec_kernel<2, false>), g, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
+    } else if (k > 0 && k % 4 == 0 && aligned16(w) && slices <= 8 * kPackWaves) {
+        // long rows: a workgroup per row (m < 2^31 blocks)
+        if (m > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
+        const dim3 gr((uint32_t)m);
+        const uint64_t per_wave = (slices + kPackWaves - 1) / kPackWaves;
+        if (per_wave <= 1) hipLaunchKernelGGL((ternary_pack_vec_kernel<1, true>), gr, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
+        else if (per_wave <= 2) hipLaunchKernelGGL((ternary_pack_vec_kernel<2, true>), gr, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
+        else if (per_wave <= 4) hipLaunchKernelGGL((ternary_pack_vec_kernel<4, true>), gr, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
+        else hipLaunchKernelGGL((ternary_pack_vec_kernel<8, true>), gr, blk, 0, s, w, m, (uint32_t)k, threshold, packed, scales);
     } else {
         hipLaunchKernelGGL(ternary_pack_kernel, g, blk, 0, s, w, m, (uint32_t)k, (uint32_t)kp, threshold, packed,
                            scales);

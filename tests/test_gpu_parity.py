@@ -719,7 +719,9 @@ def test_ternary_matmul_f32_decode_nonfinite_steps(n):
                                          # a negative and an infinite threshold (the per-weight fallback)
                                          (16, 100, -0.2), (8, 40, float("inf")),
                                          # k % 4 == 0, k % 20 != 0: a partial last chunk, byte stores
-                                         (40, 6912, 0.3), (9, 2564, 0.3), (12, 8, 0.3)])
+                                         (40, 6912, 0.3), (9, 2564, 0.3), (12, 8, 0.3),
+                                         # a workgroup per long row (up to 8 slices a wave), and past it
+                                         (3, 37120, 0.3), (2, 41000, 0.3), (2560, 6912, 0.3)])
 def test_pack_weights_ternary(m, k, threshold):
     """pack_weights_ternary on the GPU: bytes and scales bit-exact against the
     oracle (the reference's KAT shape included), with a zero row (scale 1),
