@@ -650,7 +650,9 @@ TERN_F32_SHAPES = [(1, 1, 5), (7, 1, 2560), (6912, 1, 2560), (33, 3, 161), (64, 
                    (1, 1, 60), (3, 1, 21), (2, 1, 30), (37, 1, 333), (65, 1, 245), (300, 1, 1203),
                    (2560, 1, 6912), (20000, 1, 480), (129, 1, 241),
                    # two to four columns (the same kernel with one fold wave per column)
-                   (6912, 2, 2560), (301, 4, 1203), (1, 2, 60), (129, 3, 241), (5, 4, 24), (2560, 3, 6912)]
+                   (6912, 2, 2560), (301, 4, 1203), (1, 2, 60), (129, 3, 241), (5, 4, 24), (2560, 3, 6912),
+                   # 5-8 columns on unaligned rows (eight fold waves)
+                   (300, 6, 1203), (2560, 8, 6912), (65, 5, 333)]
 
 
 @pytest.mark.parametrize("m,n,k", TERN_F32_SHAPES)
