@@ -1470,12 +1470,15 @@ extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float*
     const uint64_t gx = (m + rb - 1) / rb, gy = (n + ct - 1) / ct;
     if (gx > 0x7fffffffull || gy > 65535) return KORE_HIP_ERR_OVERFLOW;
     const dim3 g((uint32_t)gx, (uint32_t)gy);
-    // Up to 4 columns, and up to 8 where the per-lane kernel would take its
-    // unaligned-row loads (measured: 2560 x 8 x 6912 78 against 99 us; at
-    // aligned K = 2560 the two are even at 8 columns).
+    // Up to 4 columns; more where the per-lane kernel would take its
+    // unaligned-row loads, in groups of 8 columns, up to 8 columns or 512
+    // workgroups (measured: 2560 x 8 x 6912 78 against 99 us, 2560 x 64 x
+    // 6912 157 against 245 us; at 6912 x 64 x 2563, 864 workgroups, 129
+    // against 127 us; at aligned K = 2560 the two are even at 8 columns).
     const bool rows_aligned = kp % 16 == 0 && aligned16(a_packed);
-    if ((n <= 4 || (n <= 8 && !rows_aligned)) && k > 0 && mkp >= 12) {
-        const dim3 gp((uint32_t)((m + kWave - 1) / kWave));
+    const uint64_t pipe_blocks = ((m + kWave - 1) / kWave) * ((n + 7) / 8);
+    if ((n <= 4 || (!rows_aligned && (n <= 8 || pipe_blocks <= 512))) && k > 0 && mkp >= 12) {
+        const dim3 gp((uint32_t)((m + kWave - 1) / kWave), (uint32_t)(n <= 4 ? 1 : (n + 7) / 8));
         if (n == 1) hipLaunchKernelGGL(ternary_f32_pipe_kernel<1>, gp, dim3((kPfDec + 1) * kWave), 0, s, p);
         else if (n == 2) hipLaunchKernelGGL(ternary_f32_pipe_kernel<2>, gp, dim3((kPfDec + 2) * kWave), 0, s, p);
         else if (n <= 4) hipLaunchKernelGGL(ternary_f32_pipe_kernel<4>, gp, dim3((kPfDec + 4) * kWave), 0, s, p);

@@ -652,7 +652,9 @@ TERN_F32_SHAPES = [(1, 1, 5), (7, 1, 2560), (6912, 1, 2560), (33, 3, 161), (64, 
                    # two to four columns (the same kernel with one fold wave per column)
                    (6912, 2, 2560), (301, 4, 1203), (1, 2, 60), (129, 3, 241), (5, 4, 24), (2560, 3, 6912),
                    # 5-8 columns on unaligned rows (eight fold waves)
-                   (300, 6, 1203), (2560, 8, 6912), (65, 5, 333)]
+                   (300, 6, 1203), (2560, 8, 6912), (65, 5, 333),
+                   # more columns on unaligned rows: groups of 8 (a partial last group)
+                   (130, 20, 1203), (300, 64, 333)]
 
 
 @pytest.mark.parametrize("m,n,k", TERN_F32_SHAPES)
