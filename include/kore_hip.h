@@ -130,6 +130,15 @@ int kore_hip_embedding_f32(const float *table, const uint32_t *ids,
                            float *out, uint64_t n_ids, uint64_t vocab,
                            uint64_t dim, kore_stream_t stream);
 
+/* Embedding::forward's entry (crates/kore-nn/src/embedding.rs:91-98): the ids
+ * arrive as an f32 tensor and each is converted with Rust's `v as usize`
+ * (truncation; NaN and values below 1 give row 0, values >= 2^64 give
+ * usize::MAX), then looked up as kore_hip_embedding_f32 does: an index >=
+ * vocab gives a zero row.  Bit-exact. */
+int kore_hip_embedding_forward_f32(const float *table, const float *ids,
+                                   float *out, uint64_t n_ids, uint64_t vocab,
+                                   uint64_t dim, kore_stream_t stream);
+
 /* ----------------------------------------------------- BitLinear pre-quant
  * Per row r: xn = RMSNorm(x[r,:]) exactly as kore_hip_rms_norm_f32;
  * amax = max_i |xn_i| (1.0 if amax < 1e-8); scale[r] = amax / 127;

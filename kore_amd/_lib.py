@@ -38,6 +38,7 @@ SIGNATURES = {
     "kore_hip_rope_f32": [_ptr, _ptr, _u64, _u64, _u32, _u32, _u64, _int, _ptr],
     "kore_hip_rope_qk_f32": [_ptr, _ptr, _ptr, _u64, _u64, _u32, _u32, _u32, _u64, _int, _ptr],
     "kore_hip_embedding_f32": [_ptr, _ptr, _ptr, _u64, _u64, _u64, _ptr],
+    "kore_hip_embedding_forward_f32": [_ptr, _ptr, _ptr, _u64, _u64, _u64, _ptr],
     "kore_hip_rms_norm_quant_i8": [_ptr, _ptr, _ptr, _ptr, _u64, _u64, _f32, _ptr],
     "kore_hip_rms_norm_silu_gate_f32": [_ptr, _ptr, _ptr, _ptr, _u64, _u64, _f32, _ptr],
     "kore_hip_softmax_f32": [_ptr, _ptr, _u64, _u64, _ptr],

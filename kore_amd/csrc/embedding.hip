@@ -15,23 +15,36 @@
 
 namespace kore {
 
+// Token id -> row index.  u32 ids (Embedding::lookup, embedding_lookup) are
+// used as they are.  f32 ids (Embedding::forward,
+// crates/kore-nn/src/embedding.rs:91-98) go through Rust's `v as usize`:
+// truncation toward zero, NaN and everything below 1 to 0 (row 0, a valid
+// row), values >= 2^64 to usize::MAX (out of range).
+__device__ __forceinline__ uint64_t row_index(uint32_t id) { return id; }
+__device__ __forceinline__ uint64_t row_index(float v) {
+    if (!(v >= 1.0f)) return 0;
+    if (v >= 18446744073709551616.0f) return ~0ull;
+    return (uint64_t)v;
+}
+
 constexpr int kEmbBlock = 256;      // per-token loop and scalar kernels
 constexpr int kEmbMaxBlock = 1024;  // one-float4 kernel: blockDim chosen per call
 constexpr int kEmbUnroll = 4;  // float4 per thread per pass (rows > 16M floats)
 
+template <typename Id>
 __global__ __launch_bounds__(kEmbBlock) void embedding_vec_kernel(const f32x4* __restrict__ table,
-                                                                  const uint32_t* __restrict__ ids,
+                                                                  const Id* __restrict__ ids,
                                                                   f32x4* __restrict__ out, uint64_t vocab,
                                                                   uint64_t dim4) {
     const uint64_t t = blockIdx.x;
-    const uint32_t id = ids[t];
+    const uint64_t id = row_index(ids[t]);
     f32x4* dst = out + t * dim4;
-    if ((uint64_t)id >= vocab) {
+    if (id >= vocab) {
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
         for (uint64_t i = threadIdx.x; i < dim4; i += kEmbBlock) st_stream(dst + i, z);
         return;
     }
-    const f32x4* src = table + (uint64_t)id * dim4;
+    const f32x4* src = table + id * dim4;
     uint64_t i = threadIdx.x;
     for (; i + (kEmbUnroll - 1) * kEmbBlock < dim4; i += kEmbUnroll * kEmbBlock) {
         f32x4 v[kEmbUnroll];
@@ -49,32 +62,34 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_vec_kernel(const f32x4* _
 // independent requests in flight (measured on MI355X: a 1 GiB gather-copy
 // runs at 74.6% of 8 TB/s with 256-thread chunks, 81.5% with 1024, and
 // worse with several tokens per workgroup).
+template <typename Id>
 __global__ __launch_bounds__(kEmbMaxBlock) void embedding_vec1_kernel(const f32x4* __restrict__ table,
-                                                                      const uint32_t* __restrict__ ids,
+                                                                      const Id* __restrict__ ids,
                                                                       f32x4* __restrict__ out, uint64_t vocab,
                                                                       uint64_t dim4) {
     const uint64_t t = blockIdx.x;
     const uint64_t i = (uint64_t)blockIdx.y * blockDim.x + threadIdx.x;
     if (i >= dim4) return;
-    const uint32_t id = ids[t];
+    const uint64_t id = row_index(ids[t]);
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    const f32x4 v = ((uint64_t)id < vocab) ? ld_cached(table + (uint64_t)id * dim4 + i) : z;
+    const f32x4 v = (id < vocab) ? ld_cached(table + id * dim4 + i) : z;
     st_stream(out + t * dim4 + i, v);
 }
 
 // Scalar path: dim % 4 != 0 or unaligned table/out.
+template <typename Id>
 __global__ __launch_bounds__(kEmbBlock) void embedding_scalar_kernel(const float* __restrict__ table,
-                                                                     const uint32_t* __restrict__ ids,
+                                                                     const Id* __restrict__ ids,
                                                                      float* __restrict__ out, uint64_t vocab,
                                                                      uint64_t dim) {
     const uint64_t t = blockIdx.x;
-    const uint32_t id = ids[t];
+    const uint64_t id = row_index(ids[t]);
     float* dst = out + t * dim;
-    if ((uint64_t)id >= vocab) {
+    if (id >= vocab) {
         for (uint64_t i = threadIdx.x; i < dim; i += kEmbBlock) dst[i] = 0.0f;
         return;
     }
-    const float* src = table + (uint64_t)id * dim;
+    const float* src = table + id * dim;
     for (uint64_t i = threadIdx.x; i < dim; i += kEmbBlock) dst[i] = src[i];
 }
 
@@ -82,7 +97,8 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_scalar_kernel(const float
 
 using namespace kore;
 
-extern "C" int kore_hip_embedding_f32(const float* table, const uint32_t* ids, float* out, uint64_t n_ids,
+template <typename Id>
+static int embedding_launch(const float* table, const Id* ids, float* out, uint64_t n_ids,
                                       uint64_t vocab, uint64_t dim, kore_stream_t stream) {
     if (n_ids == 0 || dim == 0) return KORE_HIP_OK;
     if (!ids || !out || (vocab && !table)) return KORE_HIP_ERR_NULL_PTR;
@@ -97,15 +113,25 @@ extern "C" int kore_hip_embedding_f32(const float* table, const uint32_t* ids, f
         const uint32_t thr = dim4 >= (uint64_t)kEmbMaxBlock ? kEmbMaxBlock : (uint32_t)((dim4 + 63) / 64 * 64);
         const uint64_t chunks = (dim4 + thr - 1) / thr;
         if (chunks <= 65535) {
-            hipLaunchKernelGGL(embedding_vec1_kernel, dim3((uint32_t)n_ids, (uint32_t)chunks), dim3(thr), 0, s,
+            hipLaunchKernelGGL(embedding_vec1_kernel<Id>, dim3((uint32_t)n_ids, (uint32_t)chunks), dim3(thr), 0, s,
                                reinterpret_cast<const f32x4*>(table), ids, reinterpret_cast<f32x4*>(out), vocab,
                                dim / 4);
             return launch_status();
         }
-        hipLaunchKernelGGL(embedding_vec_kernel, grid, block, 0, s, reinterpret_cast<const f32x4*>(table), ids,
+        hipLaunchKernelGGL(embedding_vec_kernel<Id>, grid, block, 0, s, reinterpret_cast<const f32x4*>(table), ids,
                            reinterpret_cast<f32x4*>(out), vocab, dim / 4);
     } else {
-        hipLaunchKernelGGL(embedding_scalar_kernel, grid, block, 0, s, table, ids, out, vocab, dim);
+        hipLaunchKernelGGL(embedding_scalar_kernel<Id>, grid, block, 0, s, table, ids, out, vocab, dim);
     }
     return launch_status();
+}
+
+extern "C" int kore_hip_embedding_f32(const float* table, const uint32_t* ids, float* out, uint64_t n_ids,
+                                      uint64_t vocab, uint64_t dim, kore_stream_t stream) {
+    return embedding_launch(table, ids, out, n_ids, vocab, dim, stream);
+}
+
+extern "C" int kore_hip_embedding_forward_f32(const float* table, const float* ids, float* out, uint64_t n_ids,
+                                              uint64_t vocab, uint64_t dim, kore_stream_t stream) {
+    return embedding_launch(table, ids, out, n_ids, vocab, dim, stream);
 }

@@ -265,6 +265,20 @@ def rocm_embedding_f32(device_idx: int, table: HipBuffer, ids: HipBuffer, n_ids:
     return o
 
 
+def rocm_embedding_forward_f32(device_idx: int, table: HipBuffer, ids: HipBuffer, n_ids: int, vocab: int,
+                               dim: int, out: Optional[HipBuffer] = None) -> HipBuffer:
+    """``Embedding::forward`` (crates/kore-nn/src/embedding.rs:91-98) on the
+    device: ids are an f32 buffer converted like Rust's ``v as usize`` (NaN
+    and values below 1 -> 0, saturating), then looked up as ``lookup``."""
+    _require_device(device_idx)
+    _need(table, vocab * dim * 4, "embedding table")
+    _need(ids, n_ids * 4, "embedding ids")
+    o = _out(device_idx, out, n_ids * dim * 4, "embedding out")
+    _check(_lib.load().kore_hip_embedding_forward_f32(table.ptr, ids.ptr, o.ptr, n_ids, vocab, dim,
+                                                      _stream(device_idx)), "embedding_forward_f32")
+    return o
+
+
 # ----------------------------------------------------- BitLinear pre-quant
 def rocm_rms_norm_quant_i8(device_idx: int, input: HipBuffer, weight: HipBuffer, rows: int, cols: int,
                            eps: float, out_q: Optional[HipBuffer] = None,
@@ -284,7 +298,7 @@ def rocm_rms_norm_quant_i8(device_idx: int, input: HipBuffer, weight: HipBuffer,
 __all__ = [
     "RocmError", "HipBuffer", "rocm_rms_norm_f32", "rocm_gelu_f32", "rocm_silu_f32", "rocm_mul_f32",
     "rocm_swiglu_f32", "rope_inv_freq_host", "rocm_rope_inv_freq_f32", "rocm_rope_f32", "rocm_rope_qk_f32",
-    "rocm_embedding_f32", "rocm_rms_norm_quant_i8", "rocm_fused_rms_norm_silu_gate_f32",
+    "rocm_embedding_f32", "rocm_embedding_forward_f32", "rocm_rms_norm_quant_i8", "rocm_fused_rms_norm_silu_gate_f32",
 ]
 
 

@@ -182,6 +182,49 @@ void kore_oracle_embedding_f32(const float *table, const uint32_t *ids,
     }
 }
 
+/* Rust `f32 as usize` (64-bit): saturating float-to-int cast, NaN -> 0. */
+uint64_t kore_oracle_f32_as_usize(float v) {
+    if (v != v) return 0;
+    if (v <= 0.0f) return 0;
+    if (v >= 18446744073709551616.0f) return UINT64_MAX;
+    return (uint64_t)v; /* C truncates toward zero, in range here */
+}
+
+/* embedding.rs:91-98: ids.iter().map(|&v| v as usize), then lookup :55-72. */
+void kore_oracle_embedding_forward_f32(const float *table, const float *ids,
+                                       float *out, size_t n_ids, size_t vocab,
+                                       size_t dim) {
+    for (size_t t = 0; t < n_ids; ++t) {
+        uint64_t id = kore_oracle_f32_as_usize(ids[t]);
+        float *dst = out + t * dim;
+        if (id < (uint64_t)vocab) {
+            memcpy(dst, table + id * dim, dim * sizeof(float));
+        } else {
+            for (size_t i = 0; i < dim; ++i) dst[i] = 0.0f;
+        }
+    }
+}
+
+/* engine.rs:831-839: two branches on the sign of v. */
+void kore_oracle_silu_stable_f32(const float *x, float *y, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        float v = x[i];
+        if (v >= 0.0f) {
+            y[i] = v / (1.0f + expf(-v));
+        } else {
+            float exp_v = expf(v);
+            y[i] = (v * exp_v) / (1.0f + exp_v);
+        }
+    }
+}
+
+/* engine.rs:640-643: gate_activated = silu(&gate); gate_activated.mul(&up). */
+void kore_oracle_swiglu_serve_f32(const float *gate, const float *up,
+                                  float *out, size_t n) {
+    kore_oracle_silu_stable_f32(gate, out, n);
+    for (size_t i = 0; i < n; ++i) out[i] = out[i] * up[i];
+}
+
 /* ((xn * 127.0) / amax).round().clamp(-128.0, 127.0) as i8.
  * f32::round rounds half away from zero (= C roundf); f32::clamp keeps NaN;
  * `as i8` saturates and maps NaN to 0. */

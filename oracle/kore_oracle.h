@@ -73,6 +73,27 @@ void kore_oracle_embedding_f32(const float *table, const uint32_t *ids,
                                float *out, size_t n_ids, size_t vocab,
                                size_t dim);
 
+/* crates/kore-nn/src/embedding.rs:91-98 (Embedding::forward): ids arrive as
+ * f32 and are converted with Rust's `v as usize` (truncation toward zero;
+ * NaN and negatives saturate to 0, values >= 2^64 to usize::MAX), then
+ * looked up as Embedding::lookup (:55-72): id < vocab copies the row, else a
+ * zero row. */
+void kore_oracle_embedding_forward_f32(const float *table, const float *ids,
+                                       float *out, size_t n_ids, size_t vocab,
+                                       size_t dim);
+
+/* Rust's `v as usize` for an f32 on a 64-bit target (saturating cast). */
+uint64_t kore_oracle_f32_as_usize(float v);
+
+/* crates/kore-serve/src/layered/engine.rs:828-842 (the serving path's silu,
+ * which apply_transformer_block :640 composes with Tensor::mul):
+ * v >= 0: v / (1 + exp(-v)); else e = exp(v), (v * e) / (1 + e). */
+void kore_oracle_silu_stable_f32(const float *x, float *y, size_t n);
+
+/* engine.rs:640-643: silu_stable(gate) then Tensor::mul(up). */
+void kore_oracle_swiglu_serve_f32(const float *gate, const float *up,
+                                  float *out, size_t n);
+
 /* BitLinear pre-quant.  The reference has no such function; this is the
  * composition the build defines:
  *   xn    = fused_rms_norm(x, gamma, eps)   (cpu_fused.rs:160-190)

@@ -31,6 +31,10 @@ _SIGS = {
     "kore_oracle_rope_f32": (None, [_p, _sz, _sz, _sz, _sz, _f]),
     "kore_oracle_rope_interleaved_f32": (None, [_p, _sz, _sz, _sz, _sz, _p]),
     "kore_oracle_embedding_f32": (None, [_p, _p, _p, _sz, _sz, _sz]),
+    "kore_oracle_embedding_forward_f32": (None, [_p, _p, _p, _sz, _sz, _sz]),
+    "kore_oracle_f32_as_usize": (_c.c_uint64, [_f]),
+    "kore_oracle_silu_stable_f32": (None, [_p, _p, _sz]),
+    "kore_oracle_swiglu_serve_f32": (None, [_p, _p, _p, _sz]),
     "kore_oracle_rms_norm_quant_i8": (None, [_p, _p, _p, _p, _sz, _sz, _f]),
     "kore_oracle_quant_code": (_c.c_int8, [_f, _f]),
     "kore_oracle_rms_norm_silu_gate_f32": (None, [_p, _p, _p, _p, _sz, _sz, _f]),
@@ -160,6 +164,39 @@ def embedding(table, ids) -> np.ndarray:
     return out
 
 
+def embedding_forward(table, ids_f32) -> np.ndarray:
+    """Embedding::forward (crates/kore-nn/src/embedding.rs:91-98): f32 ids
+    cast with Rust's ``as usize``, then ``lookup``."""
+    t = _f32(table)
+    vocab, dim = t.shape
+    i = _f32(ids_f32).reshape(-1)
+    out = np.empty((i.size, dim), dtype=np.float32)
+    lib().kore_oracle_embedding_forward_f32(_ptr(t), _ptr(i), _ptr(out), i.size, vocab, dim)
+    return out
+
+
+def f32_as_usize(v: float) -> int:
+    """Rust ``v as usize`` for one f32 (64-bit target)."""
+    return int(lib().kore_oracle_f32_as_usize(v))
+
+
+def silu_stable(x) -> np.ndarray:
+    """kore-serve's two-branch silu (crates/kore-serve/src/layered/engine.rs:828-842)."""
+    a = _f32(x)
+    y = np.empty_like(a)
+    lib().kore_oracle_silu_stable_f32(_ptr(a), _ptr(y), a.size)
+    return y
+
+
+def swiglu_serve(gate, up) -> np.ndarray:
+    """silu_stable(gate) * up, as apply_transformer_block composes it
+    (crates/kore-serve/src/layered/engine.rs:640-643)."""
+    g, u = _f32(gate), _f32(up)
+    y = np.empty_like(g)
+    lib().kore_oracle_swiglu_serve_f32(_ptr(g), _ptr(u), _ptr(y), g.size)
+    return y
+
+
 def rms_norm_quant_i8(x, gamma, eps: float):
     """fused_rms_norm + per-row absmax int8 (composition defined in kore_oracle.h)."""
     x = _f32(x)
@@ -189,6 +226,7 @@ def quant_code(xn: float, amax: float) -> int:
 
 
 __all__ = ["build", "lib", "rms_norm", "gelu", "silu", "mul", "swiglu", "rope_inv_freq", "rope", "embedding",
+           "embedding_forward", "f32_as_usize", "silu_stable", "swiglu_serve",
            "rms_norm_quant_i8", "rms_norm_silu_gate", "quant_code", "softmax", "softmax_causal",
            "softmax_backward", "rms_norm_backward", "cross_entropy_backward", "decode_trits", "encode_trits",
            "pack_weights_ternary", "ternary_matmul", "ternary_matmul_i8", "unpack_trits"]

@@ -54,6 +54,8 @@ def test_argument_errors_are_reported_on_host():
     assert lib.kore_hip_rms_norm_f32(P, None, P, 4, 128, 1e-6, s) == _lib.KORE_HIP_ERR_NULL_PTR
     assert lib.kore_hip_rms_norm_quant_i8(P, P, P, None, 4, 128, 1e-6, s) == _lib.KORE_HIP_ERR_NULL_PTR
     assert lib.kore_hip_embedding_f32(P, None, P, 3, 10, 4, s) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert lib.kore_hip_embedding_forward_f32(P, None, P, 3, 10, 4, s) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert lib.kore_hip_embedding_forward_f32(None, None, None, 0, 10, 4, s) == 0
     assert lib.kore_hip_rope_f32(P, None, 1, 4, 2, 8, 0, 0, s) == _lib.KORE_HIP_ERR_NULL_PTR
     # bad dims
     assert lib.kore_hip_rope_f32(P, P, 1, 4, 2, 7, 0, 0, s) == _lib.KORE_HIP_ERR_BAD_DIM

@@ -265,6 +265,31 @@ def test_swiglu_gelu_baseline_full():
     log(f"gelu max abs/rel err {max_err(got, want)}")
 
 
+def test_swiglu_against_serve_silu_specials():
+    # The serving caller composes kore-serve's two-branch silu with mul
+    # (crates/kore-serve/src/layered/engine.rs:640-643, :828-842); the kernel
+    # follows kore-nn's form.  Both must sit within the f32 bar of that caller.
+    gate = np.concatenate([np.linspace(-120, 40, 40001, dtype=np.float32),
+                           np.array([-88.72, -88.73, -87.0, -103.0, -104.0, -0.0, 0.0, 1e-30, -1e-30,
+                                     np.inf, -np.inf, np.nan, 3.4e38, -3.4e38], np.float32)])
+    upv = normal(gate.shape, 16)
+    got = down(rocm.rocm_swiglu_f32(DEV, up(gate), up(upv), gate.size), np.float32, gate.shape)
+    assert_close(got, oracle.swiglu_serve(gate, upv), what="swiglu vs serve silu")
+
+
+@pytest.mark.slow
+def test_swiglu_against_serve_silu_full():
+    # BASELINE configs[2] shape against the serve composition
+    shape = (16384, 14336)
+    log("swiglu vs serve silu full")
+    gate = normal(shape, 0)
+    upv = normal(shape, 1)
+    got = down(rocm.rocm_swiglu_f32(DEV, up(gate), up(upv), gate.size), np.float32, shape)
+    want = oracle.swiglu_serve(gate, upv)
+    assert_close(got, want, what="swiglu vs serve silu full")
+    log(f"swiglu vs serve max abs/rel err {max_err(got, want)}")
+
+
 # -------------------------------------------------------------------- RoPE
 @pytest.mark.parametrize("interleaved", [False, True])
 @pytest.mark.parametrize("batch,seq,heads,hd,start", [(1, 1, 1, 4, 0), (2, 5, 3, 8, 7), (1, 3, 2, 6, 0),
@@ -353,6 +378,42 @@ def test_embedding_baseline_full():
     out = rocm.rocm_embedding_f32(DEV, up(table), up(ids), 8192, 128256, 4096)
     got = down(out, np.float32, (8192, 4096))
     assert got.tobytes() == oracle.embedding(table, ids).tobytes()
+
+
+# Embedding::forward: f32 ids through Rust's `as usize` (embedding.rs:91-98)
+F32_ID_SPECIALS = [float("nan"), -1.5, 0.9, 1e30, -0.0, float("inf"), -float("inf"), 2.0, 2.5]
+
+
+@pytest.mark.parametrize("vocab,dim,n_ids", [(10, 4, 16), (1000, 256, 513), (64, 4096, 100), (100, 4100, 12),
+                                             (30, 7, 20)])
+def test_embedding_forward_f32_ids(vocab, dim, n_ids):
+    log(f"embedding forward f32 ids vocab={vocab} dim={dim} n={n_ids}")
+    table = normal((vocab, dim), vocab + 1, 0.0, 0.02)
+    ids = embedding_ids(n_ids, vocab, seed=n_ids + 1).astype(np.float32)
+    sp = F32_ID_SPECIALS + [float(vocab - 1), float(vocab), float(vocab + 1)]
+    ids[:len(sp)] = np.array(sp[:n_ids], np.float32)
+    out = rocm.rocm_embedding_forward_f32(DEV, up(table), up(ids), n_ids, vocab, dim)
+    got = down(out, np.float32, (n_ids, dim))
+    assert got.tobytes() == oracle.embedding_forward(table, ids).tobytes()
+
+
+def test_embedding_forward_f32_ids_unaligned_table():
+    table = normal((20, 8), 3)
+    ids = np.array([3.7, float("nan"), 19.0, 20.0, -2.0], np.float32)
+    out = rocm.rocm_embedding_forward_f32(DEV, unaligned(table), up(ids), 5, 20, 8)
+    assert down(out, np.float32, (5, 8)).tobytes() == oracle.embedding_forward(table, ids).tobytes()
+
+
+@pytest.mark.slow
+def test_embedding_forward_baseline_shape():
+    # BASELINE configs[3] shape with the ids handed over as f32, as Module::forward takes them
+    log("embedding forward f32 ids baseline shape")
+    table = normal((128256, 4096), 0, 0.0, 0.02)
+    ids = embedding_ids(8192, 128256, seed=0).astype(np.float32)
+    ids[:9] = np.array(F32_ID_SPECIALS, np.float32)
+    out = rocm.rocm_embedding_forward_f32(DEV, up(table), up(ids), 8192, 128256, 4096)
+    got = down(out, np.float32, (8192, 4096))
+    assert got.tobytes() == oracle.embedding_forward(table, ids).tobytes()
 
 
 # ----------------------------------------------------------------- softmax

@@ -48,6 +48,39 @@ def test_embedding_brute_force_and_negative_ids():
         assert out[t].tobytes() == want.tobytes()
 
 
+def _rust_as_usize(v: float) -> int:
+    # Rust reference semantics of `f32 as usize` (saturating since Rust 1.45):
+    # NaN -> 0, below 0 -> 0, above usize::MAX -> usize::MAX, else truncate.
+    if math.isnan(v):
+        return 0
+    if math.isinf(v):
+        return 0 if v < 0 else 2**64 - 1
+    return min(max(math.trunc(v), 0), 2**64 - 1)
+
+
+def test_f32_as_usize_brute_force():
+    specials = [float("nan"), -float("inf"), float("inf"), -1.5, -0.0, 0.0, 0.4, 0.9, 1.0, 1.5, 2.999999,
+                3.0, 16777217.0, 1e19, 1.8446744e19, 2.0**64, 1e30, -1e30]
+    vals = np.concatenate([np.array(specials, np.float32), normal((5000,), 21) * 1000,
+                           np.float32(2.0) ** np.arange(-10, 70, dtype=np.float32)])
+    for v in vals.tolist():
+        assert oracle.f32_as_usize(v) == _rust_as_usize(np.float32(v).item()), v
+
+
+def test_embedding_forward_cast_then_lookup():
+    # crates/kore-nn/src/embedding.rs:91-98: forward = lookup(ids as usize);
+    # kore-nn's own test (:152-158) feeds [0.0, 3.0, 7.0] and checks the shape
+    table = normal((50, 7), 4)
+    assert oracle.embedding_forward(table, np.array([0.0, 3.0, 7.0], np.float32)).shape == (3, 7)
+    ids = np.array([0.0, 2.0, 1.0, float("nan"), -1.5, 0.9, 1e30, 49.0, 50.0, 51.0, 49.99, -0.0,
+                    float("inf"), -float("inf")], np.float32)
+    out = oracle.embedding_forward(table, ids)
+    for t, v in enumerate(ids.tolist()):
+        u = _rust_as_usize(v)
+        want = table[u] if u < 50 else np.zeros(7, np.float32)
+        assert out[t].tobytes() == want.tobytes(), (t, v)
+
+
 # ----------------------------------------------------------------- RMSNorm
 def test_rms_norm_unit_input_reference_kat():
     # crates/kore-nn/src/rms_norm.rs:193-202 (ones -> 1.0 within 1e-3)
@@ -123,6 +156,30 @@ def test_silu_reference_kat_and_torch():
     got = oracle.silu(x)
     rel = np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)
     assert np.max(rel[np.abs(ref) > 1e-30]) < 1e-6
+
+
+def test_silu_stable_serve_kat_and_torch():
+    # crates/kore-serve/src/layered/engine.rs:877-886 (its own KAT), then the
+    # two-branch formula of :828-842 against torch f64 on both branches
+    y = oracle.silu_stable(np.array([0.0, 1.0, -1.0], np.float32))
+    assert abs(y[0]) < 1e-5 and abs(y[1] - 0.7311) < 1e-3 and abs(y[2] + 0.2689) < 1e-3
+    torch = pytest.importorskip("torch")
+    x = np.concatenate([normal((20000,), 13) * 4, np.linspace(-120, 30, 3001, dtype=np.float32)])
+    ref = torch.nn.functional.silu(torch.from_numpy(x.astype(np.float64))).numpy()
+    got = oracle.silu_stable(x).astype(np.float64)
+    ok = (np.abs(got - ref) <= 1e-6) | (np.abs(got - ref) <= 1e-6 * np.abs(ref))
+    assert ok.all()
+    # the branch for v < 0 is not the kore-nn formula: below -88.7 the
+    # kore-nn silu is v / inf = -0 while the serve form keeps a subnormal
+    far = np.array([-95.0], np.float32)
+    assert oracle.silu(far)[0] == 0.0 and np.signbit(oracle.silu(far)[0])
+    assert oracle.silu_stable(far)[0] < 0.0
+    # specials: -inf and NaN give NaN in both forms, +inf gives +inf
+    sp = oracle.silu_stable(np.array([-np.inf, np.nan, np.inf], np.float32))
+    assert np.isnan(sp[0]) and np.isnan(sp[1]) and sp[2] == np.inf
+    # swiglu_serve is silu_stable(gate) * up, rounded once per op
+    a, b = normal((4001,), 14), normal((4001,), 15)
+    assert (oracle.swiglu_serve(a, b) == oracle.silu_stable(a) * b).all()
 
 
 def test_mul_and_swiglu_composition():
