@@ -39,6 +39,7 @@ typedef void *kore_stream_t; /* hipStream_t */
 #define KORE_HIP_ERR_BAD_DIM (-2)   /* a dimension is invalid (odd head_dim, cols == 0 with rows > 0, ...) */
 #define KORE_HIP_ERR_OVERFLOW (-3)  /* an element count overflows 64-bit or exceeds the kernel's index range */
 #define KORE_HIP_ERR_ALIAS (-4)     /* input/output overlap the op does not allow */
+#define KORE_HIP_ERR_SCRATCH (-5)   /* the work needs more scratch than the library's fixed array holds */
 
 /* Library version as 10000*major + 100*minor + patch. */
 int kore_hip_version(void);
@@ -230,6 +231,24 @@ int kore_hip_rms_norm_backward_f32(const float *grad_out, const float *x,
                                    uint64_t cols, float eps,
                                    kore_stream_t stream);
 
+/* Allocation-free variant of kore_hip_rms_norm_backward_f32 (same kernels,
+ * same results bit for bit).  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving/training loops, harnesses that forbid hipMalloc).  The dgamma
+ * partials go to a library-held device array of
+ * kore_hip_rms_norm_backward_noalloc_max_bytes() bytes (16 MiB per GPU, held
+ * until the process ends) instead of a caller workspace; work whose
+ * kore_hip_rms_norm_backward_workspace_bytes(rows, cols) exceeds it returns
+ * KORE_HIP_ERR_SCRATCH.  Calls never allocate or free.  All calls on one GPU
+ * share the array: calls that overlap in time on one GPU (other streams,
+ * other threads) race. */
+uint64_t kore_hip_rms_norm_backward_noalloc_max_bytes(void);
+
+int kore_hip_rms_norm_backward_noalloc_f32(const float *grad_out,
+                                           const float *x, const float *gamma,
+                                           float *grad_x, float *grad_gamma,
+                                           uint64_t rows, uint64_t cols,
+                                           float eps, kore_stream_t stream);
 
 /* ------------------------------------------------------ ternary (BitLinear)
  * Weights a_packed[m, ceil(k/5)] in the reference's base-243 format (five

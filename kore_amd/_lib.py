@@ -19,6 +19,7 @@ KORE_HIP_ERR_NULL_PTR = -1
 KORE_HIP_ERR_BAD_DIM = -2
 KORE_HIP_ERR_OVERFLOW = -3
 KORE_HIP_ERR_ALIAS = -4
+KORE_HIP_ERR_SCRATCH = -5
 
 _u64 = ctypes.c_uint64
 _u32 = ctypes.c_uint32
@@ -46,6 +47,7 @@ SIGNATURES = {
     "kore_hip_softmax_backward_f32": [_ptr, _ptr, _ptr, _u64, _u64, _ptr],
     "kore_hip_cross_entropy_backward_f32": [_ptr, _ptr, _ptr, _u64, _u64, _ptr],
     "kore_hip_rms_norm_backward_f32": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _f32, _ptr],
+    "kore_hip_rms_norm_backward_noalloc_f32": [_ptr, _ptr, _ptr, _ptr, _ptr, _u64, _u64, _f32, _ptr],
     "kore_hip_ternary_matmul_i8": [_ptr, _ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _ptr],
     "kore_hip_ternary_matmul_f32": [_ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _ptr],
     "kore_hip_pack_weights_ternary": [_ptr, _u64, _u64, _f32, _ptr, _ptr, _ptr],
@@ -54,6 +56,7 @@ SIGNATURES = {
 # Entry points whose return type is not int.
 RESTYPES = {
     "kore_hip_rms_norm_backward_workspace_bytes": ([_u64, _u64], _u64),
+    "kore_hip_rms_norm_backward_noalloc_max_bytes": ([], _u64),
 }
 
 

@@ -13,6 +13,7 @@ extern "C" const char* kore_hip_status_string(int status) {
         case KORE_HIP_ERR_BAD_DIM: return "invalid dimension";
         case KORE_HIP_ERR_OVERFLOW: return "element count overflows the supported range";
         case KORE_HIP_ERR_ALIAS: return "overlapping buffers";
+        case KORE_HIP_ERR_SCRATCH: return "work exceeds the library's fixed scratch array";
         default: return status > 0 ? "HIP runtime error (hipError_t)" : "unknown status";
     }
 }

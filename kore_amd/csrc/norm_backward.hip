@@ -28,6 +28,8 @@
 // Generic path (any shape): one workgroup per row writes dx and inv[r] to the
 // workspace; then one thread per column folds its dgamma over the rows in
 // the reference's order.
+#include <mutex>
+
 #include "common.hpp"
 #include "kore_hip_internal.hpp"
 
@@ -297,6 +299,37 @@ static void launch_rows(const BwArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((rms_bwd_rows_kernel<NCHW, S>), dim3((uint32_t)a.partials), dim3(kBwBlock), lds, s, a);
 }
 
+// Library-held scratch for the allocation-free entry point: the dgamma
+// partial rows (vector path) or the per-row inv (generic path), at most
+// kBwScratchBytes.  Each GPU holds its own copy for the life of the process.
+// Every call fully writes the part it reads back, so nothing needs clearing;
+// calls that overlap on one GPU share the array and race.
+constexpr uint64_t kBwScratchBytes = 16ull << 20;
+static __device__ __align__(256) float rms_bwd_scratch[kBwScratchBytes / sizeof(float)];
+
+// Device address of rms_bwd_scratch on the current device, looked up once per
+// device with that device current.  In host code the array's name is only a
+// host-side stand-in; kernels get this address instead.
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_bw_scratch_mu;
+static float* g_bw_scratch[kMaxScratchDevices];
+
+static int bwd_scratch_ptr(float** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxScratchDevices) return KORE_HIP_ERR_BAD_DIM;
+    std::lock_guard<std::mutex> lock(g_bw_scratch_mu);
+    if (!g_bw_scratch[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(rms_bwd_scratch));
+        if (e != hipSuccess) return (int)e;
+        g_bw_scratch[dev] = static_cast<float*>(p);
+    }
+    *out = g_bw_scratch[dev];
+    return KORE_HIP_OK;
+}
+
 }  // namespace kore
 
 using namespace kore;
@@ -308,13 +341,14 @@ extern "C" uint64_t kore_hip_rms_norm_backward_workspace_bytes(uint64_t rows, ui
     return bwd_ws_floats(rows, cols, nullptr, nullptr) * sizeof(float);
 }
 
-extern "C" int kore_hip_rms_norm_backward_f32(const float* grad_out, const float* x, const float* gamma,
-                                              float* grad_x, float* grad_gamma, float* workspace,
-                                              uint64_t workspace_bytes, uint64_t rows, uint64_t cols, float eps,
-                                              kore_stream_t stream) {
+// The whole entry point once the workspace is known.  ws == nullptr asks for
+// the library's own scratch array (the allocation-free entry point); it is
+// looked up only after every argument check has passed.
+static int rms_bwd_run(const float* grad_out, const float* x, const float* gamma, float* grad_x,
+                       float* grad_gamma, float* workspace, uint64_t workspace_bytes, bool own_scratch,
+                       uint64_t rows, uint64_t cols, float eps, hipStream_t s) {
     if (cols == 0) return KORE_HIP_OK;
     if (!grad_gamma || !gamma) return KORE_HIP_ERR_NULL_PTR;
-    hipStream_t s = (hipStream_t)stream;
     if (rows == 0) {  // dgamma of an empty batch is zero (the reference's vec![0.0; d])
         if (cols > kMaxElements) return KORE_HIP_ERR_OVERFLOW;
         // A fill kernel rather than hipMemsetAsync, so the call can be captured in a graph.
@@ -322,18 +356,28 @@ extern "C" int kore_hip_rms_norm_backward_f32(const float* grad_out, const float
                            grad_gamma, cols);
         return launch_status();
     }
-    if (!grad_out || !x || !grad_x || !workspace) return KORE_HIP_ERR_NULL_PTR;
+    if (!grad_out || !x || !grad_x || (!own_scratch && !workspace)) return KORE_HIP_ERR_NULL_PTR;
     uint64_t elems;
     if (!mul_ok(rows, cols, &elems) || elems > kMaxElements || rows > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
     BwArgs a{grad_out, x, gamma, grad_x, grad_gamma, workspace, rows, cols, eps, 0, 0};
     const uint64_t need = bwd_ws_floats(rows, cols, &a.partials, &a.rpw) * sizeof(float);
-    if (workspace_bytes < need) return KORE_HIP_ERR_BAD_DIM;
+    if (own_scratch) {
+        if (need > kBwScratchBytes) return KORE_HIP_ERR_SCRATCH;
+        workspace_bytes = kBwScratchBytes;
+    } else if (workspace_bytes < need) {
+        return KORE_HIP_ERR_BAD_DIM;
+    }
     // grad_x must not overlap the inputs (the row pass reads a row ahead).
     const char* o0 = (const char*)grad_x;
     const char* o1 = o0 + elems * sizeof(float);
     for (const float* in : {grad_out, x}) {
         const char* i0 = (const char*)in;
         if (i0 < o1 && o0 < i0 + elems * sizeof(float)) return KORE_HIP_ERR_ALIAS;
+    }
+    if (own_scratch) {
+        const int st = bwd_scratch_ptr(&a.ws);
+        if (st != KORE_HIP_OK) return st;
+        workspace = a.ws;
     }
     const bool vec = bwd_vec(cols) && aligned16(grad_out) && aligned16(x) && aligned16(gamma) &&
                      aligned16(grad_x) && aligned16(grad_gamma) && aligned16(workspace);
@@ -352,4 +396,21 @@ extern "C" int kore_hip_rms_norm_backward_f32(const float* grad_out, const float
                            dim3(kBwBlock), 0, s, a);
     }
     return launch_status();
+}
+
+extern "C" int kore_hip_rms_norm_backward_f32(const float* grad_out, const float* x, const float* gamma,
+                                              float* grad_x, float* grad_gamma, float* workspace,
+                                              uint64_t workspace_bytes, uint64_t rows, uint64_t cols, float eps,
+                                              kore_stream_t stream) {
+    return rms_bwd_run(grad_out, x, gamma, grad_x, grad_gamma, workspace, workspace_bytes, false, rows, cols, eps,
+                       (hipStream_t)stream);
+}
+
+extern "C" uint64_t kore_hip_rms_norm_backward_noalloc_max_bytes(void) { return kBwScratchBytes; }
+
+extern "C" int kore_hip_rms_norm_backward_noalloc_f32(const float* grad_out, const float* x, const float* gamma,
+                                                      float* grad_x, float* grad_gamma, uint64_t rows,
+                                                      uint64_t cols, float eps, kore_stream_t stream) {
+    return rms_bwd_run(grad_out, x, gamma, grad_x, grad_gamma, nullptr, 0, true, rows, cols, eps,
+                       (hipStream_t)stream);
 }

@@ -106,6 +106,19 @@ def test_ternary_argument_errors_are_reported_on_host():
     assert pack(P, 4, 16, 0.3, P + 4096, P + 60, None) == _lib.KORE_HIP_ERR_ALIAS
 
 
+def test_rms_norm_backward_noalloc_host_checks():
+    # host-side only: a size beyond the fixed scratch array, null pointers and
+    # empty work are answered before any device call
+    lib = _lib.load()
+    cap = lib.kore_hip_rms_norm_backward_noalloc_max_bytes()
+    assert cap == 16 << 20
+    f = lib.kore_hip_rms_norm_backward_noalloc_f32
+    assert f(P, P + 2**40, P, P + 2**41, P, cap // 4 + 1, 3, 1e-5, None) == _lib.KORE_HIP_ERR_SCRATCH
+    assert f(P, None, P, P, P, 16, 64, 1e-5, None) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert f(None, None, None, None, None, 16, 0, 1e-5, None) == 0
+    assert _lib.status_string(_lib.KORE_HIP_ERR_SCRATCH).startswith("work exceeds")
+
+
 def test_rms_norm_backward_workspace_size():
     ws = _lib.load().kore_hip_rms_norm_backward_workspace_bytes
     assert ws(0, 128) == 0 and ws(128, 0) == 0 and ws(2**40, 2**40) == 0
