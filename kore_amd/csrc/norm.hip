@@ -57,15 +57,14 @@
 //   inv  = 1 / sqrt(ss / cols + eps)   IEEE sqrt and division (cpu_fused.rs:181-182)
 //   xn   = (x * inv) * w                                      (cpu_fused.rs:185)
 // Pre-quant additionally:
-//   amax = max |xn| (wave max: order-free, exact); 1.0 if amax < 1e-8
-//   t    = (xn * 127) / amax  as the IEEE quotient, obtained with
-//          y = 1/amax (IEEE), q0 = a*y, r = fma(-amax, q0, a), t = fma(r, y, q0)
-//          (Markstein: with y the correctly rounded reciprocal, t is the
-//          correctly rounded quotient -- checked on the CPU by the test suite)
-//   code = trunc(t + copysign(0.5 - 2^-25, t)) clamped to [-128, 127];
-//          equal to round-half-away(t) for |t| < 2^23 (checked on the CPU over
-//          every float in range); v_cvt_i32_f32 maps NaN to 0 and saturates,
-//          like Rust's `as i8` after clamp.
+//   amax = max |xn| (wave max: order-free, exact, NaN dropped); 1.0 if
+//          amax < 1e-8 (kore-btes/src/quantize.rs:10)
+//   code = clamp(round_half_away((xn * 127) / amax), -128, 127), the
+//          quotient correctly rounded.  For rows with amax < 2^120 each code
+//          comes from one fma and one floor conversion, with a bracket test
+//          that sends the rare undecided element (and any NaN) to the exact
+//          Markstein quotient (quant_code); other rows take the exact path
+//          throughout.  Both are checked on the CPU by the test suite.
 #include "common.hpp"
 #include "kore_hip_internal.hpp"
 
@@ -108,17 +107,76 @@ __device__ __forceinline__ int32_t cvt_i32_sat(float v) {
 }
 
 // Code of one normalised value xn of a row with absmax amax (>= every |xn|
-// of the row, or 1.0 when the row's absmax is below 1e-8).  |t| cannot exceed
-// 127 * (1 + 2^-23) -- |xn| <= amax and both roundings are faithful -- so the
-// reference's clamp to [-128, 127] never binds and is not evaluated; NaN
-// (from NaN inputs or an infinite amax) converts to 0.
+// of the row, or 1.0 when the row's absmax is below 1e-8), exactly as the
+// reference computes clamp(round((xn * 127) / amax), -128, 127) as i8:
+// t is the IEEE quotient (Markstein: with y = RN(1/amax), q0 = RN(a*y),
+// r = fma(-amax, q0, a), t = fma(r, y, q0) is RN(a/amax) -- checked on the
+// CPU by the test suite), rounded half away from zero.  An infinite
+// numerator (|xn| * 127 above FLT_MAX) over a finite amax gives an infinite
+// quotient, which saturates; NaN (NaN inputs, or a NaN quotient from an
+// infinite amax) converts to 0.
 __device__ __forceinline__ int32_t quant_code(float xn, float amax, float rcp_amax) {
     float a = xn * 127.0f;
     float q0 = a * rcp_amax;
     float r = __builtin_fmaf(-amax, q0, a);
     float t = __builtin_fmaf(r, rcp_amax, q0);
+    if (__builtin_isinf(a) && __builtin_isfinite(amax)) t = a;
     float b = t + __builtin_copysignf(0.49999997f, t);
-    return cvt_i32_sat(b);
+    const int32_t c = cvt_i32_sat(b);
+    return c < -128 ? -128 : (c > 127 ? 127 : c);
+}
+
+// Fast codes for rows whose absmax M lies in [1e-8, 2^120) (or is the 1.0
+// guard).  With c = RN(127 * RN(1/M)) and e = 2^-14, v = fma(xn, c, 0.5 - e)
+// satisfies v < t + 0.5 < v + 2e for the reference quotient t
+// (|fma(xn, c, 0) - t| < 3.1e-5 < e), so when fract(v) < 1 - 2e the code
+// round-half-away(t) = floor(t + 0.5) is floor(v); an exact tie t = k + 0.5
+// puts the integer k + 1 inside (v, v + 2e) and always fails the test.
+// v_cvt_flr_i32_f32 computes floor exactly and its SDWA form writes the low
+// byte into byte B of the destination, so four codes pack with four
+// instructions.  The largest fract of a float4 is kept as integer bits (a
+// max of non-negative floats), where a NaN or infinite xn (NaN fract) sorts
+// above every threshold: those lanes, and the ~1 element in 8000 whose
+// fract is too close to 1, are recomputed with quant_code.  The identity is
+// checked on the CPU by the test suite.
+constexpr float kCodeEps = 6.103515625e-05f;             // 2^-14
+constexpr float kCodeOff = 0.5f - kCodeEps;              // exact in f32
+constexpr uint32_t kFractLimit = 0x3f7ff800u;            // bits of 1 - 2^-13
+constexpr float kFastAmaxLimit = 1.329227995784916e36f;  // 2^120
+
+template <int B>
+__device__ __forceinline__ uint32_t flr_byte(uint32_t d, float v) {
+    if (B == 0) {
+        asm("v_cvt_flr_i32_f32_sdwa %0, %1 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD" : "=v"(d) : "v"(v));
+    } else if (B == 1) {
+        asm("v_cvt_flr_i32_f32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(d) : "v"(v));
+    } else if (B == 2) {
+        asm("v_cvt_flr_i32_f32_sdwa %0, %1 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(d) : "v"(v));
+    } else {
+        asm("v_cvt_flr_i32_f32_sdwa %0, %1 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(d) : "v"(v));
+    }
+    return d;
+}
+
+__device__ __forceinline__ uint32_t fract_bits(float v) { return __float_as_uint(__builtin_amdgcn_fractf(v)); }
+
+__device__ __forceinline__ uint32_t max3_u32(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t r;
+    asm("v_max3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// Four bracketed codes of xn (see above) and the largest fract bits among them.
+__device__ __forceinline__ uint32_t flr_pack4(f32x4 xn, float c, uint32_t& fmax) {
+    const float v0 = __builtin_fmaf(xn.x, c, kCodeOff), v1 = __builtin_fmaf(xn.y, c, kCodeOff);
+    const float v2 = __builtin_fmaf(xn.z, c, kCodeOff), v3 = __builtin_fmaf(xn.w, c, kCodeOff);
+    uint32_t d = 0;
+    d = flr_byte<0>(d, v0);
+    d = flr_byte<1>(d, v1);
+    d = flr_byte<2>(d, v2);
+    d = flr_byte<3>(d, v3);
+    fmax = max3_u32(fract_bits(v0), fract_bits(v1), max3_u32(fract_bits(v2), fract_bits(v3), 0u));
+    return d;
 }
 
 // Four codes -> one dword, byte k = code k (v_perm_b32 byte selects).
@@ -166,63 +224,25 @@ __device__ __forceinline__ float wave_incl_scan(float v) {
     return v;
 }
 
-// Identity element of the run scan: F(p) = p (bits 0b10), D = 0, no head.
-constexpr int kIdBits = 2;
-
-// One element of the suffix scan over a run of segments.
-//   bits: F(0) | F(1) << 1 | head << 2 ; F(p) = parity after the span given
-//         entry parity p; head = the span already reaches its run's end.
-//   d0/d1: exact increment of the span for entry parity 0 / 1.
-struct RunElem {
-    int bits;
-    float d0, d1;
-};
-
-// x = (span that starts first) then y = (span that follows).  Exact: inside a
-// run every increment is a multiple of one ulp and sums stay below the binade
-// top whenever the resolve accepts them (see the header comment).
-__device__ __forceinline__ RunElem run_compose(RunElem x, RunElem y) {
-    const int f0 = x.bits & 1, f1 = (x.bits >> 1) & 1;
-    RunElem r;
-    r.bits = ((y.bits >> f0) & 1) | (((y.bits >> f1) & 1) << 1);
-    r.d0 = x.d0 + (f0 ? y.d1 : y.d0);
-    r.d1 = x.d1 + (f1 ? y.d1 : y.d0);
-    return r;
-}
-
+// Segmented inclusive scan over lanes of u32 values whose bit 31 marks a
+// lane that starts a segment (in lane order).  Lane L adds the value of lane
+// L - k unless its own partial already reached a segment start; the start
+// flag travels with the sum, so a lane stops accumulating once its partial
+// covers one.  Lanes without a DPP source read 0.  Used for run increments
+// in grid units: below 2^24 per segment, so 64 of them never reach bit 31.
 template <int kCtrl, int kRowMask>
-__device__ __forceinline__ int dppi(int v, int id) {
-    return __builtin_amdgcn_update_dpp(id, v, kCtrl, kRowMask, 0xf, false);
+__device__ __forceinline__ uint32_t seg_scan_step(uint32_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, kRowMask, 0xf, false);
+    return (int32_t)v < 0 ? v : v + lo;
 }
-template <int kCtrl, int kRowMask>
-__device__ __forceinline__ float dppf(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, kRowMask, 0xf, false));
-}
-
-// One Hillis-Steele step of the segmented scan: lane L takes the element k
-// lanes below it (a LATER span, since lanes hold segments in reverse order)
-// unless L's own span already ends its run.
-template <int kCtrl, int kRowMask>
-__device__ __forceinline__ void run_scan_step(RunElem& e) {
-    RunElem lo;
-    lo.bits = dppi<kCtrl, kRowMask>(e.bits, kIdBits);
-    lo.d0 = dppf<kCtrl, kRowMask>(e.d0);
-    lo.d1 = dppf<kCtrl, kRowMask>(e.d1);
-    if (!(e.bits & 4)) {
-        RunElem c = run_compose(e, lo);
-        e.bits = c.bits | (lo.bits & 4);
-        e.d0 = c.d0;
-        e.d1 = c.d1;
-    }
-}
-
-__device__ __forceinline__ void run_scan(RunElem& e) {
-    run_scan_step<0x111, 0xf>(e);  // row_shr:1
-    run_scan_step<0x112, 0xf>(e);  // row_shr:2
-    run_scan_step<0x114, 0xf>(e);  // row_shr:4
-    run_scan_step<0x118, 0xf>(e);  // row_shr:8
-    run_scan_step<0x142, 0xa>(e);  // row_bcast:15 -> rows 1, 3
-    run_scan_step<0x143, 0xc>(e);  // row_bcast:31 -> rows 2, 3
+__device__ __forceinline__ uint32_t seg_scan(uint32_t v) {
+    v = seg_scan_step<0x111, 0xf>(v);  // row_shr:1
+    v = seg_scan_step<0x112, 0xf>(v);  // row_shr:2
+    v = seg_scan_step<0x114, 0xf>(v);  // row_shr:4
+    v = seg_scan_step<0x118, 0xf>(v);  // row_shr:8
+    v = seg_scan_step<0x142, 0xa>(v);  // row_bcast:15 -> rows 1, 3
+    v = seg_scan_step<0x143, 0xc>(v);  // row_bcast:31 -> rows 2, 3
+    return v;
 }
 
 // Vector path: cols % 4 == 0, x/w/y 16-byte aligned, q 4-byte aligned,
@@ -297,14 +317,15 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
     constexpr uint32_t kWaveF4 = wave_lds_f4(SL4);
     extern __shared__ f32x4 lds4[];
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+    // Wave index as a scalar: row addresses then live in SGPRs and every
+    // load and store takes the scalar-base form with a lane offset.
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     const uint64_t row = (uint64_t)blockIdx.x * WPB + wave;
     if (row >= args.rows) return;  // uniform per wave; no block barrier follows
     const uint32_t cols4 = FULL ? (uint32_t)(kWave * SL4) : (args.cols >> 2);
     const int nseg = FULL ? kSegs : (int)((cols4 + SL4 - 1) / SL4);
     f32x4* tile = lds4 + (size_t)wave * kWaveF4;
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    const float qnan = __builtin_nanf("");
 
     // ---- HBM reads: coalesced, chunk-major, all in flight.
     const f32x4* xr = reinterpret_cast<const f32x4*>(args.x) + row * cols4;
@@ -383,23 +404,26 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
     // instead of breaking a jump.
     const bool edge = !first && (est < bot * 1.0009765625f || est + ssum >= top * 0.9990234375f);
     const bool valid = ok0 && ok1 && !edge && !bad;
-    // Scan element of this single segment.
-    RunElem el;
-    el.d0 = ok0 ? w0 - sig0 : qnan;
-    el.d1 = (seg_id == 0) ? el.d0 : (ok1 ? w1 - sig1 : qnan);
-    el.bits = (int)(__float_as_uint(w0) & 1u) | (seg_id == 0 ? 0 : (int)((__float_as_uint(w1) & 1u) << 1));
-    if (empty) {
-        el.bits = kIdBits; el.d0 = 0.0f; el.d1 = 0.0f;
-    }
-    // Runs: maximal spans of valid segments with one binade key; an invalid
-    // segment is a run of its own.  This lane's span ends its run when the
-    // next segment (lane - 1, moved here by wave_shr:1) is in another run.
-    const int key_me = empty ? 1024 : (seg_id == 0 ? 1025 : (valid ? (int)ef : 2048 + seg_id));
+    // Exact increments in grid units for entry parity 0 / 1 (0x7fffffff when
+    // the walk left the binade).  A segment whose two walks agree (no tie
+    // broke differently) maps every start s in the binade to s + inc,
+    // whatever its parity: such "simple" segments of one binade compose by
+    // adding their increments.  A valid segment with inc0 != inc1 is a run
+    // of its own whose entry keeps both increments.
+    const uint32_t inc0 = run_inc(bot, top, w0 - sig0);
+    const uint32_t inc1 = run_inc(bot, top, w1 - sig1);
+    const bool simple = valid && inc0 == inc1;
+    // Runs: maximal spans of simple segments with one binade key; any other
+    // segment is a run of its own.  This lane's segment ends its run when
+    // the next segment (lane - 1, moved here by wave_shr:1) has another key.
+    const int key_me = empty ? 1024 : (seg_id == 0 ? 1025 : (simple ? (int)ef : 2048 + seg_id));
     const int key_next = __builtin_amdgcn_update_dpp(key_me, key_me, 0x138, 0xf, 0xf, false);
     const bool ends_here = lane == 0 || key_next != key_me;
-    if (ends_here) el.bits |= 4;
     const uint64_t ends = __ballot(ends_here);
-    run_scan(el);
+    // Run increment from this segment to the run's end: a segmented sum over
+    // lanes (a forward scan adds the later segments, held by lower lanes).
+    const uint32_t run_sum =
+        seg_scan((simple ? inc0 : 0u) | (ends_here ? 0x80000000u : 0u)) & 0x7fffffffu;
     // The run of lane L ends at the highest lane <= L with its bit set; the
     // segment after it is 64 - that lane.
     const uint64_t below = ends & (lt_mask | (1ull << lane));
@@ -409,8 +433,8 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
     // after the run.  Width 0 marks a segment outside every run (a predicted
     // binade crossing, a walk that left its binade, an Inf/NaN estimate):
     // the resolve folds it without trying a jump.
-    const uint32_t inc0 = run_inc(bot, top, el.d0);
-    const uint32_t inc1 = run_inc(bot, top, el.d1);
+    const uint32_t e_inc0 = simple ? run_sum : inc0;
+    const uint32_t e_inc1 = simple ? run_sum : inc1;
     const uint32_t lo_v = __float_as_uint(bot);
     const uint32_t wd_v = valid ? __float_as_uint(top) - __float_as_uint(bot) : 0u;
 
@@ -427,7 +451,7 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
     // scalar instructions.
     uint32_t s = __builtin_amdgcn_readlane(__float_as_uint(w0), kWave - 1);
     int j = 1;
-    RunEntry cur = read_entry(inc0, inc1, lo_v, wd_v, next_seg, kSegs - 2);
+    RunEntry cur = read_entry(e_inc0, e_inc1, lo_v, wd_v, next_seg, kSegs - 2);
     while (j < nseg) {
         const int L = kSegs - 1 - j;
         if (cur.wd != 0u) {
@@ -436,7 +460,7 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
             if ((a > b ? a : b) < cur.wd) {
                 s = t;
                 j = cur.next;
-                cur = read_entry(inc0, inc1, lo_v, wd_v, next_seg, (kSegs - 1 - j) & (kWave - 1));
+                cur = read_entry(e_inc0, e_inc1, lo_v, wd_v, next_seg, (kSegs - 1 - j) & (kWave - 1));
                 continue;
             }
         }
@@ -444,7 +468,7 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
         // that its latency hides under the fold chain.  Every lane folds its
         // own segment from s (same cost as one lane under an exec mask,
         // without the mask changes); lane L's sum is the one kept.
-        cur = read_entry(inc0, inc1, lo_v, wd_v, next_seg, (L - 1) & (kWave - 1));
+        cur = read_entry(e_inc0, e_inc1, lo_v, wd_v, next_seg, (L - 1) & (kWave - 1));
         float acc = __uint_as_float(s);
 #pragma unroll
         for (int k = 0; k < SL4; ++k) acc = fold4(acc, seg[k]);
@@ -501,25 +525,57 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
             }
         }
     } else {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) xv[c] = (xv[c] * inv) * wv[c];
+        // amax: the reference's fold(0, f32::max) of |xn| (NaN dropped).
         float amax = 0.0f;
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            f32x4 xn = (xv[c] * inv) * wv[c];
-            xv[c] = xn;
-            amax = abs_max4(amax, xn);
-        }
+        for (int c = 0; c < NCH; ++c) amax = abs_max4(amax, xv[c]);
         amax = wave_max_nonneg(amax);
-        amax = amax < 1e-8f ? 1.0f : amax;  // kore-btes/src/quantize.rs:10
-        const float rcp = 1.0f / amax;
-        if (lane == 0) args.scale[row] = amax / 127.0f;
         uint32_t* qr = reinterpret_cast<uint32_t*>(args.q) + row * cols4;
+        if (amax < kFastAmaxLimit) {
+            amax = amax < 1e-8f ? 1.0f : amax;  // kore-btes/src/quantize.rs:10
+            const float rcp = 1.0f / amax;
+            const float c127 = 127.0f * rcp;
+            if (lane == 0) args.scale[row] = amax / 127.0f;
+            uint64_t redo[NCH];
+            uint64_t any = 0;
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const uint32_t f = (uint32_t)c * kWave + lane;
-            if (FULL || f < cols4) {
-                const f32x4 v = xv[c];
-                qr[f] = pack4(quant_code(v.x, amax, rcp), quant_code(v.y, amax, rcp), quant_code(v.z, amax, rcp),
-                              quant_code(v.w, amax, rcp));
+            for (int c = 0; c < NCH; ++c) {
+                const uint32_t f = (uint32_t)c * kWave + lane;
+                uint32_t fm = 0;
+                const uint32_t d = flr_pack4(xv[c], c127, fm);
+                redo[c] = __ballot((FULL || f < cols4) && fm >= kFractLimit);
+                any |= redo[c];
+                if (FULL || f < cols4) qr[f] = d;
+            }
+            if (any) {
+                // Rare: exact codes for the lanes whose brackets failed (they
+                // overwrite the stores above, in program order).
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) {
+                    if ((redo[c] >> lane) & 1u) {
+                        const f32x4 v = xv[c];
+                        qr[(uint32_t)c * kWave + lane] =
+                            pack4(quant_code(v.x, amax, rcp), quant_code(v.y, amax, rcp),
+                                  quant_code(v.z, amax, rcp), quant_code(v.w, amax, rcp));
+                    }
+                }
+            }
+        } else {
+            // An absmax of 2^120 or more, infinite, or NaN (every xn NaN):
+            // exact codes.
+            amax = amax < 1e-8f ? 1.0f : amax;  // kore-btes/src/quantize.rs:10
+            const float rcp = 1.0f / amax;
+            if (lane == 0) args.scale[row] = amax / 127.0f;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const uint32_t f = (uint32_t)c * kWave + lane;
+                if (FULL || f < cols4) {
+                    const f32x4 v = xv[c];
+                    qr[f] = pack4(quant_code(v.x, amax, rcp), quant_code(v.y, amax, rcp),
+                                  quant_code(v.z, amax, rcp), quant_code(v.w, amax, rcp));
+                }
             }
         }
     }

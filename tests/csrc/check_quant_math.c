@@ -11,6 +11,12 @@
  *     exponents, and on every a at a set of hard divisors.
  *  2. Ties-away rounding: trunc(t + copysign(0.5 - 2^-25, t)) == roundf(t)
  *     for EVERY float t with |t| < 2^23 (exhaustive over bit patterns).
+ *  3. Bracketed fast code: with M = amax in [1e-8, 2^120) (or the 1.0
+ *     guard), y = RN(1/M), c = RN(127*y), v = fma(xn, c, 0.5 - 2^-14):
+ *     whenever fract(v) < 1 - 2^-13, floor(v) (v_cvt_flr_i32_f32, exact) is
+ *     the reference code clamp(round_half_away(RN(RN(xn*127)/M))).  Checked
+ *     on random (xn, M) with |xn| <= M, and on numerators placed within a
+ *     few ulps of every tie k + 0.5.
  *
  * Exit status 0 when both hold; prints the first counterexample otherwise.
  */
@@ -53,6 +59,36 @@ static int check_round(float t) {
     return 0;
 }
 
+static long n_ambiguous = 0;
+
+/* The reference code of xn for absmax M (both finite, |xn| <= M). */
+static int32_t ref_code(float xn, float M) {
+    volatile float a = xn * 127.0f;
+    volatile float t = a / M;
+    float r = roundf(t);
+    if (r != r) return 0;
+    if (r < -128.0f) r = -128.0f;
+    if (r > 127.0f) r = 127.0f;
+    return (int32_t)r;
+}
+
+static int check_bracket(float xn, float M) {
+    const float off = 0.5f - 6.103515625e-05f; /* 0.5 - 2^-14, exact */
+    volatile float y = 1.0f / M;
+    volatile float c = 127.0f * y;
+    volatile float v = fmaf(xn, c, off);
+    volatile float fl = floorf(v);
+    volatile float fr = v - fl; /* exact: v_fract_f32 */
+    if (!(fr < 0.99987793f)) { ++n_ambiguous; return 0; } /* 1 - 2^-13 */
+    int32_t code = (int32_t)fl;
+    int32_t ref = ref_code(xn, M);
+    if (code != ref) {
+        printf("bracket mismatch: xn=%a M=%a v=%a code=%d want %d\n", xn, M, v, code, ref);
+        return 1;
+    }
+    return 0;
+}
+
 int main(int argc, char **argv) {
     long n_random = argc > 1 ? atol(argv[1]) : 50000000L;
     /* 2. exhaustive rounding over |t| < 2^23, both signs */
@@ -85,7 +121,32 @@ int main(int argc, char **argv) {
             if (check_div(a, divs[d]) || check_div(a * 0.5f, divs[d])) return 1;
         }
     }
-    printf("ok: rounding exhaustive below 2^23, %ld random quotient pairs, %u divisor sweeps\n", n_random,
-           (unsigned)(sizeof(divs) / sizeof(divs[0])));
+    /* 3a. bracketed fast code on random (xn, M), M over the fast path's range */
+    long n_br = 0;
+    for (long i = 0; i < n_random; ++i) {
+        uint32_t eb = 100 + (uint32_t)(next() % 147);      /* biased exp 100..246: M in [1e-8, 2^120) */
+        float M = bits2f((eb << 23) | (uint32_t)(next() & 0x7FFFFF));
+        if (M < 1e-8f) M = 1e-8f;
+        double u = ((double)(next() >> 11) / 9007199254740992.0) * 2.0 - 1.0;
+        float xn = (float)(M * u);
+        if (fabsf(xn) > M) xn = copysignf(M, xn);
+        if (check_bracket(xn, M) || check_bracket(M, M) || check_bracket(-M, M)) return 1;
+        /* numerators at and around a tie: 127*xn/M ~ k + 0.5, stepped by ulps */
+        int k = (int)(next() % 128);
+        float xt = (float)(((double)k + 0.5) * (double)M / 127.0);
+        for (int d = -6; d <= 6; ++d) {
+            float v = bits2f(f2bits(xt) + (uint32_t)d);
+            if (fabsf(v) <= M && (check_bracket(v, M) || check_bracket(-v, M))) return 1;
+        }
+        n_br += 29;
+    }
+    /* 3b. the guard (M = 1.0, every |xn| < 1e-8) and small/large exponents */
+    for (long i = 0; i < 1000000; ++i) {
+        float v = bits2f((uint32_t)(next() % 0x3229705Fu)); /* [0, 1e-8) */
+        if (check_bracket(v, 1.0f) || check_bracket(-v, 1.0f)) return 1;
+    }
+    printf("ok: rounding exhaustive below 2^23, %ld random quotient pairs, %u divisor sweeps, "
+           "%ld bracket checks (%ld ambiguous)\n", n_random,
+           (unsigned)(sizeof(divs) / sizeof(divs[0])), n_br, n_ambiguous);
     return 0;
 }

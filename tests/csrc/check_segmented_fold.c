@@ -189,6 +189,7 @@ static float run_fold(const float *a, int n, long *steps) {
     const int sl = 4 * sl4;
     float d0[64], d1[64], bot[64], top[64], ssum[64], est[64], w0s[64];
     int f0[64], f1[64], key[64], valid[64];
+    (void)f0; (void)f1;
     uint32_t efs[64];
     const float qnan = NAN;
     float total = 0.0f;
@@ -220,26 +221,32 @@ static float run_fold(const float *a, int n, long *steps) {
         f1[j] = (j == 0) ? 0 : (int)(f2u(w1) & 1u);
         if (!valid[j] && j != 0) key[j] = 2048 + j;
     }
-    /* suffix composition within runs, built from the run end backwards */
-    float D0[64], D1[64];
-    int F0[64], F1[64], next[64];
+    /* Runs (the kernel's integer form): a valid segment whose two walks give
+     * the same bit increment ("simple") maps every start in its binade to
+     * s + inc; consecutive simple segments with one binade key form a run
+     * whose entry is the sum of their increments.  Any other segment is a
+     * run of its own and keeps both increments. */
+    uint32_t I0[64], I1[64], inc0[64], inc1[64];
+    int simple[64], rkey[64], next[64];
+    for (int j = 0; j < 64; ++j) {
+        inc0[j] = run_inc(bot[j], top[j], d0[j]);
+        inc1[j] = run_inc(bot[j], top[j], d1[j]);
+        simple[j] = j < nseg && j != 0 && valid[j] && inc0[j] == inc1[j];
+        rkey[j] = j >= nseg ? 1024 : (j == 0 ? 1025 : (simple[j] ? (int)efs[j] : 2048 + j));
+    }
     for (int j = 63; j >= 0; --j) {
-        int end_here = (j == 63) || key[j + 1] != key[j];
-        if (end_here) { D0[j] = d0[j]; D1[j] = d1[j]; F0[j] = f0[j]; F1[j] = f1[j]; next[j] = j + 1; }
-        else {
-            int g0 = f0[j], g1 = f1[j];
-            D0[j] = d0[j] + (g0 ? D1[j + 1] : D0[j + 1]);
-            D1[j] = d1[j] + (g1 ? D1[j + 1] : D0[j + 1]);
-            F0[j] = g0 ? F1[j + 1] : F0[j + 1];
-            F1[j] = g1 ? F1[j + 1] : F0[j + 1];
-            next[j] = next[j + 1];
-        }
+        int end_here = (j == 63) || rkey[j + 1] != rkey[j];
+        uint32_t own = simple[j] ? inc0[j] : 0u;
+        uint32_t sum = end_here ? own : own + (I0[j + 1]);
+        next[j] = end_here ? j + 1 : next[j + 1];
+        I0[j] = simple[j] ? sum : inc0[j];
+        I1[j] = simple[j] ? sum : inc1[j];
     }
     uint32_t s = f2u(w0s[0]);
     int j = 1;
     while (j < nseg) {
         ++*steps;
-        uint32_t i0 = run_inc(bot[j], top[j], D0[j]), i1 = run_inc(bot[j], top[j], D1[j]);
+        uint32_t i0 = I0[j], i1 = I1[j];
         uint32_t lo = f2u(bot[j]), wd = valid[j] ? f2u(top[j]) - f2u(bot[j]) : 0u;
         uint32_t t = s + ((s & 1u) ? i1 : i0);
         uint32_t da = s - lo, db = t - lo;

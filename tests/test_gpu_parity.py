@@ -194,6 +194,52 @@ def test_prequant_special_rows_and_unaligned_q():
     assert qt[1:].cpu().numpy().tobytes() == wq.tobytes()
 
 
+@pytest.mark.parametrize("cols", [2560, 2048, 512, 36])
+def test_prequant_near_tie_codes(cols):
+    """Integer-valued rows (|x| <= 254, unit weights): many quotients
+    127 * xn / amax land within a few ulps of k + 0.5 (e.g. x = 1 against an
+    absmax element 254), so the bracketed fast codes split and the exact
+    per-lane recomputation decides them.  Bit-exact against the oracle."""
+    rows = 512
+    log(f"prequant near-tie rows cols={cols}")
+    g = np.random.default_rng(cols)
+    x = g.integers(-254, 255, size=(rows, cols)).astype(np.float32)
+    x[:, 0] = 254.0
+    x[::3, 1] = -254.0
+    x[1::4] = np.round(x[1::4] / 127.0)  # rows of -2..2 with one 254
+    w = np.ones(cols, np.float32)
+    q, s = rocm.rocm_rms_norm_quant_i8(DEV, up(x), up(w), rows, cols, 1e-6)
+    wq, ws = oracle.rms_norm_quant_i8(x, w, 1e-6)
+    assert down(s, np.float32, (rows,)).tobytes() == ws.tobytes()
+    gq = down(q, np.int8, (rows, cols))
+    diff = np.argwhere(gq != wq)
+    assert diff.size == 0, f"{len(diff)} codes differ, first {diff[:3].tolist()}"
+
+
+@pytest.mark.parametrize("cols", [2560, 512])
+def test_prequant_huge_weights_overflowing_numerator(cols):
+    """|xn| * 127 above FLT_MAX: the reference's quotient is +-inf and the
+    clamp gives 127 / -128; absmax at 2^120 and above, and just below it."""
+    rows = 8
+    log(f"prequant huge weights cols={cols}")
+    x = normal((rows, cols), 31)
+    w = np.full(cols, 1e37, np.float32)
+    w[::7] = 1.0
+    x[6, 5] = 30.0  # an outlier: a larger absmax for row 6
+    x[7, :100] = 0.0
+    wq, ws = oracle.rms_norm_quant_i8(x, w, 1e-6)
+    assert (np.abs(wq) >= 127).any()  # overflowed numerators present
+    q, s = rocm.rocm_rms_norm_quant_i8(DEV, up(x), up(w), rows, cols, 1e-6)
+    assert down(s, np.float32, (rows,)).tobytes() == ws.tobytes()
+    assert down(q, np.int8, (rows, cols)).tobytes() == wq.tobytes()
+    for wv in (2e33, 3e33, 4e33):  # absmax either side of 2^120, the fast path's top end
+        w2 = np.full(cols, wv, np.float32)
+        wq2, ws2 = oracle.rms_norm_quant_i8(x, w2, 1e-6)
+        q2, s2 = rocm.rocm_rms_norm_quant_i8(DEV, up(x), up(w2), rows, cols, 1e-6)
+        assert down(s2, np.float32, (rows,)).tobytes() == ws2.tobytes()
+        assert down(q2, np.int8, (rows, cols)).tobytes() == wq2.tobytes()
+
+
 # ------------------------------------------------------------- activations
 ACT_SIZES = [1, 3, 4, 5, 255, 1024, 1027, (1 << 20) + 3]
 
