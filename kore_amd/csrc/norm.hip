@@ -98,6 +98,7 @@ __host__ __device__ constexpr int seg_pitch4(int sl4) { return (sl4 & 1) ? sl4 :
 __host__ __device__ constexpr int tile_segs(int sl4) { return (sl4 & 1) ? kSegs : kSegs / 2; }
 __host__ __device__ constexpr uint32_t wave_lds_f4(int sl4) { return (uint32_t)(tile_segs(sl4) * seg_pitch4(sl4)); }
 
+
 __device__ __forceinline__ int32_t cvt_i32_sat(float v) {
     // v_cvt_i32_f32: round toward zero, saturating, NaN -> 0.  Written as asm
     // because a C++ float->int cast of NaN is undefined.
@@ -275,35 +276,6 @@ __device__ __forceinline__ float wave_max_nonneg(float v) {
     return read_lane(v, kWave - 1);
 }
 
-// Integer form of a run entry for the scalar resolve.  Inside the binade
-// [bot, top) of grid g the float bits are linear in the value
-// (bits(bot + n*g) = bits(bot) + n, also for the merged [0, 2^-125) range
-// of grid 2^-149), so adding an exact increment d is adding d/g to the bits.
-// d/g = bits(bot + d) - bits(bot) when bot + d < top; otherwise (or for a
-// NaN d) no start in the binade can take the jump and the entry is
-// 0x7fffffff, which fails the resolve's window check.
-__device__ __forceinline__ uint32_t run_inc(float bot, float top, float d) {
-    const float e = bot + d;
-    return (e < top) ? __float_as_uint(e) - __float_as_uint(bot) : 0x7fffffffu;
-}
-
-// Run entry of the segment held by lane L, read into scalar registers.  Lane
-// indices are taken modulo 64, so the read past the last segment is harmless.
-struct RunEntry {
-    uint32_t i0, i1, lo, wd;
-    int next;
-};
-__device__ __forceinline__ RunEntry read_entry(uint32_t inc0, uint32_t inc1, uint32_t lo, uint32_t wd,
-                                               uint32_t next, int L) {
-    RunEntry e;
-    e.i0 = (uint32_t)__builtin_amdgcn_readlane((int)inc0, L);
-    e.i1 = (uint32_t)__builtin_amdgcn_readlane((int)inc1, L);
-    e.lo = (uint32_t)__builtin_amdgcn_readlane((int)lo, L);
-    e.wd = (uint32_t)__builtin_amdgcn_readlane((int)wd, L);
-    e.next = __builtin_amdgcn_readlane((int)next, L);
-    return e;
-}
-
 // FULL: cols == 256*SL4 exactly (every chunk and segment complete, no bounds
 // checks).  Otherwise rows are ragged: loads past the end read 0, segments
 // past the end are empty.
@@ -326,6 +298,7 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
     const int nseg = FULL ? kSegs : (int)((cols4 + SL4 - 1) / SL4);
     f32x4* tile = lds4 + (size_t)wave * kWaveF4;
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    const f32x4* w4 = reinterpret_cast<const f32x4*>(args.w);
 
     // ---- HBM reads: coalesced, chunk-major, all in flight.
     const f32x4* xr = reinterpret_cast<const f32x4*>(args.x) + row * cols4;
@@ -374,19 +347,17 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
 
     // Binade of the estimate (exponent field ef; ef <= 1 is the uniform grid
     // [0, 2^-125) of step 2^-149), selected branch-free.  Segment 0 folds
-    // from its true start +0; an Inf/NaN estimate gets an empty window so the
-    // segment always falls back.
+    // from its true start +0; an Inf/NaN estimate makes the segment
+    // non-jumpable so that it always falls back.
     const uint32_t ef_raw = __float_as_uint(est) >> 23;  // est >= 0
     const uint32_t ef = ef_raw < 1u ? 1u : ef_raw;
     const bool sub = ef == 1u;
     const bool first = seg_id == 0 || empty;
-    const bool bad = !first && ef >= 255u;
-    float sig0 = sub ? 0.0f : __uint_as_float(ef << 23);
-    float sig1 = sub ? __uint_as_float(1u) : __uint_as_float((ef << 23) | 1u);
-    float bot = sig0;
-    float top = __uint_as_float((ef + 1u) << 23);  // ef + 1 == 255 -> +Inf
-    sig0 = first ? 0.0f : sig0;
-    sig1 = first ? 0.0f : sig1;
+    const bool bad = ef >= 255u;
+    const float bot = sub ? 0.0f : __uint_as_float(ef << 23);
+    const float top = __uint_as_float((ef + 1u) << 23);  // ef + 1 == 255 -> +Inf
+    const float sig0 = first ? 0.0f : bot;
+    const float sig1 = first ? 0.0f : (sub ? __uint_as_float(1u) : __uint_as_float((ef << 23) | 1u));
     float w0 = sig0, w1 = sig1;
 #pragma unroll
     for (int k = 0; k < SL4; ++k) {
@@ -396,22 +367,24 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
         w0 = w0 + a.z; w1 = w1 + a.z;
         w0 = w0 + a.w; w1 = w1 + a.w;
     }
-    const bool ok0 = first || w0 < top;
-    const bool ok1 = first || w1 < top;
     // A segment whose estimated span touches a binade edge (within 2^-10;
     // the estimate's own error is below cols * 2^-24 relative) will most
     // likely cross it: keep it out of runs so that it is folded alone
     // instead of breaking a jump.
-    const bool edge = !first && (est < bot * 1.0009765625f || est + ssum >= top * 0.9990234375f);
-    const bool valid = ok0 && ok1 && !edge && !bad;
-    // Exact increments in grid units for entry parity 0 / 1 (0x7fffffff when
-    // the walk left the binade).  A segment whose two walks agree (no tie
-    // broke differently) maps every start s in the binade to s + inc,
-    // whatever its parity: such "simple" segments of one binade compose by
-    // adding their increments.  A valid segment with inc0 != inc1 is a run
-    // of its own whose entry keeps both increments.
-    const uint32_t inc0 = run_inc(bot, top, w0 - sig0);
-    const uint32_t inc1 = run_inc(bot, top, w1 - sig1);
+    const bool edge = est < bot * 1.0009765625f || est + ssum >= top * 0.9990234375f;
+    // The merged range [0, 2^-125) is not jumped (its window would not be
+    // one exponent field); sums there are folded.
+    const bool valid = !first && !sub && w0 < top && w1 < top && !edge && !bad;
+    // Exact increments in grid units for entry parity 0 / 1: inside the
+    // binade the float bits are linear in the value, sig1 one grid step
+    // above sig0 = bot.  Meaningful for valid segments only.
+    const uint32_t inc0 = __float_as_uint(w0) - __float_as_uint(bot);
+    const uint32_t inc1 = __float_as_uint(w1) - __float_as_uint(bot) - 1u;
+    // A valid segment whose two walks agree (no tie broke differently) maps
+    // every start s in the binade to s + inc, whatever its parity: such
+    // "simple" segments of one binade compose by adding their increments.
+    // A valid segment with inc0 != inc1 is a run of its own whose entry keeps
+    // both increments.
     const bool simple = valid && inc0 == inc1;
     // Runs: maximal spans of simple segments with one binade key; any other
     // segment is a run of its own.  This lane's segment ends its run when
@@ -428,47 +401,58 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
     // segment after it is 64 - that lane.
     const uint64_t below = ends & (lt_mask | (1ull << lane));
     const uint32_t next_seg = (uint32_t)(kSegs - (63 - __builtin_clzll(below)));
-    // Integer run entry: bit increments for entry parity 0/1, the binade
-    // window as lo = bits(bot) and width = bits(top) - lo, and the segment
-    // after the run.  Width 0 marks a segment outside every run (a predicted
-    // binade crossing, a walk that left its binade, an Inf/NaN estimate):
-    // the resolve folds it without trying a jump.
-    const uint32_t e_inc0 = simple ? run_sum : inc0;
-    const uint32_t e_inc1 = simple ? run_sum : inc1;
-    const uint32_t lo_v = __float_as_uint(bot);
-    const uint32_t wd_v = valid ? __float_as_uint(top) - __float_as_uint(bot) : 0u;
+    // Run entry packed in two words, read with two lane reads:
+    //   word 0: increment for entry parity 0 (24 bits; a run below one binade
+    //           top never reaches 2^23) | exponent field of the binade << 24;
+    //   word 1: segment after the run | parity-1 increment minus parity-0
+    //           increment (7-bit signed) << 8 | jumpable << 15.
+    // Two-walk segments whose increments differ by 64 grid steps or more,
+    // runs whose increment reaches a whole binade (no start could stay
+    // inside it), and invalid segments are not jumpable: the resolve folds
+    // them.
+    const int32_t delta = simple ? 0 : (int32_t)(inc1 - inc0);
+    const uint32_t e_inc = simple ? run_sum : inc0;
+    const bool jumpable = valid && delta >= -64 && delta < 64 && e_inc < 0x800000u;
+    const uint32_t e_w0 = (e_inc & 0xffffffu) | (ef << 24);
+    const uint32_t e_w1 = next_seg | (((uint32_t)delta & 0x7fu) << 8) | (jumpable ? 0x8000u : 0u);
 
     // ---- resolve on the scalar unit.  s holds the bits of the exact running
     // sum (non-negative, so unsigned order is float order and NaN/Inf sort
-    // above every window).  Segment 0 was folded from +0 and is exact.  For
-    // segment j the run entry lives in lane 63 - j: when s lies in the run's
-    // binade [lo, lo + width) and the jump lands inside it too, s moves by
-    // the entry for its parity (the lsb of s's bits is its parity on the
-    // binade grid); otherwise (or for a width-0 entry) the owner lane folds
-    // segment j alone from s and broadcasts the sum.  With t = s + inc >= s, both window tests are
-    // max(s - lo, t - lo) < width in wrapping unsigned arithmetic (s < lo
-    // wraps to a huge value).  A step is five lane reads and about ten
-    // scalar instructions.
+    // above every window).  Segment 0 was folded from +0 and is exact.  The
+    // entry of segment j lives in lane 63 - j.  A jumpable entry applies when
+    // s lies in its binade [lo, lo + 2^23 grid steps) and the jump lands
+    // inside it too: s moves by the increment for its parity (the lsb of s's
+    // bits is its parity on the binade grid).  With t = s + inc >= s both
+    // tests are max(s - lo, t - lo) < 2^23 in wrapping unsigned arithmetic
+    // (s < lo wraps to a huge value).  Otherwise the owner lane folds the
+    // segment alone from s and broadcasts the sum.  The next entry's lane
+    // reads are issued before the test so that they overlap it.
     uint32_t s = __builtin_amdgcn_readlane(__float_as_uint(w0), kWave - 1);
     int j = 1;
-    RunEntry cur = read_entry(e_inc0, e_inc1, lo_v, wd_v, next_seg, kSegs - 2);
+    uint32_t c0 = (uint32_t)__builtin_amdgcn_readlane((int)e_w0, kSegs - 2);
+    uint32_t c1 = (uint32_t)__builtin_amdgcn_readlane((int)e_w1, kSegs - 2);
     while (j < nseg) {
-        const int L = kSegs - 1 - j;
-        if (cur.wd != 0u) {
-            const uint32_t t = s + ((s & 1u) ? cur.i1 : cur.i0);
-            const uint32_t a = s - cur.lo, b = t - cur.lo;
-            if ((a > b ? a : b) < cur.wd) {
-                s = t;
-                j = cur.next;
-                cur = read_entry(e_inc0, e_inc1, lo_v, wd_v, next_seg, (kSegs - 1 - j) & (kWave - 1));
-                continue;
-            }
+        const int nj = (int)(c1 & 0xffu);
+        const uint32_t n0 = (uint32_t)__builtin_amdgcn_readlane((int)e_w0, (kSegs - 1 - nj) & (kWave - 1));
+        const uint32_t n1 = (uint32_t)__builtin_amdgcn_readlane((int)e_w1, (kSegs - 1 - nj) & (kWave - 1));
+        const int32_t dp = (int32_t)(c1 << 17) >> 25;
+        const uint32_t t = s + (c0 & 0xffffffu) + ((s & 1u) ? (uint32_t)dp : 0u);
+        const uint32_t lo = (c0 >> 24) << 23;
+        const uint32_t da = s - lo, db = t - lo;
+        if ((c1 & 0x8000u) && (da > db ? da : db) < 0x800000u) {
+            s = t;
+            j = nj;
+            c0 = n0;
+            c1 = n1;
+            continue;
         }
         // Fold segment j alone.  The entry of segment j + 1 is read first so
         // that its latency hides under the fold chain.  Every lane folds its
         // own segment from s (same cost as one lane under an exec mask,
-        // without the mask changes); lane L's sum is the one kept.
-        cur = read_entry(e_inc0, e_inc1, lo_v, wd_v, next_seg, (L - 1) & (kWave - 1));
+        // without the mask changes); lane 63 - j's sum is the one kept.
+        const int L = kSegs - 1 - j;
+        c0 = (uint32_t)__builtin_amdgcn_readlane((int)e_w0, (L - 1) & (kWave - 1));
+        c1 = (uint32_t)__builtin_amdgcn_readlane((int)e_w1, (L - 1) & (kWave - 1));
         float acc = __uint_as_float(s);
 #pragma unroll
         for (int k = 0; k < SL4; ++k) acc = fold4(acc, seg[k]);
@@ -478,8 +462,8 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
     const float ss = __uint_as_float(s);
 
     // Weights for the epilogue (L2 hits), loaded after the resolve so their
-    // registers are free while it runs.
-    const f32x4* w4 = reinterpret_cast<const f32x4*>(args.w);
+    // registers are free while it runs (staging them in LDS at the start was
+    // measured slower: 14.0 -> 14.4 us at 4096 x 2560).
     f32x4 wv[NCH];
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {

@@ -177,86 +177,95 @@ static long rfb = 0;
  * arithmetic (lo = bits(bot), width = bits(top) - lo; both s and s + inc in
  * [bot, top)); otherwise, or when segment j is outside every run (width 0),
  * segment j is folded alone from s.  Segment 0 is folded from +0 exactly. */
-static uint32_t run_inc(float bot, float top, float d) {
-    float e = bot + d;
-    return (e < top) ? f2u(e) - f2u(bot) : 0x7fffffffu;
-}
 
+/* The kernel's current form: every segment gets its own binade guess,
+ * walks, validity and run entry.  Runs are maximal spans of "simple"
+ * segments (valid, both walks giving the same bit increment) with one
+ * binade key, whose entry is the sum of their increments; any other valid
+ * segment is a run of its own with both increments.  Entries are jumpable
+ * only when valid, outside the merged range [0, 2^-125), with
+ * |inc1 - inc0| < 64 and an increment below 2^23; others (width 0) are
+ * folded alone from s. */
 static float run_fold(const float *a, int n, long *steps) {
     const int n4 = n / 4;
     const int sl4 = (n4 + 63) / 64 ? (n4 + 63) / 64 : 1;
-    const int nseg = (n4 + sl4 - 1) / sl4;
-    const int sl = 4 * sl4;
-    float d0[64], d1[64], bot[64], top[64], ssum[64], est[64], w0s[64];
-    int f0[64], f1[64], key[64], valid[64];
-    (void)f0; (void)f1;
-    uint32_t efs[64];
-    const float qnan = NAN;
+    const int nsubper = 1;
+    const int sub4 = sl4 / nsubper;
+    const int sl = 4 * sub4;               /* terms per sub-segment */
+    const int nsub = (n4 + sub4 - 1) / sub4;
+    const int U = 64 * nsubper;
+    float ssub[128], est[128], w0s[128];
+    uint32_t inc0[128], inc1[128], lo[128], wd[128], I0[128], I1[128], efs[128];
+    int simple[128], rkey[128], next[128], valid[128];
+    for (int u = 0; u < U; ++u) {
+        ssub[u] = 0.0f;
+        for (int i = u * sl; i < u * sl + sl; i += 4) {
+            float v[4];
+            for (int q = 0; q < 4; ++q) v[q] = (i + q < n) ? a[i + q] : 0.0f;
+            ssub[u] += (v[0] + v[1]) + (v[2] + v[3]);
+        }
+    }
+    /* segment-start estimates (any order: sequential here), then per half */
     float total = 0.0f;
     for (int j = 0; j < 64; ++j) {
-        ssum[j] = 0.0f;
-        for (int i = j * sl; i < j * sl + sl; ++i) ssum[j] += (i < n) ? a[i] : 0.0f;
+        float e = total;
+        for (int h = 0; h < nsubper; ++h) { est[j * nsubper + h] = e; e = e + ssub[j * nsubper + h]; }
+        float ssum = ssub[j * nsubper];
+        if (nsubper == 2) ssum += ssub[j * nsubper + 1];
+        total += ssum;
     }
-    for (int j = 0; j < 64; ++j) { est[j] = total; total += ssum[j]; }
-    for (int j = 0; j < 64; ++j) {
-        float sig0, sig1;
-        if (j >= nseg) { d0[j] = d1[j] = 0; bot[j] = 0; top[j] = INFINITY; f0[j] = 0; f1[j] = 1; key[j] = 1024; valid[j] = 1; efs[j] = 0; continue; }
-        uint32_t ef = f2u(est[j]) >> 23;
+    for (int u = 0; u < U; ++u) {
+        int empty = u >= nsub, first = u == 0 || empty;
+        uint32_t ef = f2u(est[u]) >> 23;
         if (ef < 1u) ef = 1u;
-        int bad = j != 0 && ef >= 255u;
-        efs[j] = bad ? 0u : ef;
-        if (ef == 1u) { sig0 = 0; sig1 = u2f(1u); } else { sig0 = u2f(ef << 23); sig1 = u2f((ef << 23) | 1u); }
-        bot[j] = sig0;
-        top[j] = u2f((ef + 1u) << 23);
-        if (j == 0) { sig0 = 0; sig1 = 0; key[j] = 1025; } else key[j] = (int)ef;
+        int subn = ef == 1u, bad = !first && ef >= 255u;
+        float bot = subn ? 0.0f : u2f(ef << 23);
+        float top = u2f((ef + 1u) << 23);
+        float sig0 = first ? 0.0f : bot;
+        float sig1 = first ? 0.0f : (subn ? u2f(1u) : u2f((ef << 23) | 1u));
         float w0 = sig0, w1 = sig1;
-        for (int i = j * sl; i < j * sl + sl; ++i) { float v = i < n ? a[i] : 0.0f; w0 = w0 + v; w1 = w1 + v; }
-        w0s[j] = w0;
-        int ok0 = j == 0 || w0 < top[j], ok1 = j == 0 || w1 < top[j];
-        int edge = j != 0 && (est[j] < bot[j] * 1.0009765625f || est[j] + ssum[j] >= top[j] * 0.9990234375f);
-        valid[j] = ok0 && ok1 && !edge && !bad;
-        d0[j] = ok0 ? w0 - sig0 : qnan;
-        d1[j] = (j == 0) ? d0[j] : (ok1 ? w1 - sig1 : qnan);
-        f0[j] = (int)(f2u(w0) & 1u);
-        f1[j] = (j == 0) ? 0 : (int)(f2u(w1) & 1u);
-        if (!valid[j] && j != 0) key[j] = 2048 + j;
+        for (int i = u * sl; i < u * sl + sl; ++i) { float v = i < n ? a[i] : 0.0f; w0 = w0 + v; w1 = w1 + v; }
+        w0s[u] = w0;
+        int edge = est[u] < bot * 1.0009765625f || est[u] + ssub[u] >= top * 0.9990234375f;
+        valid[u] = !first && !subn && w0 < top && w1 < top && !edge && !bad;
+        inc0[u] = f2u(w0) - f2u(bot);
+        inc1[u] = f2u(w1) - f2u(bot) - 1u;
+        simple[u] = valid[u] && inc0[u] == inc1[u];
+        rkey[u] = empty ? 1024 : (u == 0 ? 1025 : (simple[u] ? (int)ef : 2048 + u));
+        lo[u] = f2u(bot);
+        /* two-walk sub-segments jump only with |inc1 - inc0| < 64 (7-bit field) */
+        int32_t delta = (int32_t)(inc1[u] - inc0[u]);
+        (void)delta;
+        wd[u] = f2u(top) - f2u(bot);
+        efs[u] = ef;
     }
-    /* Runs (the kernel's integer form): a valid segment whose two walks give
-     * the same bit increment ("simple") maps every start in its binade to
-     * s + inc; consecutive simple segments with one binade key form a run
-     * whose entry is the sum of their increments.  Any other segment is a
-     * run of its own and keeps both increments. */
-    uint32_t I0[64], I1[64], inc0[64], inc1[64];
-    int simple[64], rkey[64], next[64];
-    for (int j = 0; j < 64; ++j) {
-        inc0[j] = run_inc(bot[j], top[j], d0[j]);
-        inc1[j] = run_inc(bot[j], top[j], d1[j]);
-        simple[j] = j < nseg && j != 0 && valid[j] && inc0[j] == inc1[j];
-        rkey[j] = j >= nseg ? 1024 : (j == 0 ? 1025 : (simple[j] ? (int)efs[j] : 2048 + j));
-    }
-    for (int j = 63; j >= 0; --j) {
-        int end_here = (j == 63) || rkey[j + 1] != rkey[j];
-        uint32_t own = simple[j] ? inc0[j] : 0u;
-        uint32_t sum = end_here ? own : own + (I0[j + 1]);
-        next[j] = end_here ? j + 1 : next[j + 1];
-        I0[j] = simple[j] ? sum : inc0[j];
-        I1[j] = simple[j] ? sum : inc1[j];
+    (void)efs;
+    uint32_t run = 0;
+    for (int u = U - 1; u >= 0; --u) {
+        int end_here = (u == U - 1) || rkey[u + 1] != rkey[u];
+        uint32_t own = simple[u] ? inc0[u] : 0u;
+        run = end_here ? own : own + run;
+        next[u] = end_here ? u + 1 : next[u + 1];
+        I0[u] = simple[u] ? run : inc0[u];
+        I1[u] = simple[u] ? run : inc1[u];
+        {   /* jumpable: valid, |inc1 - inc0| < 64, entry increment below 2^23 */
+            int32_t dl = (int32_t)(I1[u] - I0[u]);
+            if (!(valid[u] && dl >= -64 && dl < 64 && I0[u] < 0x800000u)) wd[u] = 0u;
+        }
     }
     uint32_t s = f2u(w0s[0]);
-    int j = 1;
-    while (j < nseg) {
+    int u = 1;
+    while (u < nsub) {
         ++*steps;
-        uint32_t i0 = I0[j], i1 = I1[j];
-        uint32_t lo = f2u(bot[j]), wd = valid[j] ? f2u(top[j]) - f2u(bot[j]) : 0u;
-        uint32_t t = s + ((s & 1u) ? i1 : i0);
-        uint32_t da = s - lo, db = t - lo;
-        if (wd != 0u && (da > db ? da : db) < wd) { s = t; j = next[j]; }
+        uint32_t t = s + ((s & 1u) ? I1[u] : I0[u]);
+        uint32_t da = s - lo[u], db = t - lo[u];
+        if (wd[u] != 0u && (da > db ? da : db) < wd[u]) { s = t; u = next[u]; }
         else {
             ++rfb;
             float acc = u2f(s);
-            for (int i = j * sl; i < j * sl + sl; ++i) acc = acc + (i < n ? a[i] : 0.0f);
+            for (int i = u * sl; i < u * sl + sl; ++i) acc = acc + (i < n ? a[i] : 0.0f);
             s = f2u(acc);
-            ++j;
+            ++u;
         }
     }
     return u2f(s);
