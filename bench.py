@@ -645,9 +645,60 @@ class Copy(Workload):
         return None
 
 
+class LaunchFloor(Workload):
+    """One empty workgroup per launch (kore_hip_diag_empty): the floor of a
+    dependent kernel launch on a stream, against which the latency-bound
+    configs (a few rows) are read."""
+    name = "launch_floor"
+    kernel = "diag_empty_kernel"
+    tokens = 1
+    bytes = 0
+    desc = "empty kernel, one workgroup of 64 threads (launch floor)"
+
+    def setup(self, torch, lib):
+        self.lib = lib
+
+    def launch(self, i, stream):
+        return self.lib.kore_hip_diag_empty(stream)
+
+    def cpu_sample(self):
+        return None
+
+
+class StreamFloor(Workload):
+    """The pre-quant kernel's bytes with a trivial body
+    (kore_hip_diag_stream_rows): reads x[rows, cols] f32 once, writes one byte
+    per value and one f32 per row, one wave per row.  The streaming ceiling of
+    that shape, measured next to the real kernel."""
+    kernel = "diag_stream_rows_kernel"
+
+    def __init__(self, rows=4096, cols=2560):
+        self.rows, self.cols = rows, cols
+        self.name = f"stream_floor_{rows}x{cols}"
+        self.tokens = rows
+        self.bytes = rows * cols * 4 + rows * cols + rows * 4 + cols * 4
+        self.desc = f"pre-quant traffic with a trivial body: x[{rows},{cols}] f32 -> one byte per value + f32 per row"
+
+    def setup(self, torch, lib):
+        self.lib = lib
+        self.k = n_sets(self.rows * self.cols * 5, cap=16)
+        self._dx = [randn(torch, (self.rows, self.cols), s) for s in range(self.k)]
+        self._dq = [torch.empty((self.rows, self.cols), dtype=torch.int8, device="cuda") for _ in range(self.k)]
+        self._ds = [torch.empty((self.rows,), device="cuda") for _ in range(self.k)]
+
+    def launch(self, i, stream):
+        j = i % self.k
+        return self.lib.kore_hip_diag_stream_rows(self._dx[j].data_ptr(), self._dq[j].data_ptr(),
+                                                  self._ds[j].data_ptr(), self.rows, self.cols, stream)
+
+    def cpu_sample(self):
+        return None
+
+
 def all_workloads():
     return [RopeQK(False), RopeQK(True), RMSNorm(32, 2048), RMSNorm(16384, 2048), Swiglu(), Gelu(), Embedding(),
-            Prequant(4096), Prequant(64), Prequant(1), RmsNormSiluGate(), Softmax(), SoftmaxBackward(),
+            Prequant(4096), Prequant(64), Prequant(1), LaunchFloor(), StreamFloor(), RmsNormSiluGate(), Softmax(),
+            SoftmaxBackward(),
             RmsNormBackward(), TernaryI8(), TernaryI8(6912, 64, 2560), TernaryI8(6912, 1, 2560), TernaryF32(),
             TernaryF32(6912, 64, 2560), PackTernary(), PackTernary(2560, 6912), Copy()]
 
@@ -674,6 +725,36 @@ def time_gpu(torch, w: Workload, steps: int, warmup: int):
     wall = time.perf_counter() - t0
     ev_ms = ev0.elapsed_time(ev1)
     return ev_ms / steps, wall
+
+
+def time_graph(torch, w: Workload, per_graph: int = 20, replays: int = 20):
+    """Per-launch time with `per_graph` launches captured in one HIP graph and
+    replayed: the kernels back to back without host launch overhead.  Every
+    entry point is capturable (no allocation, synchronisation or memset)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(3):
+            w.launch(i, side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        sp = torch.cuda.current_stream().cuda_stream
+        for i in range(per_graph):
+            if w.launch(i, sp) != 0:
+                raise RuntimeError(f"{w.name}: launch failed under capture")
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (replays * per_graph)
+    del g
+    return us
 
 
 def time_cpu(w: Workload, budget_s: float):
@@ -744,6 +825,9 @@ def main():
         steps = args.steps if w.bytes >= (64 << 20) else max(args.steps, 200)
         print(f"[bench] {w.name}: {args.warmup} warmup + {steps} timed launches", file=sys.stderr, flush=True)
         ms, wall = time_gpu(torch, w, steps, args.warmup)
+        graph_us = None
+        if w.bytes < (16 << 20):  # latency-bound launches: also without host launch overhead
+            graph_us = round(time_graph(torch, w), 3)
         gbs = w.bytes / (ms * 1e-3) / 1e9
         r = {
             "workload": w.desc, "kernel": w.kernel, "bytes_per_launch": w.bytes, "tokens": w.tokens,
@@ -751,6 +835,8 @@ def main():
             "ns_per_token": round(ms * 1e6 / w.tokens, 3), "steps": steps, "wall_s": round(wall, 4),
             "wall_gbs": round(w.bytes * steps / wall / 1e9, 1),
         }
+        if graph_us is not None:
+            r["graph_us"] = graph_us
         if w.ops:
             tops = w.ops / (ms * 1e-3) / 1e12
             r.update({"bound": w.bound, "ops_per_launch": w.ops, "achieved_tops": round(tops, 3)})
@@ -805,6 +891,42 @@ def main():
         "kernels": results,
     }
     print(json.dumps(line), flush=True)
+    print_summary(results)
+
+
+# BASELINE.json configs -> workloads (configs[1] is the headline), then the
+# floors and the "next" rows.
+SUMMARY = [("cfg0 RMSNorm 32x2048", "rms_norm_32x2048"), ("cfg1 RoPE Q+K half-split", "rope_qk"),
+           ("cfg1 RoPE Q+K interleaved", "rope_qk_interleaved"), ("cfg2 SwiGLU 16384x14336", "swiglu"),
+           ("cfg2 GELU 16384x14336", "gelu"), ("cfg3 Embedding 8192x4096", "embedding"),
+           ("cfg4 pre-quant 4096x2560", "prequant_4096x2560"), ("cfg4 pre-quant 64x2560", "prequant_64x2560"),
+           ("cfg4 pre-quant 1x2560", "prequant_1x2560"), ("floor: empty launch", "launch_floor"),
+           ("floor: pre-quant bytes, trivial body", "stream_floor_4096x2560"),
+           ("next: RMSNorm 16384x2048", "rms_norm_16384x2048"), ("next: norm+SiLU gate", "rms_norm_silu_gate_4096x2560"),
+           ("next: softmax 32768x2048", "softmax_32768x2048"),
+           ("next: ternary i8 6912x4096x2560", "ternary_i8_6912x4096x2560")]
+
+
+def print_summary(results):
+    """Compact per-config lines on stderr (after the JSON line, so that a
+    captured stderr tail holds every BASELINE config)."""
+    floor = results.get("launch_floor", {}).get("kernel_us")
+    out = ["[summary] config: us (graph us) | GB/s | % of 8 TB/s | ns/token | CPU baseline"]
+    for label, name in SUMMARY:
+        r = results.get(name)
+        if not r:
+            continue
+        g = f" ({r['graph_us']})" if "graph_us" in r else ""
+        cpu = r.get("cpu_baseline") or {}
+        cpu_s = f"{cpu.get('value')} {cpu.get('unit', '')} x{cpu.get('cores', '')}" if cpu else "-"
+        tail = ""
+        if floor and "graph_us" in r and name != "launch_floor":
+            tail = f" | {r['kernel_us'] / floor:.2f}x launch floor"
+        if "achieved_tops" in r and r.get("bound") == "mfma":
+            tail += f" | {r['achieved_tops']} TOPS ({100 * r['frac_of_mfma_peak']:.1f}% int8 MFMA)"
+        out.append(f"[summary] {label}: {r['kernel_us']}{g} | {r['achieved_gbs']} | {100 * r['frac_of_peak']:.1f}% | "
+                   f"{r['ns_per_token']} | {cpu_s}{tail}")
+    print("\n".join(out), file=sys.stderr, flush=True)
 
 
 if __name__ == "__main__":
