@@ -309,6 +309,12 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
         xv[c] = (FULL || f < cols4) ? ld_stream(xr + f) : zero;
     }
 
+    // Wave priority rises with a row's progress (its loads issued: 1; its
+    // walks: 2; the scalar resolve, the latency-critical chain: 3) and drops
+    // to 0 for the element-parallel epilogue, so that on a SIMD shared by
+    // four rows the dependent chains of rows further along issue first.
+    // Measured at 4096 x 2560 pre-quant: 14.0 -> 13.2 us.
+    __builtin_amdgcn_s_setprio(1);
     // Lane L holds segment j = 63 - L, so a forward (lane-increasing) scan
     // composes each segment with the segments after it.
     const int seg_id = kSegs - 1 - lane;
@@ -336,6 +342,7 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
         }
     }
 
+    __builtin_amdgcn_s_setprio(2);
     const bool empty = !FULL && seg_id >= nseg;
     float ssum = 0.0f;
 #pragma unroll
@@ -427,6 +434,7 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
     // (s < lo wraps to a huge value).  Otherwise the owner lane folds the
     // segment alone from s and broadcasts the sum.  The next entry's lane
     // reads are issued before the test so that they overlap it.
+    __builtin_amdgcn_s_setprio(3);
     uint32_t s = __builtin_amdgcn_readlane(__float_as_uint(w0), kWave - 1);
     int j = 1;
     uint32_t c0 = (uint32_t)__builtin_amdgcn_readlane((int)e_w0, kSegs - 2);
@@ -460,6 +468,7 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
         ++j;
     }
     const float ss = __uint_as_float(s);
+    __builtin_amdgcn_s_setprio(0);
 
     // Weights for the epilogue (L2 hits), loaded after the resolve so their
     // registers are free while it runs (staging them in LDS at the start was
