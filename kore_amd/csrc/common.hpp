@@ -1,8 +1,9 @@
 // common.hpp -- shared device helpers for the gfx950 fused layer kernels.
 //
 // Everything here is written for CDNA4 (gfx950): wave64, 128-bit vector
-// memory operations, LDS, DPP/ds_swizzle cross-lane moves.  No MFMA is used
-// anywhere in this library: every op is bound by HBM bandwidth.
+// memory operations, LDS, DPP/ds_swizzle cross-lane moves.  The fused layer
+// ops are bound by HBM bandwidth and use no MFMA; only the BitLinear int8 x
+// ternary matmul (ternary.hip) is a contraction on the int8 MFMA units.
 #pragma once
 
 #include <hip/hip_runtime.h>

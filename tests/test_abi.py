@@ -141,3 +141,18 @@ def test_rope_inv_freq_table_matches_oracle_bit_exact(head_dim, base):
     assert _lib.load().kore_hip_rope_inv_freq_f32(got.ctypes.data, head_dim, base) == 0
     want = oracle.rope_inv_freq(head_dim, base)
     assert got.tobytes() == want.tobytes()
+
+
+def test_rust_binding_names_match_the_header():
+    """rust/kore-kernels-rocm/src/fused.rs (the drop-in KORE module, not
+    compiled here) loads only symbols that include/kore_hip.h declares, and
+    binds every non-diagnostic entry point."""
+    import re
+
+    rs = open(os.path.join(ROOT, "rust", "kore-kernels-rocm", "src", "fused.rs")).read()
+    loaded = set(re.findall(r'lib\.get\(b"(kore_hip_[a-z0-9_]+)\\0"\)', rs))
+    declared = set(declared_symbols())
+    assert loaded, "no symbols found in fused.rs"
+    assert loaded <= declared, loaded - declared
+    expected = {d for d in declared if not d.startswith("kore_hip_diag_") and d != "kore_hip_version"}
+    assert expected <= loaded, expected - loaded
