@@ -43,6 +43,7 @@
 // a sequential fold per output (ternary_f32_seq_kernel, and for up to four
 // columns ternary_f32_pipe_kernel, at the end).
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kore_hip_internal.hpp"
@@ -235,6 +236,302 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
                 }
             }
         }
+    }
+}
+
+// Wide path (large m and n, packed rows 16-byte aligned, K % 16 == 0): the
+// workgroup owns a 256 (m) x 256 (n) output tile; wave w owns weight rows
+// [64 w, 64 w + 64) of it against all 256 code rows: 2 x 8 MFMA tiles of
+// 32 x 32 (256 int32 accumulators per lane), one workgroup per CU.
+//   * Weights never pass through LDS as data: each lane decodes its own
+//     rows' 16 packed bytes per 160-column K step (lane half h owns columns
+//     [80 h, 80 h + 80)) straight into the operands of five 32-deep MFMA
+//     steps (step s: columns 80 h + 16 s .. + 16, natural order), through a
+//     byte -> five-trit table held in 32 copies, copy c serving lanes c and
+//     c + 32 and laid out so that every entry of copy c lies in the same two
+//     LDS banks: a half-wave's 32 lanes read 32 distinct bank pairs whatever
+//     bytes they decode.  The next K step's weights are decoded while the
+//     current step's MFMAs run (a fifth of the bytes per MFMA step).
+//   * Codes reach LDS by direct global -> LDS loads (no registers), into a
+//     double-buffered tile with a 176-byte row pitch (16 lanes reading 16
+//     bytes of 16 consecutive rows hit 16 distinct bank groups); the tile of
+//     step kt + 2 is loaded while step kt computes; one barrier per step.
+//     Code rows past n are clamped to row n - 1 (their outputs are not
+//     stored); columns past k are clamped to the step's first 16 bytes and
+//     the weights' trits there are zeroed instead.
+// LDS traffic per MFMA is ~0.7 KB (operand reads 0.5, table reads 0.2)
+// against the ~1 KB one CU delivers per MFMA of each of its four SIMDs.
+constexpr int kWdM = 256, kWdN = 256;
+constexpr int kWdPitch = 176;
+constexpr int kWdCopies = 32;
+constexpr size_t kWdBBytes = (size_t)kWdN * kWdPitch;           // one code buffer
+constexpr size_t kWdLds = 2 * kWdBBytes + 256 * kWdCopies * 8;    // 155,648 bytes
+constexpr int kWdSlots = kWdBBytes / 16 / 4;                      // 16-byte slots per wave: 704
+constexpr int kWdDma = kWdSlots / kWave;                          // 11 loads per wave per step
+
+typedef __attribute__((address_space(3))) void* lds_vptr;
+typedef __attribute__((address_space(1))) void* glb_vptr;
+
+// Trits of byte b of a 16-byte packed window: b's five trits go to bytes
+// 5b .. 5b + 4 of the 80-byte (20-dword) decoded window.
+__device__ __forceinline__ void splice_trits(uint32_t (&out)[20], int b, uint64_t v) {
+    const int off = 5 * b, d = off >> 2, sh = (off & 3) * 8;
+    out[d] |= (uint32_t)(v << sh);
+    out[d + 1] |= (uint32_t)(v >> (32 - sh));
+}
+
+__global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t wlds[];
+    uint64_t* lut = reinterpret_cast<uint64_t*>(wlds + 2 * kWdBBytes);
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    const int r = lane & 31, h = lane >> 5;
+    // Tile order: block b runs on XCD b % 8; XCD x takes the contiguous range
+    // [x * per, (x + 1) * per) of an n-major tile order, so the workgroups of
+    // one XCD share code tiles in its L2 while the weights stream.
+    const uint32_t tm_n = (p.m + kWdM - 1) / kWdM, tn_n = (p.n + kWdN - 1) / kWdN;
+    const uint32_t ntiles = tm_n * tn_n;
+    const uint32_t per = (ntiles + kXcds - 1) / kXcds;
+    const uint32_t work = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+    if (work >= ntiles) return;  // whole workgroup: no barrier reached yet
+    const uint32_t m0 = (work % tm_n) * kWdM, n0 = (work / tm_n) * kWdN;
+
+    // Table: entry e, copy c at u64 index e * 32 + c (bank pair 2c).  Thread
+    // e fills its entry's copies in a rotated order so that the 64 lanes of a
+    // write hit distinct bank pairs.
+    {
+        const uint64_t v = trit_lut_entry((uint32_t)t);
+#pragma unroll 8
+        for (int c2 = 0; c2 < kWdCopies; ++c2) lut[t * kWdCopies + ((c2 + t) & (kWdCopies - 1))] = v;
+    }
+    const uint64_t* lut_lane = lut + r;
+
+    const uint32_t nkt = (p.k + kTmK - 1) / kTmK;
+    // This lane's two weight rows (fragments i = 0, 1); rows past m read row
+    // m - 1 (their outputs are not stored).
+    const u32x4* arow[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t m = min(m0 + 64 * wave + 32 * i + r, p.m - 1u);
+        arow[i] = reinterpret_cast<const u32x4*>(p.a + (uint64_t)m * p.kp);
+    }
+    // A window past kp (the second half of a last step) reads the row's
+    // first window: it lies wholly past k, so its trits are zeroed below.
+    auto load_a = [&](uint32_t kt, u32x4 (&av)[2]) {
+        const uint32_t ab = kt * kTmKp + 16u * h;
+        const uint32_t abc = ab < p.kp ? ab : 0u;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) av[i] = arow[i][abc >> 4];
+    };
+    // Code slots of this wave: slot s (16 bytes) of a tile is row s / 11,
+    // piece s % 11 (piece 10: the row's padding, filled with piece 0).
+    uint32_t boff[kWdDma], bp16[kWdDma];
+#pragma unroll
+    for (int g = 0; g < kWdDma; ++g) {
+        const int slot = kWdSlots * wave + kWave * g + lane;
+        const int row = slot / 11, piece = slot % 11;
+        const uint32_t rowc = min(n0 + (uint32_t)row, p.n - 1u);
+        bp16[g] = piece < 10 ? 16u * piece : 0u;
+        boff[g] = rowc * p.k + bp16[g];
+    }
+    const bool k_tail = p.k % kTmK != 0;
+    // Code load g (0 .. kWdDma - 1) of step kt into buffer buf.
+    auto dma_one = [&](uint32_t kt, uint32_t buf, int g) {
+        const int8_t* base = p.q + (uint64_t)kt * kTmK;
+        const uint32_t rem = p.k - kt * kTmK;  // >= 16 bytes of this step per row
+        uint8_t* dst = wlds + buf * kWdBBytes + (size_t)kWdSlots * 16 * wave + kWave * 16 * g;
+        uint32_t off = boff[g];
+        if (k_tail && bp16[g] >= rem) off -= bp16[g];
+        __builtin_amdgcn_global_load_lds((glb_vptr)(base + off), (lds_vptr)dst, 16, 0, 0);
+    };
+    auto dma_b = [&](uint32_t kt, uint32_t buf) {
+#pragma unroll
+        for (int g = 0; g < kWdDma; ++g) dma_one(kt, buf, g);
+    };
+
+    i32x16 acc[2][8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0;
+
+    // Trits past k (last step only): zero the decoded bytes at columns >= k.
+    auto mask_tail = [&](uint32_t kt, uint32_t (&dec)[2][20]) {
+        const int rem = (int)p.k - (int)(kt * kTmK) - 80 * h;  // valid trits of this lane's window
+#pragma unroll
+        for (int d = 0; d < 20; ++d) {
+            const int keep = rem - 4 * d;  // bytes of dword d to keep
+            const uint32_t msk = keep >= 4 ? 0xffffffffu : (keep <= 0 ? 0u : (0xffffffffu >> (8 * (4 - keep))));
+#pragma unroll
+            for (int i = 0; i < 2; ++i) dec[i][d] &= msk;
+        }
+    };
+
+    // Software pipeline, per K step kt (buffer kt & 1 holds its code tile):
+    //   * the weights of step kt + 2 are loaded into registers and the code
+    //     tile of step kt + 1 is loaded into the other buffer (freed by the
+    //     barrier that ended step kt - 1), both spread over the first MFMA
+    //     group;
+    //   * the weights of step kt + 1 are decoded while the MFMAs of step kt
+    //     run; code operands are read one MFMA group ahead;
+    //   * a barrier ends the step once this wave's code loads have landed;
+    //     the reads of the next step's first operands go out right after it,
+    //     covered by the second half of the step's last MFMA group.
+    // Steps are unrolled in pairs so that the double-buffered registers swap
+    // names instead of being copied.
+    auto read_b = [&](uint32_t buf, int s, i32x4 (&bf)[8]) {
+        const uint8_t* bb = wlds + buf * kWdBBytes + r * kWdPitch + 80 * h + 16 * s;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bf[j] = *reinterpret_cast<const i32x4*>(bb + 32 * j * kWdPitch);
+    };
+    auto decode_all = [&](const u32x4 (&av)[2], uint32_t (&dec)[2][20]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int d = 0; d < 20; ++d) dec[i][d] = 0;
+#pragma unroll
+            for (int b = 0; b < 16; ++b) {
+                const uint32_t byte = (av[i][b >> 2] >> (8 * (b & 3))) & 0xffu;
+                splice_trits(dec[i], b, lut_lane[byte * kWdCopies]);
+            }
+        }
+    };
+    // One MFMA group: operands of group s from bc (read one group earlier),
+    // the next group's operands into bn, table reads and splices of the
+    // next step's weight bytes [kBy[s], kBy[s + 1]).
+    // The code loads of step kt + 1 are spread over groups 0 .. 2 (four,
+    // four, three), one after each of the group's first MFMAs: issued as one
+    // burst they stall this wave's instruction stream for the time the vector
+    // memory unit takes to accept them; issued in group 3 they have not
+    // landed by the end of the step.
+    constexpr int kDmaAt[5] = {0, 4, 8, 11, 11};
+    auto mgroup = [&](auto S_, uint32_t kt, const uint32_t (&cur)[2][20], uint32_t (&nxt)[2][20],
+                      const i32x4 (&bc)[8], i32x4 (&bn)[8], const u32x4 (&av)[2]) {
+        constexpr int s = decltype(S_)::value;
+        constexpr int dlo = s < 4 ? kDmaAt[s] : 0, dhi = s < 4 ? kDmaAt[s + 1] : 0;
+        const bool dma = kt + 1 < nkt;
+        constexpr int kBy[6] = {0, 7, 14, 20, 26, 32};
+        constexpr int lo = kBy[s], hi = kBy[s + 1];
+        uint64_t tv[hi - lo];
+#pragma unroll
+        for (int b = lo; b < hi; ++b) {
+            const int i = b >> 4, bi = b & 15;
+            const uint32_t byte = (av[i][bi >> 2] >> (8 * (bi & 3))) & 0xffu;
+            tv[b - lo] = lut_lane[byte * kWdCopies];
+        }
+        if constexpr (s < 4) read_b(kt & 1u, s + 1, bn);
+        __builtin_amdgcn_sched_barrier(0);
+        constexpr int ni = s < 4 ? 2 : 1;
+#pragma unroll
+        for (int i = 0; i < ni; ++i) {
+            const i32x4 af = {(int)cur[i][4 * s], (int)cur[i][4 * s + 1], (int)cur[i][4 * s + 2],
+                              (int)cur[i][4 * s + 3]};
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bc[j], acc[i][j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int b = lo; b < hi; ++b) splice_trits(nxt[b >> 4], b & 15, tv[b - lo]);
+        if (dma) {
+#pragma unroll
+            for (int g = dlo; g < dhi; ++g) dma_one(kt + 1, (kt + 1) & 1u, g);
+        }
+#pragma unroll
+        for (int g = 0; g < 8 * ni; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (g < dhi - dlo) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
+    using S4 = std::integral_constant<int, 4>;
+    auto kstep = [&](uint32_t kt, const uint32_t (&cur)[2][20], uint32_t (&nxt)[2][20], i32x4 (&bx)[8],
+                     i32x4 (&by)[8], const u32x4 (&av)[2], u32x4 (&av2)[2]) {
+        if (kt + 2 < nkt) load_a(kt + 2, av2);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int d = 0; d < 20; ++d) nxt[i][d] = 0;
+        mgroup(S0(), kt, cur, nxt, bx, by, av);
+        mgroup(S1(), kt, cur, nxt, by, bx, av);
+        mgroup(S2(), kt, cur, nxt, bx, by, av);
+        mgroup(S3(), kt, cur, nxt, by, bx, av);
+        mgroup(S4(), kt, cur, nxt, bx, by, av);
+        if (k_tail && kt + 2 == nkt) mask_tail(kt + 1, nxt);
+        // This wave's code loads for step kt + 1 have landed and every wave
+        // is done reading buffer kt & 1 before anyone passes the barrier.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        read_b((kt + 1) & 1u, 0, by);
+        const i32x4 af = {(int)cur[1][16], (int)cur[1][17], (int)cur[1][18], (int)cur[1][19]};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[1][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bx[j], acc[1][j], 0, 0, 0);
+    };
+
+    u32x4 ava[2], avb[2];
+    load_a(0, ava);
+    dma_b(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // table filled, first code tile staged
+    uint32_t cura[2][20], curb[2][20];
+    decode_all(ava, cura);
+    if (k_tail && nkt == 1) mask_tail(0, cura);
+    if (nkt > 1) load_a(1, ava);
+    i32x4 bfx[8], bfy[8];
+    read_b(0, 0, bfx);
+    uint32_t kt = 0;
+    for (; kt + 1 < nkt; kt += 2) {
+        kstep(kt, cura, curb, bfx, bfy, ava, avb);
+        kstep(kt + 1, curb, cura, bfy, bfx, avb, ava);
+    }
+    if (kt < nkt) kstep(kt, cura, curb, bfx, bfy, ava, avb);
+
+    // Epilogue: ((float)acc * sa[m]) * sq[n].  Accumulator register q of lane
+    // l holds row 8 (q / 4) + 4 (l / 32) + q % 4, column l % 32 of its 32 x 32
+    // tile.  Each wave stages one 32-row slab (fragment i) at a time in its
+    // own LDS region (row pitch 264 floats: the two row groups of a write land
+    // on disjoint banks) and writes it back a whole 1 KB output row per store
+    // instruction, 16 bytes per lane.
+    float sqn[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sqn[j] = p.sq[min(n0 + 32 * j + r, p.n - 1u)];
+    constexpr int kEpPitch = 264;
+    float* slab = reinterpret_cast<float*>(wlds) + wave * 32 * kEpPitch;
+    const bool vec_out = (p.n & 3u) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15u) == 0;
+    const uint32_t ncol = n0 + 4 * lane;
+    __syncthreads();  // every wave is done with the code tiles
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t mb = m0 + 64 * wave + 32 * i;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int row = 8 * (q >> 2) + 4 * h + (q & 3);
+            const float sam = p.sa[min(mb + row, p.m - 1u)];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) slab[row * kEpPitch + 32 * j + r] = ((float)acc[i][j][q] * sam) * sqn[j];
+        }
+        __syncthreads();
+        for (int row = 0; row < 32; ++row) {
+            const uint32_t m = mb + row;
+            if (m >= p.m) break;
+            const f32x4 v = *reinterpret_cast<const f32x4*>(slab + row * kEpPitch + 4 * lane);
+            float* crow = p.c + (uint64_t)m * p.n;
+            if (vec_out && ncol + 3 < p.n) {
+                __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(crow + ncol));
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (ncol + u < p.n) crow[ncol + u] = v[u];
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -1399,6 +1696,14 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
             if (nt == 1) hipLaunchKernelGGL((ternary_i8_skinny_kernel<1, false, 8>), g, dim3(8 * kWave), 0, s, p);
             else hipLaunchKernelGGL((ternary_i8_skinny_kernel<2, false, 8>), g, dim3(8 * kWave), 0, s, p);
         }
+        return launch_status();
+    }
+    if (vec && m >= 1024 && n >= 512 && kp % 16 == 0 && aligned16(a_packed) && nk < (1ull << 31)) {
+        // Many output tiles: the wide kernel (one 256 x 256 tile per CU).
+        const uint64_t tiles = ((m + kWdM - 1) / kWdM) * ((n + kWdN - 1) / kWdN);
+        const uint64_t per = (tiles + kXcds - 1) / kXcds;
+        if (per * kXcds > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
+        hipLaunchKernelGGL(ternary_i8_wide_kernel, dim3((uint32_t)(per * kXcds)), dim3(256), kWdLds, s, p);
         return launch_status();
     }
     if (vec) {

@@ -692,6 +692,24 @@ def test_ternary_matmul_i8_small_n(m, n, k):
     assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), "ternary_matmul_i8 small n")
 
 
+@pytest.mark.parametrize("m,n,k", [(1024, 512, 2560), (1100, 700, 1040), (2049, 1000, 800), (1280, 777, 6400),
+                                   (1031, 513, 80)])
+def test_ternary_matmul_i8_wide_tiles(m, n, k):
+    """The wide path (m >= 1024, n >= 512, 16-byte packed rows: 256 x 256
+    tiles, per-lane table decode): whole and ragged tiles, a partial last K
+    step (k % 160 != 0) and a single step; bit-exact against the oracle on
+    arbitrary packed bytes (bytes >= 243 included)."""
+    from inputs import int8_codes, raw_packed
+
+    log(f"ternary_matmul_i8 wide m={m} n={n} k={k}")
+    p = raw_packed(m, k, m + 3 * k)
+    q = int8_codes(n, k, n + 11)
+    sa = normal((m,), 12, 1.0, 0.1)
+    sq = np.abs(normal((n,), 13, 0.02, 0.005))
+    got = down(rocm.rocm_ternary_matmul_i8(DEV, up(p), up(sa), up(q), up(sq), m, n, k), np.float32, (m, n))
+    assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), "ternary_matmul_i8 wide")
+
+
 def test_ternary_matmul_i8_full_size_and_pipeline():
     """BitLinear 2560 -> 6912 on 4096 tokens (the pre-quant config's
     activations): bit-exact against an f64 GEMM of the decoded trits (exact
