@@ -9,7 +9,8 @@ its inputs already resident in HBM.  The headline line is BASELINE configs[1]
 other config is measured the same way and reported under "kernels".
 
 Per workload:
-  * W untimed warmup launches, then K timed launches bracketed by
+  * W untimed warmup launches (continued until 0.1 s of device time has
+    passed, so clocks have settled), then K timed launches bracketed by
     torch.cuda.synchronize(); HIP events recorded on the stream the kernels are
     launched on give the average kernel duration;
   * algorithmic bytes = every input read once + every output written once;
@@ -53,6 +54,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--only", type=str, default="")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-graph", action="store_true",
+                   help="skip the graph-replay timing (profiler runs: only warmup + timed launches dispatch)")
     p.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU work per baseline sample")
     return p.parse_args()
 
@@ -704,27 +707,43 @@ def all_workloads():
 
 
 # ------------------------------------------------------------------ measure
+MIN_WARM_S = 0.1
+
+
 def time_gpu(torch, w: Workload, steps: int, warmup: int):
+    """W warmup launches, continued in batches until at least MIN_WARM_S of
+    device time has passed (clocks settle under a sustained load; a few cold
+    launches of a compute-bound kernel run up to ~15% slower), then the timed
+    launches.  Returns (ms per timed launch, wall seconds, warmup launches)."""
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
-    for i in range(warmup):
-        rc = w.launch(i, sp)
-        if rc != 0:
-            raise RuntimeError(f"{w.name}: launch returned {rc}")
+    n_warm = 0
+    t_warm = time.perf_counter()
+    batch = max(warmup, 1)
+    while True:
+        for _ in range(batch):
+            rc = w.launch(n_warm, sp)
+            if rc != 0:
+                raise RuntimeError(f"{w.name}: launch returned {rc}")
+            n_warm += 1
+        torch.cuda.synchronize()
+        if n_warm >= warmup and time.perf_counter() - t_warm >= MIN_WARM_S:
+            break
+        batch = max(batch, 10)
     torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record(stream)
     for i in range(steps):
-        rc = w.launch(warmup + i, sp)
+        rc = w.launch(n_warm + i, sp)
         if rc != 0:
             raise RuntimeError(f"{w.name}: launch returned {rc}")
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ev_ms = ev0.elapsed_time(ev1)
-    return ev_ms / steps, wall
+    return ev_ms / steps, wall, n_warm
 
 
 def time_graph(torch, w: Workload, per_graph: int = 20, replays: int = 20):
@@ -824,15 +843,16 @@ def main():
         torch.cuda.synchronize()
         steps = args.steps if w.bytes >= (64 << 20) else max(args.steps, 200)
         print(f"[bench] {w.name}: {args.warmup} warmup + {steps} timed launches", file=sys.stderr, flush=True)
-        ms, wall = time_gpu(torch, w, steps, args.warmup)
+        ms, wall, n_warm = time_gpu(torch, w, steps, args.warmup)
         graph_us = None
-        if w.bytes < (16 << 20):  # latency-bound launches: also without host launch overhead
+        if w.bytes < (16 << 20) and not args.no_graph:  # latency-bound launches: also without host launch overhead
             graph_us = round(time_graph(torch, w), 3)
         gbs = w.bytes / (ms * 1e-3) / 1e9
         r = {
             "workload": w.desc, "kernel": w.kernel, "bytes_per_launch": w.bytes, "tokens": w.tokens,
             "kernel_us": round(ms * 1e3, 3), "achieved_gbs": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
-            "ns_per_token": round(ms * 1e6 / w.tokens, 3), "steps": steps, "wall_s": round(wall, 4),
+            "ns_per_token": round(ms * 1e6 / w.tokens, 3), "steps": steps, "warmup_launches": n_warm,
+            "wall_s": round(wall, 4),
             "wall_gbs": round(w.bytes * steps / wall / 1e9, 1),
         }
         if graph_us is not None:

@@ -287,15 +287,20 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     const int lane = t & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
     const int r = lane & 31, h = lane >> 5;
-    // Tile order: block b runs on XCD b % 8; XCD x takes the contiguous range
-    // [x * per, (x + 1) * per) of an n-major tile order, so the workgroups of
-    // one XCD share code tiles in its L2 while the weights stream.
+    // Tile order: block b runs on XCD b % 8 and XCD x takes the contiguous
+    // range [x * per, (x + 1) * per) of a panel order: panels of pw =
+    // ceil(tn / 8) n-tiles, m-major inside a panel.  One XCD then holds about
+    // one panel (its code rows once in its L2), and the workgroups it runs at
+    // the same time share weight rows pairwise instead of each fetching its own.
     const uint32_t tm_n = (p.m + kWdM - 1) / kWdM, tn_n = (p.n + kWdN - 1) / kWdN;
     const uint32_t ntiles = tm_n * tn_n;
     const uint32_t per = (ntiles + kXcds - 1) / kXcds;
     const uint32_t work = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
     if (work >= ntiles) return;  // whole workgroup: no barrier reached yet
-    const uint32_t m0 = (work % tm_n) * kWdM, n0 = (work / tm_n) * kWdN;
+    const uint32_t pw = (tn_n + kXcds - 1) / kXcds;
+    const uint32_t panel = work / (tm_n * pw), within = work % (tm_n * pw);
+    const uint32_t pwid = min(pw, tn_n - panel * pw);
+    const uint32_t m0 = (within / pwid) * kWdM, n0 = (panel * pw + within % pwid) * kWdN;
 
     // Table: entry e, copy c at u64 index e * 32 + c (bank pair 2c).  Thread
     // e fills its entry's copies in a rotated order so that the 64 lanes of a
@@ -371,10 +376,9 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     };
 
     // Software pipeline, per K step kt (buffer kt & 1 holds its code tile):
-    //   * the weights of step kt + 2 are loaded into registers and the code
-    //     tile of step kt + 1 is loaded into the other buffer (freed by the
-    //     barrier that ended step kt - 1), both spread over the first MFMA
-    //     group;
+    //   * the code tile of step kt + 1 is loaded into the other buffer (freed
+    //     by the barrier that ended step kt - 1) over the first three MFMA
+    //     groups, the weights of step kt + 2 into registers before the fourth;
     //   * the weights of step kt + 1 are decoded while the MFMAs of step kt
     //     run; code operands are read one MFMA group ahead;
     //   * a barrier ends the step once this wave's code loads have landed;
@@ -454,7 +458,6 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     using S4 = std::integral_constant<int, 4>;
     auto kstep = [&](uint32_t kt, const uint32_t (&cur)[2][20], uint32_t (&nxt)[2][20], i32x4 (&bx)[8],
                      i32x4 (&by)[8], const u32x4 (&av)[2], u32x4 (&av2)[2]) {
-        if (kt + 2 < nkt) load_a(kt + 2, av2);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -462,6 +465,7 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
         mgroup(S0(), kt, cur, nxt, bx, by, av);
         mgroup(S1(), kt, cur, nxt, by, bx, av);
         mgroup(S2(), kt, cur, nxt, bx, by, av);
+        if (kt + 2 < nkt) load_a(kt + 2, av2);
         mgroup(S3(), kt, cur, nxt, by, bx, av);
         mgroup(S4(), kt, cur, nxt, bx, by, av);
         if (k_tail && kt + 2 == nkt) mask_tail(kt + 1, nxt);
