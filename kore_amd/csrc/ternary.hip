@@ -1340,20 +1340,21 @@ void ternary_f32_pipe_kernel(TernF32Args p) {
     // past the row or past k is replaced when the step is used (a select
     // right after a load would wait for it).  A decoder's 8 bytes of a step
     // come from the three dwords around them (any row alignment), the first
-    // at floor4(address), clamped so that the three end at ceil4 of the
-    // matrix's end (the host launches this kernel for m * kp >= 12 only); the
-    // bytes are then at offset o = address - first dword (o < 4 unless
-    // clamped, and up to 11 for the matrix's last bytes).  Only the dwords
-    // holding the matrix's first and last bytes can reach past it, by at most
-    // 3 bytes that are never used; a dword never spans two pages.
+    // at floor4(address), clamped to the dwords wholly inside the matrix,
+    // [ceil4(start), floor4(end)) (the host launches this kernel for
+    // m * kp >= 20 only, so that span holds at least three dwords); the bytes
+    // are then at offset o = address - first dword.  A step whose bytes reach
+    // into the matrix's partial first or last dword (unaligned matrices only)
+    // reads those bytes one by one instead.
     static_assert(kDecB == 8, "three-dword window");
-    const uintptr_t a_end4 =
-        (reinterpret_cast<uintptr_t>(p.a) + (uintptr_t)p.m * p.kp + 3u) & ~(uintptr_t)3;
+    const uintptr_t a_lo = reinterpret_cast<uintptr_t>(p.a);
+    const uintptr_t a_hi = a_lo + (uintptr_t)p.m * p.kp;
+    const uintptr_t a_lo4 = (a_lo + 3u) & ~(uintptr_t)3, a_hi4 = a_hi & ~(uintptr_t)3;
     auto pb_of = [&](uint32_t s) { return s * (kPfStep / 5) + (uint32_t)(kDecB * d); };
     auto addr_of = [&](uint32_t s) {
         return reinterpret_cast<uintptr_t>(arow) + (pb_of(s) < p.kp ? pb_of(s) : 0u);
     };
-    auto first_of = [&](uintptr_t a) { return min(a & ~(uintptr_t)3, a_end4 - 12u); };
+    auto first_of = [&](uintptr_t a) { return min(max(a & ~(uintptr_t)3, a_lo4), a_hi4 - 12u); };
     uint32_t pk[kPfDepth][3];
     auto load = [&](uint32_t s, int r) {
         const uint32_t* w = reinterpret_cast<const uint32_t*>(first_of(addr_of(s)));
@@ -1400,6 +1401,14 @@ void ternary_f32_pipe_kernel(TernF32Args p) {
                 wd[1] = __builtin_amdgcn_alignbyte(e2, e1, sh);
                 const uint32_t pb = pb_of(s);
                 const uint32_t nvalid = pb < p.kp ? min(p.kp - pb, (uint32_t)kDecB) : 0u;  // step-uniform
+                if (a < a_lo4 || a + nvalid > a_hi4) {  // the matrix's partial first or last dword
+                    const uint8_t* ab = reinterpret_cast<const uint8_t*>(a);
+#pragma unroll
+                    for (int j = 0; j < kDecB; ++j) {
+                        const uint32_t v = (uint32_t)j < nvalid ? ab[j] : kZeroByte;
+                        wd[j / 4] = (wd[j / 4] & ~(0xffu << (8 * (j % 4)))) | (v << (8 * (j % 4)));
+                    }
+                }
                 if (nvalid < (uint32_t)kDecB) {
 #pragma unroll
                     for (int j = 0; j < kDecB; ++j)
@@ -1786,7 +1795,7 @@ extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float*
     // against 127 us; at aligned K = 2560 the two are even at 8 columns).
     const bool rows_aligned = kp % 16 == 0 && aligned16(a_packed);
     const uint64_t pipe_blocks = ((m + kWave - 1) / kWave) * ((n + 7) / 8);
-    if ((n <= 4 || (!rows_aligned && (n <= 8 || pipe_blocks <= 512))) && k > 0 && mkp >= 12) {
+    if ((n <= 4 || (!rows_aligned && (n <= 8 || pipe_blocks <= 512))) && k > 0 && mkp >= 20) {
         const dim3 gp((uint32_t)((m + kWave - 1) / kWave), (uint32_t)(n <= 4 ? 1 : (n + 7) / 8));
         if (n == 1) hipLaunchKernelGGL(ternary_f32_pipe_kernel<1>, gp, dim3((kPfDec + 1) * kWave), 0, s, p);
         else if (n == 2) hipLaunchKernelGGL(ternary_f32_pipe_kernel<2>, gp, dim3((kPfDec + 2) * kWave), 0, s, p);

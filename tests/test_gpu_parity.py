@@ -907,6 +907,26 @@ def test_ternary_matmul_f32_edges():
         assert_bitexact(got, oracle.ternary_matmul(p, sa, b, m, n, k), f"ternary_matmul_f32 unaligned b n={n}")
 
 
+@pytest.mark.parametrize("off", [1, 2, 3])
+@pytest.mark.parametrize("m,n,k", [(4, 1, 25), (5, 2, 21), (37, 1, 333), (9, 4, 241), (300, 1, 1203)])
+def test_ternary_matmul_f32_packed_at_byte_offsets(off, m, n, k):
+    """The one-to-four-column kernel reads a step's packed bytes as three
+    dwords around them; on a matrix that starts or ends inside a dword the
+    steps touching those partial dwords read their bytes one by one, so
+    nothing outside [a_packed, a_packed + m * kp) is read.  The matrix sits
+    at byte offset off and ends at the end of its tensor."""
+    from inputs import raw_packed
+
+    log(f"ternary_matmul_f32 packed at +{off} m={m} n={n} k={k}")
+    p = raw_packed(m, k, 7 * m + k + off)
+    t = torch.empty(off + p.size, dtype=torch.uint8, device="cuda")
+    t[off:].copy_(torch.from_numpy(p.ravel()))
+    sa, b = normal((m,), 8), normal((k, n), 9)
+    got = down(rocm.rocm_ternary_matmul_f32(DEV, HipBuffer.from_tensor(t[off:]), up(sa), up(b), m, n, k),
+               np.float32, (m, n))
+    assert_bitexact(got, oracle.ternary_matmul(p, sa, b, m, n, k), f"ternary_matmul_f32 packed at +{off}")
+
+
 def test_decode_chain_graph_replays_match_eager():
     """A decode step's launches (pre-quant, the BitLinear matmul on its codes
     -- the split-K path's zero/finish kernels included at 64 tokens -- the
