@@ -710,6 +710,28 @@ def test_ternary_matmul_i8_wide_tiles(m, n, k):
     assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), "ternary_matmul_i8 wide")
 
 
+def test_ternary_matmul_i8_wide_tiles_unaligned_output():
+    """The wide path with an output 4 bytes past a 16-byte boundary (n % 4 ==
+    0): its epilogue stores element by element instead of 16-byte rows."""
+    from inputs import int8_codes, raw_packed
+
+    m, n, k = 1100, 704, 1040
+    log(f"ternary_matmul_i8 wide unaligned c m={m} n={n} k={k}")
+    lib = __import__("kore_amd._lib", fromlist=["load"]).load()
+    p = raw_packed(m, k, 17)
+    q = int8_codes(n, k, 18)
+    sa = normal((m,), 19, 1.0, 0.1)
+    sq = np.abs(normal((n,), 20, 0.02, 0.005))
+    bp, bs, bq, bsq = up(p), up(sa), up(q), up(sq)
+    t = torch.full((m * n + 1,), float("nan"), dtype=torch.float32, device="cuda")
+    rc = lib.kore_hip_ternary_matmul_i8(bp.ptr, bs.ptr, bq.ptr, bsq.ptr, t[1:].data_ptr(), m, n, k, None)
+    torch.cuda.synchronize()
+    assert rc == 0
+    got = t[1:].cpu().numpy().reshape(m, n)
+    assert np.isnan(t[0].item())
+    assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), "ternary_matmul_i8 wide unaligned c")
+
+
 def test_ternary_matmul_i8_full_size_and_pipeline():
     """BitLinear 2560 -> 6912 on 4096 tokens (the pre-quant config's
     activations): bit-exact against an f64 GEMM of the decoded trits (exact
