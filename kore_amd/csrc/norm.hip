@@ -246,6 +246,33 @@ __device__ __forceinline__ uint32_t seg_scan(uint32_t v) {
     return v;
 }
 
+// Segmented inclusive scan composing run entries with the 2-state parity
+// automaton: (i0, i1) are a span's exact increments in grid units for entry
+// parity 0 / 1, so its exit parity is (p + i_p) & 1, and the span x followed
+// by the span y has increments x_p + y_(exit parity of x).  The head flag
+// (the span already reaches its run's end) rides in bit 31 of i0.  Lanes
+// without a DPP source read (0, 0), the identity.  Lane L combines with the
+// lane below it, which holds a later segment.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ void auto_scan_step(uint32_t& a, uint32_t& b) {
+    const uint32_t la = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a, kCtrl, kRowMask, 0xf, false);
+    const uint32_t lb = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)b, kCtrl, kRowMask, 0xf, false);
+    if ((int32_t)a >= 0) {
+        const uint32_t y0 = la & 0x7fffffffu;
+        const uint32_t na = a + ((a & 1u) ? lb : y0);
+        b = b + (((b + 1u) & 1u) ? lb : y0);
+        a = na | (la & 0x80000000u);
+    }
+}
+__device__ __forceinline__ void auto_scan(uint32_t& a, uint32_t& b) {
+    auto_scan_step<0x111, 0xf>(a, b);  // row_shr:1
+    auto_scan_step<0x112, 0xf>(a, b);  // row_shr:2
+    auto_scan_step<0x114, 0xf>(a, b);  // row_shr:4
+    auto_scan_step<0x118, 0xf>(a, b);  // row_shr:8
+    auto_scan_step<0x142, 0xa>(a, b);  // row_bcast:15 -> rows 1, 3
+    auto_scan_step<0x143, 0xc>(a, b);  // row_bcast:31 -> rows 2, 3
+}
+
 // Vector path: cols % 4 == 0, x/w/y 16-byte aligned, q 4-byte aligned,
 // ceil(cols/4 / 64) <= SL4.  Segment j covers float4 [j*SL4, (j+1)*SL4).
 // Grid: one block per WPB rows (one row per wave); dynamic LDS =
@@ -393,17 +420,32 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
     // A valid segment with inc0 != inc1 is a run of its own whose entry keeps
     // both increments.
     const bool simple = valid && inc0 == inc1;
-    // Runs: maximal spans of simple segments with one binade key; any other
-    // segment is a run of its own.  This lane's segment ends its run when
-    // the next segment (lane - 1, moved here by wave_shr:1) has another key.
-    const int key_me = empty ? 1024 : (seg_id == 0 ? 1025 : (simple ? (int)ef : 2048 + seg_id));
+    // Runs: maximal spans of segments with one binade key; any other segment
+    // is a run of its own.  With many rows a run holds the simple segments
+    // only, composed by a segmented sum (a light scan: four rows share each
+    // SIMD and compete for issue); with one row per workgroup (launches of
+    // few rows, bound by each row's chain) it holds every valid segment,
+    // composed by the parity automaton, for fewer resolve steps.  This lane's
+    // segment ends its run when the next segment (lane - 1, moved here by
+    // wave_shr:1) has another key.
+    constexpr bool kAuto = WPB == 1;
+    const bool in_run = kAuto ? valid : simple;
+    const int key_me = empty ? 1024 : (seg_id == 0 ? 1025 : (in_run ? (int)ef : 2048 + seg_id));
     const int key_next = __builtin_amdgcn_update_dpp(key_me, key_me, 0x138, 0xf, 0xf, false);
     const bool ends_here = lane == 0 || key_next != key_me;
     const uint64_t ends = __ballot(ends_here);
-    // Run increment from this segment to the run's end: a segmented sum over
-    // lanes (a forward scan adds the later segments, held by lower lanes).
-    const uint32_t run_sum =
-        seg_scan((simple ? inc0 : 0u) | (ends_here ? 0x80000000u : 0u)) & 0x7fffffffu;
+    // Run increments from this segment to the run's end (a forward scan
+    // composes the later segments, held by lower lanes).
+    uint32_t run_i0, run_i1;
+    if (kAuto) {
+        run_i0 = (valid ? inc0 : 0u) | (ends_here ? 0x80000000u : 0u);
+        run_i1 = valid ? inc1 : 0u;
+        auto_scan(run_i0, run_i1);
+        run_i0 &= 0x7fffffffu;
+    } else {
+        run_i0 = seg_scan((simple ? inc0 : 0u) | (ends_here ? 0x80000000u : 0u)) & 0x7fffffffu;
+        run_i1 = run_i0;
+    }
     // The run of lane L ends at the highest lane <= L with its bit set; the
     // segment after it is 64 - that lane.
     const uint64_t below = ends & (lt_mask | (1ull << lane));
@@ -417,8 +459,8 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
     // runs whose increment reaches a whole binade (no start could stay
     // inside it), and invalid segments are not jumpable: the resolve folds
     // them.
-    const int32_t delta = simple ? 0 : (int32_t)(inc1 - inc0);
-    const uint32_t e_inc = simple ? run_sum : inc0;
+    const int32_t delta = kAuto ? (int32_t)(run_i1 - run_i0) : (simple ? 0 : (int32_t)(inc1 - inc0));
+    const uint32_t e_inc = kAuto || simple ? run_i0 : inc0;
     const bool jumpable = valid && delta >= -64 && delta < 64 && e_inc < 0x800000u;
     const uint32_t e_w0 = (e_inc & 0xffffffu) | (ef << 24);
     const uint32_t e_w1 = next_seg | (((uint32_t)delta & 0x7fu) << 8) | (jumpable ? 0x8000u : 0u);

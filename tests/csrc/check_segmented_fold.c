@@ -186,7 +186,14 @@ static long rfb = 0;
  * only when valid, outside the merged range [0, 2^-125), with
  * |inc1 - inc0| < 64 and an increment below 2^23; others (width 0) are
  * folded alone from s. */
-static float run_fold(const float *a, int n, long *steps) {
+/* automaton = 0: runs of "simple" segments (both walks give one increment)
+ * composed by adding increments -- the kernel for launches of more than a
+ * few rows.  automaton = 1: runs of every valid segment of one binade,
+ * composed by the 2-state parity automaton over integer increments (parity
+ * after a span with entry parity p is (p + inc_p) & 1) -- the kernel for
+ * launches of a few rows, where fewer resolve steps matter more than the
+ * heavier scan. */
+static float run_fold_k(const float *a, int n, long *steps, int automaton) {
     const int n4 = n / 4;
     const int sl4 = (n4 + 63) / 64 ? (n4 + 63) / 64 : 1;
     const int nsubper = 1;
@@ -239,15 +246,30 @@ static float run_fold(const float *a, int n, long *steps) {
         wd[u] = f2u(top) - f2u(bot);
         efs[u] = ef;
     }
-    (void)efs;
-    uint32_t run = 0;
+    uint32_t run = 0, r0 = 0, r1 = 0;
+    for (int u = U - 1; u >= 0; --u) {
+        if (automaton) {
+            int empty = u >= nsub;
+            rkey[u] = empty ? 1024 : (u == 0 ? 1025 : (valid[u] ? (int)efs[u] : 2048 + u));
+        }
+    }
     for (int u = U - 1; u >= 0; --u) {
         int end_here = (u == U - 1) || rkey[u + 1] != rkey[u];
-        uint32_t own = simple[u] ? inc0[u] : 0u;
-        run = end_here ? own : own + run;
         next[u] = end_here ? u + 1 : next[u + 1];
-        I0[u] = simple[u] ? run : inc0[u];
-        I1[u] = simple[u] ? run : inc1[u];
+        if (automaton) {
+            /* x = this segment, y = the rest of its run */
+            uint32_t x0 = valid[u] ? inc0[u] : 0u, x1 = valid[u] ? inc1[u] : 0u;
+            uint32_t y0 = end_here ? 0u : r0, y1 = end_here ? 0u : r1;
+            r0 = x0 + ((x0 & 1u) ? y1 : y0);
+            r1 = x1 + (((1u + x1) & 1u) ? y1 : y0);
+            I0[u] = r0;
+            I1[u] = r1;
+        } else {
+            uint32_t own = simple[u] ? inc0[u] : 0u;
+            run = end_here ? own : own + run;
+            I0[u] = simple[u] ? run : inc0[u];
+            I1[u] = simple[u] ? run : inc1[u];
+        }
         {   /* jumpable: valid, |inc1 - inc0| < 64, entry increment below 2^23 */
             int32_t dl = (int32_t)(I1[u] - I0[u]);
             if (!(valid[u] && dl >= -64 && dl < 64 && I0[u] < 0x800000u)) wd[u] = 0u;
@@ -270,6 +292,10 @@ static float run_fold(const float *a, int n, long *steps) {
     }
     return u2f(s);
 }
+
+static float run_fold(const float *a, int n, long *steps) { return run_fold_k(a, n, steps, 0); }
+static long asteps = 0;
+static float run_fold_auto(const float *a, int n) { return run_fold_k(a, n, &asteps, 1); }
 
 static uint64_t rs = 88172645463325252ull;
 static uint64_t xr(void) { rs ^= rs << 13; rs ^= rs >> 7; rs ^= rs << 17; return rs; }
@@ -298,6 +324,11 @@ static int check(const float *a, int n, int K, long *fb, const char *what, long 
         float r3 = run_fold(a, n, &rsteps);
         if (f2u(r0) != f2u(r3) && !(r0 != r0 && r3 != r3)) {
             printf("MISMATCH run_fold %s row %ld n=%d: seq=%a run=%a\n", what, row, n, r0, r3);
+            return 1;
+        }
+        float r4 = run_fold_auto(a, n);
+        if (f2u(r0) != f2u(r4) && !(r0 != r0 && r4 != r4)) {
+            printf("MISMATCH run_fold (automaton runs) %s row %ld n=%d: seq=%a run=%a\n", what, row, n, r0, r4);
             return 1;
         }
     }
@@ -338,6 +369,7 @@ int main(int argc, char **argv) {
     }
     printf("ok: %ld rows, fallback segments %ld of %ld; kernel mirror: %ld rows, %.2f fallbacks/row\n", rows, fb,
            total_segs, krows, krows ? (double)kfb / krows : 0.0);
-    printf("run-jumping resolve: %.2f steps/row, %.2f fallbacks/row\n", krows ? (double)rsteps / krows : 0.0, krows ? (double)rfb / krows : 0.0);
+    printf("run-jumping resolve: %.2f steps/row, %.2f fallbacks/row; automaton runs: %.2f steps/row\n",
+           krows ? (double)rsteps / krows : 0.0, krows ? (double)rfb / krows : 0.0, krows ? (double)asteps / krows : 0.0);
     return 0;
 }
