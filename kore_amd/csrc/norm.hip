@@ -92,11 +92,16 @@ struct NormArgs {
 // Transpose tile geometry.  Segment j (SL4 consecutive float4 of the row)
 // starts at float4 j*P of the tile, with an odd pitch P: 16 lanes reading
 // float4 k of 16 consecutive segments then hit 16 distinct 16-byte bank
-// groups.  For even SL4 the tile holds half a row (32 segments = SL4/2 whole
-// load chunks) and is filled in two passes; SL4 = 1 takes one pass.
+// groups.  For even SL4 with four waves per workgroup the tile holds half a
+// row (32 segments = SL4/2 whole load chunks) and is filled in two passes;
+// odd SL4, and one wave per workgroup (launches of few rows, where LDS is
+// plentiful and the second pass's round trip is on the row's chain), take
+// one pass.
 __host__ __device__ constexpr int seg_pitch4(int sl4) { return (sl4 & 1) ? sl4 : sl4 + 1; }
-__host__ __device__ constexpr int tile_segs(int sl4) { return (sl4 & 1) ? kSegs : kSegs / 2; }
-__host__ __device__ constexpr uint32_t wave_lds_f4(int sl4) { return (uint32_t)(tile_segs(sl4) * seg_pitch4(sl4)); }
+__host__ __device__ constexpr int tile_segs(int sl4, int wpb) { return (sl4 & 1) || wpb == 1 ? kSegs : kSegs / 2; }
+__host__ __device__ constexpr uint32_t wave_lds_f4(int sl4, int wpb) {
+    return (uint32_t)(tile_segs(sl4, wpb) * seg_pitch4(sl4));
+}
 
 
 __device__ __forceinline__ int32_t cvt_i32_sat(float v) {
@@ -276,7 +281,7 @@ __device__ __forceinline__ void auto_scan(uint32_t& a, uint32_t& b) {
 // Vector path: cols % 4 == 0, x/w/y 16-byte aligned, q 4-byte aligned,
 // ceil(cols/4 / 64) <= SL4.  Segment j covers float4 [j*SL4, (j+1)*SL4).
 // Grid: one block per WPB rows (one row per wave); dynamic LDS =
-// WPB * wave_lds_f4(SL4) float4 (the transpose tiles).
+// WPB * wave_lds_f4(SL4, WPB) float4 (the transpose tiles).
 // silu(z) = z / (1 + e^-z) from the hardware exp2 and reciprocal (5 VALU
 // instead of ~25 for expf + IEEE division).  Error: v_exp_f32 and v_rcp_f32
 // are 1 ulp each; rounding z*log2(e) to f32 perturbs e^-z by |z|*2^-24*ln2
@@ -310,10 +315,10 @@ template <NormOut Out, int SL4, bool FULL, int WPB>
 __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
     constexpr int NCH = SL4;  // 64*SL4 float4 cover the row: SL4 wave-wide chunks
     constexpr int P = seg_pitch4(SL4);
-    constexpr int TS = tile_segs(SL4);
+    constexpr int TS = tile_segs(SL4, WPB);
     constexpr int NPASS = kSegs / TS;
     constexpr int CPP = NCH / NPASS;  // load chunks per tile pass
-    constexpr uint32_t kWaveF4 = wave_lds_f4(SL4);
+    constexpr uint32_t kWaveF4 = wave_lds_f4(SL4, WPB);
     extern __shared__ f32x4 lds4[];
     const int lane = threadIdx.x & (kWave - 1);
     // Wave index as a scalar: row addresses then live in SGPRs and every
@@ -652,7 +657,7 @@ __global__ __launch_bounds__(64) void row_norm_scalar_kernel(NormArgs args) {
 
 template <NormOut Out, int SL4, int WPB>
 static int launch_vec_wpb(NormArgs a, hipStream_t s) {
-    const size_t lds = (size_t)WPB * wave_lds_f4(SL4) * sizeof(f32x4);
+    const size_t lds = (size_t)WPB * wave_lds_f4(SL4, WPB) * sizeof(f32x4);
     const uint64_t blocks = (a.rows + WPB - 1) / WPB;
     if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
     if (a.cols == (uint32_t)(4 * kWave * SL4))
