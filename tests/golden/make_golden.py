@@ -62,6 +62,25 @@ def cases():
     ids[3], ids[7], ids[11] = 50, -1, 2**31  # out of range: zero rows
     c["embedding"] = ("embedding", {}, {"table": table, "ids": ids.astype(np.uint32)},
                       lambda i, p: {"out": oracle.embedding(i["table"], i["ids"])})
+    fids = np.array([0.0, 2.0, 1.0, np.nan, -1.5, 0.9, 1e30, 49.0, 50.0, 51.0, 49.99, -0.0, np.inf, -np.inf,
+                     7.7, 3.0], np.float32)  # Rust `as usize`: NaN and < 1 -> row 0, >= vocab -> zero row
+    c["embedding_forward"] = ("embedding_forward", {}, {"table": table, "ids": fids},
+                              lambda i, p: {"out": oracle.embedding_forward(i["table"], i["ids"])})
+    # many rows: the four-waves-per-workgroup kernels (simple-segment runs)
+    x, g = rmsnorm_inputs(264, 128, 24)
+    c["rms_norm_264x128"] = ("rms_norm", {"eps": 1e-6}, {"x": x, "g": g},
+                             lambda i, p: {"y": oracle.rms_norm(i["x"], i["g"], p["eps"])})
+    x, g = prequant_inputs(264, 256, 25)
+    c["rms_norm_quant_i8_264x256"] = ("rms_norm_quant_i8", {"eps": 1e-6}, {"x": x, "g": g},
+                                      lambda i, p: dict(zip(("q", "scale"),
+                                                            oracle.rms_norm_quant_i8(i["x"], i["g"], p["eps"]))))
+    w = normal((7, 333), 26, 0.0, 0.05)
+    w[2] = 0.0                    # all-zero row: the scale guard
+    w[4, 5] = np.nan              # NaN dropped from the row max, a NaN quotient packs as zero
+    w[5] *= np.float32(1e-9)      # absmax below 1e-8
+    c["pack_weights_ternary"] = ("pack_weights_ternary", {"threshold": 0.5}, {"w": w},
+                                 lambda i, p: dict(zip(("packed", "scales"),
+                                                       oracle.pack_weights_ternary(i["w"], p["threshold"]))))
     lg = normal((4, 1000), 12) * np.float32(3.0)
     c["softmax"] = ("softmax", {}, {"x": lg}, lambda i, p: {"y": oracle.softmax(i["x"])})
     c["softmax_causal"] = ("softmax_causal", {"offset": 2}, {"x": normal((6, 16), 13)},

@@ -126,6 +126,16 @@ def test_hip_path_reproduces_golden():
             n = i["ids"].size
             out = rocm.rocm_embedding_f32(0, up(i["table"]), up(i["ids"]), n, v, d)
             assert_bitexact(down(out, np.float32, (n, d)), o["out"], name)
+        elif op == "embedding_forward":
+            v, d = i["table"].shape
+            n = i["ids"].size
+            out = rocm.rocm_embedding_forward_f32(0, up(i["table"]), up(i["ids"]), n, v, d)
+            assert_bitexact(down(out, np.float32, (n, d)), o["out"], name)
+        elif op == "pack_weights_ternary":
+            m, k = i["w"].shape
+            pk, sc = rocm.rocm_pack_weights_ternary(0, up(i["w"]), m, k, p["threshold"])
+            assert_bitexact(down(pk, np.uint8, o["packed"].shape), o["packed"], name)
+            assert_bitexact(down(sc, np.float32, (m,)), o["scales"], name)
         elif op in ("softmax", "softmax_causal"):
             r, c = i["x"].shape
             y = (rocm.rocm_softmax_f32(0, up(i["x"]), r, c) if op == "softmax"
