@@ -40,9 +40,10 @@
 //   * its squares pass through a wave-private LDS tile (half a row at a time)
 //     to put segment j into lane 63 - j (odd float4 pitch: conflict-free
 //     ds_read_b128);
-//   * runs of segments in one binade are composed by a segmented DPP scan, so
-//     each lane holds its segment's run entry (d_0, d_1, window, next
-//     segment) and its squares in registers;
+//   * runs of segments in one binade are composed by a segmented DPP scan
+//     (the parity automaton over integer increments), so each lane holds
+//     its segment's run entry (increments for both entry parities, binade,
+//     next segment) and its squares in registers;
 //   * the resolve runs on the scalar unit in integers: inside one binade the
 //     float bits are linear in the value, so a run's exact increment is an
 //     integer added to the bits of the running sum, and the binade window
@@ -230,27 +231,6 @@ __device__ __forceinline__ float wave_incl_scan(float v) {
     return v;
 }
 
-// Segmented inclusive scan over lanes of u32 values whose bit 31 marks a
-// lane that starts a segment (in lane order).  Lane L adds the value of lane
-// L - k unless its own partial already reached a segment start; the start
-// flag travels with the sum, so a lane stops accumulating once its partial
-// covers one.  Lanes without a DPP source read 0.  Used for run increments
-// in grid units: below 2^24 per segment, so 64 of them never reach bit 31.
-template <int kCtrl, int kRowMask>
-__device__ __forceinline__ uint32_t seg_scan_step(uint32_t v) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, kRowMask, 0xf, false);
-    return (int32_t)v < 0 ? v : v + lo;
-}
-__device__ __forceinline__ uint32_t seg_scan(uint32_t v) {
-    v = seg_scan_step<0x111, 0xf>(v);  // row_shr:1
-    v = seg_scan_step<0x112, 0xf>(v);  // row_shr:2
-    v = seg_scan_step<0x114, 0xf>(v);  // row_shr:4
-    v = seg_scan_step<0x118, 0xf>(v);  // row_shr:8
-    v = seg_scan_step<0x142, 0xa>(v);  // row_bcast:15 -> rows 1, 3
-    v = seg_scan_step<0x143, 0xc>(v);  // row_bcast:31 -> rows 2, 3
-    return v;
-}
-
 // Segmented inclusive scan composing run entries with the 2-state parity
 // automaton: (i0, i1) are a span's exact increments in grid units for entry
 // parity 0 / 1, so its exit parity is (p + i_p) & 1, and the span x followed
@@ -419,38 +399,22 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
     // above sig0 = bot.  Meaningful for valid segments only.
     const uint32_t inc0 = __float_as_uint(w0) - __float_as_uint(bot);
     const uint32_t inc1 = __float_as_uint(w1) - __float_as_uint(bot) - 1u;
-    // A valid segment whose two walks agree (no tie broke differently) maps
-    // every start s in the binade to s + inc, whatever its parity: such
-    // "simple" segments of one binade compose by adding their increments.
-    // A valid segment with inc0 != inc1 is a run of its own whose entry keeps
-    // both increments.
-    const bool simple = valid && inc0 == inc1;
-    // Runs: maximal spans of segments with one binade key; any other segment
-    // is a run of its own.  With many rows a run holds the simple segments
-    // only, composed by a segmented sum (a light scan: four rows share each
-    // SIMD and compete for issue); with one row per workgroup (launches of
-    // few rows, bound by each row's chain) it holds every valid segment,
-    // composed by the parity automaton, for fewer resolve steps.  This lane's
-    // segment ends its run when the next segment (lane - 1, moved here by
-    // wave_shr:1) has another key.
-    constexpr bool kAuto = WPB == 1;
-    const bool in_run = kAuto ? valid : simple;
-    const int key_me = empty ? 1024 : (seg_id == 0 ? 1025 : (in_run ? (int)ef : 2048 + seg_id));
+    // Runs: maximal spans of valid segments with one binade key, composed by
+    // the parity automaton; any other segment is a run of its own.  (Runs of
+    // only the segments whose two walks agree, composed by a plain integer
+    // sum, make a lighter scan but more resolve steps: measured slower at
+    // every size.)  This lane's segment ends its run when the next segment
+    // (lane - 1, moved here by wave_shr:1) has another key.
+    const int key_me = empty ? 1024 : (seg_id == 0 ? 1025 : (valid ? (int)ef : 2048 + seg_id));
     const int key_next = __builtin_amdgcn_update_dpp(key_me, key_me, 0x138, 0xf, 0xf, false);
     const bool ends_here = lane == 0 || key_next != key_me;
     const uint64_t ends = __ballot(ends_here);
     // Run increments from this segment to the run's end (a forward scan
     // composes the later segments, held by lower lanes).
-    uint32_t run_i0, run_i1;
-    if (kAuto) {
-        run_i0 = (valid ? inc0 : 0u) | (ends_here ? 0x80000000u : 0u);
-        run_i1 = valid ? inc1 : 0u;
-        auto_scan(run_i0, run_i1);
-        run_i0 &= 0x7fffffffu;
-    } else {
-        run_i0 = seg_scan((simple ? inc0 : 0u) | (ends_here ? 0x80000000u : 0u)) & 0x7fffffffu;
-        run_i1 = run_i0;
-    }
+    uint32_t run_i0 = (valid ? inc0 : 0u) | (ends_here ? 0x80000000u : 0u);
+    uint32_t run_i1 = valid ? inc1 : 0u;
+    auto_scan(run_i0, run_i1);
+    run_i0 &= 0x7fffffffu;
     // The run of lane L ends at the highest lane <= L with its bit set; the
     // segment after it is 64 - that lane.
     const uint64_t below = ends & (lt_mask | (1ull << lane));
@@ -460,12 +424,12 @@ __global__ __launch_bounds__(kWave * WPB) void row_norm_kernel(NormArgs args) {
     //           top never reaches 2^23) | exponent field of the binade << 24;
     //   word 1: segment after the run | parity-1 increment minus parity-0
     //           increment (7-bit signed) << 8 | jumpable << 15.
-    // Two-walk segments whose increments differ by 64 grid steps or more,
-    // runs whose increment reaches a whole binade (no start could stay
+    // Runs whose parity-0 and parity-1 increments differ by 64 grid steps or
+    // more, runs whose increment reaches a whole binade (no start could stay
     // inside it), and invalid segments are not jumpable: the resolve folds
     // them.
-    const int32_t delta = kAuto ? (int32_t)(run_i1 - run_i0) : (simple ? 0 : (int32_t)(inc1 - inc0));
-    const uint32_t e_inc = kAuto || simple ? run_i0 : inc0;
+    const int32_t delta = (int32_t)(run_i1 - run_i0);
+    const uint32_t e_inc = run_i0;
     const bool jumpable = valid && delta >= -64 && delta < 64 && e_inc < 0x800000u;
     const uint32_t e_w0 = (e_inc & 0xffffffu) | (ef << 24);
     const uint32_t e_w1 = next_seg | (((uint32_t)delta & 0x7fu) << 8) | (jumpable ? 0x8000u : 0u);

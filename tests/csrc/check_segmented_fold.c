@@ -186,13 +186,12 @@ static long rfb = 0;
  * only when valid, outside the merged range [0, 2^-125), with
  * |inc1 - inc0| < 64 and an increment below 2^23; others (width 0) are
  * folded alone from s. */
-/* automaton = 0: runs of "simple" segments (both walks give one increment)
- * composed by adding increments -- the kernel for launches of more than a
- * few rows.  automaton = 1: runs of every valid segment of one binade,
- * composed by the 2-state parity automaton over integer increments (parity
- * after a span with entry parity p is (p + inc_p) & 1) -- the kernel for
- * launches of a few rows, where fewer resolve steps matter more than the
- * heavier scan. */
+/* automaton = 1 mirrors the kernel: runs of every valid segment of one
+ * binade, composed by the 2-state parity automaton over integer increments
+ * (parity after a span with entry parity p is (p + inc_p) & 1).
+ * automaton = 0 is an alternative kept as a second check of the resolve:
+ * runs of only the segments whose two walks give one increment, composed by
+ * adding increments. */
 static float run_fold_k(const float *a, int n, long *steps, int automaton) {
     const int n4 = n / 4;
     const int sl4 = (n4 + 63) / 64 ? (n4 + 63) / 64 : 1;
@@ -293,9 +292,9 @@ static float run_fold_k(const float *a, int n, long *steps, int automaton) {
     return u2f(s);
 }
 
-static float run_fold(const float *a, int n, long *steps) { return run_fold_k(a, n, steps, 0); }
+static float run_fold(const float *a, int n, long *steps) { return run_fold_k(a, n, steps, 1); }
 static long asteps = 0;
-static float run_fold_auto(const float *a, int n) { return run_fold_k(a, n, &asteps, 1); }
+static float run_fold_simple(const float *a, int n) { return run_fold_k(a, n, &asteps, 0); }
 
 static uint64_t rs = 88172645463325252ull;
 static uint64_t xr(void) { rs ^= rs << 13; rs ^= rs >> 7; rs ^= rs << 17; return rs; }
@@ -326,9 +325,9 @@ static int check(const float *a, int n, int K, long *fb, const char *what, long 
             printf("MISMATCH run_fold %s row %ld n=%d: seq=%a run=%a\n", what, row, n, r0, r3);
             return 1;
         }
-        float r4 = run_fold_auto(a, n);
+        float r4 = run_fold_simple(a, n);
         if (f2u(r0) != f2u(r4) && !(r0 != r0 && r4 != r4)) {
-            printf("MISMATCH run_fold (automaton runs) %s row %ld n=%d: seq=%a run=%a\n", what, row, n, r0, r4);
+            printf("MISMATCH run_fold (simple-segment runs) %s row %ld n=%d: seq=%a run=%a\n", what, row, n, r0, r4);
             return 1;
         }
     }
@@ -369,7 +368,7 @@ int main(int argc, char **argv) {
     }
     printf("ok: %ld rows, fallback segments %ld of %ld; kernel mirror: %ld rows, %.2f fallbacks/row\n", rows, fb,
            total_segs, krows, krows ? (double)kfb / krows : 0.0);
-    printf("run-jumping resolve: %.2f steps/row, %.2f fallbacks/row; automaton runs: %.2f steps/row\n",
+    printf("run-jumping resolve (as the kernel): %.2f steps/row, %.2f fallbacks/row; simple-segment runs: %.2f steps/row\n",
            krows ? (double)rsteps / krows : 0.0, krows ? (double)rfb / krows : 0.0, krows ? (double)asteps / krows : 0.0);
     return 0;
 }
