@@ -232,7 +232,7 @@ static float run_fold_k(const float *a, int n, long *steps, int automaton) {
         float w0 = sig0, w1 = sig1;
         for (int i = u * sl; i < u * sl + sl; ++i) { float v = i < n ? a[i] : 0.0f; w0 = w0 + v; w1 = w1 + v; }
         w0s[u] = w0;
-        int edge = est[u] < bot * 1.0009765625f || est[u] + ssub[u] >= top * 0.9990234375f;
+        int edge = est[u] < bot * 1.0001220703125f || est[u] + ssub[u] >= top * 0.9998779296875f;
         valid[u] = !first && !subn && w0 < top && w1 < top && !edge && !bad;
         inc0[u] = f2u(w0) - f2u(bot);
         inc1[u] = f2u(w1) - f2u(bot) - 1u;
