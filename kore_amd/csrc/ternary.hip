@@ -255,10 +255,13 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
 //   * Codes reach LDS by direct global -> LDS loads (no registers), into a
 //     double-buffered tile with a 176-byte row pitch (16 lanes reading 16
 //     bytes of 16 consecutive rows hit 16 distinct bank groups); the tile of
-//     step kt + 2 is loaded while step kt computes; one barrier per step.
-//     Code rows past n are clamped to row n - 1 (their outputs are not
-//     stored); columns past k are clamped to the step's first 16 bytes and
-//     the weights' trits there are zeroed instead.
+//     step kt + 1 is loaded into the other buffer during step kt's first
+//     MFMA groups; one barrier per step.  Code rows past n are clamped to
+//     row n - 1 (their outputs are not stored); columns past k are clamped
+//     to the step's first 16 bytes and the weights' trits there are zeroed
+//     instead.
+//   * The output tile leaves through LDS, 32 rows of a wave at a time, as
+//     whole 1 KB rows per store instruction.
 // LDS traffic per MFMA is ~0.7 KB (operand reads 0.5, table reads 0.2)
 // against the ~1 KB one CU delivers per MFMA of each of its four SIMDs.
 constexpr int kWdM = 256, kWdN = 256;
