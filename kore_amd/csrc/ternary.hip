@@ -265,6 +265,11 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
 // LDS traffic per MFMA is ~0.7 KB (operand reads 0.5, table reads 0.2)
 // against the ~1 KB one CU delivers per MFMA of each of its four SIMDs.
 constexpr int kWdM = 256, kWdN = 256;
+// The wide kernel runs one workgroup per CU; below ~3/4 of MI355X's 256 CUs in
+// 256 x 256 tiles the 128 x 128 kernel (more, smaller workgroups) is faster:
+// measured 1024 x 512 x 2560 19.3 vs 39.8 us, 4096 x 2048 38.5 vs 44.3 us, and
+// 6912 x 2048 (216 tiles) 73.7 vs 49.7 us.
+constexpr uint64_t kWdMinTiles = 192;
 constexpr int kWdPitch = 176;
 constexpr int kWdCopies = 32;
 constexpr size_t kWdBBytes = (size_t)kWdN * kWdPitch;           // one code buffer
@@ -1714,9 +1719,10 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
         }
         return launch_status();
     }
-    if (vec && m >= 1024 && n >= 512 && kp % 16 == 0 && aligned16(a_packed) && nk < (1ull << 31)) {
+    const uint64_t wide_tiles = ((m + kWdM - 1) / kWdM) * ((n + kWdN - 1) / kWdN);
+    if (vec && wide_tiles >= kWdMinTiles && kp % 16 == 0 && aligned16(a_packed) && nk < (1ull << 31)) {
         // Many output tiles: the wide kernel (one 256 x 256 tile per CU).
-        const uint64_t tiles = ((m + kWdM - 1) / kWdM) * ((n + kWdN - 1) / kWdN);
+        const uint64_t tiles = wide_tiles;
         const uint64_t per = (tiles + kXcds - 1) / kXcds;
         if (per * kXcds > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
         hipLaunchKernelGGL(ternary_i8_wide_kernel, dim3((uint32_t)(per * kXcds)), dim3(256), kWdLds, s, p);

@@ -692,12 +692,12 @@ def test_ternary_matmul_i8_small_n(m, n, k):
     assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), "ternary_matmul_i8 small n")
 
 
-@pytest.mark.parametrize("m,n,k", [(1024, 512, 2560), (1100, 700, 1040), (2049, 1000, 800), (1280, 777, 6400),
-                                   (1031, 513, 80)])
+@pytest.mark.parametrize("m,n,k", [(4096, 3072, 640), (4100, 3000, 560), (6400, 2000, 320), (3333, 3900, 80),
+                                   (4096, 3072, 160)])
 def test_ternary_matmul_i8_wide_tiles(m, n, k):
-    """The wide path (m >= 1024, n >= 512, 16-byte packed rows: 256 x 256
-    tiles, per-lane table decode): whole and ragged tiles, a partial last K
-    step (k % 160 != 0) and a single step; bit-exact against the oracle on
+    """The wide path (at least 192 output tiles of 256 x 256, 16-byte packed
+    rows; per-lane table decode): whole and ragged tiles, a partial last K
+    step (k % 160 != 0), a partial single step and a whole one; bit-exact against the oracle on
     arbitrary packed bytes (bytes >= 243 included)."""
     from inputs import int8_codes, raw_packed
 
@@ -715,7 +715,7 @@ def test_ternary_matmul_i8_wide_tiles_unaligned_output():
     0): its epilogue stores element by element instead of 16-byte rows."""
     from inputs import int8_codes, raw_packed
 
-    m, n, k = 1100, 704, 1040
+    m, n, k = 4100, 3072, 560
     log(f"ternary_matmul_i8 wide unaligned c m={m} n={n} k={k}")
     lib = __import__("kore_amd._lib", fromlist=["load"]).load()
     p = raw_packed(m, k, 17)
