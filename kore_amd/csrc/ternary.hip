@@ -40,8 +40,9 @@
 // reference loop order.
 //
 // kore_hip_ternary_matmul_f32: the reference's f32-activation ternary_matmul,
-// a sequential fold per output (ternary_f32_seq_kernel, and for up to four
-// columns ternary_f32_pipe_kernel, at the end).
+// a sequential fold per output (at the end): ternary_f32_rows_kernel for 33
+// columns and more, ternary_f32_pipe_kernel for up to four columns (and up to
+// 32 on unaligned rows), ternary_f32_seq_kernel otherwise.
 #include <algorithm>
 #include <type_traits>
 
@@ -1190,6 +1191,199 @@ static void launch_f32_seq(int ct, uint64_t m, dim3 g, hipStream_t s, const Tern
 #undef KORE_F32_SEQ
 }
 
+constexpr uint32_t kRowsW = 4;            // waves per workgroup
+constexpr int kBufWord3 = 0x00020000;     // buffer resource word 3 (raw dword access)
+constexpr uint64_t kRowsMinWaves = 1536;  // 1.5 per SIMD of 256 CUs
+// 33 columns and more (16-byte-aligned b with N % 4 == 0): a wave owns R rows
+// and 64 columns (one per lane), so a row's trit at each K is the same for
+// every lane.  The per-lane kernel above reads each such trit from LDS as a
+// broadcast returned to all 64 lanes, which leaves it LDS-bound (about 2.5
+// LDS cycles per fma cycle).  Here lane L decodes byte L % 16 of the chunk's
+// 16 packed bytes of each row (so every 16-lane row of the wave holds the 80
+// trits of the chunk, 5 per lane, from a table in LDS), and each fma takes
+// its trit from lane j of its own 16-lane row through the DPP operand
+// modifier row_newbcast:j: the vector unit issues one fma per term, and LDS
+// serves b and 5 table reads per row and chunk.
+//
+// Terms and zero trits as in the per-lane kernel: fma(t, b, acc) is the
+// reference's step for finite b; a chunk whose b holds an Inf or NaN (and
+// the last partial chunk) skips zero trits explicitly.
+template <int J>
+__device__ __forceinline__ float fmac_trit(float acc, float t, float b) {
+    // acc = fma(t from lane J of this lane's 16-lane row, b, acc)
+    asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(t), "v"(b), "i"(J));
+    return acc;
+}
+
+template <int R, int W>
+__global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args p) {
+    constexpr int KC = 80;                   // K columns per chunk
+    constexpr int NB = KC / 5;               // packed bytes per row and chunk (one per lane of a 16-lane row)
+    constexpr int kPitch = KC + 4;           // floats per column of the staged b: 21 x 16 bytes
+    constexpr int kThreads = W * kWave;
+    constexpr int kGroups = KC / 4 * kWave;  // 4-float groups of b per chunk
+    constexpr int kStage = kGroups / kThreads;
+    static_assert(NB == 16 && kGroups % kThreads == 0, "chunk split");
+    __shared__ __attribute__((aligned(16))) float bs[2][kWave * kPitch];  // b of a chunk, [column][k]
+    __shared__ float tlut[5 * 256];  // digit d of byte v -> trit as float at [d * 256 + v]; v >= 243: 0
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(t / kWave);
+    for (int v = t; v < 256; v += kThreads) {
+        uint32_t x = (uint32_t)v;
+#pragma unroll
+        for (int d = 0; d < 5; ++d) {
+            tlut[d * 256 + v] = v >= 243 ? 0.0f : (float)((int)(x % 3u) - 1);
+            x /= 3u;
+        }
+    }
+    const uint32_t col0 = blockIdx.y * kWave;
+    const uint32_t col = col0 + lane;
+    const uint32_t row0 = (blockIdx.x * W + wave) * R;
+    // b staging: group g of a chunk is k = 4 (g / 64) .. + 3 of column g % 64,
+    // four coalesced loads (a row of 64 columns each), one 16-byte LDS write
+    // at [column][k].  Buffer loads from a resource based at the chunk's
+    // first row of b, with byte offsets fixed for the whole kernel: the
+    // hardware range check returns zeros past K, and an offset past any
+    // range does so for columns past N.
+    uint32_t boff[kStage][4];
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) {
+        const uint32_t g = (uint32_t)t + kThreads * u;
+        const uint32_t c = col0 + g % kWave, k4 = 4u * (g / kWave);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) boff[u][q] = c < p.n ? ((k4 + q) * p.n + c) * 4u : 0x80000000u;
+    }
+    auto load_b = [&](uint32_t kc, f32x4 (&bv)[kStage]) {
+        const uint64_t left = (uint64_t)(p.k - kc) * p.n * 4u;
+        const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(p.b + (uint64_t)kc * p.n), (short)0, (int)(left < 0x7fffffffull ? left : 0x7fffffffull), kBufWord3);
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                v[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, boff[u][q], 0, 0));
+            bv[u] = f32x4{v[0], v[1], v[2], v[3]};
+        }
+    };
+    // byte lane % 16 of the chunk for each row.  Past the row's end the byte
+    // is the next row's (or 0 past the matrix, by the range check): its
+    // trits meet only b past K, which is zero, and fma(t, 0, acc) = acc.
+    const int a_bytes = (int)((uint64_t)p.m * p.kp);  // below 2^31 (checked by the launcher)
+    uint32_t aoff[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) aoff[i] = min(row0 + i, p.m - 1) * p.kp + (uint32_t)(lane & (NB - 1));
+    auto load_pb = [&](uint32_t kc, uint32_t (&pb)[R]) {
+        const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)p.a, (short)0, a_bytes, kBufWord3);
+#pragma unroll
+        for (int i = 0; i < R; ++i) pb[i] = __builtin_amdgcn_raw_buffer_load_b8(ra, aoff[i] + kc / 5u, 0, 0);
+    };
+    f32x4 bvn[kStage];
+    uint32_t pbn[R];
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = 0.0f;
+    if (p.k > 0) {
+        load_b(0, bvn);
+        load_pb(0, pbn);
+    }
+    bool slow = false;  // wave-uniform: a row's sum is Inf or NaN
+    uint32_t buf = 0;
+    for (uint32_t kc = 0; kc < p.k; kc += KC, buf ^= 1u) {
+        float* bb = bs[buf];
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const uint32_t g = (uint32_t)t + kThreads * u;
+            *reinterpret_cast<f32x4*>(bb + (g % kWave) * kPitch + 4 * (g / kWave)) = bvn[u];
+        }
+        // this chunk's trits: lane L holds the five of byte L % 16 of each row
+        uint32_t pbc[R];
+        float tr[R][5];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            pbc[i] = pbn[i];
+#pragma unroll
+            for (int d = 0; d < 5; ++d) tr[i][d] = tlut[d * 256 + pbn[i]];
+        }
+        if (kc + KC < p.k) {
+            load_b(kc + KC, bvn);
+            load_pb(kc + KC, pbn);
+        }
+        // one barrier per chunk: this chunk's b written before it is read,
+        // and the previous chunk's reads of the other buffer done before the
+        // next chunk overwrites it
+        __syncthreads();
+        const f32x4* bc = reinterpret_cast<const f32x4*>(bb + lane * kPitch);
+        if (!slow) {
+            // K advances 20 columns (4 bytes, 5 float4 of b) per group; the
+            // next group's b is read before this group's fmas
+            float saved[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) saved[i] = acc[i];
+            f32x4 bcur[5], bnxt[5];
+#pragma unroll
+            for (int q = 0; q < 5; ++q) bcur[q] = bc[q];
+            auto group = [&](auto gc) {
+                constexpr int G = decltype(gc)::value;
+                if (G < 3) {
+#pragma unroll
+                    for (int q = 0; q < 5; ++q) bnxt[q] = bc[5 * (G + 1) + q];
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                const float* bf = reinterpret_cast<const float*>(bcur);
+                auto byte = [&](auto jc) {
+                    constexpr int j = decltype(jc)::value;  // byte of the group
+#pragma unroll
+                    for (int d = 0; d < 5; ++d)
+#pragma unroll
+                        for (int i = 0; i < R; ++i) acc[i] = fmac_trit<4 * G + j>(acc[i], tr[i][d], bf[5 * j + d]);
+                };
+                byte(std::integral_constant<int, 0>{});
+                byte(std::integral_constant<int, 1>{});
+                byte(std::integral_constant<int, 2>{});
+                byte(std::integral_constant<int, 3>{});
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int q = 0; q < 5; ++q) bcur[q] = bnxt[q];
+            };
+            group(std::integral_constant<int, 0>{});
+            group(std::integral_constant<int, 1>{});
+            group(std::integral_constant<int, 2>{});
+            group(std::integral_constant<int, 3>{});
+            // An Inf or NaN b turns the sum it enters Inf or NaN (fma(0, Inf,
+            // acc) included), and so does an overflow: redo the chunk with
+            // zero trits skipped from the saved sums, and keep doing so.
+            bool nf = false;
+#pragma unroll
+            for (int i = 0; i < R; ++i) nf |= !__builtin_isfinite(acc[i]);
+            if (__builtin_expect(__ballot(nf) != 0, 0)) {
+                slow = true;
+#pragma unroll
+                for (int i = 0; i < R; ++i) acc[i] = saved[i];
+            }
+        }
+        if (slow) {
+            const uint32_t kn = min((uint32_t)KC, p.k - kc);
+            const float* bf = bb + lane * kPitch;
+            for (uint32_t ki = 0; ki < kn; ++ki) {
+                const float bv = bf[ki];
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    const uint32_t byte = (uint32_t)__builtin_amdgcn_readlane((int)pbc[i], (int)(ki / 5u));
+                    const float trv = tlut[(ki % 5u) * 256u + byte];
+                    if (trv != 0.0f) acc[i] = __builtin_fmaf(trv, bv, acc[i]);
+                }
+            }
+        }
+    }
+    if (col < p.n) {
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+            if (row0 + i < p.m) p.c[(uint64_t)(row0 + i) * p.n + col] = acc[i] * p.sa[row0 + i];
+    }
+}
+
 // One to four columns (decode steps), any row alignment.  The
 // fold is a chain of k dependent f32 operations per output, so its floor is k
 // times the latency of one dependent vector operation (about 8 cycles for a
@@ -1797,6 +1991,24 @@ extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float*
     const uint64_t gx = (m + rb - 1) / rb, gy = (n + ct - 1) / ct;
     if (gx > 0x7fffffffull || gy > 65535) return KORE_HIP_ERR_OVERFLOW;
     const dim3 g((uint32_t)gx, (uint32_t)gy);
+    // 33 columns and more: the row-broadcast kernel (any row alignment).
+    if (ct == 64 && mkp < 0x7fffffffull && (uint64_t)80 * n * 4 < 0x7fffffffull) {
+        // Rows per wave: 4 (b read from LDS once per 4 rows) while that
+        // leaves at least 1.5 waves per SIMD, else 2, else 1.
+        uint32_t r = 4;
+        if ((m + 3) / 4 * gy < kRowsMinWaves) r = 2;
+        if ((m + 1) / 2 * gy < kRowsMinWaves) r = 1;
+#ifdef KORE_ROWS_FORCE
+        r = KORE_ROWS_FORCE;
+#endif
+        const uint64_t bx = (m + r * kRowsW - 1) / (r * kRowsW);
+        if (bx > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
+        const dim3 gr((uint32_t)bx, (uint32_t)gy);
+        if (r == 4) hipLaunchKernelGGL((ternary_f32_rows_kernel<4, kRowsW>), gr, dim3(kRowsW * kWave), 0, s, p);
+        else if (r == 2) hipLaunchKernelGGL((ternary_f32_rows_kernel<2, kRowsW>), gr, dim3(kRowsW * kWave), 0, s, p);
+        else hipLaunchKernelGGL((ternary_f32_rows_kernel<1, kRowsW>), gr, dim3(kRowsW * kWave), 0, s, p);
+        return launch_status();
+    }
     // Up to 4 columns; more where the per-lane kernel would take its
     // unaligned-row loads, in groups of 8 columns, up to 8 columns or 512
     // workgroups (measured: 2560 x 8 x 6912 78 against 99 us, 2560 x 64 x

@@ -801,7 +801,11 @@ TERN_F32_SHAPES = [(1, 1, 5), (7, 1, 2560), (6912, 1, 2560), (33, 3, 161), (64, 
                    # 5-8 columns on unaligned rows (eight fold waves)
                    (300, 6, 1203), (2560, 8, 6912), (65, 5, 333),
                    # more columns on unaligned rows: groups of 8 (a partial last group)
-                   (130, 20, 1203), (300, 64, 333)]
+                   (130, 20, 1203), (300, 64, 333),
+                   # 33+ columns (the row-broadcast kernel): one, two and four rows per
+                   # wave, masked columns, several column blocks, unaligned rows, a
+                   # single whole chunk and partial last chunks
+                   (100, 64, 80), (4000, 64, 165), (6501, 40, 250), (6200, 128, 400), (1000, 100, 1000)]
 
 
 @pytest.mark.parametrize("m,n,k", TERN_F32_SHAPES)
@@ -843,6 +847,26 @@ def test_ternary_matmul_f32_order_and_nonfinite(n):
     got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
     assert_bitexact(got, want, "ternary_matmul_f32 order/non-finite")
 
+
+
+@pytest.mark.parametrize("m,n", [(130, 40), (4000, 64), (6500, 64)])
+def test_ternary_matmul_f32_rows_nonfinite(m, n):
+    """33+ columns (the row-broadcast kernel with one, two and four rows per
+    wave): Inf/NaN activations in some chunks and columns only, and finite
+    activations whose sum overflows; a chunk that meets them is redone with
+    zero trits skipped and later chunks stay on that path.  Bit-exact against
+    the oracle, non-finite outputs included."""
+    from inputs import raw_packed
+
+    k = 1203
+    log(f"ternary_matmul_f32 rows non-finite m={m} n={n} k={k}")
+    p, sa, b = raw_packed(m, k, 31), normal((m,), 32, 1.0, 0.1), normal((k, n), 33)
+    b[5, 0] = np.inf; b[250, n - 1] = -np.inf; b[777, 0] = np.nan; b[1200, n // 2] = np.inf
+    b[400:404, 3] = 3e38
+    want = oracle.ternary_matmul(p, sa, b, m, n, k)
+    assert np.isfinite(want).any() and not np.isfinite(want).all()
+    got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
+    assert_bitexact(got, want, f"ternary_matmul_f32 rows non-finite m={m} n={n}")
 
 @pytest.mark.parametrize("n", [1, 2, 3, 4])
 def test_ternary_matmul_f32_decode_nonfinite_steps(n):
