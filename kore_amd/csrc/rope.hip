@@ -3,7 +3,11 @@
 // Roofline: HBM.  Bytes per token (b, s): 2 * heads * D * 4 (read + write,
 // in place); the inv_freq table (D/2 floats) stays in L2.
 //
-// One workgroup per token.  Its first D/2 threads compute the token's
+// D in {32, 64, 128, 256} (16-byte aligned): one float4 per thread, 256
+// consecutive float4 of one token's Q or K row per workgroup, the half-split
+// partner taken from another lane (rope_lane_kernel, below).  Other D: one
+// workgroup per token (rope_vec_kernel).  Either way the first D/2 threads
+// of a workgroup compute the token's
 // (cos, sin) pairs once into LDS: angle = (start_pos + s) * inv_freq[i] is
 // the reference's f32 product (crates/kore-edge/src/ops/rope.rs:22-26 /
 // crates/kore-serve/src/layered/engine.rs:716-719) and sincosf is ocml's
@@ -131,6 +135,80 @@ __global__ __launch_bounds__(kRopeMaxBlock) void rope_vec_kernel(RopeTensor t0, 
     }
 }
 
+// Lane path: D in {32, 64, 128, 256} (a head is D/4 <= 64 float4, so a
+// pair's two halves lie in one wave), both tensors 16-byte aligned.  One
+// float4 per thread: a workgroup covers 256 consecutive float4 of one token's
+// Q or K row (whole heads), which streams at the copy's rate (measured: one
+// float4 per thread in 128-256 thread groups ~84% of HBM peak for an
+// in-place update; two per thread in 640-thread groups ~80%).  Half-split:
+// lane L holds float4 j = L % (D/4) of its head and takes its partner (the
+// float4 D/8 away) from lane L ^ (D/8) by a cross-lane swizzle; with x its
+// own and p the partner's values, the first half stores x*c - p*s and the
+// second half p*s + x*c, written as x*c + p*(-s) and x*c + p*s (negation is
+// exact and a single addition commutes), the reference's products and sum.
+constexpr int kRopeLaneBlock = 256;
+
+__device__ __forceinline__ float lane_xor(float v, uint32_t m) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((int)((threadIdx.x ^ m) << 2), __builtin_bit_cast(int, v)));
+}
+
+template <bool Interleaved>
+__global__ __launch_bounds__(kRopeLaneBlock) void rope_lane_kernel(RopeTensor t0, RopeTensor t1,
+                                                                const float* __restrict__ inv_freq,
+                                                                uint64_t seq_len, uint32_t head_dim,
+                                                                uint64_t start_pos, uint32_t blocks0,
+                                                                uint32_t blocks_tok) {
+    extern __shared__ f32x4 cs_raw[];  // [D/2] (cos, sin)
+    float2* cs = reinterpret_cast<float2*>(cs_raw);
+    const uint64_t token = blockIdx.x / blocks_tok;
+    const uint32_t bt = blockIdx.x % blocks_tok;
+    const bool first_t = bt < blocks0;
+    const RopeTensor& tt = first_t ? t0 : t1;
+    const uint32_t row4 = tt.heads * (head_dim >> 2);  // float4 per token row
+    const uint32_t f = (first_t ? bt : bt - blocks0) * kRopeLaneBlock + threadIdx.x;
+    f32x4* row = reinterpret_cast<f32x4*>(tt.data + token * (uint64_t)tt.heads * head_dim);
+    const bool ok = f < row4;
+    f32x4 x = {0.f, 0.f, 0.f, 0.f};
+    if (ok) x = ld_stream(row + f);
+    const uint32_t half = head_dim >> 1;
+    {
+        const float pos = (float)(start_pos + token % seq_len);
+        for (uint32_t i = threadIdx.x; i < half; i += kRopeLaneBlock) {
+            float angle = pos * inv_freq[i];
+            float sn, c;
+            sincosf(angle, &sn, &c);
+            cs[i] = make_float2(c, sn);
+        }
+        __syncthreads();
+    }
+    const uint32_t j = f & ((head_dim >> 2) - 1);  // float4 within the head
+    f32x4 o;
+    if (Interleaved) {
+        const f32x4 csv = *reinterpret_cast<const f32x4*>(&cs[2 * j]);  // c0 s0 c1 s1
+        const float2 r0 = rot(x.x, x.y, csv.x, csv.y);
+        const float2 r1 = rot(x.z, x.w, csv.z, csv.w);
+        o.x = r0.x; o.y = r0.y; o.z = r1.x; o.w = r1.y;
+    } else {
+        const uint32_t q8 = head_dim >> 3;  // float4 per half head
+        f32x4 p;
+        p.x = lane_xor(x.x, q8);
+        p.y = lane_xor(x.y, q8);
+        p.z = lane_xor(x.z, q8);
+        p.w = lane_xor(x.w, q8);
+        const uint32_t jj = j & (q8 - 1);
+        const f32x4 ca = *reinterpret_cast<const f32x4*>(&cs[4 * jj]);      // c0 s0 c1 s1
+        const f32x4 cb = *reinterpret_cast<const f32x4*>(&cs[4 * jj + 2]);  // c2 s2 c3 s3
+        const bool lo = j < q8;
+        const float s0 = lo ? -ca.y : ca.y, s1 = lo ? -ca.w : ca.w, s2 = lo ? -cb.y : cb.y, s3 = lo ? -cb.w : cb.w;
+        float a, b;
+        a = x.x * ca.x; b = p.x * s0; o.x = a + b;
+        a = x.y * ca.z; b = p.y * s1; o.y = a + b;
+        a = x.z * cb.x; b = p.z * s2; o.z = a + b;
+        a = x.w * cb.z; b = p.w * s3; o.w = a + b;
+    }
+    if (ok) st_stream(row + f, o);
+}
+
 // Scalar path: any even D, any 4-byte alignment.  One task per pair.
 template <bool Interleaved>
 __global__ __launch_bounds__(kRopeBlock) void rope_scalar_kernel(RopeTensor t0, RopeTensor t1,
@@ -195,6 +273,21 @@ static int rope_launch(float* q, uint32_t q_heads, float* k, uint32_t k_heads, c
     const bool vec = (head_dim % 8 == 0) && aligned16(t0.data) && (t1.heads == 0 || aligned16(t1.data));
     const size_t lds = ((size_t)(head_dim / 2) * sizeof(float2) + 15) & ~(size_t)15;
     dim3 grid((uint32_t)tokens), block(kRopeBlock);
+    const bool lane_ok = vec && (head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256);
+    if (lane_ok) {
+        const uint64_t b0 = ((uint64_t)t0.heads * (head_dim / 4) + kRopeLaneBlock - 1) / kRopeLaneBlock;
+        const uint64_t b1 = ((uint64_t)t1.heads * (head_dim / 4) + kRopeLaneBlock - 1) / kRopeLaneBlock;
+        const uint64_t blocks = tokens * (b0 + b1);
+        if (blocks > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
+        const dim3 gl((uint32_t)blocks), bl(kRopeLaneBlock);
+        if (interleaved)
+            hipLaunchKernelGGL(rope_lane_kernel<true>, gl, bl, lds, s, t0, t1, inv_freq, seq_len, head_dim, start_pos,
+                               (uint32_t)b0, (uint32_t)(b0 + b1));
+        else
+            hipLaunchKernelGGL(rope_lane_kernel<false>, gl, bl, lds, s, t0, t1, inv_freq, seq_len, head_dim, start_pos,
+                               (uint32_t)b0, (uint32_t)(b0 + b1));
+        return launch_status();
+    }
     if (vec) {
         // Threads per token: the token's tasks in at most kRopeBatch slots,
         // rounded to whole waves, capped at kRopeMaxBlock.

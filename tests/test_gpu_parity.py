@@ -340,7 +340,8 @@ def test_swiglu_against_serve_silu_full():
 @pytest.mark.parametrize("interleaved", [False, True])
 @pytest.mark.parametrize("batch,seq,heads,hd,start", [(1, 1, 1, 4, 0), (2, 5, 3, 8, 7), (1, 3, 2, 6, 0),
                                                       (2, 9, 4, 128, 100000), (1, 17, 5, 64, 3),
-                                                      (3, 4, 2, 2, 1)])
+                                                      (3, 4, 2, 2, 1), (1, 3, 3, 32, 5), (2, 3, 2, 256, 2047),
+                                                      (1, 2, 9, 128, 0)])
 def test_rope_small(interleaved, batch, seq, heads, hd, start):
     log(f"rope b={batch} s={seq} h={heads} d={hd} start={start} interleaved={interleaved}")
     x = normal((batch, seq, heads, hd), seq * hd + heads)
@@ -360,6 +361,21 @@ def test_rope_unaligned_scalar_path():
     assert_close(buf.tensor(torch.float32).cpu().numpy().reshape(x.shape), oracle.rope(x, 11, 10000.0),
                  what="rope unaligned")
 
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+@pytest.mark.parametrize("hq,hk,hd", [(5, 3, 64), (9, 1, 128), (3, 2, 32), (2, 1, 256)])
+def test_rope_qk_small(interleaved, hq, hk, hd):
+    """The fused Q+K launch on head counts whose rows fill no whole
+    workgroup, for every head_dim of the one-float4-per-thread path."""
+    log(f"rope qk small hq={hq} hk={hk} d={hd} interleaved={interleaved}")
+    q = normal((2, 7, hq, hd), 40 + hq)
+    k = normal((2, 7, hk, hd), 50 + hk)
+    qb, kb = up(q), up(k)
+    inv = rocm.rocm_rope_inv_freq_f32(DEV, hd, 10000.0)
+    rocm.rocm_rope_qk_f32(DEV, qb, kb, inv, 2, 7, hq, hk, hd, 3, interleaved)
+    assert_close(down(qb, np.float32, q.shape), oracle.rope(q, 3, 10000.0, interleaved), what="rope q")
+    assert_close(down(kb, np.float32, k.shape), oracle.rope(k, 3, 10000.0, interleaved), what="rope k")
 
 @pytest.mark.slow
 @pytest.mark.parametrize("interleaved", [False, True])
