@@ -108,7 +108,7 @@ def randn(torch, shape, seed, mean=0.0, std=1.0):
 class RopeQK(Workload):
     name = "rope_qk"
     B, S, HQ, HK, D = 8, 2048, 32, 8, 128
-    kernel = "rope_vec_kernel"
+    kernel = "rope_lane_kernel"
 
     def __init__(self, interleaved=False):
         self.interleaved = interleaved
@@ -478,6 +478,8 @@ class TernaryI8(Workload):
             self.kernel = "ternary_i8_gemv_kernel"
         elif n <= 64:
             self.kernel = "ternary_i8_skinny_kernel"
+        elif ((m + 255) // 256) * ((n + 255) // 256) >= 192:
+            self.kernel = "ternary_i8_wide_kernel"
         self.tokens = n
         self.ops = 2 * m * n * k
         self.bytes = m * self.kp + n * k + 4 * m * n + 4 * (m + n)
@@ -545,7 +547,7 @@ class TernaryF32(Workload):
 
     def __init__(self, m=6912, n=1, k=2560):
         self.m, self.n, self.k = m, n, k
-        self.kernel = "ternary_f32_pipe_kernel" if n <= 4 else "ternary_f32_seq_kernel"
+        self.kernel = "ternary_f32_pipe_kernel" if n <= 4 else ("ternary_f32_rows_kernel" if n > 32 else "ternary_f32_seq_kernel")
         self.kp = (k + 4) // 5
         self.name = f"ternary_f32_{m}x{n}x{k}"
         self.tokens = n
