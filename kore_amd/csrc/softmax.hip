@@ -23,9 +23,10 @@
 // own CUDA kernel is.  exp(d) is evaluated on the reference's d = x - m
 // (rounded the same way) as the hardware exp2(d * log2(e)); see exp_diff.
 //
-// Shapes: a row of up to 4096 floats is held in one wave's registers (one
-// wave per row, 4 rows per workgroup); up to 16384 floats in one 256-thread
-// workgroup; longer rows (vocab-sized) stream through a workgroup in three
+// Shapes: a row of up to 1024 floats, or of 2049-4096, is held in one wave's
+// registers (one wave per row, 4 rows per workgroup); 1025-2048 floats and
+// up to 16384 in one workgroup's (256 threads; 512 for the 1025-2048
+// backward); longer rows (vocab-sized) stream through a workgroup in three
 // passes.  Unaligned views and cols % 4 != 0 use the looped kernel with
 // scalar accesses.  Every kernel reads a row fully before writing it, so out
 // may alias an input.
@@ -83,7 +84,7 @@ __device__ __forceinline__ uint64_t row_limit(const SmArgs& a, uint64_t row) {
 
 // Block-wide reduction of one value per wave through LDS, combined in wave
 // order (deterministic).  `red` holds kSmWaves floats.
-template <bool IsMax>
+template <bool IsMax, int Waves = kSmWaves>
 __device__ __forceinline__ float block_combine(float v, float* red) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -92,20 +93,22 @@ __device__ __forceinline__ float block_combine(float v, float* red) {
     __syncthreads();
     float r = red[0];
 #pragma unroll
-    for (int w = 1; w < kSmWaves; ++w) r = IsMax ? fmaxf(r, red[w]) : r + red[w];
+    for (int w = 1; w < Waves; ++w) r = IsMax ? fmaxf(r, red[w]) : r + red[w];
     return r;
 }
 
 // Row in registers.  Wave mode (Block = false): one wave per row, element f4
-// index = c*64 + lane.  Block mode: one workgroup per row, index = c*256 + tid.
-template <SmKind K, int NCH, bool Block>
-__global__ __launch_bounds__(kSmBlock) void softmax_reg_kernel(SmArgs a) {
-    __shared__ float red[kSmWaves];
+// index = c*64 + lane, 4 rows per 256-thread workgroup.  Block mode: one
+// workgroup of BS threads per row, index = c*BS + tid.
+template <SmKind K, int NCH, bool Block, int BS = kSmBlock>
+__global__ __launch_bounds__(BS) void softmax_reg_kernel(SmArgs a) {
+    constexpr int kWavesB = BS / kWave;
+    __shared__ float red[kWavesB];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const uint64_t row = Block ? (uint64_t)blockIdx.x : (uint64_t)blockIdx.x * kSmWaves + wave;
     if (!Block && row >= a.rows) return;  // uniform per wave; no block barrier in wave mode
-    const int step = Block ? kSmBlock : kWave;
+    const int step = Block ? BS : kWave;
     const int me = Block ? (int)threadIdx.x : lane;
     const uint32_t cols4 = (uint32_t)(a.cols >> 2);      // <= 4096 here
     const uint32_t lim = (uint32_t)row_limit<K>(a, row);  // <= cols
@@ -131,7 +134,7 @@ __global__ __launch_bounds__(kSmBlock) void softmax_reg_kernel(SmArgs a) {
             dot += (p.x + p.y) + (p.z + p.w);
         }
         dot = wave_sum(dot);
-        if (Block) dot = block_combine<false>(dot, red);
+        if (Block) dot = block_combine<false, kWavesB>(dot, red);
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             const uint32_t f = (uint32_t)(c * step + me);
@@ -152,7 +155,7 @@ __global__ __launch_bounds__(kSmBlock) void softmax_reg_kernel(SmArgs a) {
         }
     }
     m = wave_max(m);
-    if (Block) m = block_combine<true>(m, red);
+    if (Block) m = block_combine<true, kWavesB>(m, red);
     float s = 0.0f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
@@ -166,7 +169,7 @@ __global__ __launch_bounds__(kSmBlock) void softmax_reg_kernel(SmArgs a) {
         }
     }
     s = wave_sum(s);
-    if (Block) s = block_combine<false>(s, red);
+    if (Block) s = block_combine<false, kWavesB>(s, red);
     const float inv = (K == SmKind::Causal) ? (s > 0.0f ? 1.0f / s : 0.0f) : 1.0f / s;
     if (K == SmKind::CeBwd) {
         const float inv_batch = 1.0f / (float)a.rows;
@@ -291,7 +294,16 @@ static int softmax_launch(const SmArgs& a, hipStream_t s) {
     if (vec && cols4 <= 64) launch_wave<K, 1>(a, s);
     else if (vec && cols4 <= 128) launch_wave<K, 2>(a, s);
     else if (vec && cols4 <= 256) launch_wave<K, 4>(a, s);
-    else if (vec && cols4 <= 512) launch_wave<K, 8>(a, s);
+    else if (vec && cols4 <= 512) {
+        // 1025-2048 columns: one workgroup per row streams faster than one
+        // wave per row (measured at 32768 x 2048: forward 85.8 -> 83.3 us
+        // with 256 threads x 2 float4, backward 129.3 -> 121.7 us with 512
+        // threads x 1 float4 each of y and dy)
+        if (K == SmKind::Bwd)
+            hipLaunchKernelGGL((softmax_reg_kernel<K, 1, true, 512>), dim3((uint32_t)a.rows), dim3(512), 0, s, a);
+        else
+            hipLaunchKernelGGL((softmax_reg_kernel<K, 2, true>), dim3((uint32_t)a.rows), dim3(kSmBlock), 0, s, a);
+    }
     else if (vec && cols4 <= 1024) launch_wave<K, 16>(a, s);
     else if (vec && cols4 <= 2048)
         hipLaunchKernelGGL((softmax_reg_kernel<K, 8, true>), dim3((uint32_t)a.rows), dim3(kSmBlock), 0, s, a);

@@ -497,6 +497,7 @@ def _softmax64(x):
 # one shape per kernel path: wave per row (<= 256/512/1024/2048/4096 cols),
 # workgroup per row (<= 8192/16384), looped (longer rows, cols % 4 != 0)
 SOFTMAX_SHAPES = [(1, 1), (3, 7), (5, 4), (4, 256), (7, 260), (9, 512), (6, 1000), (33, 2048), (5, 4096),
+                  (5, 1028), (3, 1500),
                   (3, 8192), (2, 16384), (2, 20000), (3, 4099), (2, 128256)]
 
 
@@ -534,7 +535,8 @@ def test_softmax_special_rows_in_place_and_unaligned():
 
 
 @pytest.mark.parametrize("rows,cols,offset", [(6, 8, 0), (6, 8, 3), (40, 64, 0), (300, 256, 0), (17, 2048, 1000),
-                                              (3, 8192, 4000), (2, 20000, 9999), (9, 4099, 10), (4, 33, 100)])
+                                              (3, 8192, 4000), (2, 20000, 9999), (9, 4099, 10), (4, 33, 100),
+                                              (7, 1028, 5), (5, 1500, 700)])
 def test_softmax_causal(rows, cols, offset):
     log(f"softmax_causal rows={rows} cols={cols} offset={offset}")
     x = normal((rows, cols), rows + cols + offset) * 3
@@ -558,7 +560,7 @@ def _softmax_bwd_scale(y, dy):
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 1), (3, 7), (4, 256), (9, 512), (33, 2048), (5, 4096), (3, 8192),
-                                       (2, 16384), (2, 20000), (3, 4099)])
+                                       (2, 16384), (2, 20000), (3, 4099), (4, 1028), (6, 1500)])
 def test_softmax_backward(rows, cols):
     log(f"softmax_backward rows={rows} cols={cols}")
     y = oracle.softmax(normal((rows, cols), cols) * 3)
@@ -637,7 +639,7 @@ def test_rms_norm_backward_deterministic_and_edge_cases():
 
 # -------------------------------------------------- cross-entropy backward
 @pytest.mark.parametrize("batch,classes", [(1, 1), (3, 7), (2, 3), (64, 256), (17, 1000), (8, 4096), (4, 8192),
-                                           (3, 32000), (2, 128256), (5, 4099)])
+                                           (3, 32000), (2, 128256), (5, 4099), (9, 2048), (5, 1500)])
 def test_cross_entropy_backward(batch, classes):
     log(f"cross_entropy_backward batch={batch} classes={classes}")
     x = normal((batch, classes), batch + classes) * 3
