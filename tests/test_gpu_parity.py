@@ -711,7 +711,7 @@ def test_ternary_matmul_i8_small_n(m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(4096, 3072, 640), (4100, 3000, 560), (6400, 2000, 320), (3333, 3900, 80),
-                                   (4096, 3072, 160)])
+                                   (4096, 3072, 160), (300, 49152, 160), (49200, 300, 160)])
 def test_ternary_matmul_i8_wide_tiles(m, n, k):
     """The wide path (at least 192 output tiles of 256 x 256, 16-byte packed
     rows; per-lane table decode): whole and ragged tiles, a partial last K
