@@ -886,6 +886,27 @@ def test_ternary_matmul_f32_rows_nonfinite(m, n):
     got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
     assert_bitexact(got, want, f"ternary_matmul_f32 rows non-finite m={m} n={n}")
 
+
+@pytest.mark.parametrize("n", [1, 64])
+def test_ternary_matmul_f32_subnormal_activations(n):
+    """Subnormal activations and signed zeros: every fold step is the
+    reference's IEEE f32 add with gradual underflow (no flush to zero),
+    bit-exact against the oracle (one column: the decode-step kernel; 64:
+    the row-broadcast kernel)."""
+    from inputs import raw_packed
+
+    m, k = 257, 803
+    log(f"ternary_matmul_f32 subnormal m={m} n={n} k={k}")
+    p, sa = raw_packed(m, k, 41), normal((m,), 42, 1.0, 0.1)
+    b = (normal((k, n), 43) * np.float32(1e-39)).astype(np.float32)
+    b[::7] = np.float32(-0.0)
+    b[::11] = np.float32(0.0)
+    b[5::13] = np.float32(1e-45)
+    assert (np.abs(b[b != 0]) < np.finfo(np.float32).tiny).all()
+    want = oracle.ternary_matmul(p, sa, b, m, n, k)
+    got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
+    assert_bitexact(got, want, f"ternary_matmul_f32 subnormal n={n}")
+
 @pytest.mark.parametrize("n", [1, 2, 3, 4])
 def test_ternary_matmul_f32_decode_nonfinite_steps(n):
     """One to four columns over several K steps and workgroups, Inf/NaN
