@@ -3,7 +3,7 @@
 // Roofline: HBM.  Bytes per token (b, s): 2 * heads * D * 4 (read + write,
 // in place); the inv_freq table (D/2 floats) stays in L2.
 //
-// D in {32, 64, 128, 256} (16-byte aligned): one float4 per thread, 256
+// D in {32, 64, 128, 256} (16-byte aligned): one float4 per thread, 128
 // consecutive float4 of one token's Q or K row per workgroup, the half-split
 // partner taken from another lane (rope_lane_kernel, below).  Other D: one
 // workgroup per token (rope_vec_kernel).  Either way the first D/2 threads
@@ -137,16 +137,17 @@ __global__ __launch_bounds__(kRopeMaxBlock) void rope_vec_kernel(RopeTensor t0, 
 
 // Lane path: D in {32, 64, 128, 256} (a head is D/4 <= 64 float4, so a
 // pair's two halves lie in one wave), both tensors 16-byte aligned.  One
-// float4 per thread: a workgroup covers 256 consecutive float4 of one token's
+// float4 per thread: a workgroup covers 128 consecutive float4 of one token's
 // Q or K row (whole heads), which streams at the copy's rate (measured: one
 // float4 per thread in 128-256 thread groups ~84% of HBM peak for an
-// in-place update; two per thread in 640-thread groups ~80%).  Half-split:
+// in-place update; two per thread in 640-thread groups ~80%; 128 threads
+// 0.4-1.6% faster than 256 on the headline).  Half-split:
 // lane L holds float4 j = L % (D/4) of its head and takes its partner (the
 // float4 D/8 away) from lane L ^ (D/8) by a cross-lane swizzle; with x its
 // own and p the partner's values, the first half stores x*c - p*s and the
 // second half p*s + x*c, written as x*c + p*(-s) and x*c + p*s (negation is
 // exact and a single addition commutes), the reference's products and sum.
-constexpr int kRopeLaneBlock = 256;
+constexpr int kRopeLaneBlock = 128;
 
 __device__ __forceinline__ float lane_xor(float v, uint32_t m) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((int)((threadIdx.x ^ m) << 2), __builtin_bit_cast(int, v)));
