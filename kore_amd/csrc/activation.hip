@@ -58,8 +58,10 @@ struct SwigluOp {
 
 // One float4 per thread per operand: on MI355X many short waves keep more
 // independent requests in flight than fewer threads with unrolled loads
-// (a plain copy reaches ~82% of 8 TB/s this way, ~76% at 4 float4/thread).
-constexpr int kEwBlock = 256;
+// (a plain copy reaches ~82% of 8 TB/s this way, ~76% at 4 float4/thread),
+// and 128-thread workgroups measured faster than 256 (GELU 16384 x 14336
+// 283.2 -> 278.4 us, SwiGLU 428.1 -> 425.9 us; 512 slower).
+constexpr int kEwBlock = 128;
 constexpr int kEwUnroll = 1;  // float4 per thread
 
 constexpr uint64_t kEwTile = (uint64_t)kEwBlock * kEwUnroll;  // float4 per block
