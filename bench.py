@@ -854,7 +854,7 @@ def main():
             "workload": w.desc, "kernel": w.kernel, "bytes_per_launch": w.bytes, "tokens": w.tokens,
             "kernel_us": round(ms * 1e3, 3), "achieved_gbs": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
             "ns_per_token": round(ms * 1e6 / w.tokens, 3), "steps": steps, "warmup_launches": n_warm,
-            "wall_s": round(wall, 4),
+            "wall_s": round(wall, 7),
             "wall_gbs": round(w.bytes * steps / wall / 1e9, 1),
         }
         if graph_us is not None:
