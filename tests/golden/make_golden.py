@@ -101,7 +101,7 @@ def cases():
             {"a": raw_packed(m, k, seed), "sa": normal((m,), seed + 1, 1.0, 0.1), "q": int8_codes(n, k, seed + 2),
              "sq": np.abs(normal((n,), seed + 3, 0.02, 0.005))},
             lambda i, p: {"c": oracle.ternary_matmul_i8(i["a"], i["sa"], i["q"], i["sq"], p["m"], p["n"], p["k"])})
-    for (m, n, k, seed) in ((40, 5, 333, 22), (70, 1, 2560, 23)):
+    for (m, n, k, seed) in ((40, 5, 333, 22), (70, 1, 2560, 23), (37, 48, 333, 26)):
         c[f"ternary_f32_{m}x{n}x{k}"] = (
             "ternary_matmul_f32", {"m": m, "n": n, "k": k},
             {"a": raw_packed(m, k, seed), "sa": normal((m,), seed + 1, 1.0, 0.1), "b": normal((k, n), seed + 2)},
