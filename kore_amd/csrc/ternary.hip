@@ -33,7 +33,8 @@
 //   column l % 32.
 // n <= 8: the small-n path (dot4 on decoded windows, no MFMA); 8 < n <= 64:
 // the skinny path (32 weight rows per workgroup, K split over its waves and
-// summed exactly in LDS); few output tiles beyond that: the tile kernel over
+// summed exactly in LDS); at least 192 tiles of 256 x 256: the wide kernel
+// (below); few output tiles beyond that: the tile kernel over
 // K ranges, summed with exact int32 atomics into the output (zeroed first,
 // finished in place).
 // Generic path (any shape and alignment): one thread per output, the
@@ -240,7 +241,7 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
     }
 }
 
-// Wide path (large m and n, packed rows 16-byte aligned, K % 16 == 0): the
+// Wide path (at least 192 output tiles, packed rows 16-byte aligned, K % 16 == 0): the
 // workgroup owns a 256 (m) x 256 (n) output tile; wave w owns weight rows
 // [64 w, 64 w + 64) of it against all 256 code rows: 2 x 8 MFMA tiles of
 // 32 x 32 (256 int32 accumulators per lane), one workgroup per CU.
