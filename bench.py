@@ -702,7 +702,8 @@ class StreamFloor(Workload):
 
 def all_workloads():
     return [RopeQK(False), RopeQK(True), RMSNorm(32, 2048), RMSNorm(16384, 2048), Swiglu(), Gelu(), Embedding(),
-            Prequant(4096), Prequant(64), Prequant(1), LaunchFloor(), StreamFloor(), RmsNormSiluGate(), Softmax(),
+            Prequant(4096), Prequant(64), Prequant(1), LaunchFloor(), StreamFloor(), StreamFloor(1, 2560),
+            StreamFloor(64, 2560), StreamFloor(32, 2048), RmsNormSiluGate(), Softmax(),
             SoftmaxBackward(),
             RmsNormBackward(), TernaryI8(), TernaryI8(6912, 64, 2560), TernaryI8(6912, 1, 2560), TernaryF32(),
             TernaryF32(6912, 64, 2560), PackTernary(), PackTernary(2560, 6912), Copy()]
@@ -924,9 +925,19 @@ SUMMARY = [("cfg0 RMSNorm 32x2048", "rms_norm_32x2048"), ("cfg1 RoPE Q+K half-sp
            ("cfg4 pre-quant 4096x2560", "prequant_4096x2560"), ("cfg4 pre-quant 64x2560", "prequant_64x2560"),
            ("cfg4 pre-quant 1x2560", "prequant_1x2560"), ("floor: empty launch", "launch_floor"),
            ("floor: pre-quant bytes, trivial body", "stream_floor_4096x2560"),
+           ("floor: 1x2560 read + byte writes, one wave", "stream_floor_1x2560"),
+           ("floor: 64x2560 read + byte writes", "stream_floor_64x2560"),
+           ("floor: 32x2048 read + byte writes", "stream_floor_32x2048"),
            ("next: RMSNorm 16384x2048", "rms_norm_16384x2048"), ("next: norm+SiLU gate", "rms_norm_silu_gate_4096x2560"),
            ("next: softmax 32768x2048", "softmax_32768x2048"),
            ("next: ternary i8 6912x4096x2560", "ternary_i8_6912x4096x2560")]
+
+
+# Latency-bound configs -> the trivial-body kernel moving their rows (reads
+# every value, writes a byte per value): any kernel that writes memory pays
+# about 1 us more per launch than an empty one.
+SAME_SHAPE_FLOOR = {"rms_norm_32x2048": "stream_floor_32x2048", "prequant_64x2560": "stream_floor_64x2560",
+                    "prequant_1x2560": "stream_floor_1x2560"}
 
 
 def print_summary(results):
@@ -942,8 +953,11 @@ def print_summary(results):
         cpu = r.get("cpu_baseline") or {}
         cpu_s = f"{cpu.get('value')} {cpu.get('unit', '')} x{cpu.get('cores', '')}" if cpu else "-"
         tail = ""
-        if floor and "graph_us" in r and name != "launch_floor":
+        if floor and "graph_us" in r and name != "launch_floor" and not name.startswith("stream_floor"):
             tail = f" | {r['kernel_us'] / floor:.2f}x launch floor"
+            same = results.get(SAME_SHAPE_FLOOR.get(name, ""), {}).get("kernel_us")
+            if same:
+                tail += f", {r['kernel_us'] / same:.2f}x its shape's read/write floor"
         if "achieved_tops" in r and r.get("bound") == "mfma":
             tail += f" | {r['achieved_tops']} TOPS ({100 * r['frac_of_mfma_peak']:.1f}% int8 MFMA)"
         out.append(f"[summary] {label}: {r['kernel_us']}{g} | {r['achieved_gbs']} | {100 * r['frac_of_peak']:.1f}% | "
