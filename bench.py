@@ -957,7 +957,7 @@ def print_summary(results):
             tail = f" | {r['kernel_us'] / floor:.2f}x launch floor"
             same = results.get(SAME_SHAPE_FLOOR.get(name, ""), {}).get("kernel_us")
             if same:
-                tail += f", {r['kernel_us'] / same:.2f}x its shape's read/write floor"
+                tail += f", {r['kernel_us'] / same:.2f}x its shape's read/write floor per launch"
         if "achieved_tops" in r and r.get("bound") == "mfma":
             tail += f" | {r['achieved_tops']} TOPS ({100 * r['frac_of_mfma_peak']:.1f}% int8 MFMA)"
         out.append(f"[summary] {label}: {r['kernel_us']}{g} | {r['achieved_gbs']} | {100 * r['frac_of_peak']:.1f}% | "
