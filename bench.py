@@ -547,7 +547,7 @@ class TernaryF32(Workload):
 
     def __init__(self, m=6912, n=1, k=2560):
         self.m, self.n, self.k = m, n, k
-        self.kernel = "ternary_f32_pipe_kernel" if n <= 4 else ("ternary_f32_rows_kernel" if n > 32 else "ternary_f32_seq_kernel")
+        self.kernel = "ternary_f32_pipe_kernel" if n <= 4 else "ternary_f32_rows_kernel"
         self.kp = (k + 4) // 5
         self.name = f"ternary_f32_{m}x{n}x{k}"
         self.tokens = n
@@ -706,7 +706,7 @@ def all_workloads():
             StreamFloor(64, 2560), StreamFloor(32, 2048), RmsNormSiluGate(), Softmax(),
             SoftmaxBackward(),
             RmsNormBackward(), TernaryI8(), TernaryI8(6912, 64, 2560), TernaryI8(6912, 1, 2560), TernaryF32(),
-            TernaryF32(6912, 64, 2560), PackTernary(), PackTernary(2560, 6912), Copy()]
+            TernaryF32(6912, 16, 2560), TernaryF32(6912, 64, 2560), PackTernary(), PackTernary(2560, 6912), Copy()]
 
 
 # ------------------------------------------------------------------ measure
@@ -836,6 +836,9 @@ def main():
     torch.cuda.set_device(0)
     only = set(filter(None, args.only.split(",")))
     works = [w for w in all_workloads() if not only or w.name in only]
+    if not works:
+        sys.exit(f"--only {args.only}: no workload of that name "
+                 f"(names: {', '.join(w.name for w in all_workloads())})")
     if not only:
         works = [w for w in works if w.name != "copy_1gib"]
     traffic = load_traffic()

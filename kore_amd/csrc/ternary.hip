@@ -41,9 +41,9 @@
 // reference loop order.
 //
 // kore_hip_ternary_matmul_f32: the reference's f32-activation ternary_matmul,
-// a sequential fold per output (at the end): ternary_f32_rows_kernel for 33
-// columns and more, ternary_f32_pipe_kernel for up to four columns (and up to
-// 32 on unaligned rows), ternary_f32_seq_kernel otherwise.
+// a sequential fold per output (at the end): ternary_f32_rows_kernel for five
+// columns and more, ternary_f32_pipe_kernel for one to four columns,
+// ternary_f32_seq_kernel for K = 0 and matrices of fewer than 20 packed bytes.
 #include <algorithm>
 #include <type_traits>
 
@@ -1169,42 +1169,37 @@ __global__ __launch_bounds__(kW * kWave) void ternary_f32_seq_kernel(TernF32Args
         if (live[i]) p.c[(uint64_t)rows[i] * p.n + col] = acc[i] * p.sa[rows[i]];
 }
 
-// Rows per lane (R) and waves per block (W): narrow column tiles take one
-// fold per lane and 4 waves (many waves in flight); 16-32 columns 2 rows per
-// lane; 64 columns 8 waves with 4 rows per lane when m gives >= 200 blocks of
-// 32 rows (b staged once for more rows), else 2 (more blocks).
+// One to four columns (K = 0 or fewer than 20 packed bytes): one fold per
+// lane, 4 waves.
 template <bool kAligned16>
-static void launch_f32_seq(int ct, uint64_t m, dim3 g, hipStream_t s, const TernF32Args& p) {
-#define KORE_F32_SEQ(C, R, W) \
-    hipLaunchKernelGGL((ternary_f32_seq_kernel<C, R, W, kAligned16>), g, dim3((W) * kWave), 0, s, p)
-    switch (ct) {
-        case 1: KORE_F32_SEQ(1, 1, 4); break;
-        case 2: KORE_F32_SEQ(2, 1, 4); break;
-        case 4: KORE_F32_SEQ(4, 1, 4); break;
-        case 8: KORE_F32_SEQ(8, 1, 4); break;
-        case 16: KORE_F32_SEQ(16, 2, 4); break;
-        case 32: KORE_F32_SEQ(32, 2, 4); break;
-        default:
-            if (m >= 32 * 200) KORE_F32_SEQ(64, 4, 8);
-            else KORE_F32_SEQ(64, 2, 8);
-            break;
-    }
+static void launch_f32_seq(int ct, dim3 g, hipStream_t s, const TernF32Args& p) {
+#define KORE_F32_SEQ(C) \
+    hipLaunchKernelGGL((ternary_f32_seq_kernel<C, 1, 4, kAligned16>), g, dim3(4 * kWave), 0, s, p)
+    if (ct == 1) KORE_F32_SEQ(1);
+    else if (ct == 2) KORE_F32_SEQ(2);
+    else KORE_F32_SEQ(4);
 #undef KORE_F32_SEQ
 }
 
 constexpr uint32_t kRowsW = 4;            // waves per workgroup
 constexpr int kBufWord3 = 0x00020000;     // buffer resource word 3 (raw dword access)
 constexpr uint64_t kRowsMinWaves = 1536;  // 1.5 per SIMD of 256 CUs
-// 33 columns and more (16-byte-aligned b with N % 4 == 0): a wave owns R rows
-// and 64 columns (one per lane), so a row's trit at each K is the same for
-// every lane.  The per-lane kernel above reads each such trit from LDS as a
-// broadcast returned to all 64 lanes, which leaves it LDS-bound (about 2.5
-// LDS cycles per fma cycle).  Here lane L decodes byte L % 16 of the chunk's
-// 16 packed bytes of each row (so every 16-lane row of the wave holds the 80
-// trits of the chunk, 5 per lane, from a table in LDS), and each fma takes
-// its trit from lane j of its own 16-lane row through the DPP operand
-// modifier row_newbcast:j: the vector unit issues one fma per term, and LDS
-// serves b and 5 table reads per row and chunk.
+#ifndef KORE_ROWS_MINCOLS
+#define KORE_ROWS_MINCOLS 5
+#endif
+constexpr uint64_t kRowsMinCols = KORE_ROWS_MINCOLS;  // narrower: the fold-wave kernel
+// Five columns and more, any alignment: a wave is 64 / CT row slots of CT
+// columns (CT = 16, 32 or 64, one column per lane), and slot s owns R rows,
+// so a row's trit at each K is the same for all CT lanes of its slot.  The
+// per-lane kernel above reads each such trit from LDS as a broadcast
+// returned to all 64 lanes, which leaves it LDS-bound (about 2.5 LDS cycles
+// per fma cycle).  Here lane L decodes byte L % 16 of the chunk's 16 packed
+// bytes of each of its slot's rows (so every 16-lane row of the wave holds
+// the 80 trits of the chunk of its slot's rows, 5 per lane, from a table in
+// LDS), and each fma takes its trit from lane j of its own 16-lane row
+// through the DPP operand modifier row_newbcast:j: the vector unit issues one
+// fma per term, and LDS serves b and 5 table reads per row and chunk.  A slot
+// is at least one 16-lane row, so 5-15 columns leave lanes idle.
 //
 // Terms and zero trits as in the per-lane kernel: fma(t, b, acc) is the
 // reference's step for finite b; a chunk whose b holds an Inf or NaN (and
@@ -1216,16 +1211,18 @@ __device__ __forceinline__ float fmac_trit(float acc, float t, float b) {
     return acc;
 }
 
-template <int R, int W>
+template <int CT, int R, int W>
 __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args p) {
-    constexpr int KC = 80;                   // K columns per chunk
-    constexpr int NB = KC / 5;               // packed bytes per row and chunk (one per lane of a 16-lane row)
-    constexpr int kPitch = KC + 4;           // floats per column of the staged b: 21 x 16 bytes
+    constexpr int KC = 80;                 // K columns per chunk
+    constexpr int NB = KC / 5;             // packed bytes per row and chunk (one per lane of a 16-lane row)
+    constexpr int kPitch = KC + 4;         // floats per column of the staged b: 21 x 16 bytes
+    constexpr int kSlots = kWave / CT;     // row slots of a wave (CT lanes each)
     constexpr int kThreads = W * kWave;
-    constexpr int kGroups = KC / 4 * kWave;  // 4-float groups of b per chunk
-    constexpr int kStage = kGroups / kThreads;
-    static_assert(NB == 16 && kGroups % kThreads == 0, "chunk split");
-    __shared__ __attribute__((aligned(16))) float bs[2][kWave * kPitch];  // b of a chunk, [column][k]
+    constexpr int kGroups = KC / 4 * CT;   // 4-float groups of b per chunk
+    constexpr int kStage = (kGroups + kThreads - 1) / kThreads;
+    static_assert(NB == 16 && CT % 16 == 0 && kWave % CT == 0, "chunk split");
+    static_assert(kGroups % kWave == 0, "staging is wave-uniform");
+    __shared__ __attribute__((aligned(16))) float bs[2][CT * kPitch];  // b of a chunk, [column][k]
     __shared__ float tlut[5 * 256];  // digit d of byte v -> trit as float at [d * 256 + v]; v >= 243: 0
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
@@ -1238,9 +1235,11 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args
             x /= 3u;
         }
     }
-    const uint32_t col0 = blockIdx.y * kWave;
-    const uint32_t col = col0 + lane;
-    const uint32_t row0 = (blockIdx.x * W + wave) * R;
+    __syncthreads();  // the table is read before the first chunk's barrier
+    const uint32_t col0 = blockIdx.y * CT;
+    const uint32_t col = col0 + (uint32_t)(lane % CT);
+    // row slot lane / CT of the wave owns rows row0 .. row0 + R - 1
+    const uint32_t row0 = ((blockIdx.x * W + wave) * kSlots + (uint32_t)(lane / CT)) * R;
     // b staging: group g of a chunk is k = 4 (g / 64) .. + 3 of column g % 64,
     // four coalesced loads (a row of 64 columns each), one 16-byte LDS write
     // at [column][k].  Buffer loads from a resource based at the chunk's
@@ -1251,7 +1250,7 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args
 #pragma unroll
     for (int u = 0; u < kStage; ++u) {
         const uint32_t g = (uint32_t)t + kThreads * u;
-        const uint32_t c = col0 + g % kWave, k4 = 4u * (g / kWave);
+        const uint32_t c = col0 + g % CT, k4 = 4u * (g / CT);
 #pragma unroll
         for (int q = 0; q < 4; ++q) boff[u][q] = c < p.n ? ((k4 + q) * p.n + c) * 4u : 0x80000000u;
     }
@@ -1261,6 +1260,7 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args
             (void*)(p.b + (uint64_t)kc * p.n), (short)0, (int)(left < 0x7fffffffull ? left : 0x7fffffffull), kBufWord3);
 #pragma unroll
         for (int u = 0; u < kStage; ++u) {
+            if (kGroups % kThreads != 0 && u == kStage - 1 && t >= kGroups % kThreads) break;
             float v[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q)
@@ -1295,8 +1295,9 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args
         float* bb = bs[buf];
 #pragma unroll
         for (int u = 0; u < kStage; ++u) {
+            if (kGroups % kThreads != 0 && u == kStage - 1 && t >= kGroups % kThreads) break;
             const uint32_t g = (uint32_t)t + kThreads * u;
-            *reinterpret_cast<f32x4*>(bb + (g % kWave) * kPitch + 4 * (g / kWave)) = bvn[u];
+            *reinterpret_cast<f32x4*>(bb + (g % CT) * kPitch + 4 * (g / CT)) = bvn[u];
         }
         // this chunk's trits: lane L holds the five of byte L % 16 of each row
         uint32_t pbc[R];
@@ -1315,7 +1316,7 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args
         // and the previous chunk's reads of the other buffer done before the
         // next chunk overwrites it
         __syncthreads();
-        const f32x4* bc = reinterpret_cast<const f32x4*>(bb + lane * kPitch);
+        const f32x4* bc = reinterpret_cast<const f32x4*>(bb + (lane % CT) * kPitch);
         if (!slow) {
             // K advances 20 columns (4 bytes, 5 float4 of b) per group; the
             // next group's b is read before this group's fmas
@@ -1366,12 +1367,13 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args
         }
         if (slow) {
             const uint32_t kn = min((uint32_t)KC, p.k - kc);
-            const float* bf = bb + lane * kPitch;
+            const float* bf = bb + (lane % CT) * kPitch;
             for (uint32_t ki = 0; ki < kn; ++ki) {
                 const float bv = bf[ki];
 #pragma unroll
                 for (int i = 0; i < R; ++i) {
-                    const uint32_t byte = (uint32_t)__builtin_amdgcn_readlane((int)pbc[i], (int)(ki / 5u));
+                    // byte ki / 5 of the row, held by lane ki / 5 of this lane's 16-lane row
+                    const uint32_t byte = (uint32_t)__shfl((int)pbc[i], (lane & ~15) + (int)(ki / 5u), kWave);
                     const float trv = tlut[(ki % 5u) * 256u + byte];
                     if (trv != 0.0f) acc[i] = __builtin_fmaf(trv, bv, acc[i]);
                 }
@@ -1383,6 +1385,35 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args
         for (int i = 0; i < R; ++i)
             if (row0 + i < p.m) p.c[(uint64_t)(row0 + i) * p.n + col] = acc[i] * p.sa[row0 + i];
     }
+}
+
+// Rows per lane: 4 for 64-column tiles and 2 for narrower ones (b read from
+// LDS once per R rows; measured: 16- and 32-column tiles ran 6-12% slower
+// with 4 than with 2 at every m tried, 64-column tiles 8-20% faster) while
+// that leaves at least 1.5 waves per SIMD, else fewer.
+template <int CT>
+static int launch_f32_rows(uint64_t m, uint64_t n, hipStream_t s, const TernF32Args& p) {
+    constexpr uint64_t kSlots = kWave / CT;
+    const uint64_t gy = (n + CT - 1) / CT;
+    uint32_t r = CT == 64 ? 4 : 2;
+    if (r == 4 && (m + 4 * kSlots - 1) / (4 * kSlots) * gy < kRowsMinWaves) r = 2;
+    if ((m + 2 * kSlots - 1) / (2 * kSlots) * gy < kRowsMinWaves) r = 1;
+#ifdef KORE_ROWS_FORCE
+    r = KORE_ROWS_FORCE;
+#endif
+    const uint64_t rows = r * kSlots * kRowsW;  // rows per workgroup
+    const uint64_t bx = (m + rows - 1) / rows;
+    if (bx > 0x7fffffffull || gy > 65535) return KORE_HIP_ERR_OVERFLOW;
+    const dim3 gr((uint32_t)bx, (uint32_t)gy), blk(kRowsW * kWave);
+    if constexpr (CT == 64) {
+        if (r == 4) {
+            hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 4, kRowsW>), gr, blk, 0, s, p);
+            return launch_status();
+        }
+    }
+    if (r == 2) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 2, kRowsW>), gr, blk, 0, s, p);
+    else hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 1, kRowsW>), gr, blk, 0, s, p);
+    return launch_status();
 }
 
 // One to four columns (decode steps), any row alignment.  The
@@ -1683,11 +1714,6 @@ void ternary_f32_pipe_kernel(TernF32Args p) {
     __syncthreads();  // the fold of the last step
 }
 
-static uint64_t f32_rows_per_block(int ct, uint64_t m) {
-    if (ct <= 8) return 4 * (kWave / ct);
-    if (ct <= 32) return 4 * (kWave / ct) * 2;
-    return m >= 32 * 200 ? 8 * 4 : 8 * 2;
-}
 
 // ---------------------------------------------------------------------------
 // Weight packing, the weight-side format of the matmuls above
@@ -1988,45 +2014,37 @@ extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float*
     hipStream_t s = (hipStream_t)stream;
     int ct = 64;
     while (ct > 1 && (uint64_t)(ct / 2) >= n) ct /= 2;  // smallest power of two >= n (<= 64)
-    const uint64_t rb = f32_rows_per_block(ct, m);
-    const uint64_t gx = (m + rb - 1) / rb, gy = (n + ct - 1) / ct;
-    if (gx > 0x7fffffffull || gy > 65535) return KORE_HIP_ERR_OVERFLOW;
-    const dim3 g((uint32_t)gx, (uint32_t)gy);
-    // 33 columns and more: the row-broadcast kernel (any row alignment).
-    if (ct == 64 && mkp < 0x7fffffffull && (uint64_t)80 * n * 4 < 0x7fffffffull) {
-        // Rows per wave: 4 (b read from LDS once per 4 rows) while that
-        // leaves at least 1.5 waves per SIMD, else 2, else 1.
-        uint32_t r = 4;
-        if ((m + 3) / 4 * gy < kRowsMinWaves) r = 2;
-        if ((m + 1) / 2 * gy < kRowsMinWaves) r = 1;
-#ifdef KORE_ROWS_FORCE
-        r = KORE_ROWS_FORCE;
-#endif
-        const uint64_t bx = (m + r * kRowsW - 1) / (r * kRowsW);
-        if (bx > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
-        const dim3 gr((uint32_t)bx, (uint32_t)gy);
-        if (r == 4) hipLaunchKernelGGL((ternary_f32_rows_kernel<4, kRowsW>), gr, dim3(kRowsW * kWave), 0, s, p);
-        else if (r == 2) hipLaunchKernelGGL((ternary_f32_rows_kernel<2, kRowsW>), gr, dim3(kRowsW * kWave), 0, s, p);
-        else hipLaunchKernelGGL((ternary_f32_rows_kernel<1, kRowsW>), gr, dim3(kRowsW * kWave), 0, s, p);
-        return launch_status();
+    // Five columns and more: the row-broadcast kernel (any row alignment) in
+    // 16-, 32- or 64-column tiles, over row ranges of less than 2 GiB of
+    // packed weights each (its buffer offsets are 31-bit).
+    if (n >= kRowsMinCols) {
+        const uint64_t span = kp ? std::min<uint64_t>(m, 0x7fffffffull / kp) : m;  // rows per launch
+        for (uint64_t r0 = 0; r0 < m; r0 += span) {
+            TernF32Args q = p;
+            q.a += r0 * kp;
+            q.sa += r0;
+            q.c += r0 * n;
+            q.m = (uint32_t)std::min<uint64_t>(span, m - r0);
+            const int st = ct <= 16 ? launch_f32_rows<16>(q.m, n, s, q)
+                         : ct == 32 ? launch_f32_rows<32>(q.m, n, s, q)
+                                    : launch_f32_rows<64>(q.m, n, s, q);
+            if (st != KORE_HIP_OK) return st;
+        }
+        return KORE_HIP_OK;
     }
-    // Up to 4 columns; more where the per-lane kernel would take its
-    // unaligned-row loads, in groups of 8 columns, up to 8 columns or 512
-    // workgroups (measured: 2560 x 8 x 6912 78 against 99 us, 2560 x 64 x
-    // 6912 157 against 245 us; at 6912 x 64 x 2563, 864 workgroups, 129
-    // against 127 us; at aligned K = 2560 the two are even at 8 columns).
-    const bool rows_aligned = kp % 16 == 0 && aligned16(a_packed);
-    const uint64_t pipe_blocks = ((m + kWave - 1) / kWave) * ((n + 7) / 8);
-    if ((n <= 4 || (!rows_aligned && (n <= 8 || pipe_blocks <= 512))) && k > 0 && mkp >= 20) {
-        const dim3 gp((uint32_t)((m + kWave - 1) / kWave), (uint32_t)(n <= 4 ? 1 : (n + 7) / 8));
+    // One to four columns: the fold-wave kernel; the per-lane kernel for K = 0
+    // and for matrices of fewer than 20 packed bytes (the fold-wave kernel's
+    // 8-byte windows).
+    if (k > 0 && mkp >= 20) {
+        const dim3 gp((uint32_t)((m + kWave - 1) / kWave));
         if (n == 1) hipLaunchKernelGGL(ternary_f32_pipe_kernel<1>, gp, dim3((kPfDec + 1) * kWave), 0, s, p);
         else if (n == 2) hipLaunchKernelGGL(ternary_f32_pipe_kernel<2>, gp, dim3((kPfDec + 2) * kWave), 0, s, p);
-        else if (n <= 4) hipLaunchKernelGGL(ternary_f32_pipe_kernel<4>, gp, dim3((kPfDec + 4) * kWave), 0, s, p);
-        else hipLaunchKernelGGL(ternary_f32_pipe_kernel<8>, gp, dim3((kPfDec + 8) * kWave), 0, s, p);
+        else hipLaunchKernelGGL(ternary_f32_pipe_kernel<4>, gp, dim3((kPfDec + 4) * kWave), 0, s, p);
         return launch_status();
     }
-    if (kp % 16 == 0 && aligned16(a_packed)) launch_f32_seq<true>(ct, m, g, s, p);
-    else launch_f32_seq<false>(ct, m, g, s, p);
+    const dim3 g((uint32_t)((m + 4 * (kWave / ct) - 1) / (4 * (kWave / ct))));  // 4 waves of 64 / ct rows
+    if (kp % 16 == 0 && aligned16(a_packed)) launch_f32_seq<true>(ct, g, s, p);
+    else launch_f32_seq<false>(ct, g, s, p);
     return launch_status();
 }
 

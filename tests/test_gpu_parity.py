@@ -816,14 +816,17 @@ TERN_F32_SHAPES = [(1, 1, 5), (7, 1, 2560), (6912, 1, 2560), (33, 3, 161), (64, 
                    (2560, 1, 6912), (20000, 1, 480), (129, 1, 241),
                    # two to four columns (the same kernel with one fold wave per column)
                    (6912, 2, 2560), (301, 4, 1203), (1, 2, 60), (129, 3, 241), (5, 4, 24), (2560, 3, 6912),
-                   # 5-8 columns on unaligned rows (eight fold waves)
-                   (300, 6, 1203), (2560, 8, 6912), (65, 5, 333),
-                   # more columns on unaligned rows: groups of 8 (a partial last group)
-                   (130, 20, 1203), (300, 64, 333),
-                   # 33+ columns (the row-broadcast kernel): one, two and four rows per
-                   # wave, masked columns, several column blocks, unaligned rows, a
-                   # single whole chunk and partial last chunks
-                   (100, 64, 80), (4000, 64, 165), (6501, 40, 250), (6200, 128, 400), (1000, 100, 1000)]
+                   # fewer than 20 packed bytes with up to four columns (the per-lane kernel)
+                   (3, 4, 25), (1, 3, 90),
+                   # 5+ columns (the row-broadcast kernel): 16-column tiles (5-16 columns,
+                   # four row slots a wave), 32-column tiles (17-32, two slots) and
+                   # 64-column tiles; one, two and four rows per lane, masked columns,
+                   # several column blocks, unaligned rows, a single whole chunk and
+                   # partial last chunks
+                   (300, 6, 1203), (2560, 8, 6912), (65, 5, 333), (6912, 16, 2560), (12300, 9, 160),
+                   (1, 16, 80), (7, 12, 85), (130, 20, 1203), (6200, 20, 320), (2001, 32, 2563), (13, 17, 5),
+                   (300, 64, 333), (100, 64, 80), (4000, 64, 165), (6501, 40, 250), (6200, 128, 400),
+                   (1000, 100, 1000)]
 
 
 @pytest.mark.parametrize("m,n,k", TERN_F32_SHAPES)
@@ -867,10 +870,10 @@ def test_ternary_matmul_f32_order_and_nonfinite(n):
 
 
 
-@pytest.mark.parametrize("m,n", [(130, 40), (4000, 64), (6500, 64)])
+@pytest.mark.parametrize("m,n", [(130, 40), (4000, 64), (6500, 64), (300, 8), (12300, 16), (2000, 24), (6200, 32)])
 def test_ternary_matmul_f32_rows_nonfinite(m, n):
-    """33+ columns (the row-broadcast kernel with one, two and four rows per
-    wave): Inf/NaN activations in some chunks and columns only, and finite
+    """5+ columns (the row-broadcast kernel: 16-, 32- and 64-column tiles,
+    one, two and four rows per lane): Inf/NaN activations in some chunks and columns only, and finite
     activations whose sum overflows; a chunk that meets them is redone with
     zero trits skipped and later chunks stay on that path.  Bit-exact against
     the oracle, non-finite outputs included."""
@@ -887,12 +890,12 @@ def test_ternary_matmul_f32_rows_nonfinite(m, n):
     assert_bitexact(got, want, f"ternary_matmul_f32 rows non-finite m={m} n={n}")
 
 
-@pytest.mark.parametrize("n", [1, 64])
+@pytest.mark.parametrize("n", [1, 3, 16, 64])
 def test_ternary_matmul_f32_subnormal_activations(n):
     """Subnormal activations and signed zeros: every fold step is the
     reference's IEEE f32 add with gradual underflow (no flush to zero),
-    bit-exact against the oracle (one column: the decode-step kernel; 64:
-    the row-broadcast kernel)."""
+    bit-exact against the oracle (one and three columns: the decode-step
+    kernel; 16 and 64: the row-broadcast kernel)."""
     from inputs import raw_packed
 
     m, k = 257, 803
@@ -906,6 +909,28 @@ def test_ternary_matmul_f32_subnormal_activations(n):
     want = oracle.ternary_matmul(p, sa, b, m, n, k)
     got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
     assert_bitexact(got, want, f"ternary_matmul_f32 subnormal n={n}")
+
+def test_ternary_matmul_f32_row_ranges():
+    """A packed matrix of more than 2 GiB (32769 rows of 65536 packed bytes):
+    the row-broadcast kernel runs over row ranges of less than 2 GiB each;
+    the rows on both sides of the range boundary and the last rows are
+    bit-exact against the oracle (rows are independent)."""
+    m, n, kp = 32769, 5, 65536
+    k = 5 * kp
+    log(f"ternary_matmul_f32 row ranges m={m} n={n} k={k}")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(61)
+    p = torch.randint(0, 256, (m, kp), dtype=torch.uint8, device="cuda", generator=gen)
+    sa, b = normal((m,), 62, 1.0, 0.1), normal((k, n), 63)
+    got = down(rocm.rocm_ternary_matmul_f32(DEV, HipBuffer.from_tensor(p), up(sa), up(b), m, n, k),
+               np.float32, (m, n))
+    span = 0x7FFFFFFF // kp
+    rows = np.array([0, 1, span - 2, span - 1, span, m - 1])
+    want = oracle.ternary_matmul(p[torch.from_numpy(rows).cuda()].cpu().numpy(), sa[rows], b, len(rows), n, k)
+    del p
+    torch.cuda.empty_cache()
+    assert_bitexact(got[rows], want, "ternary_matmul_f32 row ranges")
+
 
 @pytest.mark.parametrize("n", [1, 2, 3, 4])
 def test_ternary_matmul_f32_decode_nonfinite_steps(n):
