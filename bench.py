@@ -705,7 +705,8 @@ def all_workloads():
             Prequant(4096), Prequant(64), Prequant(1), LaunchFloor(), StreamFloor(), StreamFloor(1, 2560),
             StreamFloor(64, 2560), StreamFloor(32, 2048), RmsNormSiluGate(), Softmax(),
             SoftmaxBackward(),
-            RmsNormBackward(), TernaryI8(), TernaryI8(6912, 64, 2560), TernaryI8(6912, 1, 2560), TernaryF32(),
+            RmsNormBackward(), TernaryI8(), TernaryI8(2560, 4096, 6912), TernaryI8(6912, 64, 2560),
+            TernaryI8(6912, 1, 2560), TernaryF32(),
             TernaryF32(6912, 16, 2560), TernaryF32(6912, 64, 2560), PackTernary(), PackTernary(2560, 6912), Copy()]
 
 

@@ -36,9 +36,10 @@
 // summed exactly in LDS); at least 192 tiles of 256 x 256: the wide kernel
 // (below); few output tiles beyond that: the tile kernel over
 // K ranges, summed with exact int32 atomics into the output (zeroed first,
-// finished in place).
-// Generic path (any shape and alignment): one thread per output, the
-// reference loop order.
+// finished in place).  Code rows that are not 16-byte aligned (K % 16 != 0
+// or an unaligned q) take the tile kernel with dword-window loads.
+// Generic path (K = 0, or an output not 4-byte aligned): one thread per
+// output, the reference loop order.
 //
 // kore_hip_ternary_matmul_f32: the reference's f32-activation ternary_matmul,
 // a sequential fold per output (at the end): ternary_f32_rows_kernel for five
@@ -87,12 +88,14 @@ __device__ __forceinline__ uint64_t trit_lut_entry(uint32_t b) {
 }
 
 // kAlignedA: packed rows are 16-byte aligned (Kp % 16 == 0) and read as
-// dwordx4; otherwise byte by byte.
+// dwordx4; otherwise as the five dwords around the 16 bytes, shifted into
+// place (a row's last partial piece, and the matrix's last bytes, byte by
+// byte).
 // kSplit: the workgroup covers K-tiles [split * kt_per, (split + 1) * kt_per)
 // of its output tile and adds its int32 sums into c (zeroed, read as int32)
 // with integer atomics -- exact and order-free, so the result is the same on
 // every run; ternary_i8_finish_kernel then applies the epilogue in place.
-template <bool kAlignedA, bool kSplit>
+template <bool kAlignedA, bool kAlignedB, bool kSplit>
 __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
     __shared__ uint64_t lut[256];
     __shared__ __attribute__((aligned(16))) uint8_t As[kTmM * kTmPitch];
@@ -133,10 +136,64 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
                               kZeroByte * 0x01010101u};
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
+    const uintptr_t a_hi = reinterpret_cast<uintptr_t>(p.a) + (uintptr_t)p.m * p.kp;
+    const uintptr_t q_hi = reinterpret_cast<uintptr_t>(p.q) + (uintptr_t)p.n * p.k;
+    auto load_b = [&](uint32_t kt, u32x4* bv) {
+#pragma unroll
+        for (int u = 0; u < 5; ++u) {
+            const int c = t + kTmBlock * u;
+            const int row = c / 10, piece = c % 10;
+            const uint32_t kb = kt * kTmK + 16u * piece;
+            const bool ok = n0 + row < p.n && kb < p.k;
+            const int8_t* src = p.q + (uint64_t)(n0 + row) * p.k + kb;
+            if (kAlignedB) {
+                bv[u] = ok ? *reinterpret_cast<const u32x4*>(src) : zero4;
+                continue;
+            }
+            // code rows not 16-byte aligned (K % 16 != 0 or an unaligned q):
+            // the five dwords around the piece, shifted into place; a piece
+            // that reaches past k, or whose dwords would pass the codes' end,
+            // byte by byte with zeros at columns >= k
+            const uintptr_t wa = reinterpret_cast<uintptr_t>(src);
+            const uintptr_t w0 = wa & ~(uintptr_t)3;
+            if (ok && kb + 16u <= p.k && w0 + 20u <= q_hi) {
+                const uint32_t* d = reinterpret_cast<const uint32_t*>(w0);
+                const uint32_t d0 = d[0], d1 = d[1], d2 = d[2], d3 = d[3], d4 = d[4];
+                const uint32_t sh = (uint32_t)(wa & 3u);
+                bv[u] = u32x4{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
+                              __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh)};
+            } else {
+                uint32_t w[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    w[q] = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t o = kb + 4 * q + e;
+                        w[q] |= (ok && o < p.k ? (uint32_t)(uint8_t)src[4 * q + e] : 0u) << (8 * e);
+                    }
+                }
+                bv[u] = u32x4{w[0], w[1], w[2], w[3]};
+            }
+        }
+    };
     auto load_tile = [&](uint32_t kt, u32x4& av, u32x4* bv) {
         const uint32_t ab = kt * kTmKp + 16u * ah;  // packed byte offset
         if (kAlignedA) {
             av = (arow_ok && ab < p.kp) ? arow[ab >> 4] : zero_bytes;
+            load_b(kt, bv);
+            return;
+        }
+        // unaligned rows: the five dwords around the 16 bytes, shifted (the
+        // row's last partial piece and the matrix's last bytes byte by byte)
+        const uintptr_t wa = reinterpret_cast<uintptr_t>(arow8 + ab);
+        const uintptr_t w0 = wa & ~(uintptr_t)3;
+        if (arow_ok && ab + 16u <= p.kp && w0 + 20u <= a_hi) {
+            const uint32_t* d = reinterpret_cast<const uint32_t*>(w0);
+            const uint32_t d0 = d[0], d1 = d[1], d2 = d[2], d3 = d[3], d4 = d[4];
+            const uint32_t sh = (uint32_t)(wa & 3u);
+            av = u32x4{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
+                       __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh)};
         } else {
             uint32_t w[4];
 #pragma unroll
@@ -151,14 +208,7 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
             }
             av = u32x4{w[0], w[1], w[2], w[3]};
         }
-#pragma unroll
-        for (int u = 0; u < 5; ++u) {
-            const int c = t + kTmBlock * u;
-            const int row = c / 10, piece = c % 10;
-            const uint32_t kb = kt * kTmK + 16u * piece;
-            const bool ok = n0 + row < p.n && kb < p.k;
-            bv[u] = ok ? *reinterpret_cast<const u32x4*>(p.q + (uint64_t)(n0 + row) * p.k + kb) : zero4;
-        }
+        load_b(kt, bv);
     };
 
     i32x16 acc[2][2];
@@ -290,6 +340,7 @@ __device__ __forceinline__ void splice_trits(uint32_t (&out)[20], int b, uint64_
     out[d + 1] |= (uint32_t)(v >> (32 - sh));
 }
 
+template <bool kAlignedA>
 __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t wlds[];
     uint64_t* lut = reinterpret_cast<uint64_t*>(wlds + 2 * kWdBBytes);
@@ -325,19 +376,50 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     const uint32_t nkt = (p.k + kTmK - 1) / kTmK;
     // This lane's two weight rows (fragments i = 0, 1); rows past m read row
     // m - 1 (their outputs are not stored).
-    const u32x4* arow[2];
+    const uint8_t* arow[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const uint32_t m = min(m0 + 64 * wave + 32 * i + r, p.m - 1u);
-        arow[i] = reinterpret_cast<const u32x4*>(p.a + (uint64_t)m * p.kp);
+        arow[i] = p.a + (uint64_t)m * p.kp;
     }
+    const uintptr_t a_hi = reinterpret_cast<uintptr_t>(p.a) + (uintptr_t)p.m * p.kp;
     // A window past kp (the second half of a last step) reads the row's
     // first window: it lies wholly past k, so its trits are zeroed below.
+    // Unaligned rows: the five dwords around the window, shifted into place;
+    // a window that straddles the row's end (last step only) takes the next
+    // row's bytes, at columns >= k, zeroed below as well; only where the
+    // five dwords would pass the matrix's end are the bytes read one by one.
     auto load_a = [&](uint32_t kt, u32x4 (&av)[2]) {
         const uint32_t ab = kt * kTmKp + 16u * h;
         const uint32_t abc = ab < p.kp ? ab : 0u;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) av[i] = arow[i][abc >> 4];
+        for (int i = 0; i < 2; ++i) {
+            if (kAlignedA) {
+                av[i] = *reinterpret_cast<const u32x4*>(arow[i] + abc);
+                continue;
+            }
+            const uintptr_t wa = reinterpret_cast<uintptr_t>(arow[i] + abc);
+            const uintptr_t w0 = wa & ~(uintptr_t)3;
+            if (__builtin_expect(w0 + 20u <= a_hi, 1)) {
+                const uint32_t* d = reinterpret_cast<const uint32_t*>(w0);
+                const uint32_t d0 = d[0], d1 = d[1], d2 = d[2], d3 = d[3], d4 = d[4];
+                const uint32_t sh = (uint32_t)(wa & 3u);
+                av[i] = u32x4{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
+                              __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh)};
+            } else {
+                uint32_t w[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    w[q] = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uintptr_t o = wa + 4 * q + e;
+                        w[q] |= (o < a_hi ? (uint32_t)*reinterpret_cast<const uint8_t*>(o) : 0u) << (8 * e);
+                    }
+                }
+                av[i] = u32x4{w[0], w[1], w[2], w[3]};
+            }
+        }
     };
     // Code slots of this wave: slot s (16 bytes) of a tile is row s / 11,
     // piece s % 11 (piece 10: the row's padding, filled with piece 0).
@@ -1881,6 +1963,16 @@ __global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_kernel(const 
 
 }  // namespace kore
 
+namespace kore {
+template <bool kSplit>
+static void launch_mfma(bool aligned_a, bool aligned_b, dim3 grid, hipStream_t s, const TernArgs& p) {
+    if (aligned_a && aligned_b) hipLaunchKernelGGL((ternary_i8_mfma_kernel<true, true, kSplit>), grid, dim3(kTmBlock), 0, s, p);
+    else if (aligned_b) hipLaunchKernelGGL((ternary_i8_mfma_kernel<false, true, kSplit>), grid, dim3(kTmBlock), 0, s, p);
+    else if (aligned_a) hipLaunchKernelGGL((ternary_i8_mfma_kernel<true, false, kSplit>), grid, dim3(kTmBlock), 0, s, p);
+    else hipLaunchKernelGGL((ternary_i8_mfma_kernel<false, false, kSplit>), grid, dim3(kTmBlock), 0, s, p);
+}
+}  // namespace kore
+
 using namespace kore;
 
 extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* a_scales, const int8_t* q,
@@ -1941,15 +2033,20 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
         return launch_status();
     }
     const uint64_t wide_tiles = ((m + kWdM - 1) / kWdM) * ((n + kWdN - 1) / kWdN);
-    if (vec && wide_tiles >= kWdMinTiles && kp % 16 == 0 && aligned16(a_packed) && nk < (1ull << 31)) {
+    if (vec && wide_tiles >= kWdMinTiles && nk < (1ull << 31)) {
         // Many output tiles: the wide kernel (one 256 x 256 tile per CU).
         const uint64_t tiles = wide_tiles;
         const uint64_t per = (tiles + kXcds - 1) / kXcds;
         if (per * kXcds > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
-        hipLaunchKernelGGL(ternary_i8_wide_kernel, dim3((uint32_t)(per * kXcds)), dim3(256), kWdLds, s, p);
+        const dim3 g((uint32_t)(per * kXcds));
+        if (kp % 16 == 0 && aligned16(a_packed))
+            hipLaunchKernelGGL((ternary_i8_wide_kernel<true>), g, dim3(256), kWdLds, s, p);
+        else
+            hipLaunchKernelGGL((ternary_i8_wide_kernel<false>), g, dim3(256), kWdLds, s, p);
         return launch_status();
     }
-    if (vec) {
+    if (k > 0 && c_ok) {
+        // codes 16-byte aligned row by row (vec) or not
         const uint64_t tiles = ((m + kTmM - 1) / kTmM) * ((n + kTmN - 1) / kTmN);
         const uint64_t nkt = (k + kTmK - 1) / kTmK;
         // Few output tiles (small m * n): split K so that ~512 workgroups run,
@@ -1970,15 +2067,10 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
         if (splits > 1) {
             const dim3 eg((uint32_t)((mn + kTmBlock - 1) / kTmBlock));
             hipLaunchKernelGGL(ternary_i8_zero_kernel, eg, dim3(kTmBlock), 0, s, reinterpret_cast<int32_t*>(c), mn);
-            if (al)
-                hipLaunchKernelGGL((ternary_i8_mfma_kernel<true, true>), grid, dim3(kTmBlock), 0, s, p);
-            else
-                hipLaunchKernelGGL((ternary_i8_mfma_kernel<false, true>), grid, dim3(kTmBlock), 0, s, p);
+            launch_mfma<true>(al, vec, grid, s, p);
             hipLaunchKernelGGL(ternary_i8_finish_kernel, eg, dim3(kTmBlock), 0, s, p);
-        } else if (al) {
-            hipLaunchKernelGGL((ternary_i8_mfma_kernel<true, false>), grid, dim3(kTmBlock), 0, s, p);
         } else {
-            hipLaunchKernelGGL((ternary_i8_mfma_kernel<false, false>), grid, dim3(kTmBlock), 0, s, p);
+            launch_mfma<false>(al, vec, grid, s, p);
         }
     } else {
         const uint64_t blocks = (mn + kTmBlock - 1) / kTmBlock;

@@ -776,6 +776,46 @@ def test_ternary_matmul_i8_full_size_and_pipeline():
     assert_bitexact(got[:96, :rows].cpu().numpy(), ref, "prequant -> ternary chain")
 
 
+@pytest.mark.parametrize("m,n,k,offset", [(300, 49152, 176, 0), (49200, 300, 176, 0), (4100, 3000, 336, 0),
+                                          (300, 49152, 160, 1), (4096, 3072, 640, 3)])
+def test_ternary_matmul_i8_wide_tiles_unaligned_rows(m, n, k, offset):
+    """The wide path on packed rows that are not 16-byte aligned: K = 176 and
+    336 (rows of 36 and 68 bytes: a row's last window reaches into the next
+    row, whose trits sit past k; the last row's last window reaches the end
+    of the matrix), and aligned row lengths at a base 1 or 3 bytes past a
+    16-byte boundary.  Bit-exact against the oracle."""
+    from inputs import int8_codes, raw_packed
+
+    log(f"ternary_matmul_i8 wide unaligned rows m={m} n={n} k={k} offset={offset}")
+    p = raw_packed(m, k, m + 5 * k)
+    q = int8_codes(n, k, n + 17)
+    sa = normal((m,), 14, 1.0, 0.1)
+    sq = np.abs(normal((n,), 15, 0.02, 0.005))
+    t = torch.empty(p.size + offset, dtype=torch.uint8, device="cuda")
+    t[offset:].copy_(torch.from_numpy(p.ravel()))
+    got = down(rocm.rocm_ternary_matmul_i8(DEV, HipBuffer.from_tensor(t[offset:]), up(sa), up(q), up(sq), m, n, k),
+               np.float32, (m, n))
+    assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), "ternary_matmul_i8 wide unaligned rows")
+
+
+@pytest.mark.parametrize("m,n,k", [(6912, 64, 2563), (1000, 300, 1001), (2560, 3, 6915), (130, 129, 1203),
+                                   (7, 9, 3), (2000, 2000, 1001), (33, 17, 2570)])
+def test_ternary_matmul_i8_unaligned_code_rows(m, n, k):
+    """Code rows that are not 16-byte aligned (K % 16 != 0): the 128 x 128 tile
+    kernel with dword-window code loads, zeros at columns >= k, the codes'
+    last bytes read one by one; few tiles (split K, integer atomics) and many.
+    Bit-exact against the oracle on arbitrary packed bytes."""
+    from inputs import int8_codes, raw_packed
+
+    log(f"ternary_matmul_i8 unaligned code rows m={m} n={n} k={k}")
+    p = raw_packed(m, k, 7 * m + k)
+    q = int8_codes(n, k, n + 19)
+    sa = normal((m,), 16, 1.0, 0.1)
+    sq = np.abs(normal((n,), 17, 0.02, 0.005))
+    got = down(rocm.rocm_ternary_matmul_i8(DEV, up(p), up(sa), up(q), up(sq), m, n, k), np.float32, (m, n))
+    assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), "ternary_matmul_i8 unaligned code rows")
+
+
 def test_ternary_matmul_i8_edges():
     log("ternary_matmul_i8 edges")
     lib = __import__("kore_amd._lib", fromlist=["load"]).load()
@@ -793,7 +833,7 @@ def test_ternary_matmul_i8_edges():
     # the output may not overlap an input
     cb = up(np.zeros(64 * 64 + 64 * 16, np.float32))
     assert lib.kore_hip_ternary_matmul_i8(1 << 40, 1 << 41, cb.ptr, 1 << 42, cb.ptr, 4, 4, 16, None) == -4
-    # unaligned codes take the generic path with identical results
+    # codes 1 byte past an aligned base (the tile kernel's window loads)
     m, n, k = 40, 9, 320
     from inputs import int8_codes, raw_packed
 
