@@ -1266,6 +1266,7 @@ static void launch_f32_seq(int ct, dim3 g, hipStream_t s, const TernF32Args& p) 
 constexpr uint32_t kRowsW = 4;            // waves per workgroup
 constexpr int kBufWord3 = 0x00020000;     // buffer resource word 3 (raw dword access)
 constexpr uint64_t kRowsMinWaves = 1536;  // 1.5 per SIMD of 256 CUs
+constexpr uint64_t kSimds = 1024;         // 256 CUs x 4
 #ifndef KORE_ROWS_MINCOLS
 #define KORE_ROWS_MINCOLS 5
 #endif
@@ -1479,6 +1480,20 @@ static int launch_f32_rows(uint64_t m, uint64_t n, hipStream_t s, const TernF32A
     const uint64_t gy = (n + CT - 1) / CT;
     uint32_t r = CT == 64 ? 4 : 2;
     if (r == 4 && (m + 4 * kSlots - 1) / (4 * kSlots) * gy < kRowsMinWaves) r = 2;
+    if (r == 4) {
+        // Many rows: the SIMDs run the waves in rounds, so R rows per wave
+        // cost R * ceil(waves / 1024); 5 or 7 rows where that is lower and
+        // still leaves two rounds (one wave alone on a SIMD hides less
+        // latency).  Measured: 13824 x 64 x 2560 111.5 (R = 4) against 104.1
+        // (5) and 99.7 us (7); 6912 x 64 x 2560 65.8 (4) against 67.3 (7,
+        // one round).
+        uint64_t best = 0;
+        for (const uint32_t rr : {4u, 5u, 7u}) {
+            const uint64_t rounds = ((m + rr - 1) / rr * gy + kSimds - 1) / kSimds;
+            if (rr > 4 && rounds < 2) continue;
+            if (best == 0 || rr * rounds < best) best = rr * rounds, r = rr;
+        }
+    }
     if ((m + 2 * kSlots - 1) / (2 * kSlots) * gy < kRowsMinWaves) r = 1;
 #ifdef KORE_ROWS_FORCE
     r = KORE_ROWS_FORCE;
@@ -1488,10 +1503,10 @@ static int launch_f32_rows(uint64_t m, uint64_t n, hipStream_t s, const TernF32A
     if (bx > 0x7fffffffull || gy > 65535) return KORE_HIP_ERR_OVERFLOW;
     const dim3 gr((uint32_t)bx, (uint32_t)gy), blk(kRowsW * kWave);
     if constexpr (CT == 64) {
-        if (r == 4) {
-            hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 4, kRowsW>), gr, blk, 0, s, p);
-            return launch_status();
-        }
+        if (r == 4) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 4, kRowsW>), gr, blk, 0, s, p);
+        else if (r == 5) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 5, kRowsW>), gr, blk, 0, s, p);
+        else if (r == 7) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 7, kRowsW>), gr, blk, 0, s, p);
+        if (r >= 4) return launch_status();
     }
     if (r == 2) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 2, kRowsW>), gr, blk, 0, s, p);
     else hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 1, kRowsW>), gr, blk, 0, s, p);
@@ -1873,19 +1888,26 @@ __global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_vec_kernel(co
     // so with xh the largest float whose quotient is <= threshold,
     // quotient > threshold <=> w > xh and quotient < -threshold <=> w < -xh
     // (NaN: neither).  xh is found from fl(threshold * scale), within a few
-    // ulps, by stepping with IEEE divisions (the same for every lane).  If
+    // ulps, by stepping with IEEE divisions (the same for every lane; each
+    // quotient computed once, stepping stops at the bound).  If
     // that fails (an infinite scale or threshold, a NaN threshold), each
     // weight is divided instead, as w * (1 / scale) -- within 3 ulp of the
     // quotient -- with the IEEE division for values within 2^-20 (relative)
     // of +-threshold (below 2^-100 for a zero threshold).
     float xh = threshold * scale;
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-        if (xh / scale > threshold) xh = float_next(xh, false);
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-        if (float_next(xh, true) / scale <= threshold) xh = float_next(xh, true);
-    const bool bounds = __builtin_isfinite(xh) && xh / scale <= threshold && !(float_next(xh, true) / scale <= threshold);
+    float qx = xh / scale;
+    for (int it = 0; it < 4 && qx > threshold; ++it) {
+        xh = float_next(xh, false);
+        qx = xh / scale;
+    }
+    float xn = float_next(xh, true), qn = xn / scale;
+    for (int it = 0; it < 4 && qn <= threshold; ++it) {
+        xh = xn;
+        qx = qn;
+        xn = float_next(xh, true);
+        qn = xn / scale;
+    }
+    const bool bounds = __builtin_isfinite(xh) && qx <= threshold && !(qn <= threshold);
     const float rcp = 1.0f / scale;
     const float tt = fabsf(threshold);
     const float tol = fmaxf(tt * 0x1p-20f, 0x1p-100f);

@@ -866,7 +866,9 @@ TERN_F32_SHAPES = [(1, 1, 5), (7, 1, 2560), (6912, 1, 2560), (33, 3, 161), (64, 
                    (300, 6, 1203), (2560, 8, 6912), (65, 5, 333), (6912, 16, 2560), (12300, 9, 160),
                    (1, 16, 80), (7, 12, 85), (130, 20, 1203), (6200, 20, 320), (2001, 32, 2563), (13, 17, 5),
                    (300, 64, 333), (100, 64, 80), (4000, 64, 165), (6501, 40, 250), (6200, 128, 400),
-                   (1000, 100, 1000)]
+                   (1000, 100, 1000),
+                   # 64-column tiles with five and seven rows per lane (many rows)
+                   (10000, 64, 165), (13824, 64, 320), (6912, 128, 85)]
 
 
 @pytest.mark.parametrize("m,n,k", TERN_F32_SHAPES)
@@ -910,10 +912,11 @@ def test_ternary_matmul_f32_order_and_nonfinite(n):
 
 
 
-@pytest.mark.parametrize("m,n", [(130, 40), (4000, 64), (6500, 64), (300, 8), (12300, 16), (2000, 24), (6200, 32)])
+@pytest.mark.parametrize("m,n", [(130, 40), (4000, 64), (6500, 64), (300, 8), (12300, 16), (2000, 24), (6200, 32),
+                                 (10000, 64), (13824, 64)])
 def test_ternary_matmul_f32_rows_nonfinite(m, n):
     """5+ columns (the row-broadcast kernel: 16-, 32- and 64-column tiles,
-    one, two and four rows per lane): Inf/NaN activations in some chunks and columns only, and finite
+    one, two, four, five and seven rows per lane): Inf/NaN activations in some chunks and columns only, and finite
     activations whose sum overflows; a chunk that meets them is redone with
     zero trits skipped and later chunks stay on that path.  Bit-exact against
     the oracle, non-finite outputs included."""
