@@ -478,7 +478,7 @@ class TernaryI8(Workload):
             self.kernel = "ternary_i8_gemv_kernel"
         elif n <= 64:
             self.kernel = "ternary_i8_skinny_kernel"
-        elif ((m + 255) // 256) * ((n + 255) // 256) >= 192:
+        elif ((m + 255) // 256) * ((n + 255) // 256) >= 144:
             self.kernel = "ternary_i8_wide_kernel"
         self.tokens = n
         self.ops = 2 * m * n * k

@@ -33,7 +33,7 @@
 //   column l % 32.
 // n <= 8: the small-n path (dot4 on decoded windows, no MFMA); 8 < n <= 64:
 // the skinny path (32 weight rows per workgroup, K split over its waves and
-// summed exactly in LDS); at least 192 tiles of 256 x 256: the wide kernel
+// summed exactly in LDS); at least 144 tiles of 256 x 256: the wide kernel
 // (below); few output tiles beyond that: the tile kernel over
 // K ranges, summed with exact int32 atomics into the output (zeroed first,
 // finished in place).  Code rows that are not 16-byte aligned (K % 16 != 0
@@ -73,6 +73,19 @@ struct TernArgs {
     uint32_t m, n, k, kp;
     uint32_t splits, kt_per;  // split-K: K-tile ranges of kt_per per workgroup
 };
+
+// The 16 bytes at byte address wa (any alignment): one dwordx4 at the dword
+// boundary below (global loads need dword alignment only) and the dword
+// after it, shifted into place.  Reads the 20 bytes from wa & ~3.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ u32x4 load16_window(uintptr_t wa) {
+    const uintptr_t w0 = wa & ~(uintptr_t)3;
+    const u32x4_a4 lo = *reinterpret_cast<const u32x4_a4*>(w0);
+    const uint32_t d4 = *reinterpret_cast<const uint32_t*>(w0 + 16);
+    const uint32_t sh = (uint32_t)(wa & 3u);
+    return u32x4{__builtin_amdgcn_alignbyte(lo[1], lo[0], sh), __builtin_amdgcn_alignbyte(lo[2], lo[1], sh),
+                 __builtin_amdgcn_alignbyte(lo[3], lo[2], sh), __builtin_amdgcn_alignbyte(d4, lo[3], sh)};
+}
 
 // Five trits of byte b as int8 in the low 40 bits (byte j = trit j).
 __device__ __forceinline__ uint64_t trit_lut_entry(uint32_t b) {
@@ -157,11 +170,7 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
             const uintptr_t wa = reinterpret_cast<uintptr_t>(src);
             const uintptr_t w0 = wa & ~(uintptr_t)3;
             if (ok && kb + 16u <= p.k && w0 + 20u <= q_hi) {
-                const uint32_t* d = reinterpret_cast<const uint32_t*>(w0);
-                const uint32_t d0 = d[0], d1 = d[1], d2 = d[2], d3 = d[3], d4 = d[4];
-                const uint32_t sh = (uint32_t)(wa & 3u);
-                bv[u] = u32x4{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
-                              __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh)};
+                bv[u] = load16_window(wa);
             } else {
                 uint32_t w[4];
 #pragma unroll
@@ -189,11 +198,7 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
         const uintptr_t wa = reinterpret_cast<uintptr_t>(arow8 + ab);
         const uintptr_t w0 = wa & ~(uintptr_t)3;
         if (arow_ok && ab + 16u <= p.kp && w0 + 20u <= a_hi) {
-            const uint32_t* d = reinterpret_cast<const uint32_t*>(w0);
-            const uint32_t d0 = d[0], d1 = d[1], d2 = d[2], d3 = d[3], d4 = d[4];
-            const uint32_t sh = (uint32_t)(wa & 3u);
-            av = u32x4{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
-                       __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh)};
+            av = load16_window(wa);
         } else {
             uint32_t w[4];
 #pragma unroll
@@ -291,7 +296,7 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
     }
 }
 
-// Wide path (at least 192 output tiles, packed rows 16-byte aligned, K % 16 == 0): the
+// Wide path (at least 144 output tiles, code rows 16-byte aligned (K % 16 == 0), packed rows of any alignment): the
 // workgroup owns a 256 (m) x 256 (n) output tile; wave w owns weight rows
 // [64 w, 64 w + 64) of it against all 256 code rows: 2 x 8 MFMA tiles of
 // 32 x 32 (256 int32 accumulators per lane), one workgroup per CU.
@@ -317,11 +322,12 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
 // LDS traffic per MFMA is ~0.7 KB (operand reads 0.5, table reads 0.2)
 // against the ~1 KB one CU delivers per MFMA of each of its four SIMDs.
 constexpr int kWdM = 256, kWdN = 256;
-// The wide kernel runs one workgroup per CU; below ~3/4 of MI355X's 256 CUs in
-// 256 x 256 tiles the 128 x 128 kernel (more, smaller workgroups) is faster:
-// measured 1024 x 512 x 2560 19.3 vs 39.8 us, 4096 x 2048 38.5 vs 44.3 us, and
-// 6912 x 2048 (216 tiles) 73.7 vs 49.7 us.
-constexpr uint64_t kWdMinTiles = 192;
+// The wide kernel runs one workgroup per CU; below 144 tiles of 256 x 256
+// the 128 x 128 kernel (more, smaller workgroups) is faster: measured wide
+// against 128 x 128 at 4096 x 2048 x 2560 (128 tiles) 45.9 vs 39.7 us, and at
+// 3072 x 3072 x 2560 (144) 41.2 vs 49.0, 2560 x 4096 x 6912 (160, unaligned
+// rows) 107.1 vs 133.6, 6912 x 2048 (216) 49.7 vs 73.7.
+constexpr uint64_t kWdMinTiles = 144;
 constexpr int kWdPitch = 176;
 constexpr int kWdCopies = 32;
 constexpr size_t kWdBBytes = (size_t)kWdN * kWdPitch;           // one code buffer
@@ -385,11 +391,17 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     const uintptr_t a_hi = reinterpret_cast<uintptr_t>(p.a) + (uintptr_t)p.m * p.kp;
     // A window past kp (the second half of a last step) reads the row's
     // first window: it lies wholly past k, so its trits are zeroed below.
-    // Unaligned rows: the five dwords around the window, shifted into place;
-    // a window that straddles the row's end (last step only) takes the next
-    // row's bytes, at columns >= k, zeroed below as well; only where the
-    // five dwords would pass the matrix's end are the bytes read one by one.
-    auto load_a = [&](uint32_t kt, u32x4 (&av)[2]) {
+    // Unaligned rows: the 20 bytes from the dword boundary below the window
+    // (av and ae), shifted into place by the row's byte offset sh only where
+    // the step decodes them (align_a), so that no wait on these loads -- whose
+    // counter the code tiles' loads share -- lands in the step that issues
+    // them.  A window that straddles the row's end (last step only) takes the
+    // next row's bytes, at columns >= k, zeroed below as well; only where the
+    // 20 bytes would pass the matrix's end are they read one by one.
+    uint32_t sh[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) sh[i] = (uint32_t)(reinterpret_cast<uintptr_t>(arow[i]) & 3u);
+    auto load_a = [&](uint32_t kt, u32x4 (&av)[2], uint32_t (&ae)[2]) {
         const uint32_t ab = kt * kTmKp + 16u * h;
         const uint32_t abc = ab < p.kp ? ab : 0u;
 #pragma unroll
@@ -398,27 +410,37 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
                 av[i] = *reinterpret_cast<const u32x4*>(arow[i] + abc);
                 continue;
             }
-            const uintptr_t wa = reinterpret_cast<uintptr_t>(arow[i] + abc);
-            const uintptr_t w0 = wa & ~(uintptr_t)3;
+            const uintptr_t w0 = reinterpret_cast<uintptr_t>(arow[i] + abc) & ~(uintptr_t)3;
             if (__builtin_expect(w0 + 20u <= a_hi, 1)) {
-                const uint32_t* d = reinterpret_cast<const uint32_t*>(w0);
-                const uint32_t d0 = d[0], d1 = d[1], d2 = d[2], d3 = d[3], d4 = d[4];
-                const uint32_t sh = (uint32_t)(wa & 3u);
-                av[i] = u32x4{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
-                              __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh)};
+                av[i] = *reinterpret_cast<const u32x4_a4*>(w0);
+                ae[i] = *reinterpret_cast<const uint32_t*>(w0 + 16);
             } else {
-                uint32_t w[4];
+                uint32_t w[5];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < 5; ++q) {
                     w[q] = 0;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const uintptr_t o = wa + 4 * q + e;
+                        const uintptr_t o = w0 + 4 * q + e;
                         w[q] |= (o < a_hi ? (uint32_t)*reinterpret_cast<const uint8_t*>(o) : 0u) << (8 * e);
                     }
                 }
                 av[i] = u32x4{w[0], w[1], w[2], w[3]};
+                ae[i] = w[4];
             }
+        }
+    };
+    auto align_a = [&](const u32x4 (&av)[2], const uint32_t (&ae)[2], u32x4 (&aa)[2]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            if (kAlignedA) {
+                aa[i] = av[i];
+                continue;
+            }
+            aa[i] = u32x4{__builtin_amdgcn_alignbyte(av[i][1], av[i][0], sh[i]),
+                          __builtin_amdgcn_alignbyte(av[i][2], av[i][1], sh[i]),
+                          __builtin_amdgcn_alignbyte(av[i][3], av[i][2], sh[i]),
+                          __builtin_amdgcn_alignbyte(ae[i], av[i][3], sh[i])};
         }
     };
     // Code slots of this wave: slot s (16 bytes) of a tile is row s / 11,
@@ -549,7 +571,10 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     using S3 = std::integral_constant<int, 3>;
     using S4 = std::integral_constant<int, 4>;
     auto kstep = [&](uint32_t kt, const uint32_t (&cur)[2][20], uint32_t (&nxt)[2][20], i32x4 (&bx)[8],
-                     i32x4 (&by)[8], const u32x4 (&av)[2], u32x4 (&av2)[2]) {
+                     i32x4 (&by)[8], const u32x4 (&avr)[2], const uint32_t (&aer)[2], u32x4 (&av2)[2],
+                     uint32_t (&ae2)[2]) {
+        u32x4 av[2];
+        align_a(avr, aer, av);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -557,7 +582,7 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
         mgroup(S0(), kt, cur, nxt, bx, by, av);
         mgroup(S1(), kt, cur, nxt, by, bx, av);
         mgroup(S2(), kt, cur, nxt, bx, by, av);
-        if (kt + 2 < nkt) load_a(kt + 2, av2);
+        if (kt + 2 < nkt) load_a(kt + 2, av2, ae2);
         mgroup(S3(), kt, cur, nxt, by, bx, av);
         mgroup(S4(), kt, cur, nxt, bx, by, av);
         if (k_tail && kt + 2 == nkt) mask_tail(kt + 1, nxt);
@@ -572,22 +597,27 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     };
 
     u32x4 ava[2], avb[2];
-    load_a(0, ava);
+    uint32_t aea[2] = {0u, 0u}, aeb[2] = {0u, 0u};
+    load_a(0, ava, aea);
     dma_b(0, 0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // table filled, first code tile staged
     uint32_t cura[2][20], curb[2][20];
-    decode_all(ava, cura);
+    {
+        u32x4 a0[2];
+        align_a(ava, aea, a0);
+        decode_all(a0, cura);
+    }
     if (k_tail && nkt == 1) mask_tail(0, cura);
-    if (nkt > 1) load_a(1, ava);
+    if (nkt > 1) load_a(1, ava, aea);
     i32x4 bfx[8], bfy[8];
     read_b(0, 0, bfx);
     uint32_t kt = 0;
     for (; kt + 1 < nkt; kt += 2) {
-        kstep(kt, cura, curb, bfx, bfy, ava, avb);
-        kstep(kt + 1, curb, cura, bfy, bfx, avb, ava);
+        kstep(kt, cura, curb, bfx, bfy, ava, aea, avb, aeb);
+        kstep(kt + 1, curb, cura, bfy, bfx, avb, aeb, ava, aea);
     }
-    if (kt < nkt) kstep(kt, cura, curb, bfx, bfy, ava, avb);
+    if (kt < nkt) kstep(kt, cura, curb, bfx, bfy, ava, aea, avb, aeb);
 
     // Epilogue: ((float)acc * sa[m]) * sq[n].  Accumulator register q of lane
     // l holds row 8 (q / 4) + 4 (l / 32) + q % 4, column l % 32 of its 32 x 32
@@ -678,11 +708,7 @@ __global__ __launch_bounds__(kWaves * kWave) void ternary_i8_skinny_kernel(TernA
         const uintptr_t wa = reinterpret_cast<uintptr_t>(arow8 + ab);
         const uintptr_t w0 = wa & ~(uintptr_t)3;
         if (row_ok && ab + 16u <= p.kp && w0 + 20u <= a_hi) {
-            const uint32_t* d = reinterpret_cast<const uint32_t*>(w0);
-            const uint32_t d0 = d[0], d1 = d[1], d2 = d[2], d3 = d[3], d4 = d[4];
-            const uint32_t sh = (uint32_t)(wa & 3u);
-            return u32x4{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
-                         __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh)};
+            return load16_window(wa);
         }
         uint32_t w[4];
 #pragma unroll

@@ -713,7 +713,7 @@ def test_ternary_matmul_i8_small_n(m, n, k):
 @pytest.mark.parametrize("m,n,k", [(4096, 3072, 640), (4100, 3000, 560), (6400, 2000, 320), (3333, 3900, 80),
                                    (4096, 3072, 160), (300, 49152, 160), (49200, 300, 160)])
 def test_ternary_matmul_i8_wide_tiles(m, n, k):
-    """The wide path (at least 192 output tiles of 256 x 256, 16-byte packed
+    """The wide path (at least 144 output tiles of 256 x 256, 16-byte packed
     rows; per-lane table decode): whole and ragged tiles, a partial last K
     step (k % 160 != 0), a partial single step and a whole one; bit-exact against the oracle on
     arbitrary packed bytes (bytes >= 243 included)."""
@@ -777,7 +777,8 @@ def test_ternary_matmul_i8_full_size_and_pipeline():
 
 
 @pytest.mark.parametrize("m,n,k,offset", [(300, 49152, 176, 0), (49200, 300, 176, 0), (4100, 3000, 336, 0),
-                                          (300, 49152, 160, 1), (4096, 3072, 640, 3)])
+                                          (300, 49152, 160, 1), (4096, 3072, 640, 3), (2560, 4096, 336, 0),
+                                          (3072, 3072, 336, 2)])
 def test_ternary_matmul_i8_wide_tiles_unaligned_rows(m, n, k, offset):
     """The wide path on packed rows that are not 16-byte aligned: K = 176 and
     336 (rows of 36 and 68 bytes: a row's last window reaches into the next
