@@ -74,18 +74,8 @@ struct TernArgs {
     uint32_t splits, kt_per;  // split-K: K-tile ranges of kt_per per workgroup
 };
 
-// The 16 bytes at byte address wa (any alignment): one dwordx4 at the dword
-// boundary below (global loads need dword alignment only) and the dword
-// after it, shifted into place.  Reads the 20 bytes from wa & ~3.
+// Sixteen bytes at a dword boundary: global loads need dword alignment only.
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
-__device__ __forceinline__ u32x4 load16_window(uintptr_t wa) {
-    const uintptr_t w0 = wa & ~(uintptr_t)3;
-    const u32x4_a4 lo = *reinterpret_cast<const u32x4_a4*>(w0);
-    const uint32_t d4 = *reinterpret_cast<const uint32_t*>(w0 + 16);
-    const uint32_t sh = (uint32_t)(wa & 3u);
-    return u32x4{__builtin_amdgcn_alignbyte(lo[1], lo[0], sh), __builtin_amdgcn_alignbyte(lo[2], lo[1], sh),
-                 __builtin_amdgcn_alignbyte(lo[3], lo[2], sh), __builtin_amdgcn_alignbyte(d4, lo[3], sh)};
-}
 
 // Five trits of byte b as int8 in the low 40 bits (byte j = trit j).
 __device__ __forceinline__ uint64_t trit_lut_entry(uint32_t b) {
@@ -151,69 +141,70 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
 
     const uintptr_t a_hi = reinterpret_cast<uintptr_t>(p.a) + (uintptr_t)p.m * p.kp;
     const uintptr_t q_hi = reinterpret_cast<uintptr_t>(p.q) + (uintptr_t)p.n * p.k;
-    auto load_b = [&](uint32_t kt, u32x4* bv) {
+    // Unaligned rows (packed weights) and code rows (K % 16 != 0 or an
+    // unaligned q): each 16-byte piece is loaded as the 20 bytes from the
+    // dword boundary below it (x and its fifth dword e) and shifted into
+    // place only when it is staged, after the barrier that waits for the
+    // loads anyway: a shift right after the loads would wait on every load
+    // in flight.  The shift is fixed per piece slot (pieces start at
+    // multiples of 16 bytes of a row).  Only where the 20 bytes would pass a
+    // matrix's end are they read byte by byte.  Code bytes at columns >= k
+    // (and code rows past n, read clamped to row n - 1) are zeroed at
+    // staging; weight bytes past a row's end meet only those zero codes.
+    auto load20 = [&](uintptr_t w0, uintptr_t hi, u32x4& x, uint32_t& e) {
+        if (__builtin_expect(w0 + 20u <= hi, 1)) {
+            x = *reinterpret_cast<const u32x4_a4*>(w0);
+            e = *reinterpret_cast<const uint32_t*>(w0 + 16);
+        } else {
+            uint32_t w[5];
+#pragma unroll
+            for (int d = 0; d < 5; ++d) {
+                w[d] = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uintptr_t o = w0 + 4 * d + j;
+                    w[d] |= (o < hi ? (uint32_t)*reinterpret_cast<const uint8_t*>(o) : 0u) << (8 * j);
+                }
+            }
+            x = u32x4{w[0], w[1], w[2], w[3]};
+            e = w[4];
+        }
+    };
+    auto shift20 = [](const u32x4& x, uint32_t e, uint32_t sh) {
+        return u32x4{__builtin_amdgcn_alignbyte(x[1], x[0], sh), __builtin_amdgcn_alignbyte(x[2], x[1], sh),
+                     __builtin_amdgcn_alignbyte(x[3], x[2], sh), __builtin_amdgcn_alignbyte(e, x[3], sh)};
+    };
+    const uint32_t sh_a = (uint32_t)(reinterpret_cast<uintptr_t>(arow8) & 3u);
+    uint32_t sh_b[5];
+    const int8_t* brow[5];
+#pragma unroll
+    for (int u = 0; u < 5; ++u) {
+        const int c = t + kTmBlock * u;
+        const uint32_t rowc = min(n0 + (uint32_t)(c / 10), p.n - 1u);
+        brow[u] = p.q + (uint64_t)rowc * p.k + 16u * (uint32_t)(c % 10);
+        sh_b[u] = (uint32_t)(reinterpret_cast<uintptr_t>(brow[u]) & 3u);
+    }
+    auto load_b = [&](uint32_t kt, u32x4* bv, uint32_t* be) {
 #pragma unroll
         for (int u = 0; u < 5; ++u) {
             const int c = t + kTmBlock * u;
             const int row = c / 10, piece = c % 10;
             const uint32_t kb = kt * kTmK + 16u * piece;
-            const bool ok = n0 + row < p.n && kb < p.k;
-            const int8_t* src = p.q + (uint64_t)(n0 + row) * p.k + kb;
             if (kAlignedB) {
-                bv[u] = ok ? *reinterpret_cast<const u32x4*>(src) : zero4;
+                const bool ok = n0 + row < p.n && kb < p.k;
+                bv[u] = ok ? *reinterpret_cast<const u32x4*>(p.q + (uint64_t)(n0 + row) * p.k + kb) : zero4;
                 continue;
             }
-            // code rows not 16-byte aligned (K % 16 != 0 or an unaligned q):
-            // the five dwords around the piece, shifted into place; a piece
-            // that reaches past k, or whose dwords would pass the codes' end,
-            // byte by byte with zeros at columns >= k
-            const uintptr_t wa = reinterpret_cast<uintptr_t>(src);
-            const uintptr_t w0 = wa & ~(uintptr_t)3;
-            if (ok && kb + 16u <= p.k && w0 + 20u <= q_hi) {
-                bv[u] = load16_window(wa);
-            } else {
-                uint32_t w[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    w[q] = 0;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const uint32_t o = kb + 4 * q + e;
-                        w[q] |= (ok && o < p.k ? (uint32_t)(uint8_t)src[4 * q + e] : 0u) << (8 * e);
-                    }
-                }
-                bv[u] = u32x4{w[0], w[1], w[2], w[3]};
-            }
+            load20(reinterpret_cast<uintptr_t>(brow[u] + kt * kTmK) & ~(uintptr_t)3, q_hi, bv[u], be[u]);
         }
     };
-    auto load_tile = [&](uint32_t kt, u32x4& av, u32x4* bv) {
+    auto load_tile = [&](uint32_t kt, u32x4& av, uint32_t& ae, u32x4* bv, uint32_t* be) {
         const uint32_t ab = kt * kTmKp + 16u * ah;  // packed byte offset
-        if (kAlignedA) {
+        if (kAlignedA)
             av = (arow_ok && ab < p.kp) ? arow[ab >> 4] : zero_bytes;
-            load_b(kt, bv);
-            return;
-        }
-        // unaligned rows: the five dwords around the 16 bytes, shifted (the
-        // row's last partial piece and the matrix's last bytes byte by byte)
-        const uintptr_t wa = reinterpret_cast<uintptr_t>(arow8 + ab);
-        const uintptr_t w0 = wa & ~(uintptr_t)3;
-        if (arow_ok && ab + 16u <= p.kp && w0 + 20u <= a_hi) {
-            av = load16_window(wa);
-        } else {
-            uint32_t w[4];
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                w[d] = 0;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t o = ab + 4 * d + e;
-                    const uint32_t b = (arow_ok && o < p.kp) ? arow8[o] : kZeroByte;
-                    w[d] |= b << (8 * e);
-                }
-            }
-            av = u32x4{w[0], w[1], w[2], w[3]};
-        }
-        load_b(kt, bv);
+        else
+            load20(reinterpret_cast<uintptr_t>(arow8 + ab) & ~(uintptr_t)3, a_hi, av, ae);
+        load_b(kt, bv, be);
     };
 
     i32x16 acc[2][2];
@@ -225,9 +216,27 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
     u32x4 av, bv[5];
-    load_tile(kt_lo, av, bv);
+    uint32_t ae = 0u, be[5] = {0u, 0u, 0u, 0u, 0u};
+    load_tile(kt_lo, av, ae, bv, be);
     for (uint32_t kt = kt_lo; kt < nkt; ++kt) {
         __syncthreads();  // previous tile's MFMA reads (and the LUT fill) are done
+        if (!kAlignedA) av = shift20(av, ae, sh_a);
+        if (!kAlignedB) {
+#pragma unroll
+            for (int u = 0; u < 5; ++u) {
+                const int c = t + kTmBlock * u;
+                const int row = c / 10, piece = c % 10;
+                // bytes of the piece to keep: columns below k of a row below n
+                const int keep = n0 + row < p.n ? (int)p.k - (int)(kt * kTmK + 16u * piece) : 0;
+                u32x4 x = shift20(bv[u], be[u], sh_b[u]);
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const int kd = keep - 4 * d;
+                    x[d] &= kd >= 4 ? 0xffffffffu : (kd <= 0 ? 0u : (0xffffffffu >> (8 * (4 - kd))));
+                }
+                bv[u] = x;
+            }
+        }
         // decode 16 packed bytes -> 80 trit bytes, little-endian in 20 dwords
         uint32_t out[20];
 #pragma unroll
@@ -253,7 +262,7 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
             *reinterpret_cast<u32x4*>(Bs + row * kTmPitch + 16 * piece) = bv[u];
         }
         __syncthreads();
-        if (kt + 1 < nkt) load_tile(kt + 1, av, bv);
+        if (kt + 1 < nkt) load_tile(kt + 1, av, ae, bv, be);
 #pragma unroll
         for (int s = 0; s < 5; ++s) {
             const int koff = 32 * s + 16 * (lane >> 5);
@@ -701,27 +710,33 @@ __global__ __launch_bounds__(kWaves * kWave) void ternary_i8_skinny_kernel(TernA
     const u32x4 zero_bytes = {kZeroByte * 0x01010101u, kZeroByte * 0x01010101u, kZeroByte * 0x01010101u,
                               kZeroByte * 0x01010101u};
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
-    auto load_a = [&](uint32_t kb) -> u32x4 {
+    // Unaligned rows: the 20 bytes from the dword boundary below the 16
+    // (x and its fifth dword e), shifted into place by the row's byte offset
+    // only when the block is decoded -- a shift right after the loads would
+    // wait for them (and the code loads behind them) before the MFMAs that
+    // are meant to cover them.  Bytes past a row's end meet only zero codes
+    // (code pieces at columns >= k are zero); only where the 20 bytes would
+    // pass the matrix's end are they read byte by byte.
+    const uint32_t sh_a = (uint32_t)(reinterpret_cast<uintptr_t>(arow8) & 3u);
+    auto load_a = [&](uint32_t kb, uint32_t& e) -> u32x4 {
         const uint32_t ab = kb * kTmKp + 16u * h;
         if (kAlignedA) return (row_ok && ab < p.kp) ? *reinterpret_cast<const u32x4*>(arow8 + ab) : zero_bytes;
-        // unaligned rows: the five dwords around the 16 bytes, shifted
-        const uintptr_t wa = reinterpret_cast<uintptr_t>(arow8 + ab);
-        const uintptr_t w0 = wa & ~(uintptr_t)3;
-        if (row_ok && ab + 16u <= p.kp && w0 + 20u <= a_hi) {
-            return load16_window(wa);
+        const uintptr_t w0 = reinterpret_cast<uintptr_t>(arow8 + ab) & ~(uintptr_t)3;
+        if (__builtin_expect(w0 + 20u <= a_hi, 1)) {
+            e = *reinterpret_cast<const uint32_t*>(w0 + 16);
+            return *reinterpret_cast<const u32x4_a4*>(w0);
         }
-        uint32_t w[4];
+        uint32_t w[5];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
+        for (int d = 0; d < 5; ++d) {
             w[d] = 0;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t o = ab + 4 * d + e;
-                const bool ok = row_ok && o < p.kp;
-                const uint32_t b = arow8[ok ? o : 0u];
-                w[d] |= (ok ? b : kZeroByte) << (8 * e);
+            for (int j = 0; j < 4; ++j) {
+                const uintptr_t o = w0 + 4 * d + j;
+                w[d] |= (o < a_hi ? (uint32_t)*reinterpret_cast<const uint8_t*>(o) : 0u) << (8 * j);
             }
         }
+        e = w[4];
         return u32x4{w[0], w[1], w[2], w[3]};
     };
     // piece u of this lane: row (u * 64 + lane) / 10, 16-byte piece % 10
@@ -744,9 +759,10 @@ __global__ __launch_bounds__(kWaves * kWave) void ternary_i8_skinny_kernel(TernA
     __syncthreads();  // table filled
     uint32_t kb = (uint32_t)wave;
     u32x4 av = zero_bytes;
+    uint32_t ae = 0u;
     u32x4 bv[kPieces];
     if (kb < nkb) {
-        av = load_a(kb);
+        av = load_a(kb, ae);
         load_b(kb, bv);
     }
     for (; kb < nkb; kb += kWaves) {
@@ -761,6 +777,9 @@ __global__ __launch_bounds__(kWaves * kWave) void ternary_i8_skinny_kernel(TernA
         uint32_t out[20];
 #pragma unroll
         for (int d = 0; d < 20; ++d) out[d] = 0;
+        if (!kAlignedA)
+            av = u32x4{__builtin_amdgcn_alignbyte(av[1], av[0], sh_a), __builtin_amdgcn_alignbyte(av[2], av[1], sh_a),
+                       __builtin_amdgcn_alignbyte(av[3], av[2], sh_a), __builtin_amdgcn_alignbyte(ae, av[3], sh_a)};
         uint64_t lv[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) lv[i] = lut[(av[i >> 2] >> (8 * (i & 3))) & 0xffu];
@@ -772,7 +791,7 @@ __global__ __launch_bounds__(kWaves * kWave) void ternary_i8_skinny_kernel(TernA
         }
         const uint32_t kn = kb + kWaves;
         if (kn < nkb) {
-            av = load_a(kn);
+            av = load_a(kn, ae);
             load_b(kn, bv);
         }
         wave_lds_sync();
