@@ -776,6 +776,27 @@ def test_ternary_matmul_i8_full_size_and_pipeline():
     assert_bitexact(got[:96, :rows].cpu().numpy(), ref, "prequant -> ternary chain")
 
 
+@pytest.mark.parametrize("m,n,k", [(2560, 4096, 6912), (6912, 1024, 2563)])
+def test_ternary_matmul_i8_full_size_unaligned(m, n, k):
+    """Full-size shapes with unaligned rows: the FFN down-projection 6912 ->
+    2560 on 4096 tokens (1383-byte packed rows, 160 wide tiles) and K = 2563
+    (code rows not 16-byte aligned: the tile kernel's window code loads),
+    bit-exact against an f64 GEMM of the decoded trits (exact for these
+    integer sums) with the same f32 epilogue."""
+    from inputs import int8_codes, ternary_weights
+
+    log(f"ternary_matmul_i8 full size unaligned m={m} n={n} k={k}")
+    p, sa = ternary_weights(m, k, 23)
+    q = int8_codes(n, k, 24)
+    sq = np.abs(normal((n,), 25, 0.02, 0.005))
+    c = rocm.rocm_ternary_matmul_i8(DEV, up(p), up(sa), up(q), up(sq), m, n, k)
+    got = torch.from_numpy(down(c, np.float32, (m, n))).cuda()
+    t = torch.from_numpy(oracle.unpack_trits(p, k)).cuda().double()
+    acc = (t @ torch.from_numpy(q).cuda().double().T).float()
+    want = (acc * torch.from_numpy(sa).cuda()[:, None]) * torch.from_numpy(sq).cuda()[None, :]
+    assert torch.equal(got, want), f"ternary_matmul_i8 {m}x{n}x{k} vs f64 GEMM"
+
+
 @pytest.mark.parametrize("m,n,k,offset", [(300, 49152, 176, 0), (49200, 300, 176, 0), (4100, 3000, 336, 0),
                                           (300, 49152, 160, 1), (4096, 3072, 640, 3), (2560, 4096, 336, 0),
                                           (3072, 3072, 336, 2)])
