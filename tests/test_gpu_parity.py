@@ -975,6 +975,45 @@ def test_ternary_matmul_f32_subnormal_activations(n):
     got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
     assert_bitexact(got, want, f"ternary_matmul_f32 subnormal n={n}")
 
+def _offset_buffer(arr: np.ndarray, offset: int, dtype) -> HipBuffer:
+    """Device copy of arr starting `offset` bytes past a 16-byte boundary."""
+    t = torch.empty(arr.nbytes + offset, dtype=torch.uint8, device="cuda")
+    t[offset:].copy_(torch.from_numpy(np.ascontiguousarray(arr).view(np.uint8).ravel()))
+    return HipBuffer.from_tensor(t[offset:])
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_ternary_matmuls_random_shapes(seed):
+    """Seeded random shapes and base offsets for both ternary matmuls, so that
+    every dispatch path (decode-step, row-broadcast at each tile width and
+    rows-per-lane count, small-n, skinny, split-K and 128 x 128 tiles with
+    aligned and unaligned weight and code rows) meets ragged sizes:
+    bit-exact against the oracle on arbitrary packed bytes."""
+    from inputs import int8_codes, raw_packed
+
+    r = np.random.default_rng(1000 + seed)
+    for case in range(8):
+        m = int(r.integers(1, 3000))
+        n = int(r.choice([1, 2, 3, 4, 5, 8, 9, 16, 17, 31, 33, 64, 65, 100, 200, 300]))
+        k = int(r.integers(1, 3000))
+        while m * n * k > 150_000_000:
+            m = max(1, m // 2)
+        oa, ob = int(r.integers(0, 4)), 4 * int(r.integers(0, 4))
+        log(f"ternary random seed={seed} case={case} m={m} n={n} k={k} a+{oa} b+{ob}")
+        p = raw_packed(m, k, 17 * seed + case)
+        sa = normal((m,), 50 + case, 1.0, 0.1)
+        bf = normal((k, n), 60 + case)
+        got = down(rocm.rocm_ternary_matmul_f32(DEV, _offset_buffer(p, oa, np.uint8), up(sa),
+                                                _offset_buffer(bf, ob, np.float32), m, n, k), np.float32, (m, n))
+        assert_bitexact(got, oracle.ternary_matmul(p, sa, bf, m, n, k), f"f32 {m}x{n}x{k}")
+        q = int8_codes(n, k, 70 + case)
+        sq = np.abs(normal((n,), 80 + case, 0.02, 0.005))
+        oq = int(r.integers(0, 4))
+        got = down(rocm.rocm_ternary_matmul_i8(DEV, _offset_buffer(p, oa, np.uint8), up(sa),
+                                               _offset_buffer(q, oq, np.int8), up(sq), m, n, k), np.float32, (m, n))
+        assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), f"i8 {m}x{n}x{k}")
+
+
 def test_ternary_matmul_f32_row_ranges():
     """A packed matrix of more than 2 GiB (32769 rows of 65536 packed bytes):
     the row-broadcast kernel runs over row ranges of less than 2 GiB each;
