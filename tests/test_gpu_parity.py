@@ -45,6 +45,13 @@ def unaligned(arr: np.ndarray) -> HipBuffer:
     return HipBuffer.from_tensor(t[1:])
 
 
+def _offset_buffer(arr: np.ndarray, offset: int) -> HipBuffer:
+    """Device copy of arr starting `offset` bytes past a 16-byte boundary."""
+    t = torch.empty(arr.nbytes + offset, dtype=torch.uint8, device="cuda")
+    t[offset:].copy_(torch.from_numpy(np.ascontiguousarray(arr).view(np.uint8).ravel()))
+    return HipBuffer.from_tensor(t[offset:])
+
+
 # ----------------------------------------------------------------- RMSNorm
 RMS_SHAPES = [(1, 1), (3, 7), (2, 4), (5, 256), (17, 260), (6, 1000), (32, 2048), (9, 2560), (7, 4096),
               (3, 5000), (65, 512)]
@@ -94,6 +101,33 @@ def test_rms_norm_special_rows():
         got = down(rocm.rocm_rms_norm_f32(DEV, up(x), up(g), 6, cols, eps), np.float32, (6, cols))
         want = oracle.rms_norm(x, g, eps)
         assert_bitexact(got, want, f"special rows eps={eps}")
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_row_kernels_random_shapes(seed):
+    """Seeded random shapes and input offsets for RMSNorm and the BitLinear
+    pre-quant (every column-chunk count of the vector kernels, one or four
+    waves per workgroup, the scalar path for odd widths or unaligned inputs),
+    with random row scales spanning many binades: bit-exact against the
+    oracle (normalised values, int8 codes and scales)."""
+    r = np.random.default_rng(2000 + seed)
+    for case in range(6):
+        rows = int(r.choice([1, 2, 7, 31, 64, 100, 255, 256, 257, 700]))
+        cols = int(r.choice([4, 8, 60, 256, 260, 512, 1000, 1024, 2048, 2560, 3000, 4096, 6144, 8192]))
+        if r.random() < 0.2:
+            cols += int(r.integers(1, 4))  # odd width: scalar path
+        off = 4 * int(r.integers(0, 4)) if r.random() < 0.3 else 0
+        x = normal((rows, cols), 100 * seed + case)
+        x *= np.exp2(r.integers(-60, 60, size=(rows, 1))).astype(np.float32)
+        g = normal((cols,), 7 * seed + case, 1.0, 0.02)
+        log(f"row kernels random seed={seed} case={case} rows={rows} cols={cols} x+{off}")
+        xb = _offset_buffer(x, off) if off else up(x)
+        got = down(rocm.rocm_rms_norm_f32(DEV, xb, up(g), rows, cols, 1e-6), np.float32, (rows, cols))
+        assert_bitexact(got, oracle.rms_norm(x, g, 1e-6), f"rms_norm {rows}x{cols}")
+        q, sc = rocm.rocm_rms_norm_quant_i8(DEV, xb, up(g), rows, cols, 1e-6)
+        wq, ws = oracle.rms_norm_quant_i8(x, g, 1e-6)
+        assert down(sc, np.float32, (rows,)).tobytes() == ws.tobytes(), f"scales {rows}x{cols}"
+        assert (down(q, np.int8, (rows, cols)) == wq).all(), f"codes {rows}x{cols}"
 
 
 # ------------------------------------------------------- RMSNorm + SiLU gate
@@ -975,13 +1009,6 @@ def test_ternary_matmul_f32_subnormal_activations(n):
     got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
     assert_bitexact(got, want, f"ternary_matmul_f32 subnormal n={n}")
 
-def _offset_buffer(arr: np.ndarray, offset: int, dtype) -> HipBuffer:
-    """Device copy of arr starting `offset` bytes past a 16-byte boundary."""
-    t = torch.empty(arr.nbytes + offset, dtype=torch.uint8, device="cuda")
-    t[offset:].copy_(torch.from_numpy(np.ascontiguousarray(arr).view(np.uint8).ravel()))
-    return HipBuffer.from_tensor(t[offset:])
-
-
 @pytest.mark.parametrize("seed", range(20))
 def test_ternary_matmuls_random_shapes(seed):
     """Seeded random shapes and base offsets for both ternary matmuls, so that
@@ -1003,14 +1030,14 @@ def test_ternary_matmuls_random_shapes(seed):
         p = raw_packed(m, k, 17 * seed + case)
         sa = normal((m,), 50 + case, 1.0, 0.1)
         bf = normal((k, n), 60 + case)
-        got = down(rocm.rocm_ternary_matmul_f32(DEV, _offset_buffer(p, oa, np.uint8), up(sa),
-                                                _offset_buffer(bf, ob, np.float32), m, n, k), np.float32, (m, n))
+        got = down(rocm.rocm_ternary_matmul_f32(DEV, _offset_buffer(p, oa), up(sa),
+                                                _offset_buffer(bf, ob), m, n, k), np.float32, (m, n))
         assert_bitexact(got, oracle.ternary_matmul(p, sa, bf, m, n, k), f"f32 {m}x{n}x{k}")
         q = int8_codes(n, k, 70 + case)
         sq = np.abs(normal((n,), 80 + case, 0.02, 0.005))
         oq = int(r.integers(0, 4))
-        got = down(rocm.rocm_ternary_matmul_i8(DEV, _offset_buffer(p, oa, np.uint8), up(sa),
-                                               _offset_buffer(q, oq, np.int8), up(sq), m, n, k), np.float32, (m, n))
+        got = down(rocm.rocm_ternary_matmul_i8(DEV, _offset_buffer(p, oa), up(sa),
+                                               _offset_buffer(q, oq), up(sq), m, n, k), np.float32, (m, n))
         assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), f"i8 {m}x{n}x{k}")
 
 
