@@ -387,6 +387,36 @@ def test_rope_small(interleaved, batch, seq, heads, hd, start):
     assert_close(got, want, what="rope")
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_rope_and_embedding_random_shapes(seed):
+    """Seeded random shapes for RoPE (both layouts, every head width the
+    per-lane kernel takes and some it does not, start positions, table and
+    data offsets) and for the embedding gather (row widths on each side of
+    the one-float4 kernel's limits, ids out of range): RoPE within the
+    element-wise tolerance, the gather bit-exact."""
+    r = np.random.default_rng(3000 + seed)
+    for case in range(6):
+        hd = int(r.choice([2, 4, 6, 8, 16, 32, 64, 128, 256, 96, 200]))
+        batch, seq, heads = int(r.integers(1, 4)), int(r.integers(1, 300)), int(r.integers(1, 9))
+        start, interleaved = int(r.integers(0, 5000)), bool(r.integers(0, 2))
+        off = 4 * int(r.integers(0, 4)) if r.random() < 0.3 else 0
+        log(f"rope random seed={seed} case={case} b={batch} s={seq} h={heads} d={hd} start={start} "
+            f"interleaved={interleaved} x+{off}")
+        x = normal((batch, seq, heads, hd), 500 * seed + case)
+        buf = _offset_buffer(x, off) if off else up(x)
+        inv = rocm.rocm_rope_inv_freq_f32(DEV, hd, 10000.0)
+        rocm.rocm_rope_f32(DEV, buf, inv, batch, seq, heads, hd, start, interleaved)
+        assert_close(down(buf, np.float32, x.shape), oracle.rope(x, start, 10000.0, interleaved), what="rope random")
+        vocab = int(r.integers(1, 3000))
+        dim = int(r.choice([1, 3, 4, 8, 100, 256, 1000, 4096, 4100, 8192, 12288]))
+        n_ids = int(r.integers(1, 300))
+        log(f"embedding random seed={seed} case={case} vocab={vocab} dim={dim} n={n_ids}")
+        table = normal((vocab, dim), 600 * seed + case, 0.0, 0.02)
+        ids = r.integers(0, vocab + 3, size=n_ids).astype(np.int32)  # some past the vocabulary
+        out = rocm.rocm_embedding_f32(DEV, up(table), up(ids), n_ids, vocab, dim)
+        assert down(out, np.float32, (n_ids, dim)).tobytes() == oracle.embedding(table, ids).tobytes()
+
+
 def test_rope_unaligned_scalar_path():
     x = normal((2, 6, 3, 16), 5)
     buf = unaligned(x)
