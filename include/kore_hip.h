@@ -15,7 +15,10 @@
  *   - A call with zero elements of work returns 0 and launches nothing, as the
  *     reference CPU ops return empty tensors.
  *   - Pointers that are not 16-byte aligned, or rows whose length is not a
- *     multiple of 4 floats, take a scalar path with identical results.
+ *     multiple of 4 floats, take a scalar path with identical results (the
+ *     ternary matmuls read unaligned packed rows and code rows through
+ *     dword windows in their vector kernels; only an output that is not
+ *     4-byte aligned, or K = 0, takes their one-thread-per-output path).
  *   - Entry points are reentrant and keep no state between calls.
  *
  * Each declaration names the reference function it replaces (paths relative
