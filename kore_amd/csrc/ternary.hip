@@ -337,12 +337,23 @@ constexpr int kWdM = 256, kWdN = 256;
 // 3072 x 3072 x 2560 (144) 41.2 vs 49.0, 2560 x 4096 x 6912 (160, unaligned
 // rows) 107.1 vs 133.6, 6912 x 2048 (216) 49.7 vs 73.7.
 constexpr uint64_t kWdMinTiles = 144;
+constexpr uint64_t kCus = 256;  // MI355X compute units
 constexpr int kWdPitch = 176;
 constexpr int kWdCopies = 32;
-constexpr size_t kWdBBytes = (size_t)kWdN * kWdPitch;           // one code buffer
-constexpr size_t kWdLds = 2 * kWdBBytes + 256 * kWdCopies * 8;    // 155,648 bytes
-constexpr int kWdSlots = kWdBBytes / 16 / 4;                      // 16-byte slots per wave: 704
-constexpr int kWdDma = kWdSlots / kWave;                          // 11 loads per wave per step
+// A tile of NJ 32-column groups (NJ = 8: 256 columns; 6: 192): its code
+// buffer, LDS, and 16-byte code slots and loads per wave and step (the last
+// load covering only the slots left).
+template <int NJ> struct WideTile {
+    static constexpr int kN = 32 * NJ;
+    static constexpr size_t kBBytes = (size_t)kN * kWdPitch;
+    // the K loop's buffers and table, or the epilogue's four 32-row slabs of
+    // 264 floats, whichever is larger
+    static constexpr size_t kLoop = 2 * kBBytes + 256 * kWdCopies * 8;
+    static constexpr size_t kEpi = (size_t)4 * 32 * 264 * 4;
+    static constexpr size_t kLds = kLoop > kEpi ? kLoop : kEpi;
+    static constexpr int kSlots = (int)(kBBytes / 16 / 4);
+    static constexpr int kDma = (kSlots + kWave - 1) / kWave;
+};
 
 typedef __attribute__((address_space(3))) void* lds_vptr;
 typedef __attribute__((address_space(1))) void* glb_vptr;
@@ -355,10 +366,15 @@ __device__ __forceinline__ void splice_trits(uint32_t (&out)[20], int b, uint64_
     out[d + 1] |= (uint32_t)(v >> (32 - sh));
 }
 
-template <bool kAlignedA>
+template <bool kAlignedA, int NJ>
 __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
+    using Tile = WideTile<NJ>;
+    constexpr int kN = Tile::kN;
+    constexpr size_t kBB = Tile::kBBytes;
+    static_assert(Tile::kLds >= Tile::kEpi && Tile::kLds <= 160 * 1024, "wide kernel LDS");
+    constexpr int kSl = Tile::kSlots, kDm = Tile::kDma;
     extern __shared__ __attribute__((aligned(16))) uint8_t wlds[];
-    uint64_t* lut = reinterpret_cast<uint64_t*>(wlds + 2 * kWdBBytes);
+    uint64_t* lut = reinterpret_cast<uint64_t*>(wlds + 2 * kBB);
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
@@ -368,7 +384,7 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     // ceil(tn / 8) n-tiles, m-major inside a panel.  One XCD then holds about
     // one panel (its code rows once in its L2), and the workgroups it runs at
     // the same time share weight rows pairwise instead of each fetching its own.
-    const uint32_t tm_n = (p.m + kWdM - 1) / kWdM, tn_n = (p.n + kWdN - 1) / kWdN;
+    const uint32_t tm_n = (p.m + kWdM - 1) / kWdM, tn_n = (p.n + kN - 1) / kN;
     const uint32_t ntiles = tm_n * tn_n;
     const uint32_t per = (ntiles + kXcds - 1) / kXcds;
     const uint32_t work = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
@@ -376,7 +392,7 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     const uint32_t pw = (tn_n + kXcds - 1) / kXcds;
     const uint32_t panel = work / (tm_n * pw), within = work % (tm_n * pw);
     const uint32_t pwid = min(pw, tn_n - panel * pw);
-    const uint32_t m0 = (within / pwid) * kWdM, n0 = (panel * pw + within % pwid) * kWdN;
+    const uint32_t m0 = (within / pwid) * kWdM, n0 = (panel * pw + within % pwid) * kN;
 
     // Table: entry e, copy c at u64 index e * 32 + c (bank pair 2c).  Thread
     // e fills its entry's copies in a rotated order so that the 64 lanes of a
@@ -454,35 +470,37 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     };
     // Code slots of this wave: slot s (16 bytes) of a tile is row s / 11,
     // piece s % 11 (piece 10: the row's padding, filled with piece 0).
-    uint32_t boff[kWdDma], bp16[kWdDma];
+    uint32_t boff[kDm], bp16[kDm];
 #pragma unroll
-    for (int g = 0; g < kWdDma; ++g) {
-        const int slot = kWdSlots * wave + kWave * g + lane;
+    for (int g = 0; g < kDm; ++g) {
+        const int slot = kSl * wave + kWave * g + lane;
         const int row = slot / 11, piece = slot % 11;
         const uint32_t rowc = min(n0 + (uint32_t)row, p.n - 1u);
         bp16[g] = piece < 10 ? 16u * piece : 0u;
         boff[g] = rowc * p.k + bp16[g];
     }
     const bool k_tail = p.k % kTmK != 0;
-    // Code load g (0 .. kWdDma - 1) of step kt into buffer buf.
+    // Code load g (0 .. kDm - 1) of step kt into buffer buf (the last one
+    // only for the lanes whose slot exists).
     auto dma_one = [&](uint32_t kt, uint32_t buf, int g) {
         const int8_t* base = p.q + (uint64_t)kt * kTmK;
         const uint32_t rem = p.k - kt * kTmK;  // >= 16 bytes of this step per row
-        uint8_t* dst = wlds + buf * kWdBBytes + (size_t)kWdSlots * 16 * wave + kWave * 16 * g;
+        uint8_t* dst = wlds + buf * kBB + (size_t)kSl * 16 * wave + kWave * 16 * g;
         uint32_t off = boff[g];
         if (k_tail && bp16[g] >= rem) off -= bp16[g];
-        __builtin_amdgcn_global_load_lds((glb_vptr)(base + off), (lds_vptr)dst, 16, 0, 0);
+        if (kSl % kWave == 0 || g < kDm - 1 || kWave * g + lane < kSl)
+            __builtin_amdgcn_global_load_lds((glb_vptr)(base + off), (lds_vptr)dst, 16, 0, 0);
     };
     auto dma_b = [&](uint32_t kt, uint32_t buf) {
 #pragma unroll
-        for (int g = 0; g < kWdDma; ++g) dma_one(kt, buf, g);
+        for (int g = 0; g < kDm; ++g) dma_one(kt, buf, g);
     };
 
-    i32x16 acc[2][8];
+    i32x16 acc[2][NJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int q = 0; q < 16; ++q) acc[i][j][q] = 0;
 
@@ -509,10 +527,10 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     //     covered by the second half of the step's last MFMA group.
     // Steps are unrolled in pairs so that the double-buffered registers swap
     // names instead of being copied.
-    auto read_b = [&](uint32_t buf, int s, i32x4 (&bf)[8]) {
-        const uint8_t* bb = wlds + buf * kWdBBytes + r * kWdPitch + 80 * h + 16 * s;
+    auto read_b = [&](uint32_t buf, int s, i32x4 (&bf)[NJ]) {
+        const uint8_t* bb = wlds + buf * kBB + r * kWdPitch + 80 * h + 16 * s;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) bf[j] = *reinterpret_cast<const i32x4*>(bb + 32 * j * kWdPitch);
+        for (int j = 0; j < NJ; ++j) bf[j] = *reinterpret_cast<const i32x4*>(bb + 32 * j * kWdPitch);
     };
     auto decode_all = [&](const u32x4 (&av)[2], uint32_t (&dec)[2][20]) {
 #pragma unroll
@@ -534,9 +552,10 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     // burst they stall this wave's instruction stream for the time the vector
     // memory unit takes to accept them; issued in group 3 they have not
     // landed by the end of the step.
-    constexpr int kDmaAt[5] = {0, 4, 8, 11, 11};
+    // the code loads spread over MFMA groups 0 .. 2 (11 = 4 + 4 + 3; 9 = 3 + 3 + 3)
+    constexpr int kDmaAt[5] = {0, (kDm + 2) / 3, 2 * ((kDm + 2) / 3), kDm, kDm};
     auto mgroup = [&](auto S_, uint32_t kt, const uint32_t (&cur)[2][20], uint32_t (&nxt)[2][20],
-                      const i32x4 (&bc)[8], i32x4 (&bn)[8], const u32x4 (&av)[2]) {
+                      const i32x4 (&bc)[NJ], i32x4 (&bn)[NJ], const u32x4 (&av)[2]) {
         constexpr int s = decltype(S_)::value;
         constexpr int dlo = s < 4 ? kDmaAt[s] : 0, dhi = s < 4 ? kDmaAt[s + 1] : 0;
         const bool dma = kt + 1 < nkt;
@@ -557,7 +576,7 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
             const i32x4 af = {(int)cur[i][4 * s], (int)cur[i][4 * s + 1], (int)cur[i][4 * s + 2],
                               (int)cur[i][4 * s + 3]};
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
+            for (int j = 0; j < NJ; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bc[j], acc[i][j], 0, 0, 0);
         }
 #pragma unroll
@@ -567,7 +586,7 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
             for (int g = dlo; g < dhi; ++g) dma_one(kt + 1, (kt + 1) & 1u, g);
         }
 #pragma unroll
-        for (int g = 0; g < 8 * ni; ++g) {
+        for (int g = 0; g < NJ * ni; ++g) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             if (g < dhi - dlo) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
@@ -579,8 +598,8 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     using S2 = std::integral_constant<int, 2>;
     using S3 = std::integral_constant<int, 3>;
     using S4 = std::integral_constant<int, 4>;
-    auto kstep = [&](uint32_t kt, const uint32_t (&cur)[2][20], uint32_t (&nxt)[2][20], i32x4 (&bx)[8],
-                     i32x4 (&by)[8], const u32x4 (&avr)[2], const uint32_t (&aer)[2], u32x4 (&av2)[2],
+    auto kstep = [&](uint32_t kt, const uint32_t (&cur)[2][20], uint32_t (&nxt)[2][20], i32x4 (&bx)[NJ],
+                     i32x4 (&by)[NJ], const u32x4 (&avr)[2], const uint32_t (&aer)[2], u32x4 (&av2)[2],
                      uint32_t (&ae2)[2]) {
         u32x4 av[2];
         align_a(avr, aer, av);
@@ -602,7 +621,7 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
         read_b((kt + 1) & 1u, 0, by);
         const i32x4 af = {(int)cur[1][16], (int)cur[1][17], (int)cur[1][18], (int)cur[1][19]};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[1][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bx[j], acc[1][j], 0, 0, 0);
+        for (int j = 0; j < NJ; ++j) acc[1][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bx[j], acc[1][j], 0, 0, 0);
     };
 
     u32x4 ava[2], avb[2];
@@ -619,7 +638,7 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     }
     if (k_tail && nkt == 1) mask_tail(0, cura);
     if (nkt > 1) load_a(1, ava, aea);
-    i32x4 bfx[8], bfy[8];
+    i32x4 bfx[NJ], bfy[NJ];
     read_b(0, 0, bfx);
     uint32_t kt = 0;
     for (; kt + 1 < nkt; kt += 2) {
@@ -634,9 +653,9 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     // own LDS region (row pitch 264 floats: the two row groups of a write land
     // on disjoint banks) and writes it back a whole 1 KB output row per store
     // instruction, 16 bytes per lane.
-    float sqn[8];
+    float sqn[NJ];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) sqn[j] = p.sq[min(n0 + 32 * j + r, p.n - 1u)];
+    for (int j = 0; j < NJ; ++j) sqn[j] = p.sq[min(n0 + 32 * j + r, p.n - 1u)];
     constexpr int kEpPitch = 264;
     float* slab = reinterpret_cast<float*>(wlds) + wave * 32 * kEpPitch;
     const bool vec_out = (p.n & 3u) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15u) == 0;
@@ -650,12 +669,13 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
             const int row = 8 * (q >> 2) + 4 * h + (q & 3);
             const float sam = p.sa[min(mb + row, p.m - 1u)];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) slab[row * kEpPitch + 32 * j + r] = ((float)acc[i][j][q] * sam) * sqn[j];
+            for (int j = 0; j < NJ; ++j) slab[row * kEpPitch + 32 * j + r] = ((float)acc[i][j][q] * sam) * sqn[j];
         }
         __syncthreads();
         for (int row = 0; row < 32; ++row) {
             const uint32_t m = mb + row;
             if (m >= p.m) break;
+            if (4 * lane >= kN) continue;  // columns of the next tile
             const f32x4 v = *reinterpret_cast<const f32x4*>(slab + row * kEpPitch + 4 * lane);
             float* crow = p.c + (uint64_t)m * p.n;
             if (vec_out && ncol + 3 < p.n) {
@@ -2098,15 +2118,27 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
     }
     const uint64_t wide_tiles = ((m + kWdM - 1) / kWdM) * ((n + kWdN - 1) / kWdN);
     if (vec && wide_tiles >= kWdMinTiles && nk < (1ull << 31)) {
-        // Many output tiles: the wide kernel (one 256 x 256 tile per CU).
-        const uint64_t tiles = wide_tiles;
+        // Many output tiles: the wide kernel (one 256 x 256 tile per CU), or
+        // 256 x 192 tiles where the rounds of 256 CUs they need, at ~0.8 of a
+        // 256 x 256 tile's time each, are fewer.
+        const uint64_t t192 = ((m + kWdM - 1) / kWdM) * ((n + 191) / 192);
+        const uint64_t r192 = (t192 + kCus - 1) / kCus, r256 = (wide_tiles + kCus - 1) / kCus;
+        // (measured: 2560 x 8192 x 6912 215 -> 182 us, 2560 x 4096 x 6912 113 ->
+        // 103; with few K steps the narrower tile loses: 2600 x 4000 x 336
+        // 20.1 -> 22.3)
+        const bool n192 = 4 * r192 < 5 * r256 && (k + kTmK - 1) / kTmK >= 8;  // 0.8 r192 < r256
+        const uint64_t tiles = n192 ? t192 : wide_tiles;
         const uint64_t per = (tiles + kXcds - 1) / kXcds;
         if (per * kXcds > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
         const dim3 g((uint32_t)(per * kXcds));
-        if (kp % 16 == 0 && aligned16(a_packed))
-            hipLaunchKernelGGL((ternary_i8_wide_kernel<true>), g, dim3(256), kWdLds, s, p);
-        else
-            hipLaunchKernelGGL((ternary_i8_wide_kernel<false>), g, dim3(256), kWdLds, s, p);
+        const bool al = kp % 16 == 0 && aligned16(a_packed);
+        if (n192) {
+            if (al) hipLaunchKernelGGL((ternary_i8_wide_kernel<true, 6>), g, dim3(256), WideTile<6>::kLds, s, p);
+            else hipLaunchKernelGGL((ternary_i8_wide_kernel<false, 6>), g, dim3(256), WideTile<6>::kLds, s, p);
+        } else {
+            if (al) hipLaunchKernelGGL((ternary_i8_wide_kernel<true, 8>), g, dim3(256), WideTile<8>::kLds, s, p);
+            else hipLaunchKernelGGL((ternary_i8_wide_kernel<false, 8>), g, dim3(256), WideTile<8>::kLds, s, p);
+        }
         return launch_status();
     }
     if (k > 0 && c_ok) {

@@ -840,11 +840,13 @@ def test_ternary_matmul_i8_full_size_and_pipeline():
     assert_bitexact(got[:96, :rows].cpu().numpy(), ref, "prequant -> ternary chain")
 
 
-@pytest.mark.parametrize("m,n,k", [(2560, 4096, 6912), (6912, 1024, 2563)])
+@pytest.mark.parametrize("m,n,k", [(2560, 4096, 6912), (6912, 1024, 2563), (2560, 3900, 1280), (3072, 3072, 1360),
+                                   (2600, 4100, 1296)])
 def test_ternary_matmul_i8_full_size_unaligned(m, n, k):
-    """Full-size shapes with unaligned rows: the FFN down-projection 6912 ->
-    2560 on 4096 tokens (1383-byte packed rows, 160 wide tiles) and K = 2563
-    (code rows not 16-byte aligned: the tile kernel's window code loads),
+    """Full-size shapes: the FFN down-projection 6912 -> 2560 on 4096 tokens
+    (1383-byte packed rows, 256 x 192 wide tiles), K = 2563 (code rows not
+    16-byte aligned: the tile kernel's window code loads), and 256 x 192 tiles
+    with a partial last column tile, aligned and unaligned packed rows;
     bit-exact against an f64 GEMM of the decoded trits (exact for these
     integer sums) with the same f32 epilogue."""
     from inputs import int8_codes, ternary_weights
