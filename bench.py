@@ -4,9 +4,11 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME[,NAME]] [--no-cpu]
 
 A step is one launch of a fused kernel over one full BASELINE.json config with
-its inputs already resident in HBM.  The headline line is BASELINE configs[1]
-(RoPE over Q[8,2048,32,128] + K[8,2048,8,128], one fused Q+K launch); every
-other config is measured the same way and reported under "kernels".
+its inputs already resident in HBM.  The headline line is the largest
+BASELINE.json config that runs on one GPU, configs[2]'s SwiGLU over gate and
+up [16384, 14336] (2.8 GB per launch); every other config (RoPE Q+K, RMSNorm,
+GELU, the embedding gather, the pre-quant step) is measured the same way and
+reported under "kernels" and in the summary lines on stderr.
 
 Per workload:
   * W untimed warmup launches (continued until 0.1 s of device time has
@@ -45,6 +47,8 @@ MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
 # 2 flops x 2.4 GHz
 VALU_F32_PEAK_TFLOPS = 78.6
 MALL_BYTES = 256 << 20
+# The headline workload: BASELINE.json's largest single-GPU config.
+HEADLINE = "swiglu"
 
 
 def parse():
@@ -92,6 +96,26 @@ def n_sets(bytes_per_set: int, cap: int = 16) -> int:
     # four MALLs' worth: a buffer set is reused only after enough other
     # traffic to evict it even where some of that traffic bypasses the MALL
     return max(1, min(cap, math.ceil(4 * MALL_BYTES / max(bytes_per_set, 1))))
+
+
+_DIAG = None
+
+
+def diag_library():
+    """libkore_bench_diag.so (bench_diag/): the floor probes, kept out of the
+    product library.  Built by bench_diag/Makefile (__graft_entry__.build)."""
+    global _DIAG
+    if _DIAG is None:
+        import ctypes
+
+        path = os.path.join(ROOT, "bench_diag", "libkore_bench_diag.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} not found: run `make -C bench_diag`")
+        lib = ctypes.CDLL(path)
+        lib.kore_hip_diag_empty.argtypes = [ctypes.c_void_p]
+        lib.kore_hip_diag_stream_rows.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_uint64] * 2 + [ctypes.c_void_p]
+        _DIAG = lib
+    return _DIAG
 
 
 def randn(torch, shape, seed, mean=0.0, std=1.0):
@@ -661,7 +685,7 @@ class LaunchFloor(Workload):
     desc = "empty kernel, one workgroup of 64 threads (launch floor)"
 
     def setup(self, torch, lib):
-        self.lib = lib
+        self.lib = diag_library()
 
     def launch(self, i, stream):
         return self.lib.kore_hip_diag_empty(stream)
@@ -685,7 +709,7 @@ class StreamFloor(Workload):
         self.desc = f"pre-quant traffic with a trivial body: x[{rows},{cols}] f32 -> one byte per value + f32 per row"
 
     def setup(self, torch, lib):
-        self.lib = lib
+        self.lib = diag_library()
         self.k = n_sets(self.rows * self.cols * 5, cap=16)
         self._dx = [randn(torch, (self.rows, self.cols), s) for s in range(self.k)]
         self._dq = [torch.empty((self.rows, self.cols), dtype=torch.int8, device="cuda") for _ in range(self.k)]
@@ -884,7 +908,7 @@ def main():
         torch.cuda.empty_cache()
         if not args.no_cpu:
             print(f"[bench] {w.name}: cpu baseline", file=sys.stderr, flush=True)
-            r["cpu_baseline"] = time_cpu(w, args.cpu_seconds if w.name == "rope_qk" else args.cpu_seconds / 3)
+            r["cpu_baseline"] = time_cpu(w, args.cpu_seconds if w.name == HEADLINE else args.cpu_seconds / 3)
         results[w.name] = r
         extra = ""
         if w.ops and w.bound == "mfma":
@@ -894,7 +918,7 @@ def main():
         print(f"[bench] {w.name}: {r['kernel_us']} us, {r['achieved_gbs']} GB/s ({100 * r['frac_of_peak']:.1f}% "
               f"of peak), {r['ns_per_token']} ns/token{extra}", file=sys.stderr, flush=True)
 
-    head_name = "rope_qk" if "rope_qk" in results else next(iter(results))
+    head_name = HEADLINE if HEADLINE in results else next(iter(results))
     h = results[head_name]
     steps = h["steps"]
     line = {
@@ -921,7 +945,7 @@ def main():
     print_summary(results)
 
 
-# BASELINE.json configs -> workloads (configs[1] is the headline), then the
+# BASELINE.json configs -> workloads (configs[2]'s SwiGLU is the headline), then the
 # floors and the "next" rows.
 SUMMARY = [("cfg0 RMSNorm 32x2048", "rms_norm_32x2048"), ("cfg1 RoPE Q+K half-split", "rope_qk"),
            ("cfg1 RoPE Q+K interleaved", "rope_qk_interleaved"), ("cfg2 SwiGLU 16384x14336", "swiglu"),

@@ -298,20 +298,6 @@ int kore_hip_pack_weights_ternary(const float *w, uint64_t m, uint64_t k,
                                   float threshold, uint8_t *packed,
                                   float *scales, kore_stream_t stream);
 
-/* ------------------------------------------------------------ diagnostics
- * Measurement probes with no counterpart in the reference (the benchmark's
- * floors).  kore_hip_diag_empty launches one empty workgroup: the launch
- * floor of a dependent kernel.  kore_hip_diag_stream_rows moves exactly the
- * pre-quant kernel's bytes -- reads x[rows, cols] f32 once, writes one byte
- * per value into q and one f32 per row into scale -- in its launch geometry
- * with a trivial body (cols 2048 or 2560, x 16-byte aligned, q 4-byte
- * aligned); the bytes written are not a quantisation. */
-int kore_hip_diag_empty(kore_stream_t stream);
-
-int kore_hip_diag_stream_rows(const float *x, int8_t *q, float *scale,
-                              uint64_t rows, uint64_t cols,
-                              kore_stream_t stream);
-
 #ifdef __cplusplus
 }
 #endif

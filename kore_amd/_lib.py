@@ -51,8 +51,6 @@ SIGNATURES = {
     "kore_hip_ternary_matmul_i8": [_ptr, _ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _ptr],
     "kore_hip_ternary_matmul_f32": [_ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _ptr],
     "kore_hip_pack_weights_ternary": [_ptr, _u64, _u64, _f32, _ptr, _ptr, _ptr],
-    "kore_hip_diag_empty": [_ptr],
-    "kore_hip_diag_stream_rows": [_ptr, _ptr, _ptr, _u64, _u64, _ptr],
 }
 
 # Entry points whose return type is not int.

@@ -321,9 +321,18 @@ static int bwd_scratch_ptr(float** out) {
     if (dev < 0 || dev >= kMaxScratchDevices) return KORE_HIP_ERR_BAD_DIM;
     std::lock_guard<std::mutex> lock(g_bw_scratch_mu);
     if (!g_bw_scratch[dev]) {
+        // The first call on a device may come from code under stream capture.
+        // The lookup enqueues nothing, but a strict capture mode can refuse
+        // runtime calls it does not know to be safe: this thread switches to
+        // relaxed mode for the lookup and restores its mode afterwards.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        e = hipThreadExchangeStreamCaptureMode(&mode);
+        if (e != hipSuccess) return (int)e;
         void* p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(rms_bwd_scratch));
+        const hipError_t r = hipThreadExchangeStreamCaptureMode(&mode);
         if (e != hipSuccess) return (int)e;
+        if (r != hipSuccess) return (int)r;
         g_bw_scratch[dev] = static_cast<float*>(p);
     }
     *out = g_bw_scratch[dev];

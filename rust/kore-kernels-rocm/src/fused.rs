@@ -129,6 +129,14 @@ fn check(code: c_int, context: &str) -> Result<(), RocmError> {
     }
 }
 
+/// The product of a buffer's dimensions, or a MemoryError where it overflows usize (an oversized
+/// shape must not wrap around to a small byte count and pass the size checks).
+fn prod(dims: &[usize]) -> Result<usize, RocmError> {
+    dims.iter()
+        .try_fold(1usize, |acc, &d| acc.checked_mul(d))
+        .ok_or_else(|| RocmError::MemoryError(format!("shape {dims:?}: byte count overflows usize")))
+}
+
 fn need(buf: &HipBuffer, bytes: usize, what: &str) -> Result<(), RocmError> {
     if buf.len() < bytes {
         return Err(RocmError::MemoryError(format!("{what}: {} bytes < {bytes}", buf.len())));
@@ -139,10 +147,10 @@ fn need(buf: &HipBuffer, bytes: usize, what: &str) -> Result<(), RocmError> {
 /// Mirrors `cuda_rms_norm_f32` (cuda/ops.rs:517-541); bit-exact vs `fused_rms_norm`.
 pub fn rocm_rms_norm_f32(dev: usize, input: &HipBuffer, weight: &HipBuffer, rows: usize, cols: usize,
                          eps: f32) -> Result<HipBuffer, RocmError> {
-    need(input, rows * cols * 4, "rms_norm input")?;
-    need(weight, cols * 4, "rms_norm weight")?;
+    need(input, prod(&[rows, cols, 4])?, "rms_norm input")?;
+    need(weight, prod(&[cols, 4])?, "rms_norm weight")?;
     set_device(dev)?;
-    let out = HipBuffer::zeros(dev, rows * cols * 4)?;
+    let out = HipBuffer::zeros(dev, prod(&[rows, cols, 4])?)?;
     check(unsafe { (api()?.rms_norm)(input.as_device_ptr() as _, weight.as_device_ptr() as _,
                                      out.as_device_ptr() as _, rows as u64, cols as u64, eps,
                                      std::ptr::null_mut()) }, "rms_norm_f32")?;
@@ -157,9 +165,9 @@ pub fn rocm_silu_f32(dev: usize, a: &HipBuffer, n: usize) -> Result<HipBuffer, R
     unary(dev, a, n, api()?.silu, "silu_f32")
 }
 fn unary(dev: usize, a: &HipBuffer, n: usize, f: FnUnary, ctx: &str) -> Result<HipBuffer, RocmError> {
-    need(a, n * 4, ctx)?;
+    need(a, prod(&[n, 4])?, ctx)?;
     set_device(dev)?;
-    let out = HipBuffer::zeros(dev, n * 4)?;
+    let out = HipBuffer::zeros(dev, prod(&[n, 4])?)?;
     check(unsafe { f(a.as_device_ptr() as _, out.as_device_ptr() as _, n as u64, std::ptr::null_mut()) }, ctx)?;
     Ok(out)
 }
@@ -173,10 +181,10 @@ pub fn rocm_swiglu_f32(dev: usize, gate: &HipBuffer, up: &HipBuffer, n: usize) -
 }
 fn binary(dev: usize, a: &HipBuffer, b: &HipBuffer, n: usize, f: FnBinary, ctx: &str)
           -> Result<HipBuffer, RocmError> {
-    need(a, n * 4, ctx)?;
-    need(b, n * 4, ctx)?;
+    need(a, prod(&[n, 4])?, ctx)?;
+    need(b, prod(&[n, 4])?, ctx)?;
     set_device(dev)?;
-    let out = HipBuffer::zeros(dev, n * 4)?;
+    let out = HipBuffer::zeros(dev, prod(&[n, 4])?)?;
     check(unsafe { f(a.as_device_ptr() as _, b.as_device_ptr() as _, out.as_device_ptr() as _, n as u64,
                      std::ptr::null_mut()) }, ctx)?;
     Ok(out)
@@ -195,7 +203,7 @@ pub fn rocm_rope_inv_freq_f32(dev: usize, head_dim: usize, theta: f32) -> Result
 pub fn rocm_rope_f32(dev: usize, data: &HipBuffer, inv_freq: &HipBuffer, batch: usize, seq_len: usize,
                      num_heads: usize, head_dim: usize, start_pos: usize, interleaved: bool)
                      -> Result<(), RocmError> {
-    need(data, batch * seq_len * num_heads * head_dim * 4, "rope data")?;
+    need(data, prod(&[batch, seq_len, num_heads, head_dim, 4])?, "rope data")?;
     need(inv_freq, head_dim / 2 * 4, "rope inv_freq")?;
     set_device(dev)?;
     check(unsafe { (api()?.rope)(data.as_device_ptr() as _, inv_freq.as_device_ptr() as _, batch as u64,
@@ -206,10 +214,10 @@ pub fn rocm_rope_f32(dev: usize, data: &HipBuffer, inv_freq: &HipBuffer, batch: 
 /// `Embedding::lookup` (crates/kore-nn/src/embedding.rs:55-72) on the device.
 pub fn rocm_embedding_f32(dev: usize, table: &HipBuffer, ids: &HipBuffer, n_ids: usize, vocab: usize,
                           dim: usize) -> Result<HipBuffer, RocmError> {
-    need(table, vocab * dim * 4, "embedding table")?;
-    need(ids, n_ids * 4, "embedding ids")?;
+    need(table, prod(&[vocab, dim, 4])?, "embedding table")?;
+    need(ids, prod(&[n_ids, 4])?, "embedding ids")?;
     set_device(dev)?;
-    let out = HipBuffer::zeros(dev, n_ids * dim * 4)?;
+    let out = HipBuffer::zeros(dev, prod(&[n_ids, dim, 4])?)?;
     check(unsafe { (api()?.embedding)(table.as_device_ptr() as _, ids.as_device_ptr() as _,
                                       out.as_device_ptr() as _, n_ids as u64, vocab as u64, dim as u64,
                                       std::ptr::null_mut()) }, "embedding_f32")?;
@@ -221,8 +229,8 @@ pub fn rocm_embedding_f32(dev: usize, table: &HipBuffer, ids: &HipBuffer, n_ids:
 pub fn rocm_rope_qk_f32(dev: usize, q: &HipBuffer, k: &HipBuffer, inv_freq: &HipBuffer, batch: usize,
                         seq_len: usize, q_heads: usize, k_heads: usize, head_dim: usize, start_pos: usize,
                         interleaved: bool) -> Result<(), RocmError> {
-    need(q, batch * seq_len * q_heads * head_dim * 4, "rope q")?;
-    need(k, batch * seq_len * k_heads * head_dim * 4, "rope k")?;
+    need(q, prod(&[batch, seq_len, q_heads, head_dim, 4])?, "rope q")?;
+    need(k, prod(&[batch, seq_len, k_heads, head_dim, 4])?, "rope k")?;
     need(inv_freq, head_dim / 2 * 4, "rope inv_freq")?;
     set_device(dev)?;
     check(unsafe { (api()?.rope_qk)(q.as_device_ptr() as _, k.as_device_ptr() as _, inv_freq.as_device_ptr() as _,
@@ -236,10 +244,10 @@ pub fn rocm_rope_qk_f32(dev: usize, q: &HipBuffer, k: &HipBuffer, inv_freq: &Hip
 /// row 0, saturating), then looked up as `lookup` does.
 pub fn rocm_embedding_forward_f32(dev: usize, table: &HipBuffer, ids: &HipBuffer, n_ids: usize, vocab: usize,
                                   dim: usize) -> Result<HipBuffer, RocmError> {
-    need(table, vocab * dim * 4, "embedding table")?;
-    need(ids, n_ids * 4, "embedding ids")?;
+    need(table, prod(&[vocab, dim, 4])?, "embedding table")?;
+    need(ids, prod(&[n_ids, 4])?, "embedding ids")?;
     set_device(dev)?;
-    let out = HipBuffer::zeros(dev, n_ids * dim * 4)?;
+    let out = HipBuffer::zeros(dev, prod(&[n_ids, dim, 4])?)?;
     check(unsafe { (api()?.embedding_forward)(table.as_device_ptr() as _, ids.as_device_ptr() as _,
                                               out.as_device_ptr() as _, n_ids as u64, vocab as u64, dim as u64,
                                               std::ptr::null_mut()) }, "embedding_forward_f32")?;
@@ -249,11 +257,11 @@ pub fn rocm_embedding_forward_f32(dev: usize, table: &HipBuffer, ids: &HipBuffer
 /// RMSNorm + per-row absmax int8 (the BitLinear pre-quant): (codes, scales).
 pub fn rocm_rms_norm_quant_i8(dev: usize, input: &HipBuffer, weight: &HipBuffer, rows: usize, cols: usize,
                               eps: f32) -> Result<(HipBuffer, HipBuffer), RocmError> {
-    need(input, rows * cols * 4, "prequant input")?;
-    need(weight, cols * 4, "prequant weight")?;
+    need(input, prod(&[rows, cols, 4])?, "prequant input")?;
+    need(weight, prod(&[cols, 4])?, "prequant weight")?;
     set_device(dev)?;
-    let q = HipBuffer::zeros(dev, rows * cols)?;
-    let s = HipBuffer::zeros(dev, rows * 4)?;
+    let q = HipBuffer::zeros(dev, prod(&[rows, cols])?)?;
+    let s = HipBuffer::zeros(dev, prod(&[rows, 4])?)?;
     check(unsafe { (api()?.prequant)(input.as_device_ptr() as _, weight.as_device_ptr() as _,
                                      q.as_device_ptr() as _, s.as_device_ptr() as _, rows as u64,
                                      cols as u64, eps, std::ptr::null_mut()) }, "rms_norm_quant_i8")?;
@@ -263,11 +271,11 @@ pub fn rocm_rms_norm_quant_i8(dev: usize, input: &HipBuffer, weight: &HipBuffer,
 /// Mirrors `cuda_fused_rms_norm_silu_gate_f32` (cuda/ops.rs:717-751): y = RMSNorm(x) * silu(z).
 pub fn rocm_fused_rms_norm_silu_gate_f32(dev: usize, input: &HipBuffer, gamma: &HipBuffer, gate: &HipBuffer,
                                          rows: usize, cols: usize, eps: f32) -> Result<HipBuffer, RocmError> {
-    need(input, rows * cols * 4, "silu_gate input")?;
-    need(gamma, cols * 4, "silu_gate gamma")?;
-    need(gate, rows * cols * 4, "silu_gate gate")?;
+    need(input, prod(&[rows, cols, 4])?, "silu_gate input")?;
+    need(gamma, prod(&[cols, 4])?, "silu_gate gamma")?;
+    need(gate, prod(&[rows, cols, 4])?, "silu_gate gate")?;
     set_device(dev)?;
-    let out = HipBuffer::zeros(dev, rows * cols * 4)?;
+    let out = HipBuffer::zeros(dev, prod(&[rows, cols, 4])?)?;
     check(unsafe { (api()?.silu_gate)(input.as_device_ptr() as _, gamma.as_device_ptr() as _,
                                       gate.as_device_ptr() as _, out.as_device_ptr() as _, rows as u64,
                                       cols as u64, eps, std::ptr::null_mut()) }, "rms_norm_silu_gate_f32")?;
@@ -276,9 +284,9 @@ pub fn rocm_fused_rms_norm_silu_gate_f32(dev: usize, input: &HipBuffer, gamma: &
 
 /// Mirrors `cuda_softmax_f32` (cuda/ops.rs:486-511); `fused_softmax` semantics.
 pub fn rocm_softmax_f32(dev: usize, a: &HipBuffer, rows: usize, cols: usize) -> Result<HipBuffer, RocmError> {
-    need(a, rows * cols * 4, "softmax input")?;
+    need(a, prod(&[rows, cols, 4])?, "softmax input")?;
     set_device(dev)?;
-    let out = HipBuffer::zeros(dev, rows * cols * 4)?;
+    let out = HipBuffer::zeros(dev, prod(&[rows, cols, 4])?)?;
     check(unsafe { (api()?.softmax)(a.as_device_ptr() as _, out.as_device_ptr() as _, rows as u64, cols as u64,
                                     std::ptr::null_mut()) }, "softmax_f32")?;
     Ok(out)
@@ -288,9 +296,9 @@ pub fn rocm_softmax_f32(dev: usize, a: &HipBuffer, rows: usize, cols: usize) -> 
 /// reference never wraps: row r keeps columns < seq_offset + r + 1.
 pub fn rocm_softmax_causal_f32(dev: usize, a: &HipBuffer, rows: usize, cols: usize, seq_offset: usize)
                                -> Result<HipBuffer, RocmError> {
-    need(a, rows * cols * 4, "softmax_causal input")?;
+    need(a, prod(&[rows, cols, 4])?, "softmax_causal input")?;
     set_device(dev)?;
-    let out = HipBuffer::zeros(dev, rows * cols * 4)?;
+    let out = HipBuffer::zeros(dev, prod(&[rows, cols, 4])?)?;
     check(unsafe { (api()?.softmax_causal)(a.as_device_ptr() as _, out.as_device_ptr() as _, rows as u64,
                                            cols as u64, seq_offset as u64, std::ptr::null_mut()) },
           "softmax_causal_f32")?;
@@ -300,10 +308,10 @@ pub fn rocm_softmax_causal_f32(dev: usize, a: &HipBuffer, rows: usize, cols: usi
 /// `fused_softmax_backward` (cpu_fused_backward.rs:86-115) on the device.
 pub fn rocm_softmax_backward_f32(dev: usize, grad_output: &HipBuffer, output: &HipBuffer, rows: usize,
                                  cols: usize) -> Result<HipBuffer, RocmError> {
-    need(grad_output, rows * cols * 4, "softmax_backward grad_output")?;
-    need(output, rows * cols * 4, "softmax_backward output")?;
+    need(grad_output, prod(&[rows, cols, 4])?, "softmax_backward grad_output")?;
+    need(output, prod(&[rows, cols, 4])?, "softmax_backward output")?;
     set_device(dev)?;
-    let dx = HipBuffer::zeros(dev, rows * cols * 4)?;
+    let dx = HipBuffer::zeros(dev, prod(&[rows, cols, 4])?)?;
     check(unsafe { (api()?.softmax_bwd)(grad_output.as_device_ptr() as _, output.as_device_ptr() as _,
                                         dx.as_device_ptr() as _, rows as u64, cols as u64,
                                         std::ptr::null_mut()) }, "softmax_backward_f32")?;
@@ -314,10 +322,10 @@ pub fn rocm_softmax_backward_f32(dev: usize, grad_output: &HipBuffer, output: &H
 /// f32 class indices, as in the reference.
 pub fn rocm_cross_entropy_backward_f32(dev: usize, logits: &HipBuffer, targets: &HipBuffer, batch: usize,
                                        classes: usize) -> Result<HipBuffer, RocmError> {
-    need(logits, batch * classes * 4, "cross_entropy_backward logits")?;
-    need(targets, batch * 4, "cross_entropy_backward targets")?;
+    need(logits, prod(&[batch, classes, 4])?, "cross_entropy_backward logits")?;
+    need(targets, prod(&[batch, 4])?, "cross_entropy_backward targets")?;
     set_device(dev)?;
-    let g = HipBuffer::zeros(dev, batch * classes * 4)?;
+    let g = HipBuffer::zeros(dev, prod(&[batch, classes, 4])?)?;
     check(unsafe { (api()?.ce_bwd)(logits.as_device_ptr() as _, targets.as_device_ptr() as _,
                                    g.as_device_ptr() as _, batch as u64, classes as u64,
                                    std::ptr::null_mut()) }, "cross_entropy_backward_f32")?;
@@ -329,12 +337,12 @@ pub fn rocm_cross_entropy_backward_f32(dev: usize, logits: &HipBuffer, targets: 
 pub fn rocm_rms_norm_backward_f32(dev: usize, grad_output: &HipBuffer, input: &HipBuffer, gamma: &HipBuffer,
                                   rows: usize, cols: usize, eps: f32)
                                   -> Result<(HipBuffer, HipBuffer), RocmError> {
-    need(grad_output, rows * cols * 4, "rms_norm_backward grad_output")?;
-    need(input, rows * cols * 4, "rms_norm_backward input")?;
-    need(gamma, cols * 4, "rms_norm_backward gamma")?;
+    need(grad_output, prod(&[rows, cols, 4])?, "rms_norm_backward grad_output")?;
+    need(input, prod(&[rows, cols, 4])?, "rms_norm_backward input")?;
+    need(gamma, prod(&[cols, 4])?, "rms_norm_backward gamma")?;
     set_device(dev)?;
-    let dx = HipBuffer::zeros(dev, rows * cols * 4)?;
-    let dg = HipBuffer::zeros(dev, cols * 4)?;
+    let dx = HipBuffer::zeros(dev, prod(&[rows, cols, 4])?)?;
+    let dg = HipBuffer::zeros(dev, prod(&[cols, 4])?)?;
     let wsb = unsafe { (api()?.rms_bwd_ws)(rows as u64, cols as u64) } as usize;
     let ws = HipBuffer::zeros(dev, wsb.max(16))?;
     check(unsafe { (api()?.rms_bwd)(grad_output.as_device_ptr() as _, input.as_device_ptr() as _,
@@ -347,20 +355,22 @@ pub fn rocm_rms_norm_backward_f32(dev: usize, grad_output: &HipBuffer, input: &H
 /// The same op for callers that cannot allocate device memory (graph capture, tight loops): no
 /// counterpart in the reference.  The caller owns grad_input and grad_gamma; the dgamma partial
 /// sums go to the library's fixed per-GPU scratch array (`rocm_rms_norm_backward_noalloc_max_bytes`);
-/// calls that overlap on one GPU race.
+/// calls that overlap on one GPU race.  `stream` is the HIP stream the kernels are enqueued on:
+/// the capturing stream under graph capture (the legacy null stream cannot be captured), or null.
 pub fn rocm_rms_norm_backward_noalloc_f32(dev: usize, grad_output: &HipBuffer, input: &HipBuffer,
                                           gamma: &HipBuffer, grad_input: &HipBuffer, grad_gamma: &HipBuffer,
-                                          rows: usize, cols: usize, eps: f32) -> Result<(), RocmError> {
-    need(grad_output, rows * cols * 4, "rms_norm_backward grad_output")?;
-    need(input, rows * cols * 4, "rms_norm_backward input")?;
-    need(gamma, cols * 4, "rms_norm_backward gamma")?;
-    need(grad_input, rows * cols * 4, "rms_norm_backward grad_input")?;
-    need(grad_gamma, cols * 4, "rms_norm_backward grad_gamma")?;
+                                          rows: usize, cols: usize, eps: f32, stream: Stream)
+                                          -> Result<(), RocmError> {
+    need(grad_output, prod(&[rows, cols, 4])?, "rms_norm_backward grad_output")?;
+    need(input, prod(&[rows, cols, 4])?, "rms_norm_backward input")?;
+    need(gamma, prod(&[cols, 4])?, "rms_norm_backward gamma")?;
+    need(grad_input, prod(&[rows, cols, 4])?, "rms_norm_backward grad_input")?;
+    need(grad_gamma, prod(&[cols, 4])?, "rms_norm_backward grad_gamma")?;
     set_device(dev)?;
     check(unsafe { (api()?.rms_bwd_noalloc)(grad_output.as_device_ptr() as _, input.as_device_ptr() as _,
                                             gamma.as_device_ptr() as _, grad_input.as_device_ptr() as _,
                                             grad_gamma.as_device_ptr() as _, rows as u64, cols as u64, eps,
-                                            std::ptr::null_mut()) }, "rms_norm_backward_noalloc_f32")
+                                            stream) }, "rms_norm_backward_noalloc_f32")
 }
 
 /// Bytes of the fixed scratch array behind `rocm_rms_norm_backward_noalloc_f32`.
@@ -375,12 +385,12 @@ pub fn rocm_rms_norm_backward_noalloc_max_bytes() -> Result<usize, RocmError> {
 pub fn rocm_ternary_matmul_i8(dev: usize, a_packed: &HipBuffer, a_scales: &HipBuffer, q: &HipBuffer,
                               q_scales: &HipBuffer, m: usize, n: usize, k: usize)
                               -> Result<HipBuffer, RocmError> {
-    need(a_packed, m * k.div_ceil(5), "ternary weights")?;
-    need(a_scales, m * 4, "ternary scales")?;
-    need(q, n * k, "ternary codes")?;
-    need(q_scales, n * 4, "ternary code scales")?;
+    need(a_packed, prod(&[m, k.div_ceil(5)])?, "ternary weights")?;
+    need(a_scales, prod(&[m, 4])?, "ternary scales")?;
+    need(q, prod(&[n, k])?, "ternary codes")?;
+    need(q_scales, prod(&[n, 4])?, "ternary code scales")?;
     set_device(dev)?;
-    let c = HipBuffer::zeros(dev, m * n * 4)?;
+    let c = HipBuffer::zeros(dev, prod(&[m, n, 4])?)?;
     check(unsafe { (api()?.ternary_i8)(a_packed.as_device_ptr() as _, a_scales.as_device_ptr() as _,
                                        q.as_device_ptr() as _, q_scales.as_device_ptr() as _,
                                        c.as_device_ptr() as _, m as u64, n as u64, k as u64,
@@ -393,11 +403,11 @@ pub fn rocm_ternary_matmul_i8(dev: usize, a_packed: &HipBuffer, a_scales: &HipBu
 /// transposed input).  The sum is the reference's sequential f32 fold, so c is bit-exact.
 pub fn rocm_ternary_matmul_f32(dev: usize, a_packed: &HipBuffer, a_scales: &HipBuffer, b: &HipBuffer,
                                m: usize, n: usize, k: usize) -> Result<HipBuffer, RocmError> {
-    need(a_packed, m * k.div_ceil(5), "ternary weights")?;
-    need(a_scales, m * 4, "ternary scales")?;
-    need(b, k * n * 4, "ternary activations")?;
+    need(a_packed, prod(&[m, k.div_ceil(5)])?, "ternary weights")?;
+    need(a_scales, prod(&[m, 4])?, "ternary scales")?;
+    need(b, prod(&[k, n, 4])?, "ternary activations")?;
     set_device(dev)?;
-    let c = HipBuffer::zeros(dev, m * n * 4)?;
+    let c = HipBuffer::zeros(dev, prod(&[m, n, 4])?)?;
     check(unsafe { (api()?.ternary_f32)(a_packed.as_device_ptr() as _, a_scales.as_device_ptr() as _,
                                         b.as_device_ptr() as _, c.as_device_ptr() as _, m as u64, n as u64,
                                         k as u64, std::ptr::null_mut()) }, "ternary_matmul_f32")?;
@@ -408,10 +418,10 @@ pub fn rocm_ternary_matmul_f32(dev: usize, a_packed: &HipBuffer, a_scales: &HipB
 /// (base-243 bytes [m, ceil(k/5)], per-row scales [m]), bit-identical to the CPU function.
 pub fn rocm_pack_weights_ternary(dev: usize, w: &HipBuffer, m: usize, k: usize, threshold: f32)
                                  -> Result<(HipBuffer, HipBuffer), RocmError> {
-    need(w, m * k * 4, "weights")?;
+    need(w, prod(&[m, k, 4])?, "weights")?;
     set_device(dev)?;
-    let packed = HipBuffer::zeros(dev, m * k.div_ceil(5))?;
-    let scales = HipBuffer::zeros(dev, m * 4)?;
+    let packed = HipBuffer::zeros(dev, prod(&[m, k.div_ceil(5)])?)?;
+    let scales = HipBuffer::zeros(dev, prod(&[m, 4])?)?;
     check(unsafe { (api()?.pack_ternary)(w.as_device_ptr() as _, m as u64, k as u64, threshold,
                                          packed.as_device_ptr() as _, scales.as_device_ptr() as _,
                                          std::ptr::null_mut()) }, "pack_weights_ternary")?;

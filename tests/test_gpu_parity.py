@@ -814,6 +814,36 @@ def test_ternary_matmul_i8_wide_tiles_unaligned_output():
     assert_bitexact(got, oracle.ternary_matmul_i8(p, sa, q, sq, m, n, k), "ternary_matmul_i8 wide unaligned c")
 
 
+@pytest.mark.parametrize("m,n,k,c_off", [(2560, 3901, 1280, 0), (2560, 4096, 1280, 1), (2560, 3901, 1280, 3)])
+def test_ternary_matmul_i8_wide_192_ragged_and_unaligned_output(m, n, k, c_off):
+    """The 256 x 192 wide tiles (chosen here: 210 such tiles fit one round of
+    256 CUs, K has 8 steps) with n % 4 != 0 and with the output 4 or 12
+    bytes past a 16-byte boundary: the epilogue's element stores, including
+    the skip of lanes past n, on 192-wide tiles.  Bit-exact against an f64
+    GEMM of the decoded trits (exact for these integer sums) with the same
+    f32 epilogue; the float before the output stays untouched."""
+    from inputs import int8_codes, ternary_weights
+
+    log(f"ternary_matmul_i8 wide 192 m={m} n={n} k={k} c_off={c_off}")
+    lib = __import__("kore_amd._lib", fromlist=["load"]).load()
+    p, sa = ternary_weights(m, k, 41)
+    q = int8_codes(n, k, 42)
+    sq = np.abs(normal((n,), 43, 0.02, 0.005))
+    bp, bs, bq, bsq = up(p), up(sa), up(q), up(sq)
+    t = torch.full((m * n + 4,), float("nan"), dtype=torch.float32, device="cuda")
+    rc = lib.kore_hip_ternary_matmul_i8(bp.ptr, bs.ptr, bq.ptr, bsq.ptr, t[c_off:].data_ptr(), m, n, k, None)
+    torch.cuda.synchronize()
+    assert rc == 0
+    got = t[c_off:c_off + m * n].reshape(m, n)
+    if c_off:
+        assert torch.isnan(t[:c_off]).all()
+    assert torch.isnan(t[c_off + m * n:]).all()
+    tr = torch.from_numpy(oracle.unpack_trits(p, k)).cuda().double()
+    acc = (tr @ torch.from_numpy(q).cuda().double().T).float()
+    want = (acc * torch.from_numpy(sa).cuda()[:, None]) * torch.from_numpy(sq).cuda()[None, :]
+    assert torch.equal(got, want), f"ternary_matmul_i8 wide 192 {m}x{n}x{k} c_off={c_off}"
+
+
 def test_ternary_matmul_i8_full_size_and_pipeline():
     """BitLinear 2560 -> 6912 on 4096 tokens (the pre-quant config's
     activations): bit-exact against an f64 GEMM of the decoded trits (exact

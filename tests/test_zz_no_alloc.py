@@ -42,6 +42,47 @@ def _run_pair(rows: int, cols: int, seed: int):
     assert gg.cpu().numpy().tobytes() == gg_ref.cpu().numpy().tobytes()
 
 
+def test_no_alloc_first_call_under_graph_capture():
+    """The first call on the device (when the library looks up its scratch
+    array) made inside a HIP graph capture on a side stream: the capture
+    succeeds, and every replay -- with eager work and synchronisation between
+    replays -- gives dx and dgamma bit-identical to the workspace entry point.
+    Collected first in this module, so the lookup has not run before it."""
+    rows, cols = 300, 2560
+    print(f"no-alloc rms_norm_backward under capture rows={rows} cols={cols}", flush=True)
+    lib = _lib.load()
+    dy, x = _dev(normal((rows, cols), 11)), _dev(normal((rows, cols), 12))
+    g = _dev(normal((cols,), 13, 1.0, 0.02))
+    need = lib.kore_hip_rms_norm_backward_workspace_bytes(rows, cols)
+    ws = torch.empty(need // 4 + 4, dtype=torch.float32, device="cuda:0")
+    gx_ref, gg_ref = torch.empty_like(x), torch.empty_like(g)
+    assert lib.kore_hip_rms_norm_backward_f32(dy.data_ptr(), x.data_ptr(), g.data_ptr(), gx_ref.data_ptr(),
+                                              gg_ref.data_ptr(), ws.data_ptr(), ws.numel() * 4, rows, cols,
+                                              1e-5, torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    gx, gg = torch.full_like(x, float("nan")), torch.full_like(g, float("nan"))
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    rcs = []
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            rcs.append(lib.kore_hip_rms_norm_backward_noalloc_f32(
+                dy.data_ptr(), x.data_ptr(), g.data_ptr(), gx.data_ptr(), gg.data_ptr(), rows, cols, 1e-5,
+                side.cuda_stream))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert rcs == [0]
+    for rep in range(3):
+        gx.fill_(float("nan"))
+        gg.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gx, gx_ref), f"replay {rep}: dx"
+        assert torch.equal(gg, gg_ref), f"replay {rep}: dgamma"
+
+
 def test_no_alloc_matches_workspace_entry_point():
     # vector plan at full scratch use (512 partial rows x 2048), then smaller
     # vector plans, then the generic plan (cols % 4 != 0: per-row inv)
