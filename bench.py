@@ -494,10 +494,11 @@ class TernaryI8(Workload):
     kernel = "ternary_i8_mfma_kernel"
     bound = "mfma"
 
-    def __init__(self, m=6912, n=4096, k=2560):
+    def __init__(self, m=6912, n=4096, k=2560, layer=False):
         self.m, self.n, self.k = m, n, k
+        self.layer = layer
         self.kp = (k + 4) // 5
-        self.name = f"ternary_i8_{m}x{n}x{k}"
+        self.name = f"{'bit_linear_i8' if layer else 'ternary_i8'}_{m}x{n}x{k}"
         if n <= 8:
             self.kernel = "ternary_i8_gemv_kernel"
         elif n <= 64:
@@ -506,9 +507,12 @@ class TernaryI8(Workload):
             self.kernel = "ternary_i8_wide_kernel"
         self.tokens = n
         self.ops = 2 * m * n * k
-        self.bytes = m * self.kp + n * k + 4 * m * n + 4 * (m + n)
+        self.bytes = m * self.kp + n * k + 4 * m * n + 4 * (m + n) + (4 * m if layer else 0)
         self.desc = (f"BitLinear int8 x ternary matmul c[{m},{n}] = ((float)(trits[{m},{k}] . q[{n},{k}]) * "
                      f"a_scale) * q_scale, base-243 weights, int8 codes (bit-exact)")
+        if layer:
+            self.desc = (f"BitLinear layer on int8 codes (kore_hip_bit_linear_i8): y[{n},{m}] = c^T + bias, the "
+                         f"layer's output layout, one launch (bit-exact)")
 
     def setup(self, torch, lib):
         self.lib = lib
@@ -521,10 +525,16 @@ class TernaryI8(Workload):
                     for _ in range(self.k_sets)]
         self._dsa = torch.rand(self.m, generator=g, device="cuda")
         self._dsq = torch.rand(self.n, generator=g, device="cuda")
+        self._dbias = torch.randn(self.m, generator=g, device="cuda")
         self._dc = [torch.empty(self.m * self.n, device="cuda") for _ in range(self.k_sets)]
 
     def launch(self, i, stream):
         j = i % self.k_sets
+        if self.layer:
+            return self.lib.kore_hip_bit_linear_i8(self._da[j].data_ptr(), self._dsa.data_ptr(),
+                                                   self._dq[j].data_ptr(), self._dsq.data_ptr(),
+                                                   self._dbias.data_ptr(), self._dc[j].data_ptr(), self.m, self.n,
+                                                   self.k, stream)
         return self.lib.kore_hip_ternary_matmul_i8(self._da[j].data_ptr(), self._dsa.data_ptr(),
                                                    self._dq[j].data_ptr(), self._dsq.data_ptr(),
                                                    self._dc[j].data_ptr(), self.m, self.n, self.k, stream)
@@ -569,16 +579,21 @@ class TernaryF32(Workload):
     throughput (2 flops per term) next to the bytes."""
     bound = "valu"
 
-    def __init__(self, m=6912, n=1, k=2560):
+    def __init__(self, m=6912, n=1, k=2560, layer=False):
         self.m, self.n, self.k = m, n, k
+        self.layer = layer
         self.kernel = "ternary_f32_pipe_kernel" if n <= 4 else "ternary_f32_rows_kernel"
         self.kp = (k + 4) // 5
-        self.name = f"ternary_f32_{m}x{n}x{k}"
+        self.name = f"{'bit_linear_f32' if layer else 'ternary_f32'}_{m}x{n}x{k}"
         self.tokens = n
         self.ops = 2 * m * n * k
         self.bytes = m * self.kp + 4 * k * n + 4 * m * n + 4 * m
         self.desc = (f"BitLinear f32 x ternary matmul c[{m},{n}] = (sum_k trits[{m},{k}] * b[{k},{n}]) * a_scale, "
                      "sequential f32 fold in k order (bit-exact)")
+        if layer:
+            self.bytes += 4 * m
+            self.desc = (f"BitLinear::forward (kore_hip_bit_linear_f32): y[{n},{m}] = ternary_matmul(W, s, x^T)^T + "
+                         f"bias with x[{n},{k}] as stored, one launch (bit-exact)")
 
     def setup(self, torch, lib):
         self.lib = lib
@@ -589,10 +604,15 @@ class TernaryF32(Workload):
                     for _ in range(self.k_sets)]
         self._db = [torch.randn((self.k * self.n,), generator=g, device="cuda") for _ in range(self.k_sets)]
         self._dsa = torch.rand(self.m, generator=g, device="cuda")
+        self._dbias = torch.randn(self.m, generator=g, device="cuda")
         self._dc = [torch.empty(self.m * self.n, device="cuda") for _ in range(self.k_sets)]
 
     def launch(self, i, stream):
         j = i % self.k_sets
+        if self.layer:
+            return self.lib.kore_hip_bit_linear_f32(self._da[j].data_ptr(), self._dsa.data_ptr(),
+                                                    self._db[j].data_ptr(), self._dbias.data_ptr(),
+                                                    self._dc[j].data_ptr(), self.m, self.n, self.k, stream)
         return self.lib.kore_hip_ternary_matmul_f32(self._da[j].data_ptr(), self._dsa.data_ptr(),
                                                     self._db[j].data_ptr(), self._dc[j].data_ptr(), self.m, self.n,
                                                     self.k, stream)
@@ -730,8 +750,10 @@ def all_workloads():
             StreamFloor(64, 2560), StreamFloor(32, 2048), RmsNormSiluGate(), Softmax(),
             SoftmaxBackward(),
             RmsNormBackward(), TernaryI8(), TernaryI8(2560, 4096, 6912), TernaryI8(6912, 64, 2560),
-            TernaryI8(6912, 1, 2560), TernaryF32(),
-            TernaryF32(6912, 16, 2560), TernaryF32(6912, 64, 2560), PackTernary(), PackTernary(2560, 6912), Copy()]
+            TernaryI8(6912, 1, 2560), TernaryI8(6912, 4096, 2560, layer=True), TernaryI8(2560, 4096, 6912, layer=True),
+            TernaryI8(6912, 64, 2560, layer=True), TernaryF32(), TernaryF32(6912, 16, 2560), TernaryF32(6912, 64, 2560),
+            TernaryF32(6912, 1, 2560, layer=True), TernaryF32(6912, 64, 2560, layer=True), PackTernary(),
+            PackTernary(2560, 6912), Copy()]
 
 
 # ------------------------------------------------------------------ measure
@@ -899,7 +921,7 @@ def main():
             r["hbm_traffic_bytes"] = traffic[w.name]
         if hasattr(w, "library_reference") and getattr(w, "n", 8) % 8 != 0:
             r["library_reference"] = {"skipped": "torch._int_mm needs n % 8 == 0"}
-        elif hasattr(w, "library_reference"):
+        elif hasattr(w, "library_reference") and not getattr(w, "layer", False):
             try:
                 r["library_reference"] = w.library_reference(torch)
             except Exception as ex:  # the reference is context only
@@ -958,7 +980,14 @@ SUMMARY = [("cfg0 RMSNorm 32x2048", "rms_norm_32x2048"), ("cfg1 RoPE Q+K half-sp
            ("floor: 32x2048 read + byte writes", "stream_floor_32x2048"),
            ("next: RMSNorm 16384x2048", "rms_norm_16384x2048"), ("next: norm+SiLU gate", "rms_norm_silu_gate_4096x2560"),
            ("next: softmax 32768x2048", "softmax_32768x2048"),
-           ("next: ternary i8 6912x4096x2560", "ternary_i8_6912x4096x2560")]
+           ("next: ternary i8 6912x4096x2560", "ternary_i8_6912x4096x2560"),
+           ("next: BitLinear layer i8 6912x4096x2560 (y[n,m] + bias)", "bit_linear_i8_6912x4096x2560"),
+           ("next: ternary i8 2560x4096x6912", "ternary_i8_2560x4096x6912"),
+           ("next: BitLinear layer i8 2560x4096x6912 (y[n,m])", "bit_linear_i8_2560x4096x6912"),
+           ("next: ternary f32 6912x1x2560", "ternary_f32_6912x1x2560"),
+           ("next: BitLinear::forward f32 6912x1x2560", "bit_linear_f32_6912x1x2560"),
+           ("next: ternary f32 6912x64x2560", "ternary_f32_6912x64x2560"),
+           ("next: BitLinear::forward f32 6912x64x2560", "bit_linear_f32_6912x64x2560")]
 
 
 # Latency-bound configs -> the trivial-body kernel moving their rows (reads

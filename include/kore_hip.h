@@ -285,6 +285,31 @@ int kore_hip_ternary_matmul_f32(const uint8_t *a_packed, const float *a_scales,
                                 const float *b, float *c, uint64_t m,
                                 uint64_t n, uint64_t k, kore_stream_t stream);
 
+/* BitLinear::forward (crates/kore-nn/src/bit_linear.rs:175-237) as one
+ * launch: y[batch, out] = ternary_matmul(W, scales, x^T)^T + bias, with the
+ * layer's input x[batch, in] as it is stored (token-major) and its output in
+ * the layer's layout -- the transposes at :200 and :218 and the bias add at
+ * :222 need no passes of their own.  y[b, o] is the f32 fold of
+ * kore_hip_ternary_matmul_f32 for output row o and column b, rounded, then
+ * + bias[o] (one f32 add, as Tensor::add does); bias may be NULL (a layer
+ * without bias).  Bit-exact.  in_features <= 2^23.  y must not overlap the
+ * inputs (KORE_HIP_ERR_ALIAS). */
+int kore_hip_bit_linear_f32(const uint8_t *a_packed, const float *a_scales,
+                            const float *x, const float *bias, float *y,
+                            uint64_t out_features, uint64_t batch,
+                            uint64_t in_features, kore_stream_t stream);
+
+/* The same layer on pre-quant codes (kore_hip_rms_norm_quant_i8's q[batch,
+ * in] and q_scales[batch]): y[b, o] = c[o, b] + bias[o] with c of
+ * kore_hip_ternary_matmul_i8, in the layer's [batch, out] layout; bias may be
+ * NULL.  Bit-exact.  in_features <= 2^24.  y must not overlap the inputs
+ * (KORE_HIP_ERR_ALIAS). */
+int kore_hip_bit_linear_i8(const uint8_t *a_packed, const float *a_scales,
+                           const int8_t *q, const float *q_scales,
+                           const float *bias, float *y, uint64_t out_features,
+                           uint64_t batch, uint64_t in_features,
+                           kore_stream_t stream);
+
 /* Quantise f32 weights w[m, k] (row-major) to ternary with a per-row scale
  * and pack them base-243, the weight format both matmuls read: replaces
  * pack_weights_ternary (crates/kore-kernels/src/cpu_ternary_matmul.rs:198-240;

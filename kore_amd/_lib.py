@@ -50,6 +50,8 @@ SIGNATURES = {
     "kore_hip_rms_norm_backward_noalloc_f32": [_ptr, _ptr, _ptr, _ptr, _ptr, _u64, _u64, _f32, _ptr],
     "kore_hip_ternary_matmul_i8": [_ptr, _ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _ptr],
     "kore_hip_ternary_matmul_f32": [_ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _ptr],
+    "kore_hip_bit_linear_f32": [_ptr, _ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _ptr],
+    "kore_hip_bit_linear_i8": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _u64, _u64, _u64, _ptr],
     "kore_hip_pack_weights_ternary": [_ptr, _u64, _u64, _f32, _ptr, _ptr, _ptr],
 }
 

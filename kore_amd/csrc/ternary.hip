@@ -69,10 +69,30 @@ struct TernArgs {
     const float* sa;    // [M]
     const int8_t* q;    // [N, K]
     const float* sq;    // [N]
-    float* c;           // [M, N]
+    float* c;           // [M, N], or [N, M] with trans
     uint32_t m, n, k, kp;
     uint32_t splits, kt_per;  // split-K: K-tile ranges of kt_per per workgroup
+    const float* bias;  // [M] added to every output of row m, or null
+    uint32_t trans;     // 1: output (m, n) at c[n * M + m] (BitLinear::forward's layout)
 };
+
+// Index of output (m, n) in c, and the layer's bias add: the output is
+// rounded first, then the bias is added to it (bit_linear.rs:220-224 adds
+// the bias to the finished matmul output).
+__device__ __forceinline__ uint64_t out_idx(const TernArgs& p, uint32_t m, uint32_t n) {
+    return p.trans ? (uint64_t)n * p.m + m : (uint64_t)m * p.n + n;
+}
+__device__ __forceinline__ float add_bias(const float* bias, float v, uint32_t m) { return bias ? v + bias[m] : v; }
+
+// An MFMA with the weight and code operands in either order: kTrans puts
+// the codes first, so that accumulator rows run over n and lanes over m --
+// the transposed output's contiguous dimension.  The int32 sums are the same
+// either way (exact integer arithmetic).
+template <bool kTrans>
+__device__ __forceinline__ i32x16 mfma_wq(i32x4 w, i32x4 q, i32x16 acc) {
+    return kTrans ? __builtin_amdgcn_mfma_i32_32x32x32_i8(q, w, acc, 0, 0, 0)
+                  : __builtin_amdgcn_mfma_i32_32x32x32_i8(w, q, acc, 0, 0, 0);
+}
 
 // Sixteen bytes at a dword boundary: global loads need dword alignment only.
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -98,7 +118,7 @@ __device__ __forceinline__ uint64_t trit_lut_entry(uint32_t b) {
 // of its output tile and adds its int32 sums into c (zeroed, read as int32)
 // with integer atomics -- exact and order-free, so the result is the same on
 // every run; ternary_i8_finish_kernel then applies the epilogue in place.
-template <bool kAlignedA, bool kAlignedB, bool kSplit>
+template <bool kAlignedA, bool kAlignedB, bool kSplit, bool kTrans>
 __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
     __shared__ uint64_t lut[256];
     __shared__ __attribute__((aligned(16))) uint8_t As[kTmM * kTmPitch];
@@ -277,27 +297,30 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_mfma_kernel(TernArgs p) {
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = mfma_wq<kTrans>(a[i], b[j], acc[i][j]);
         }
     }
 
-    // epilogue: ((float)acc * sa[m]) * sq[n]
+    // epilogue: ((float)acc * sa[m]) * sq[n] (+ bias[m]).  Register r of
+    // lane l is row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32 of its
+    // 32 x 32 tile: rows over m and columns over n, or (kTrans) the reverse,
+    // so that the lanes of a store always run along the output's rows.
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const uint32_t n = n0 + wn * 64 + j * 32 + (lane & 31);
-        const bool n_ok = n < p.n;
-        const float sqn = n_ok ? p.sq[n] : 0.0f;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (n_ok && m < p.m) {
+                const uint32_t rr = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), cc = lane & 31;
+                const uint32_t m = m0 + wm * 64 + i * 32 + (kTrans ? cc : rr);
+                const uint32_t n = n0 + wn * 64 + j * 32 + (kTrans ? rr : cc);
+                if (n < p.n && m < p.m) {
+                    const uint64_t o = out_idx(p, m, n);
                     if (kSplit) {
-                        atomicAdd(reinterpret_cast<int*>(p.c) + (uint64_t)m * p.n + n, acc[i][j][r]);
+                        atomicAdd(reinterpret_cast<int*>(p.c) + o, acc[i][j][r]);
                     } else {
-                        const float v = ((float)acc[i][j][r] * p.sa[m]) * sqn;
-                        __builtin_nontemporal_store(v, p.c + (uint64_t)m * p.n + n);
+                        const float v = ((float)acc[i][j][r] * p.sa[m]) * p.sq[n];
+                        __builtin_nontemporal_store(add_bias(p.bias, v, m), p.c + o);
                     }
                 }
             }
@@ -366,7 +389,7 @@ __device__ __forceinline__ void splice_trits(uint32_t (&out)[20], int b, uint64_
     out[d + 1] |= (uint32_t)(v >> (32 - sh));
 }
 
-template <bool kAlignedA, int NJ>
+template <bool kAlignedA, int NJ, bool kTrans>
 __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     using Tile = WideTile<NJ>;
     constexpr int kN = Tile::kN;
@@ -577,7 +600,7 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
                               (int)cur[i][4 * s + 3]};
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bc[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = mfma_wq<kTrans>(af, bc[j], acc[i][j]);
         }
 #pragma unroll
         for (int b = lo; b < hi; ++b) splice_trits(nxt[b >> 4], b & 15, tv[b - lo]);
@@ -621,7 +644,7 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
         read_b((kt + 1) & 1u, 0, by);
         const i32x4 af = {(int)cur[1][16], (int)cur[1][17], (int)cur[1][18], (int)cur[1][19]};
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) acc[1][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bx[j], acc[1][j], 0, 0, 0);
+        for (int j = 0; j < NJ; ++j) acc[1][j] = mfma_wq<kTrans>(af, bx[j], acc[1][j]);
     };
 
     u32x4 ava[2], avb[2];
@@ -647,20 +670,76 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     }
     if (kt < nkt) kstep(kt, cura, curb, bfx, bfy, ava, aea, avb, aeb);
 
-    // Epilogue: ((float)acc * sa[m]) * sq[n].  Accumulator register q of lane
-    // l holds row 8 (q / 4) + 4 (l / 32) + q % 4, column l % 32 of its 32 x 32
-    // tile.  Each wave stages one 32-row slab (fragment i) at a time in its
-    // own LDS region (row pitch 264 floats: the two row groups of a write land
-    // on disjoint banks) and writes it back a whole 1 KB output row per store
-    // instruction, 16 bytes per lane.
+    // Epilogue: ((float)acc * sa[m]) * sq[n] (+ bias[m]).  Accumulator
+    // register q of lane l holds row 8 (q / 4) + 4 (l / 32) + q % 4, column
+    // l % 32 of its 32 x 32 tile.  Each wave stages its results in its own
+    // LDS region and writes them back as whole output rows, 16 bytes per lane:
+    //   * c[m, n]: one 32-row slab (fragment i: 32 m x kN n, row pitch 264
+    //     floats: the two row groups of a write land on disjoint banks) at a
+    //     time, a 1 KB output row per store instruction;
+    //   * c[n, m] (kTrans, the MFMA operands swapped: rows over n, columns
+    //     over m): one 32-row slab per column group j (32 n x the wave's 64 m,
+    //     row pitch 72 floats), four 256-byte output rows per store
+    //     instruction; the slab holds (float)acc * sa[m], and sq[n] is applied
+    //     as it is read back.
+    constexpr int kEpPitch = 264;
+    __syncthreads();  // every wave is done with the code tiles
+    if constexpr (kTrans) {
+        constexpr int kTp = 72;
+        float* slab = reinterpret_cast<float*>(wlds) + wave * 32 * kTp;
+        // the tile's sq[n0 .. n0 + kN), read per output row in the store phase
+        float* sqs = reinterpret_cast<float*>(wlds) + 4 * 32 * kTp;
+        if (t < kN) sqs[t] = p.sq[min(n0 + (uint32_t)t, p.n - 1u)];
+        __syncthreads();
+        const uint32_t mw = m0 + 64 * wave;  // this wave's 64 rows of m
+        float sam[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) sam[i] = p.sa[min(mw + 32 * i + r, p.m - 1u)];
+        // store phase: lane l writes m = mw + 4 (l % 16) .. + 3 of row 4 it + l / 16
+        const uint32_t mc = mw + 4 * (lane & 15);
+        const bool vec_out = (p.m & 3u) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15u) == 0;
+        f32x4 bias4 = {0.f, 0.f, 0.f, 0.f};
+        if (p.bias) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) bias4[u] = p.bias[min(mc + u, p.m - 1u)];
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int row = 8 * (q >> 2) + 4 * h + (q & 3);
+#pragma unroll
+                for (int i = 0; i < 2; ++i) slab[row * kTp + 32 * i + r] = (float)acc[i][j][q] * sam[i];
+            }
+            wave_lds_sync();
+#pragma unroll
+            for (int it = 0; it < 8; ++it) {
+                const int row = 4 * it + (lane >> 4);
+                const uint32_t n = n0 + 32 * j + row;
+                if (n >= p.n) continue;
+                const float sqn = sqs[32 * j + row];
+                f32x4 v = *reinterpret_cast<const f32x4*>(slab + row * kTp + 4 * (lane & 15));
+                v = v * sqn;
+                if (p.bias) v = v + bias4;
+                float* crow = p.c + (uint64_t)n * p.m;
+                if (vec_out && mc + 3 < p.m) {
+                    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(crow + mc));
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (mc + u < p.m) crow[mc + u] = v[u];
+                }
+            }
+            wave_lds_sync();  // the slab is rewritten for the next j
+        }
+        return;
+    }
     float sqn[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) sqn[j] = p.sq[min(n0 + 32 * j + r, p.n - 1u)];
-    constexpr int kEpPitch = 264;
     float* slab = reinterpret_cast<float*>(wlds) + wave * 32 * kEpPitch;
     const bool vec_out = (p.n & 3u) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15u) == 0;
     const uint32_t ncol = n0 + 4 * lane;
-    __syncthreads();  // every wave is done with the code tiles
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const uint32_t mb = m0 + 64 * wave + 32 * i;
@@ -676,7 +755,8 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
             const uint32_t m = mb + row;
             if (m >= p.m) break;
             if (4 * lane >= kN) continue;  // columns of the next tile
-            const f32x4 v = *reinterpret_cast<const f32x4*>(slab + row * kEpPitch + 4 * lane);
+            f32x4 v = *reinterpret_cast<const f32x4*>(slab + row * kEpPitch + 4 * lane);
+            if (p.bias) v = v + p.bias[m];
             float* crow = p.c + (uint64_t)m * p.n;
             if (vec_out && ncol + 3 < p.n) {
                 __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(crow + ncol));
@@ -707,7 +787,7 @@ constexpr int kSkRows = 32;
 constexpr uint64_t kSkMaxN = 64;
 constexpr int kSkPitch = 176;  // LDS bytes per code row of a block (160 + 16)
 
-template <int NT, bool kAlignedA, int kWaves>
+template <int NT, bool kAlignedA, int kWaves, bool kTrans>
 __global__ __launch_bounds__(kWaves * kWave) void ternary_i8_skinny_kernel(TernArgs p) {
     constexpr int kRowsB = 32 * NT;                   // code rows of the workgroup
     constexpr int kPieces = kRowsB * 10 / kWave;     // 16-byte code pieces per lane and block
@@ -821,7 +901,7 @@ __global__ __launch_bounds__(kWaves * kWave) void ternary_i8_skinny_kernel(TernA
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
                 const i32x4 b = *reinterpret_cast<const i32x4*>(region + (32 * j + r) * kSkPitch + 80 * h + 16 * s);
-                acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[j], 0, 0, 0);
+                acc[j] = mfma_wq<kTrans>(a, b, acc[j]);
             }
         }
     }
@@ -843,13 +923,26 @@ __global__ __launch_bounds__(kWaves * kWave) void ternary_i8_skinny_kernel(TernA
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) sum += reinterpret_cast<const i32x4*>(smem + w * kRegion)[g * kWave + lane];
         const int j = g / 4, q4 = g % 4;
+        if (kTrans) {
+            // accumulator rows over n, lanes over m: stores run along c[n, m]'s rows
+            const uint32_t m = m0 + (uint32_t)r;
+            if (m < p.m) {
+                const float sam = p.sa[m];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t n = (uint32_t)j * 32u + 8u * q4 + 4u * h + e;  // register 4 q4 + e
+                    if (n < p.n) p.c[out_idx(p, m, n)] = add_bias(p.bias, ((float)sum[e] * sam) * p.sq[n], m);
+                }
+            }
+            continue;
+        }
         const uint32_t n = (uint32_t)j * 32u + (uint32_t)r;
         if (n < p.n) {
             const float sqn = p.sq[n];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t m = m0 + 8 * q4 + 4 * h + e;  // register 4 q4 + e
-                if (m < p.m) p.c[(uint64_t)m * p.n + n] = ((float)sum[e] * p.sa[m]) * sqn;
+                if (m < p.m) p.c[out_idx(p, m, n)] = add_bias(p.bias, ((float)sum[e] * p.sa[m]) * sqn, m);
             }
         }
     }
@@ -866,9 +959,9 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_zero_kernel(int32_t* c, u
 __global__ __launch_bounds__(kTmBlock) void ternary_i8_finish_kernel(TernArgs p) {
     const uint64_t i = (uint64_t)blockIdx.x * kTmBlock + threadIdx.x;
     if (i >= (uint64_t)p.m * p.n) return;
-    const uint32_t m = (uint32_t)(i / p.n), n = (uint32_t)(i % p.n);
+    const uint32_t m = (uint32_t)(p.trans ? i % p.m : i / p.n), n = (uint32_t)(p.trans ? i / p.m : i % p.n);
     const int32_t acc = reinterpret_cast<const int32_t*>(p.c)[i];
-    p.c[i] = ((float)acc * p.sa[m]) * p.sq[n];
+    p.c[i] = add_bias(p.bias, ((float)acc * p.sa[m]) * p.sq[n], m);
 }
 
 // Small-n path (n <= 8, k % 8 == 0, 8-byte aligned codes): a group of waves
@@ -1048,7 +1141,7 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_gemv_kernel(TernArgs p) {
 #pragma unroll
             for (int n = 0; n < NT; ++n) {
                 if (n0 + n >= p.n || m >= p.m) continue;
-                p.c[(uint64_t)m * p.n + n0 + n] = ((float)tot[r][n] * p.sa[m]) * p.sq[n0 + n];
+                p.c[out_idx(p, m, n0 + n)] = add_bias(p.bias, ((float)tot[r][n] * p.sa[m]) * p.sq[n0 + n], m);
             }
         }
     }
@@ -1073,7 +1166,7 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_generic_kernel(TernArgs p
     __syncthreads();
     const uint64_t idx = (uint64_t)blockIdx.x * kTmBlock + threadIdx.x;
     if (idx >= (uint64_t)p.m * p.n) return;
-    const uint32_t m = (uint32_t)(idx / p.n), n = (uint32_t)(idx % p.n);
+    const uint32_t m = (uint32_t)(p.trans ? idx % p.m : idx / p.n), n = (uint32_t)(p.trans ? idx / p.m : idx % p.n);
     const uint8_t* ar = p.a + (uint64_t)m * p.kp;
     const int8_t* qr = p.q + (uint64_t)n * p.k;
     int32_t acc = 0;
@@ -1082,7 +1175,7 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_generic_kernel(TernArgs p
         const int8_t tr = (int8_t)(uint8_t)(v >> (8 * (k % 5)));
         acc += (int32_t)tr * (int32_t)qr[k];
     }
-    p.c[idx] = ((float)acc * p.sa[m]) * p.sq[n];
+    p.c[idx] = add_bias(p.bias, ((float)acc * p.sa[m]) * p.sq[n], m);
 }
 
 // ---------------------------------------------------------------------------
@@ -1108,10 +1201,18 @@ __global__ __launch_bounds__(kTmBlock) void ternary_i8_generic_kernel(TernArgs p
 struct TernF32Args {
     const uint8_t* a;   // packed [M, Kp]
     const float* sa;    // [M]
-    const float* b;     // [K, N]
-    float* c;           // [M, N]
+    const float* b;     // element (k, col) at b[k * bk + col * bn]: [K, N] (bk = N, bn = 1) or token-major [N, K]
+    float* c;           // [M, N], or [N, M] with trans
     uint32_t m, n, k, kp;
+    uint64_t bk, bn;
+    const float* bias;  // [M] added to every output of row m, or null
+    uint32_t trans;     // 1: output (m, col) at c[col * ldt + m]
+    uint64_t ldt;       // row stride of the transposed output (the full M)
 };
+
+__device__ __forceinline__ uint64_t out_idx(const TernF32Args& p, uint32_t m, uint32_t n) {
+    return p.trans ? (uint64_t)n * p.ldt + m : (uint64_t)m * p.n + n;
+}
 
 template <int CT, int R, int kW, bool kAligned16>
 __global__ __launch_bounds__(kW * kWave) void ternary_f32_seq_kernel(TernF32Args p) {
@@ -1219,7 +1320,7 @@ __global__ __launch_bounds__(kW * kWave) void ternary_f32_seq_kernel(TernF32Args
             const uint32_t e = (uint32_t)t + kThreads * u;
             const uint32_t ki = e / CT, c = e % CT;
             const bool ok = e < kn * CT && col0 + c < p.n;
-            const float v = p.b[ok ? (uint64_t)(kc + ki) * p.n + col0 + c : 0u];
+            const float v = p.b[ok ? (uint64_t)(kc + ki) * p.bk + (uint64_t)(col0 + c) * p.bn : 0u];
             bvn[u] = ok ? v : 0.0f;
         }
     };
@@ -1313,7 +1414,7 @@ __global__ __launch_bounds__(kW * kWave) void ternary_f32_seq_kernel(TernF32Args
     }
 #pragma unroll
     for (int i = 0; i < R; ++i)
-        if (live[i]) p.c[(uint64_t)rows[i] * p.n + col] = acc[i] * p.sa[rows[i]];
+        if (live[i]) p.c[out_idx(p, rows[i], col)] = add_bias(p.bias, acc[i] * p.sa[rows[i]], rows[i]);
 }
 
 // One to four columns (K = 0 or fewer than 20 packed bytes): one fold per
@@ -1328,7 +1429,13 @@ static void launch_f32_seq(int ct, dim3 g, hipStream_t s, const TernF32Args& p) 
 #undef KORE_F32_SEQ
 }
 
-constexpr uint32_t kRowsW = 4;            // waves per workgroup
+constexpr uint32_t kRowsW = 4;            // waves per workgroup (b[K, N])
+// Token-major b (the layer's input as stored): a staged chunk is a 320-byte
+// piece of every column, which straddles cache lines, so every workgroup's
+// share of L2 reads grows; eight waves share each staged chunk instead of
+// four (measured at 6912 x 64 x 2560: 82.3 -> 71.1 us; 16 columns 25.6 ->
+// 23.1 us).
+constexpr uint32_t kRowsWTm = 8;
 constexpr int kBufWord3 = 0x00020000;     // buffer resource word 3 (raw dword access)
 constexpr uint64_t kRowsMinWaves = 1536;  // 1.5 per SIMD of 256 CUs
 constexpr uint64_t kSimds = 1024;         // 256 CUs x 4
@@ -1358,7 +1465,7 @@ __device__ __forceinline__ float fmac_trit(float acc, float t, float b) {
     return acc;
 }
 
-template <int CT, int R, int W>
+template <int CT, int R, int W, bool TM>
 __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args p) {
     constexpr int KC = 80;                 // K columns per chunk
     constexpr int NB = KC / 5;             // packed bytes per row and chunk (one per lane of a 16-lane row)
@@ -1387,31 +1494,61 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args
     const uint32_t col = col0 + (uint32_t)(lane % CT);
     // row slot lane / CT of the wave owns rows row0 .. row0 + R - 1
     const uint32_t row0 = ((blockIdx.x * W + wave) * kSlots + (uint32_t)(lane / CT)) * R;
-    // b staging: group g of a chunk is k = 4 (g / 64) .. + 3 of column g % 64,
-    // four coalesced loads (a row of 64 columns each), one 16-byte LDS write
-    // at [column][k].  Buffer loads from a resource based at the chunk's
-    // first row of b, with byte offsets fixed for the whole kernel: the
-    // hardware range check returns zeros past K, and an offset past any
-    // range does so for columns past N.
+    // b staging: group g of a chunk is k = 4 (g / CT) .. + 3 of column g % CT,
+    // one 16-byte LDS write at [column][k].  Buffer loads from a resource
+    // based at the chunk's first k of the tile's first column, with byte
+    // offsets fixed for the whole kernel; an offset past any range returns
+    // zeros for columns past N.  b[K, N] (TM false): four coalesced loads (a
+    // row of CT columns each), and the hardware range check returns zeros
+    // past K.  Token-major b[N, K] (TM true: the layer's input x as it is
+    // stored): the four k of a group are consecutive in one column, and the
+    // last chunk zeroes k >= K itself (those offsets lie in the next column).
+    // Token-major groups run along k (cl = g / 20, k4 = 4 (g % 20)), so that
+    // consecutive lanes read consecutive bytes of one column.
     uint32_t boff[kStage][4];
+    uint32_t bk4[kStage];
+    auto g_col = [](uint32_t g) { return TM ? g / (KC / 4) : g % CT; };
+    auto g_k4 = [](uint32_t g) { return TM ? 4u * (g % (KC / 4)) : 4u * (g / CT); };
 #pragma unroll
     for (int u = 0; u < kStage; ++u) {
         const uint32_t g = (uint32_t)t + kThreads * u;
-        const uint32_t c = col0 + g % CT, k4 = 4u * (g / CT);
+        const uint32_t cl = g_col(g), k4 = g_k4(g);
+        bk4[u] = k4;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) boff[u][q] = c < p.n ? ((k4 + q) * p.n + c) * 4u : 0x80000000u;
+        for (int q = 0; q < 4; ++q)
+            boff[u][q] = col0 + cl < p.n ? (TM ? (cl * p.k + k4 + q) * 4u : ((k4 + q) * p.n + cl) * 4u) : 0x80000000u;
     }
     auto load_b = [&](uint32_t kc, f32x4 (&bv)[kStage]) {
-        const uint64_t left = (uint64_t)(p.k - kc) * p.n * 4u;
+        const uint64_t left = TM ? ((uint64_t)(p.n - col0) * p.k - kc) * 4u : ((uint64_t)(p.k - kc) * p.n - col0) * 4u;
         const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(p.b + (uint64_t)kc * p.n), (short)0, (int)(left < 0x7fffffffull ? left : 0x7fffffffull), kBufWord3);
+            (void*)(p.b + (uint64_t)kc * p.bk + (uint64_t)col0 * p.bn), (short)0,
+            (int)(left < 0x7fffffffull ? left : 0x7fffffffull), kBufWord3);
+        const uint32_t kleft = p.k - kc;
 #pragma unroll
         for (int u = 0; u < kStage; ++u) {
             if (kGroups % kThreads != 0 && u == kStage - 1 && t >= kGroups % kThreads) break;
             float v[4];
+            if (TM) {
+                // the group's four k are consecutive in its column: one
+                // 16-byte load (global loads need dword alignment only) in a
+                // whole chunk, single elements checked against K in the last
+                const float* src = p.b + (boff[u][0] == 0x80000000u ? 0u : (uint64_t)boff[u][0] / 4u + kc +
+                                                                              (uint64_t)col0 * p.k);
+                if (kleft >= (uint32_t)KC) {
+                    const u32x4 wu = boff[u][0] == 0x80000000u ? u32x4{0u, 0u, 0u, 0u}
+                                                               : (u32x4)*reinterpret_cast<const u32x4_a4*>(src);
+                    const f32x4 w = __builtin_bit_cast(f32x4, wu);
+                    v[0] = w[0]; v[1] = w[1]; v[2] = w[2]; v[3] = w[3];
+                } else {
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                v[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, boff[u][q], 0, 0));
+                    for (int q = 0; q < 4; ++q)
+                        v[q] = (boff[u][0] != 0x80000000u && bk4[u] + q < kleft) ? src[q] : 0.0f;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    v[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, boff[u][q], 0, 0));
+            }
             bv[u] = f32x4{v[0], v[1], v[2], v[3]};
         }
     };
@@ -1444,7 +1581,7 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args
         for (int u = 0; u < kStage; ++u) {
             if (kGroups % kThreads != 0 && u == kStage - 1 && t >= kGroups % kThreads) break;
             const uint32_t g = (uint32_t)t + kThreads * u;
-            *reinterpret_cast<f32x4*>(bb + (g % CT) * kPitch + 4 * (g / CT)) = bvn[u];
+            *reinterpret_cast<f32x4*>(bb + g_col(g) * kPitch + g_k4(g)) = bvn[u];
         }
         // this chunk's trits: lane L holds the five of byte L % 16 of each row
         uint32_t pbc[R];
@@ -1528,9 +1665,19 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args
         }
     }
     if (col < p.n) {
+        // c[n, m] with four rows per lane: the lane's rows are four
+        // consecutive floats of one output row, stored as one 16-byte write
+        if (R == 4 && p.trans && row0 + 3 < p.m && (p.ldt & 3u) == 0 &&
+            (reinterpret_cast<uintptr_t>(p.c) & 15u) == 0) {
+            f32x4 v;
+#pragma unroll
+            for (int i = 0; i < R && i < 4; ++i) v[i] = add_bias(p.bias, acc[i] * p.sa[row0 + i], row0 + i);
+            *reinterpret_cast<f32x4*>(p.c + out_idx(p, row0, col)) = v;
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < R; ++i)
-            if (row0 + i < p.m) p.c[(uint64_t)(row0 + i) * p.n + col] = acc[i] * p.sa[row0 + i];
+            if (row0 + i < p.m) p.c[out_idx(p, row0 + i, col)] = add_bias(p.bias, acc[i] * p.sa[row0 + i], row0 + i);
     }
 }
 
@@ -1538,7 +1685,7 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args
 // LDS once per R rows; measured: 16- and 32-column tiles ran 6-12% slower
 // with 4 than with 2 at every m tried, 64-column tiles 8-20% faster) while
 // that leaves at least 1.5 waves per SIMD, else fewer.
-template <int CT>
+template <int CT, bool TM>
 static int launch_f32_rows(uint64_t m, uint64_t n, hipStream_t s, const TernF32Args& p) {
     constexpr uint64_t kSlots = kWave / CT;
     const uint64_t gy = (n + CT - 1) / CT;
@@ -1559,18 +1706,19 @@ static int launch_f32_rows(uint64_t m, uint64_t n, hipStream_t s, const TernF32A
         }
     }
     if ((m + 2 * kSlots - 1) / (2 * kSlots) * gy < kRowsMinWaves) r = 1;
-    const uint64_t rows = r * kSlots * kRowsW;  // rows per workgroup
+    constexpr uint32_t W = TM ? kRowsWTm : kRowsW;
+    const uint64_t rows = r * kSlots * W;  // rows per workgroup
     const uint64_t bx = (m + rows - 1) / rows;
     if (bx > 0x7fffffffull || gy > 65535) return KORE_HIP_ERR_OVERFLOW;
-    const dim3 gr((uint32_t)bx, (uint32_t)gy), blk(kRowsW * kWave);
+    const dim3 gr((uint32_t)bx, (uint32_t)gy), blk(W * kWave);
     if constexpr (CT == 64) {
-        if (r == 4) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 4, kRowsW>), gr, blk, 0, s, p);
-        else if (r == 5) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 5, kRowsW>), gr, blk, 0, s, p);
-        else if (r == 7) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 7, kRowsW>), gr, blk, 0, s, p);
+        if (r == 4) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 4, W, TM>), gr, blk, 0, s, p);
+        else if (r == 5) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 5, W, TM>), gr, blk, 0, s, p);
+        else if (r == 7) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 7, W, TM>), gr, blk, 0, s, p);
         if (r >= 4) return launch_status();
     }
-    if (r == 2) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 2, kRowsW>), gr, blk, 0, s, p);
-    else hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 1, kRowsW>), gr, blk, 0, s, p);
+    if (r == 2) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 2, W, TM>), gr, blk, 0, s, p);
+    else hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 1, W, TM>), gr, blk, 0, s, p);
     return launch_status();
 }
 
@@ -1649,7 +1797,8 @@ void ternary_f32_pipe_kernel(TernF32Args p) {
     };
     auto b_idx = [&](uint32_t s, int h) {
         const int i = e + kSL * h;
-        return b_ok(s, h) ? (uint64_t)(s * kPfStep + (uint32_t)(i / CT)) * p.n + col0 + (uint32_t)(i % CT) : 0u;
+        return b_ok(s, h) ? (uint64_t)(s * kPfStep + (uint32_t)(i / CT)) * p.bk + (uint64_t)(col0 + (uint32_t)(i % CT)) * p.bn
+                          : 0u;
     };
     float bv[kPfDepth][kStageN];
     // stage b of step s into bb[s % 3]; bflag[buf][d]: the columns in which
@@ -1723,7 +1872,7 @@ void ternary_f32_pipe_kernel(TernF32Args p) {
             }
             __syncthreads();
         }
-        if (row < p.m && col0 + c < p.n) p.c[(uint64_t)row * p.n + col0 + c] = acc * p.sa[row];
+        if (row < p.m && col0 + c < p.n) p.c[out_idx(p, row, col0 + c)] = add_bias(p.bias, acc * p.sa[row], row);
         return;
     }
     const int d = wave - CT;
@@ -2048,20 +2197,41 @@ __global__ __launch_bounds__(kPackWaves * kWave) void ternary_pack_kernel(const 
 }  // namespace kore
 
 namespace kore {
+template <bool kSplit, bool kTrans>
+static void launch_mfma_t(bool aligned_a, bool aligned_b, dim3 grid, hipStream_t s, const TernArgs& p) {
+    if (aligned_a && aligned_b)
+        hipLaunchKernelGGL((ternary_i8_mfma_kernel<true, true, kSplit, kTrans>), grid, dim3(kTmBlock), 0, s, p);
+    else if (aligned_b)
+        hipLaunchKernelGGL((ternary_i8_mfma_kernel<false, true, kSplit, kTrans>), grid, dim3(kTmBlock), 0, s, p);
+    else if (aligned_a)
+        hipLaunchKernelGGL((ternary_i8_mfma_kernel<true, false, kSplit, kTrans>), grid, dim3(kTmBlock), 0, s, p);
+    else hipLaunchKernelGGL((ternary_i8_mfma_kernel<false, false, kSplit, kTrans>), grid, dim3(kTmBlock), 0, s, p);
+}
 template <bool kSplit>
 static void launch_mfma(bool aligned_a, bool aligned_b, dim3 grid, hipStream_t s, const TernArgs& p) {
-    if (aligned_a && aligned_b) hipLaunchKernelGGL((ternary_i8_mfma_kernel<true, true, kSplit>), grid, dim3(kTmBlock), 0, s, p);
-    else if (aligned_b) hipLaunchKernelGGL((ternary_i8_mfma_kernel<false, true, kSplit>), grid, dim3(kTmBlock), 0, s, p);
-    else if (aligned_a) hipLaunchKernelGGL((ternary_i8_mfma_kernel<true, false, kSplit>), grid, dim3(kTmBlock), 0, s, p);
-    else hipLaunchKernelGGL((ternary_i8_mfma_kernel<false, false, kSplit>), grid, dim3(kTmBlock), 0, s, p);
+    if (p.trans) launch_mfma_t<kSplit, true>(aligned_a, aligned_b, grid, s, p);
+    else launch_mfma_t<kSplit, false>(aligned_a, aligned_b, grid, s, p);
+}
+template <int NJ, bool kTrans>
+static void launch_wide_t(bool aligned_a, dim3 g, hipStream_t s, const TernArgs& p) {
+    if (aligned_a)
+        hipLaunchKernelGGL((ternary_i8_wide_kernel<true, NJ, kTrans>), g, dim3(256), WideTile<NJ>::kLds, s, p);
+    else hipLaunchKernelGGL((ternary_i8_wide_kernel<false, NJ, kTrans>), g, dim3(256), WideTile<NJ>::kLds, s, p);
+}
+template <int NJ>
+static void launch_wide(bool aligned_a, dim3 g, hipStream_t s, const TernArgs& p) {
+    if (p.trans) launch_wide_t<NJ, true>(aligned_a, g, s, p);
+    else launch_wide_t<NJ, false>(aligned_a, g, s, p);
 }
 }  // namespace kore
 
 using namespace kore;
 
-extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* a_scales, const int8_t* q,
-                                          const float* q_scales, float* c, uint64_t m, uint64_t n, uint64_t k,
-                                          kore_stream_t stream) {
+// The int8 matmul with the output in either layout (trans: c[n, m]) and an
+// optional bias per weight row.
+static int ternary_i8_run(const uint8_t* a_packed, const float* a_scales, const int8_t* q, const float* q_scales,
+                          const float* bias, float* c, uint64_t m, uint64_t n, uint64_t k, bool trans,
+                          hipStream_t s) {
     if (m == 0 || n == 0) return KORE_HIP_OK;
     if (!c || !a_scales || !q_scales) return KORE_HIP_ERR_NULL_PTR;
     if (k > 0 && (!a_packed || !q)) return KORE_HIP_ERR_NULL_PTR;
@@ -2077,14 +2247,15 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
         const char* c0 = reinterpret_cast<const char*>(c);
         const char* c1 = c0 + mn * sizeof(float);
         const struct { const void* p; uint64_t bytes; } ins[] = {
-            {a_packed, m * kp}, {q, nk}, {a_scales, m * sizeof(float)}, {q_scales, n * sizeof(float)}};
+            {a_packed, m * kp}, {q, nk}, {a_scales, m * sizeof(float)}, {q_scales, n * sizeof(float)},
+            {bias, bias ? m * sizeof(float) : 0u}};
         for (const auto& in : ins) {
             const char* i0 = reinterpret_cast<const char*>(in.p);
             if (in.p && in.bytes && i0 < c1 && c0 < i0 + in.bytes) return KORE_HIP_ERR_ALIAS;
         }
     }
-    TernArgs p{a_packed, a_scales, q, q_scales, c, (uint32_t)m, (uint32_t)n, (uint32_t)k, (uint32_t)kp, 1u, 0u};
-    hipStream_t s = (hipStream_t)stream;
+    TernArgs p{a_packed, a_scales, q,  q_scales, c, (uint32_t)m, (uint32_t)n, (uint32_t)k, (uint32_t)kp, 1u, 0u,
+               bias,     trans ? 1u : 0u};
     const bool c_ok = (reinterpret_cast<uintptr_t>(c) & 3u) == 0;
     if (n <= kGvMaxN && k > 0 && k % 8 == 0 && (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && c_ok) {
         // grid: at most m / 4 blocks of one wave group (m < 2^31)
@@ -2107,13 +2278,15 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
         const bool al = kp % 16 == 0 && aligned16(a_packed);
         const dim3 g((uint32_t)blocks);
         const int nt = (int)((n + 31) / 32);
-        if (al) {
-            if (nt == 1) hipLaunchKernelGGL((ternary_i8_skinny_kernel<1, true, 8>), g, dim3(8 * kWave), 0, s, p);
-            else hipLaunchKernelGGL((ternary_i8_skinny_kernel<2, true, 8>), g, dim3(8 * kWave), 0, s, p);
+#define KORE_SKINNY(NT, AL, TR) hipLaunchKernelGGL((ternary_i8_skinny_kernel<NT, AL, 8, TR>), g, dim3(8 * kWave), 0, s, p)
+        if (trans) {
+            if (al) { if (nt == 1) KORE_SKINNY(1, true, true); else KORE_SKINNY(2, true, true); }
+            else { if (nt == 1) KORE_SKINNY(1, false, true); else KORE_SKINNY(2, false, true); }
         } else {
-            if (nt == 1) hipLaunchKernelGGL((ternary_i8_skinny_kernel<1, false, 8>), g, dim3(8 * kWave), 0, s, p);
-            else hipLaunchKernelGGL((ternary_i8_skinny_kernel<2, false, 8>), g, dim3(8 * kWave), 0, s, p);
+            if (al) { if (nt == 1) KORE_SKINNY(1, true, false); else KORE_SKINNY(2, true, false); }
+            else { if (nt == 1) KORE_SKINNY(1, false, false); else KORE_SKINNY(2, false, false); }
         }
+#undef KORE_SKINNY
         return launch_status();
     }
     const uint64_t wide_tiles = ((m + kWdM - 1) / kWdM) * ((n + kWdN - 1) / kWdN);
@@ -2132,13 +2305,8 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
         if (per * kXcds > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
         const dim3 g((uint32_t)(per * kXcds));
         const bool al = kp % 16 == 0 && aligned16(a_packed);
-        if (n192) {
-            if (al) hipLaunchKernelGGL((ternary_i8_wide_kernel<true, 6>), g, dim3(256), WideTile<6>::kLds, s, p);
-            else hipLaunchKernelGGL((ternary_i8_wide_kernel<false, 6>), g, dim3(256), WideTile<6>::kLds, s, p);
-        } else {
-            if (al) hipLaunchKernelGGL((ternary_i8_wide_kernel<true, 8>), g, dim3(256), WideTile<8>::kLds, s, p);
-            else hipLaunchKernelGGL((ternary_i8_wide_kernel<false, 8>), g, dim3(256), WideTile<8>::kLds, s, p);
-        }
+        if (n192) launch_wide<6>(al, g, s, p);
+        else launch_wide<8>(al, g, s, p);
         return launch_status();
     }
     if (k > 0 && c_ok) {
@@ -2176,8 +2344,23 @@ extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* 
     return launch_status();
 }
 
-extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float* a_scales, const float* b, float* c,
-                                           uint64_t m, uint64_t n, uint64_t k, kore_stream_t stream) {
+extern "C" int kore_hip_ternary_matmul_i8(const uint8_t* a_packed, const float* a_scales, const int8_t* q,
+                                          const float* q_scales, float* c, uint64_t m, uint64_t n, uint64_t k,
+                                          kore_stream_t stream) {
+    return ternary_i8_run(a_packed, a_scales, q, q_scales, nullptr, c, m, n, k, false, (hipStream_t)stream);
+}
+
+extern "C" int kore_hip_bit_linear_i8(const uint8_t* a_packed, const float* a_scales, const int8_t* q,
+                                      const float* q_scales, const float* bias, float* y, uint64_t out_features,
+                                      uint64_t batch, uint64_t in_features, kore_stream_t stream) {
+    return ternary_i8_run(a_packed, a_scales, q, q_scales, bias, y, out_features, batch, in_features, true,
+                          (hipStream_t)stream);
+}
+
+// The f32-activation matmul with b either [K, N] or token-major [N, K]
+// (tm), the output in either layout (trans: c[n, m]) and an optional bias.
+static int ternary_f32_run(const uint8_t* a_packed, const float* a_scales, const float* b, const float* bias,
+                           float* c, uint64_t m, uint64_t n, uint64_t k, bool tm, bool trans, hipStream_t s) {
     if (m == 0 || n == 0) return KORE_HIP_OK;
     if (!c || !a_scales) return KORE_HIP_ERR_NULL_PTR;
     if (k > 0 && (!a_packed || !b)) return KORE_HIP_ERR_NULL_PTR;
@@ -2192,14 +2375,18 @@ extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float*
         const char* c0 = reinterpret_cast<const char*>(c);
         const char* c1 = c0 + mn * sizeof(float);
         const struct { const void* p; uint64_t bytes; } ins[] = {
-            {a_packed, mkp}, {b, kn * sizeof(float)}, {a_scales, m * sizeof(float)}};
+            {a_packed, mkp}, {b, kn * sizeof(float)}, {a_scales, m * sizeof(float)},
+            {bias, bias ? m * sizeof(float) : 0u}};
         for (const auto& in : ins) {
             const char* i0 = reinterpret_cast<const char*>(in.p);
             if (in.p && in.bytes && i0 < c1 && c0 < i0 + in.bytes) return KORE_HIP_ERR_ALIAS;
         }
     }
-    TernF32Args p{a_packed, a_scales, b, c, (uint32_t)m, (uint32_t)n, (uint32_t)k, (uint32_t)kp};
-    hipStream_t s = (hipStream_t)stream;
+    // token-major b: the rows kernel's buffer offsets (column x K x 4 bytes
+    // within a 64-column tile) stay below 2^31
+    if (tm && k > (1ull << 23)) return KORE_HIP_ERR_OVERFLOW;
+    TernF32Args p{a_packed, a_scales, b, c, (uint32_t)m, (uint32_t)n, (uint32_t)k, (uint32_t)kp,
+                  tm ? 1u : n, tm ? k : 1u, bias, trans ? 1u : 0u, m};
     int ct = 64;
     while (ct > 1 && (uint64_t)(ct / 2) >= n) ct /= 2;  // smallest power of two >= n (<= 64)
     // Five columns and more: the row-broadcast kernel (any row alignment) in
@@ -2211,11 +2398,15 @@ extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float*
             TernF32Args q = p;
             q.a += r0 * kp;
             q.sa += r0;
-            q.c += r0 * n;
             q.m = (uint32_t)std::min<uint64_t>(span, m - r0);
-            const int st = ct <= 16 ? launch_f32_rows<16>(q.m, n, s, q)
-                         : ct == 32 ? launch_f32_rows<32>(q.m, n, s, q)
-                                    : launch_f32_rows<64>(q.m, n, s, q);
+            q.c += trans ? r0 : r0 * n;  // c[n, m]: columns r0 .. of every row, row stride m
+            if (bias) q.bias += r0;
+            const int st = tm ? (ct <= 16 ? launch_f32_rows<16, true>(q.m, n, s, q)
+                                 : ct == 32 ? launch_f32_rows<32, true>(q.m, n, s, q)
+                                            : launch_f32_rows<64, true>(q.m, n, s, q))
+                              : (ct <= 16 ? launch_f32_rows<16, false>(q.m, n, s, q)
+                                 : ct == 32 ? launch_f32_rows<32, false>(q.m, n, s, q)
+                                            : launch_f32_rows<64, false>(q.m, n, s, q));
             if (st != KORE_HIP_OK) return st;
         }
         return KORE_HIP_OK;
@@ -2234,6 +2425,18 @@ extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float*
     if (kp % 16 == 0 && aligned16(a_packed)) launch_f32_seq<true>(ct, g, s, p);
     else launch_f32_seq<false>(ct, g, s, p);
     return launch_status();
+}
+
+extern "C" int kore_hip_ternary_matmul_f32(const uint8_t* a_packed, const float* a_scales, const float* b, float* c,
+                                           uint64_t m, uint64_t n, uint64_t k, kore_stream_t stream) {
+    return ternary_f32_run(a_packed, a_scales, b, nullptr, c, m, n, k, false, false, (hipStream_t)stream);
+}
+
+extern "C" int kore_hip_bit_linear_f32(const uint8_t* a_packed, const float* a_scales, const float* x,
+                                       const float* bias, float* y, uint64_t out_features, uint64_t batch,
+                                       uint64_t in_features, kore_stream_t stream) {
+    return ternary_f32_run(a_packed, a_scales, x, bias, y, out_features, batch, in_features, true, true,
+                           (hipStream_t)stream);
 }
 
 extern "C" int kore_hip_pack_weights_ternary(const float* w, uint64_t m, uint64_t k, float threshold,

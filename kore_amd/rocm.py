@@ -417,6 +417,46 @@ def rocm_ternary_matmul_f32(device_idx: int, a_packed: HipBuffer, a_scales: HipB
     return c
 
 
+def rocm_bit_linear_f32(device_idx: int, a_packed: HipBuffer, a_scales: HipBuffer, x: HipBuffer,
+                        bias: Optional[HipBuffer], out_features: int, batch: int, in_features: int,
+                        out: Optional[HipBuffer] = None) -> HipBuffer:
+    """``BitLinear::forward`` (bit_linear.rs:175-237) in one launch: y[batch,
+    out] = ternary_matmul(W, scales, x^T)^T + bias with the layer's input
+    x[batch, in] as stored and the output in the layer's layout; bias None for
+    a layer without bias (bit-exact)."""
+    _require_device(device_idx)
+    _need(a_packed, out_features * ((in_features + 4) // 5), "ternary weights")
+    _need(a_scales, out_features * 4, "ternary scales")
+    _need(x, batch * in_features * 4, "layer input")
+    if bias is not None:
+        _need(bias, out_features * 4, "bias")
+    y = _out(device_idx, out, batch * out_features * 4, "layer output")
+    _check(_lib.load().kore_hip_bit_linear_f32(a_packed.ptr, a_scales.ptr, x.ptr, bias.ptr if bias else None, y.ptr,
+                                               out_features, batch, in_features, _stream(device_idx)),
+           "bit_linear_f32")
+    return y
+
+
+def rocm_bit_linear_i8(device_idx: int, a_packed: HipBuffer, a_scales: HipBuffer, q: HipBuffer, q_scales: HipBuffer,
+                       bias: Optional[HipBuffer], out_features: int, batch: int, in_features: int,
+                       out: Optional[HipBuffer] = None) -> HipBuffer:
+    """The BitLinear layer on pre-quant codes q[batch, in] / q_scales[batch]:
+    y[b, o] = c[o, b] + bias[o] with c of ``rocm_ternary_matmul_i8``, in the
+    layer's [batch, out] layout (bit-exact)."""
+    _require_device(device_idx)
+    _need(a_packed, out_features * ((in_features + 4) // 5), "ternary weights")
+    _need(a_scales, out_features * 4, "ternary scales")
+    _need(q, batch * in_features, "codes")
+    _need(q_scales, batch * 4, "code scales")
+    if bias is not None:
+        _need(bias, out_features * 4, "bias")
+    y = _out(device_idx, out, batch * out_features * 4, "layer output")
+    _check(_lib.load().kore_hip_bit_linear_i8(a_packed.ptr, a_scales.ptr, q.ptr, q_scales.ptr,
+                                              bias.ptr if bias else None, y.ptr, out_features, batch, in_features,
+                                              _stream(device_idx)), "bit_linear_i8")
+    return y
+
+
 def rocm_pack_weights_ternary(device_idx: int, w: HipBuffer, m: int, k: int, threshold: float,
                               packed: Optional[HipBuffer] = None,
                               scales: Optional[HipBuffer] = None) -> Tuple[HipBuffer, HipBuffer]:
@@ -433,4 +473,5 @@ def rocm_pack_weights_ternary(device_idx: int, w: HipBuffer, m: int, k: int, thr
     return p, sc
 
 
-__all__ += ["rocm_ternary_matmul_i8", "rocm_ternary_matmul_f32", "rocm_pack_weights_ternary"]
+__all__ += ["rocm_ternary_matmul_i8", "rocm_ternary_matmul_f32", "rocm_bit_linear_f32", "rocm_bit_linear_i8",
+            "rocm_pack_weights_ternary"]

@@ -229,7 +229,8 @@ __all__ = ["build", "lib", "rms_norm", "gelu", "silu", "mul", "swiglu", "rope_in
            "embedding_forward", "f32_as_usize", "silu_stable", "swiglu_serve",
            "rms_norm_quant_i8", "rms_norm_silu_gate", "quant_code", "softmax", "softmax_causal",
            "softmax_backward", "rms_norm_backward", "cross_entropy_backward", "decode_trits", "encode_trits",
-           "pack_weights_ternary", "ternary_matmul", "ternary_matmul_i8", "unpack_trits"]
+           "pack_weights_ternary", "ternary_matmul", "ternary_matmul_i8", "unpack_trits", "bit_linear_forward",
+           "bit_linear_i8"]
 
 
 def _rows_cols(x: np.ndarray):
@@ -325,6 +326,28 @@ def ternary_matmul_i8(packed, scales, q, q_scales, m: int, n: int, k: int) -> np
     c = np.empty((m, n), np.float32)
     lib().kore_oracle_ternary_matmul_i8(_ptr(packed), _ptr(scales), _ptr(q), _ptr(q_scales), _ptr(c), m, n, k)
     return c
+
+
+def bit_linear_forward(packed, scales, x, bias, out_features: int, batch: int, in_features: int) -> np.ndarray:
+    """BitLinear::forward (crates/kore-nn/src/bit_linear.rs:175-237) composed
+    as the reference composes it: input_t = x^T made contiguous (:200),
+    output = ternary_matmul(packed, scales, input_t, out, batch, in) (:202-209),
+    transposed back to [batch, out] (:213), then output.add(bias) (:217-219),
+    an f32 add per element broadcasting bias[out] over the batch."""
+    xt = np.ascontiguousarray(_f32(x).reshape(batch, in_features).T)
+    y = np.ascontiguousarray(ternary_matmul(packed, scales, xt, out_features, batch, in_features).T)
+    if bias is not None:
+        y = (y + _f32(bias).reshape(1, out_features)).astype(np.float32)
+    return y
+
+
+def bit_linear_i8(packed, scales, q, q_scales, bias, out_features: int, batch: int, in_features: int) -> np.ndarray:
+    """The BitLinear layer on pre-quant codes, composed like bit_linear_forward
+    with ternary_matmul_i8 in place of ternary_matmul: y = c^T + bias."""
+    y = np.ascontiguousarray(ternary_matmul_i8(packed, scales, q, q_scales, out_features, batch, in_features).T)
+    if bias is not None:
+        y = (y + _f32(bias).reshape(1, out_features)).astype(np.float32)
+    return y
 
 
 def unpack_trits(packed, k: int) -> np.ndarray:

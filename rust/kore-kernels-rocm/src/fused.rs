@@ -45,6 +45,10 @@ type FnTernaryI8 = unsafe extern "C" fn(*const u8, *const f32, *const i8, *const
                                         Stream) -> c_int;
 type FnTernaryF32 = unsafe extern "C" fn(*const u8, *const f32, *const f32, *mut f32, u64, u64, u64,
                                          Stream) -> c_int;
+type FnBitLinearF32 = unsafe extern "C" fn(*const u8, *const f32, *const f32, *const f32, *mut f32, u64, u64, u64,
+                                          Stream) -> c_int;
+type FnBitLinearI8 = unsafe extern "C" fn(*const u8, *const f32, *const i8, *const f32, *const f32, *mut f32, u64,
+                                         u64, u64, Stream) -> c_int;
 type FnPackTernary = unsafe extern "C" fn(*const f32, u64, u64, f32, *mut u8, *mut f32, Stream) -> c_int;
 type FnStatus = unsafe extern "C" fn(c_int) -> *const c_char;
 
@@ -72,6 +76,8 @@ struct FusedApi {
     rms_bwd_noalloc_max: FnMaxBytes,
     ternary_i8: FnTernaryI8,
     ternary_f32: FnTernaryF32,
+    bit_linear_f32: FnBitLinearF32,
+    bit_linear_i8: FnBitLinearI8,
     pack_ternary: FnPackTernary,
     status: FnStatus,
 }
@@ -107,6 +113,8 @@ fn api() -> Result<&'static FusedApi, RocmError> {
             rms_bwd_noalloc_max: *lib.get(b"kore_hip_rms_norm_backward_noalloc_max_bytes\0").ok()?,
             ternary_i8: *lib.get(b"kore_hip_ternary_matmul_i8\0").ok()?,
             ternary_f32: *lib.get(b"kore_hip_ternary_matmul_f32\0").ok()?,
+            bit_linear_f32: *lib.get(b"kore_hip_bit_linear_f32\0").ok()?,
+            bit_linear_i8: *lib.get(b"kore_hip_bit_linear_i8\0").ok()?,
             pack_ternary: *lib.get(b"kore_hip_pack_weights_ternary\0").ok()?,
             status: *lib.get(b"kore_hip_status_string\0").ok()?,
             _lib: lib,
@@ -412,6 +420,51 @@ pub fn rocm_ternary_matmul_f32(dev: usize, a_packed: &HipBuffer, a_scales: &HipB
                                         b.as_device_ptr() as _, c.as_device_ptr() as _, m as u64, n as u64,
                                         k as u64, std::ptr::null_mut()) }, "ternary_matmul_f32")?;
     Ok(c)
+}
+
+/// `BitLinear::forward` (bit_linear.rs:175-237) in one launch: the layer's input x[batch, in] as
+/// stored, output y[batch, out] = ternary_matmul(W, scales, x^T)^T + bias in the layer's layout
+/// (the transposes and the bias add of :200-224 need no passes of their own).  Bit-exact.
+pub fn rocm_bit_linear_f32(dev: usize, a_packed: &HipBuffer, a_scales: &HipBuffer, x: &HipBuffer,
+                           bias: Option<&HipBuffer>, out_features: usize, batch: usize, in_features: usize)
+                           -> Result<HipBuffer, RocmError> {
+    need(a_packed, prod(&[out_features, in_features.div_ceil(5)])?, "ternary weights")?;
+    need(a_scales, prod(&[out_features, 4])?, "ternary scales")?;
+    need(x, prod(&[batch, in_features, 4])?, "layer input")?;
+    if let Some(b) = bias {
+        need(b, prod(&[out_features, 4])?, "bias")?;
+    }
+    set_device(dev)?;
+    let y = HipBuffer::zeros(dev, prod(&[batch, out_features, 4])?)?;
+    let bp = bias.map_or(std::ptr::null(), |b| b.as_device_ptr() as *const f32);
+    check(unsafe { (api()?.bit_linear_f32)(a_packed.as_device_ptr() as _, a_scales.as_device_ptr() as _,
+                                           x.as_device_ptr() as _, bp, y.as_device_ptr() as _,
+                                           out_features as u64, batch as u64, in_features as u64,
+                                           std::ptr::null_mut()) }, "bit_linear_f32")?;
+    Ok(y)
+}
+
+/// The BitLinear layer on pre-quant codes (`rocm_rms_norm_quant_i8`'s q[batch, in], q_scales):
+/// y[b, o] = c[o, b] + bias[o] with c of `rocm_ternary_matmul_i8`, in the layer's [batch, out]
+/// layout.  Bit-exact.
+pub fn rocm_bit_linear_i8(dev: usize, a_packed: &HipBuffer, a_scales: &HipBuffer, q: &HipBuffer,
+                          q_scales: &HipBuffer, bias: Option<&HipBuffer>, out_features: usize, batch: usize,
+                          in_features: usize) -> Result<HipBuffer, RocmError> {
+    need(a_packed, prod(&[out_features, in_features.div_ceil(5)])?, "ternary weights")?;
+    need(a_scales, prod(&[out_features, 4])?, "ternary scales")?;
+    need(q, prod(&[batch, in_features])?, "codes")?;
+    need(q_scales, prod(&[batch, 4])?, "code scales")?;
+    if let Some(b) = bias {
+        need(b, prod(&[out_features, 4])?, "bias")?;
+    }
+    set_device(dev)?;
+    let y = HipBuffer::zeros(dev, prod(&[batch, out_features, 4])?)?;
+    let bp = bias.map_or(std::ptr::null(), |b| b.as_device_ptr() as *const f32);
+    check(unsafe { (api()?.bit_linear_i8)(a_packed.as_device_ptr() as _, a_scales.as_device_ptr() as _,
+                                          q.as_device_ptr() as _, q_scales.as_device_ptr() as _, bp,
+                                          y.as_device_ptr() as _, out_features as u64, batch as u64,
+                                          in_features as u64, std::ptr::null_mut()) }, "bit_linear_i8")?;
+    Ok(y)
 }
 
 /// `pack_weights_ternary` (cpu_ternary_matmul.rs:198-240) on the device: f32 weights [m, k] ->

@@ -96,6 +96,18 @@ def test_ternary_argument_errors_are_reported_on_host():
         # the output may not overlap the weights, scales or activations
         assert f(P, P + 2**20, P + 2**21, P + 2**21 + 64, 4, 4, 16, None) == _lib.KORE_HIP_ERR_ALIAS
     assert lib.kore_hip_ternary_matmul_i8(P, None, P, P, P + 4096, 4, 4, 16, None) == _lib.KORE_HIP_ERR_NULL_PTR
+    # BitLinear::forward entry points: same checks, the bias (optional) included
+    blf, bli = lib.kore_hip_bit_linear_f32, lib.kore_hip_bit_linear_i8
+    assert blf(None, None, None, None, None, 0, 4, 16, None) == 0
+    assert bli(None, None, None, None, None, None, 4, 0, 16, None) == 0
+    assert blf(P, P, P, None, None, 4, 4, 16, None) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert bli(P, P, None, P, None, P + 4096, 4, 4, 16, None) == _lib.KORE_HIP_ERR_NULL_PTR
+    assert blf(P, P, P, None, P, 2**32, 2**32, 16, None) == _lib.KORE_HIP_ERR_OVERFLOW
+    assert blf(P, P + 2**30, P + 2**31, None, P + 2**40, 4, 4, 2**24, None) == _lib.KORE_HIP_ERR_OVERFLOW  # in > 2^23
+    # the output may not overlap the bias
+    assert blf(P, P + 2**20, P + 2**21, P + 2**22, P + 2**22 + 8, 4, 4, 16, None) == _lib.KORE_HIP_ERR_ALIAS
+    assert bli(P, P + 2**20, P + 2**21, P + 2**21 + 4096, P + 2**22, P + 2**22 + 8, 4, 4, 16, None) == \
+        _lib.KORE_HIP_ERR_ALIAS
     pack = lib.kore_hip_pack_weights_ternary
     assert pack(None, 0, 16, 0.3, None, None, None) == 0
     assert pack(P, 4, 16, 0.3, P + 4096, None, None) == _lib.KORE_HIP_ERR_NULL_PTR

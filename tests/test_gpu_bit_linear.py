@@ -1,0 +1,228 @@
+"""GPU parity of the BitLinear layer entry points (kore_hip_bit_linear_f32 /
+_i8): the reference's BitLinear::forward (crates/kore-nn/src/bit_linear.rs:
+175-237) is transpose(x) -> ternary_matmul -> transpose -> add(bias); the
+device computes it in one launch, reading the layer's input as stored and
+writing the output in the layer's [batch, out] layout.
+
+Bar: bit-exact.  Against the oracle's composition of that chain
+(oracle.bit_linear_forward / bit_linear_i8) wherever the CPU oracle finishes
+in seconds; at the full FFN shape with 4096 tokens, against an f64 GEMM of the
+decoded trits (exact for the int8 path's integer sums) and against the
+device's own ternary matmuls -- themselves checked bit-exact against the
+oracle -- composed with exact transposes and f32 bias adds, plus the oracle
+on a slice of tokens.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from inputs import assert_bitexact, int8_codes, normal, prequant_inputs, raw_packed, ternary_weights
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+from kore_amd import rocm  # noqa: E402
+from kore_amd.rocm import HipBuffer  # noqa: E402
+
+DEV = 0
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def up(arr) -> HipBuffer:
+    return HipBuffer.from_host(DEV, np.ascontiguousarray(arr))
+
+
+def down(buf: HipBuffer, dtype, shape):
+    return buf.to_host(dtype)[: int(np.prod(shape))].reshape(shape)
+
+
+def _offset_buffer(arr: np.ndarray, offset: int) -> HipBuffer:
+    """Device copy of arr starting `offset` bytes past a 16-byte boundary."""
+    t = torch.empty(arr.nbytes + offset, dtype=torch.uint8, device="cuda")
+    t[offset:].copy_(torch.from_numpy(np.ascontiguousarray(arr).view(np.uint8).ravel()))
+    return HipBuffer.from_tensor(t[offset:])
+
+
+def test_bit_linear_reference_kats_on_device():
+    """bit_linear.rs tests on the device, weights packed by
+    kore_hip_pack_weights_ternary: test_bit_linear_approximates_linear gives
+    exactly [3, 4]; test_bit_linear_bias gives [11, 21]; with and without a
+    bias through both entry points."""
+    w = np.array([[1.0, -1.0, 0.0, 1.0], [-1.0, 1.0, 1.0, 0.0]], np.float32)
+    p, s = rocm.rocm_pack_weights_ternary(DEV, up(w), 2, 4, 0.3)
+    y = rocm.rocm_bit_linear_f32(DEV, p, s, up(np.array([[1.0, 2.0, 3.0, 4.0]], np.float32)), None, 2, 1, 4)
+    assert down(y, np.float32, (1, 2)).tolist() == [[3.0, 4.0]]
+    p, s = rocm.rocm_pack_weights_ternary(DEV, up(np.eye(2, dtype=np.float32)), 2, 2, 0.3)
+    bias = up(np.array([10.0, 20.0], np.float32))
+    y = rocm.rocm_bit_linear_f32(DEV, p, s, up(np.ones((1, 2), np.float32)), bias, 2, 1, 2)
+    assert down(y, np.float32, (1, 2)).tolist() == [[11.0, 21.0]]
+    # the int8 layer on codes of [1, 1] (scale 1/127 per code 127)
+    q = up(np.array([[127, 127]], np.int8))
+    qs = up(np.array([1.0 / 127.0], np.float32))
+    y = rocm.rocm_bit_linear_i8(DEV, p, s, q, qs, bias, 2, 1, 2)
+    want = oracle.bit_linear_i8(down(p, np.uint8, (2, 1)), down(s, np.float32, (2,)), np.array([[127, 127]], np.int8),
+                                np.array([1.0 / 127.0], np.float32), np.array([10.0, 20.0], np.float32), 2, 1, 2)
+    assert_bitexact(down(y, np.float32, (1, 2)), want, "bit_linear_i8 KAT")
+
+
+@pytest.mark.parametrize("batch", [1, 64, 4096])
+def test_bit_linear_f32_layer_ffn_shape(batch):
+    """BitLinear 2560 -> 6912 (the pre-quant config's width) on 1, 64 and
+    4096 tokens, with a bias: bit-exact against the oracle's composition
+    (all tokens at 1 and 64; the first 8 and the last token at 4096, plus
+    every token against the device's ternary_matmul_f32 on x^T transposed
+    back, + bias)."""
+    m, k = 6912, 2560
+    log(f"bit_linear_f32 m={m} batch={batch} k={k}")
+    p, sa = ternary_weights(m, k, 31)
+    x = normal((batch, k), 32)
+    bias = normal((m,), 33)
+    bp, bs, bx, bb = up(p), up(sa), up(x), up(bias)
+    got = down(rocm.rocm_bit_linear_f32(DEV, bp, bs, bx, bb, m, batch, k), np.float32, (batch, m))
+    if batch <= 64:
+        assert_bitexact(got, oracle.bit_linear_forward(p, sa, x, bias, m, batch, k), f"bit_linear_f32 batch={batch}")
+        return
+    for rows in (slice(0, 8), slice(batch - 1, batch)):
+        xs = x[rows]
+        assert_bitexact(got[rows], oracle.bit_linear_forward(p, sa, xs, bias, m, xs.shape[0], k),
+                        f"bit_linear_f32 batch={batch} tokens {rows}")
+    xt = torch.from_numpy(x).cuda().t().contiguous()
+    c = rocm.rocm_ternary_matmul_f32(DEV, bp, bs, HipBuffer.from_tensor(xt), m, batch, k)
+    ct = torch.from_numpy(down(c, np.float32, (m, batch))).cuda()
+    want = ct.t().contiguous() + torch.from_numpy(bias).cuda()[None, :]
+    assert torch.equal(torch.from_numpy(got).cuda(), want), "bit_linear_f32 vs ternary_matmul_f32 composition"
+
+
+@pytest.mark.parametrize("batch", [1, 64, 4096])
+def test_bit_linear_i8_layer_ffn_shape(batch):
+    """Pre-quant -> BitLinear 2560 -> 6912 on 1, 64 and 4096 tokens, with a
+    bias: the codes of kore_hip_rms_norm_quant_i8 fed to kore_hip_bit_linear_i8;
+    bit-exact against the oracle's composition (1 and 64 tokens; a slice at
+    4096) and against an f64 GEMM of the decoded trits and codes (exact) with
+    the f32 epilogue, transposed, + bias (every token)."""
+    m, k = 6912, 2560
+    log(f"bit_linear_i8 m={m} batch={batch} k={k}")
+    p, sa = ternary_weights(m, k, 34)
+    x, g = prequant_inputs(batch, k, 0)
+    bias = normal((m,), 35)
+    qb, sb = rocm.rocm_rms_norm_quant_i8(DEV, up(x), up(g), batch, k, 1e-6)
+    bp, bs, bb = up(p), up(sa), up(bias)
+    got = down(rocm.rocm_bit_linear_i8(DEV, bp, bs, qb, sb, bb, m, batch, k), np.float32, (batch, m))
+    q = down(qb, np.int8, (batch, k))
+    qs = down(sb, np.float32, (batch,))
+    if batch <= 64:
+        assert_bitexact(got, oracle.bit_linear_i8(p, sa, q, qs, bias, m, batch, k), f"bit_linear_i8 batch={batch}")
+    else:
+        rows = slice(0, 4)
+        assert_bitexact(got[rows], oracle.bit_linear_i8(p, sa, q[rows], qs[rows], bias, m, 4, k),
+                        f"bit_linear_i8 batch={batch} first tokens")
+    t = torch.from_numpy(oracle.unpack_trits(p, k)).cuda().double()
+    acc = (t @ torch.from_numpy(q).cuda().double().T).float()
+    c = (acc * torch.from_numpy(sa).cuda()[:, None]) * torch.from_numpy(qs).cuda()[None, :]
+    want = c.t().contiguous() + torch.from_numpy(bias).cuda()[None, :]
+    assert torch.equal(torch.from_numpy(got).cuda(), want), f"bit_linear_i8 batch={batch} vs f64 GEMM"
+
+
+def test_bit_linear_i8_down_projection_shape():
+    """FFN down-projection 6912 -> 2560 on 4096 tokens (1383-byte packed rows,
+    256 x 192 wide tiles) through the layer entry point, no bias: bit-exact
+    against an f64 GEMM of the decoded trits, transposed."""
+    m, n, k = 2560, 4096, 6912
+    log(f"bit_linear_i8 down-projection m={m} n={n} k={k}")
+    p, sa = ternary_weights(m, k, 36)
+    q = int8_codes(n, k, 37)
+    sq = np.abs(normal((n,), 38, 0.02, 0.005))
+    got = down(rocm.rocm_bit_linear_i8(DEV, up(p), up(sa), up(q), up(sq), None, m, n, k), np.float32, (n, m))
+    t = torch.from_numpy(oracle.unpack_trits(p, k)).cuda().double()
+    acc = (t @ torch.from_numpy(q).cuda().double().T).float()
+    c = (acc * torch.from_numpy(sa).cuda()[:, None]) * torch.from_numpy(sq).cuda()[None, :]
+    assert torch.equal(torch.from_numpy(got).cuda(), c.t().contiguous()), "down-projection layer vs f64 GEMM"
+
+
+# (m, batch, k): every kernel of both layers -- i8: small-n (batch <= 8), skinny
+# (<= 64), 128 x 128 tiles with and without split K, wide tiles of 256 and 192
+# columns, code rows that are not 16-byte aligned (k % 16 != 0), the
+# one-thread-per-output kernel (k % 8 != 0 at small batch); f32: the fold-wave
+# kernel (1-4 tokens), the row-broadcast kernel in 16/32/64-token tiles with a
+# partial last K chunk (k % 80 != 0), the per-lane kernel (tiny matrices);
+# outputs whose rows are not a multiple of 4 floats.
+LAYER_SHAPES = [(7, 1, 25), (130, 2, 1000), (257, 3, 2563), (64, 4, 8), (300, 5, 1203), (6912, 8, 2560),
+                (1001, 16, 640), (555, 33, 1283), (2560, 64, 6912), (4100, 300, 560), (1000, 1000, 1001),
+                (3333, 3900, 80), (4096, 3072, 640), (2560, 3901, 1280), (4099, 2050, 336), (3, 1, 4), (5, 9, 3)]
+
+
+def _i8_want(p, sa, q, qs, bias, k):
+    """((float)acc * sa) * qs transposed, + bias, on the device: acc from an
+    f64 GEMM of the decoded trits and codes (exact integer sums)."""
+    t = torch.from_numpy(oracle.unpack_trits(p, k)).cuda().double()
+    acc = (t @ torch.from_numpy(q).cuda().double().T).float()
+    c = (acc * torch.from_numpy(sa).cuda()[:, None]) * torch.from_numpy(qs).cuda()[None, :]
+    y = c.t().contiguous()
+    return y + torch.from_numpy(bias).cuda()[None, :] if bias is not None else y
+
+
+@pytest.mark.parametrize("m,batch,k", LAYER_SHAPES)
+def test_bit_linear_layers_every_kernel(m, batch, k):
+    """Both layer entry points at shapes that reach every kernel, with and
+    without a bias, on arbitrary packed bytes (bytes >= 243 included):
+    bit-exact against the oracle's composition on the tokens the CPU oracle
+    finishes in seconds, and on every token against an f64 GEMM (int8 layer)
+    or the device's ternary_matmul_f32 on x^T (f32 layer), transposed, + bias."""
+    log(f"bit_linear layers m={m} batch={batch} k={k}")
+    p = raw_packed(m, k, m + 7 * k)
+    sa = normal((m,), 40, 1.0, 0.1)
+    bias = normal((m,), 41)
+    q = int8_codes(batch, k, batch + 3)
+    qs = np.abs(normal((batch,), 42, 0.02, 0.005))
+    x = normal((batch, k), 43)
+    bp, bs, bbias = up(p), up(sa), up(bias)
+    tok = slice(0, min(batch, max(1, 300_000_000 // max(1, m * k))))
+    xt = torch.from_numpy(x).cuda().t().contiguous()
+    c = rocm.rocm_ternary_matmul_f32(DEV, bp, bs, HipBuffer.from_tensor(xt), m, batch, k)
+    cf = torch.from_numpy(down(c, np.float32, (m, batch))).cuda().t().contiguous()
+    for with_bias in (True, False):
+        b_np = bias if with_bias else None
+        b_dev = bbias if with_bias else None
+        y8 = down(rocm.rocm_bit_linear_i8(DEV, bp, bs, up(q), up(qs), b_dev, m, batch, k), np.float32, (batch, m))
+        assert_bitexact(y8[tok], oracle.bit_linear_i8(p, sa, q[tok], qs[tok], b_np, m, q[tok].shape[0], k),
+                        f"bit_linear_i8 bias={with_bias}")
+        assert torch.equal(torch.from_numpy(y8).cuda(), _i8_want(p, sa, q, qs, b_np, k)), \
+            f"bit_linear_i8 bias={with_bias} vs f64 GEMM"
+        yf = down(rocm.rocm_bit_linear_f32(DEV, bp, bs, up(x), b_dev, m, batch, k), np.float32, (batch, m))
+        xs = x[tok]
+        assert_bitexact(yf[tok], oracle.bit_linear_forward(p, sa, xs, b_np, m, xs.shape[0], k),
+                        f"bit_linear_f32 bias={with_bias}")
+        want = cf + torch.from_numpy(bias).cuda()[None, :] if with_bias else cf
+        assert torch.equal(torch.from_numpy(yf).cuda(), want), f"bit_linear_f32 bias={with_bias} vs composition"
+
+
+@pytest.mark.parametrize("off", [4, 8, 12])
+def test_bit_linear_unaligned_buffers(off):
+    """Input, codes and output at 4/8/12 bytes past a 16-byte boundary (the
+    vector stores fall back to element stores, the token-major loads stay
+    in bounds): bit-exact against the oracle's composition."""
+    m, batch, k = 4096, 320, 480
+    log(f"bit_linear unaligned off={off} m={m} batch={batch} k={k}")
+    p, sa = ternary_weights(m, k, 44)
+    bias = normal((m,), 45)
+    x = normal((batch, k), 46)
+    q = int8_codes(batch, k, 47)
+    qs = np.abs(normal((batch,), 48, 0.02, 0.005))
+    yt = torch.full((batch * m + 4,), float("nan"), dtype=torch.float32, device="cuda")
+    yb = HipBuffer.from_tensor(yt[off // 4:])
+    rocm.rocm_bit_linear_i8(DEV, up(p), up(sa), _offset_buffer(q, off), up(qs), up(bias), m, batch, k, out=yb)
+    torch.cuda.synchronize()
+    assert_bitexact(yt[off // 4: off // 4 + batch * m].cpu().numpy().reshape(batch, m),
+                    oracle.bit_linear_i8(p, sa, q, qs, bias, m, batch, k), "bit_linear_i8 unaligned")
+    yt.fill_(float("nan"))
+    rocm.rocm_bit_linear_f32(DEV, up(p), up(sa), _offset_buffer(x, off), up(bias), m, batch, k, out=yb)
+    torch.cuda.synchronize()
+    got = yt[off // 4: off // 4 + batch * m].cpu().numpy().reshape(batch, m)
+    assert_bitexact(got[:16], oracle.bit_linear_forward(p, sa, x[:16], bias, m, 16, k), "bit_linear_f32 unaligned")
+    assert torch.isnan(yt[:off // 4]).all() and torch.isnan(yt[off // 4 + batch * m:]).all()

@@ -565,3 +565,64 @@ def test_ternary_matmul_i8_exact():
     ref = oracle.ternary_matmul(p, sa, b, m, n, k)
     bound = (k + 3) * 2.0 ** -24 * (np.abs(oracle.unpack_trits(p, k)) @ np.abs(b.astype(np.float64))) * sa[:, None]
     assert (np.abs(c.astype(np.float64) - ref) <= bound + 1e-30).all()
+
+
+# ------------------------------------------------------ BitLinear::forward
+def test_bit_linear_forward_reference_kats():
+    """crates/kore-nn/src/bit_linear.rs tests: test_bit_linear_approximates_linear
+    (ternary-friendly weights pack to themselves with scale 1, so y is the
+    exact integer product [3, 4]) and test_bit_linear_bias (identity weights,
+    bias [10, 20], x = [1, 1] -> [11, 21]); test_bit_linear_forward_shape's
+    shapes ([4, 16] -> [4, 8])."""
+    w = np.array([[1.0, -1.0, 0.0, 1.0], [-1.0, 1.0, 1.0, 0.0]], np.float32)
+    p, s = oracle.pack_weights_ternary(w, 0.3)
+    y = oracle.bit_linear_forward(p, s, np.array([[1.0, 2.0, 3.0, 4.0]], np.float32), None, 2, 1, 4)
+    assert y.shape == (1, 2) and y.tolist() == [[3.0, 4.0]]
+    p, s = oracle.pack_weights_ternary(np.array([[1.0, 0.0], [0.0, 1.0]], np.float32), 0.3)
+    y = oracle.bit_linear_forward(p, s, np.ones((1, 2), np.float32), np.array([10.0, 20.0], np.float32), 2, 1, 2)
+    assert y.tolist() == [[11.0, 21.0]]
+    r = np.random.default_rng(5)
+    p, s = oracle.pack_weights_ternary(r.standard_normal((8, 16)).astype(np.float32), 0.3)
+    assert oracle.bit_linear_forward(p, s, np.ones((4, 16), np.float32), None, 8, 4, 16).shape == (4, 8)
+
+
+def test_bit_linear_forward_composition():
+    """The layer is out[b, o] = c[o, b] + bias[o] where c = ternary_matmul on
+    the transposed input: against an f64 recomputation from the decoded trits
+    (within the sequential-sum bound of c plus one rounding of the add), and
+    column b of the output depends on row b of x only (the transposes put
+    tokens on the output's rows)."""
+    r = np.random.default_rng(6)
+    m, n, k = 37, 5, 203
+    p, s = oracle.pack_weights_ternary(r.standard_normal((m, k)).astype(np.float32), 0.5)
+    x = r.standard_normal((n, k)).astype(np.float32)
+    bias = r.standard_normal(m).astype(np.float32)
+    y = oracle.bit_linear_forward(p, s, x, bias, m, n, k)
+    t = oracle.unpack_trits(p, k).astype(np.float64)
+    c64 = (x.astype(np.float64) @ t.T) * s.astype(np.float64)[None, :]
+    bound = (k + 2) * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(t).T) * np.abs(s)[None, :]
+    want = c64 + bias[None, :]
+    assert np.all(np.abs(y - want) <= bound + 2.0 ** -23 * np.abs(want) + 1e-30)
+    # token b's output row is the same when computed alone
+    y1 = oracle.bit_linear_forward(p, s, x[2:3], bias, m, 1, k)
+    assert y1.tobytes() == y[2:3].tobytes()
+    # no bias: the matmul output itself, transposed
+    y0 = oracle.bit_linear_forward(p, s, x, None, m, n, k)
+    assert y0.tobytes() == np.ascontiguousarray(oracle.ternary_matmul(p, s, np.ascontiguousarray(x.T), m, n, k).T).tobytes()
+    # the bias add is one f32 rounding of the finished output
+    assert y.tobytes() == (y0 + bias[None, :]).astype(np.float32).tobytes()
+
+
+def test_bit_linear_i8_composition():
+    """The layer on pre-quant codes: exact integer products (int64 numpy) with
+    the f32 epilogue, transposed, + bias."""
+    r = np.random.default_rng(7)
+    m, n, k = 29, 6, 160
+    p, s = oracle.pack_weights_ternary(r.standard_normal((m, k)).astype(np.float32), 0.5)
+    q = r.integers(-128, 128, size=(n, k)).astype(np.int8)
+    qs = np.abs(r.standard_normal(n)).astype(np.float32) * 0.01
+    bias = r.standard_normal(m).astype(np.float32)
+    y = oracle.bit_linear_i8(p, s, q, qs, bias, m, n, k)
+    acc = oracle.unpack_trits(p, k).astype(np.int64) @ q.astype(np.int64).T
+    c = (acc.astype(np.float32) * s[:, None]) * qs[None, :]
+    assert y.tobytes() == (np.ascontiguousarray(c.T) + bias[None, :]).astype(np.float32).tobytes()
