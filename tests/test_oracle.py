@@ -626,3 +626,21 @@ def test_bit_linear_i8_composition():
     acc = oracle.unpack_trits(p, k).astype(np.int64) @ q.astype(np.int64).T
     c = (acc.astype(np.float32) * s[:, None]) * qs[None, :]
     assert y.tobytes() == (np.ascontiguousarray(c.T) + bias[None, :]).astype(np.float32).tobytes()
+
+
+def test_ternary_fold_crossing_statistics(tmp_path):
+    """The f32-activation ternary fold (a signed random walk) leaves its start
+    binade in most 40-term segments at K = 2560 (tests/csrc/
+    ternary_fold_crossings.c), so a segmented exact fold would fold ~40 of 64
+    segments one by one: more dependent adds than the plain fold."""
+    import os
+    import re
+    import subprocess
+
+    src = os.path.join(os.path.dirname(__file__), "csrc", "ternary_fold_crossings.c")
+    exe = str(tmp_path / "xstat")
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-o", exe, src, "-lm"], check=True)
+    out = subprocess.run([exe, "2560", "4000"], capture_output=True, text=True, timeout=120).stdout
+    folded = float(re.search(r"([0-9.]+) segments leave", out).group(1))
+    changes = float(re.search(r"([0-9.]+) binade/sign changes", out).group(1))
+    assert folded > 30 and changes > 200, out
