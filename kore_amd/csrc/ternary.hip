@@ -739,7 +739,6 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
     for (int j = 0; j < NJ; ++j) sqn[j] = p.sq[min(n0 + 32 * j + r, p.n - 1u)];
     float* slab = reinterpret_cast<float*>(wlds) + wave * 32 * kEpPitch;
     const bool vec_out = (p.n & 3u) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15u) == 0;
-    const uint32_t ncol = n0 + 4 * lane;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const uint32_t mb = m0 + 64 * wave + 32 * i;
@@ -751,19 +750,31 @@ __global__ __launch_bounds__(256, 1) void ternary_i8_wide_kernel(TernArgs p) {
             for (int j = 0; j < NJ; ++j) slab[row * kEpPitch + 32 * j + r] = ((float)acc[i][j][q] * sam) * sqn[j];
         }
         __syncthreads();
-        for (int row = 0; row < 32; ++row) {
-            const uint32_t m = mb + row;
-            if (m >= p.m) break;
-            if (4 * lane >= kN) continue;  // columns of the next tile
-            f32x4 v = *reinterpret_cast<const f32x4*>(slab + row * kEpPitch + 4 * lane);
-            if (p.bias) v = v + p.bias[m];
-            float* crow = p.c + (uint64_t)m * p.n;
-            if (vec_out && ncol + 3 < p.n) {
-                __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(crow + ncol));
-            } else {
+        // kN / 4 lanes cover a row: 256-wide tiles store one row per
+        // instruction; 192-wide ones a block of four rows in three
+        // instructions (lane L of instruction s takes floats 256 s + 4 L of
+        // the block: 48 lanes per row, every lane busy)
+        constexpr int kLpr = kN / 4;                  // lanes per row
+        constexpr int kRows = kWave % kLpr == 0 ? kWave / kLpr : 4;  // rows per block
+        constexpr int kIns = kRows * kLpr / kWave;    // store instructions per block
+        for (int rb = 0; rb < 32; rb += kRows) {
 #pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    if (ncol + u < p.n) crow[ncol + u] = v[u];
+            for (int s = 0; s < kIns; ++s) {
+                const int f = s * kWave + lane;  // 4-float group of the block
+                const int row = rb + f / kLpr, col = 4 * (f % kLpr);
+                const uint32_t m = mb + row;
+                if (m >= p.m) continue;
+                f32x4 v = *reinterpret_cast<const f32x4*>(slab + row * kEpPitch + col);
+                if (p.bias) v = v + p.bias[m];
+                float* crow = p.c + (uint64_t)m * p.n;
+                const uint32_t nc = n0 + col;
+                if (vec_out && nc + 3 < p.n) {
+                    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(crow + nc));
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (nc + u < p.n) crow[nc + u] = v[u];
+                }
             }
         }
         __syncthreads();
