@@ -1233,7 +1233,8 @@ def test_ternary_matmul_f32_packed_at_byte_offsets(off, m, n, k):
 def test_decode_chain_graph_replays_match_eager():
     """A decode step's launches (pre-quant, the BitLinear matmul on its codes
     -- the split-K path's zero/finish kernels included at 64 tokens -- the
-    RMSNorm+SiLU gate, RoPE, softmax and the f32 matmul) captured in one HIP
+    RMSNorm+SiLU gate, RoPE, softmax, the f32 matmul and both BitLinear layer
+    entry points with a bias) captured in one HIP
     graph on a side stream: no entry point allocates, synchronises or records
     a memset, so every replay, with eager work between replays, reproduces the
     eager outputs bit for bit."""
@@ -1263,6 +1264,9 @@ def test_decode_chain_graph_replays_match_eager():
         t["probs"] = torch.empty(tokens, vocab, device=dev)
         t["cf"] = torch.empty(m, tokens, device=dev)
         t["xt"] = t["x"].t().contiguous()
+        t["bias"] = torch.randn(m, generator=g, device=dev)
+        t["y8"] = torch.empty(tokens, m, device=dev)
+        t["yf"] = torch.empty(tokens, m, device=dev)
         return t
 
     def step(t, tokens, s):
@@ -1272,7 +1276,10 @@ def test_decode_chain_graph_replays_match_eager():
               lib.kore_hip_rms_norm_silu_gate_f32(P("x"), P("w"), P("z"), P("gate"), tokens, k, 1e-6, s),
               lib.kore_hip_rope_qk_f32(P("q"), P("kk"), P("inv"), 1, tokens, 4, 2, 128, 5, 0, s),
               lib.kore_hip_softmax_f32(P("logits"), P("probs"), tokens, vocab, s),
-              lib.kore_hip_ternary_matmul_f32(P("a"), P("sa"), P("xt"), P("cf"), m, tokens, k, s)]
+              lib.kore_hip_ternary_matmul_f32(P("a"), P("sa"), P("xt"), P("cf"), m, tokens, k, s),
+              lib.kore_hip_bit_linear_i8(P("a"), P("sa"), P("codes"), P("scales"), P("bias"), P("y8"), m, tokens, k,
+                                         s),
+              lib.kore_hip_bit_linear_f32(P("a"), P("sa"), P("x"), P("bias"), P("yf"), m, tokens, k, s)]
         assert rc == [0] * len(rc), rc
 
     for tokens in (1, 64):
@@ -1281,7 +1288,7 @@ def test_decode_chain_graph_replays_match_eager():
         q0, k0 = t["q"].clone(), t["kk"].clone()
         step(t, tokens, torch.cuda.current_stream(dev).cuda_stream)
         torch.cuda.synchronize(dev)
-        want = {n: t[n].clone() for n in ("codes", "scales", "c", "gate", "q", "kk", "probs", "cf")}
+        want = {n: t[n].clone() for n in ("codes", "scales", "c", "gate", "q", "kk", "probs", "cf", "y8", "yf")}
         side = torch.cuda.Stream(device=dev)
         graph = torch.cuda.CUDAGraph()
         t["q"].copy_(q0)
@@ -1292,7 +1299,7 @@ def test_decode_chain_graph_replays_match_eager():
                 step(t, tokens, side.cuda_stream)
         torch.cuda.synchronize(dev)
         for rep in range(3):
-            for n in ("codes", "scales", "c", "gate", "probs", "cf"):
+            for n in ("codes", "scales", "c", "gate", "probs", "cf", "y8", "yf"):
                 t[n].fill_(float("nan") if t[n].is_floating_point() else 0)
             t["q"].copy_(q0)
             t["kk"].copy_(k0)
