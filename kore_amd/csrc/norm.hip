@@ -634,15 +634,26 @@ static int launch_vec_wpb(NormArgs a, hipStream_t s) {
     return launch_status();
 }
 
-// Up to kSmallRows rows (decode batches) one wave per workgroup: the
-// workgroups spread over more dispatchers and start sooner (32 x 2048
-// RMSNorm 4.4 -> 4.0 us, 64 x 2560 gate 6.0 -> 5.6 us); four waves per
-// workgroup otherwise.
+// One wave per workgroup (its tile holds the whole row: one LDS pass) for
+// launches of up to kSmallRows rows (decode batches: the workgroups spread
+// over more dispatchers and start sooner; 32 x 2048 RMSNorm 4.4 -> 4.0 us,
+// 64 x 2560 gate 6.0 -> 5.6 us) and, at any row count, for the row lengths
+// where the whole-row tiles still leave the register-bound occupancy: up to
+// 2048 columns, and 4096 or 8192 (RMSNorm 16384 x 2048 47.2 -> 46.0 us,
+// 8192 x 2048 26.5 -> 24.5, 16384 x 4096 94.7 -> 90.6, 16384 x 8192 202 ->
+// 182, pre-quant 4096 x 8192 54.7 -> 46.9; ties within 1% elsewhere).  For
+// SL4 = 10, 12 and 24 (2560, 3072 and 6144 columns) the whole-row tiles cap
+// a CU below the waves its registers allow, and four waves per workgroup
+// sharing half-row tiles are faster (pre-quant 4096 x 2560 13.0 against
+// 15.1 us, RMSNorm 4096 x 3072 16.3 against 21.4).
 constexpr uint64_t kSmallRows = 256;
 
 template <NormOut Out, int SL4>
 static int launch_vec(NormArgs a, hipStream_t s) {
-    return a.rows <= kSmallRows ? launch_vec_wpb<Out, SL4, 1>(a, s) : launch_vec_wpb<Out, SL4, kWavesPerBlock>(a, s);
+    if constexpr (SL4 == 10 || SL4 == 12 || SL4 == 24) {
+        if (a.rows > kSmallRows) return launch_vec_wpb<Out, SL4, kWavesPerBlock>(a, s);
+    }
+    return launch_vec_wpb<Out, SL4, 1>(a, s);
 }
 
 template <NormOut Out>
