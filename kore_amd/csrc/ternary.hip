@@ -54,6 +54,7 @@
 namespace kore {
 
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kTmBlock = 256;
 constexpr int kTmM = 128, kTmN = 128;  // workgroup tile; each wave 64 x 64
@@ -1733,6 +1734,298 @@ static int launch_f32_rows(uint64_t m, uint64_t n, hipStream_t s, const TernF32A
     return launch_status();
 }
 
+// Many columns on the fp32 matrix cores.  v_mfma_f32_16x16x1_4b_f32 takes
+// one K column: each of its 64 x 16 products is added to its accumulator as
+// one fused multiply-add with a single rounding (checked on the GPU against
+// fmaf on 5 million random operands including denormals, infinities, NaN
+// and signed zeros, and on 3000-step chains: no difference), and a
+// dependent MFMA that directly follows the one it depends on issues back to
+// back at the full rate (32 cycles for 1024 fmas; any instruction between
+// the two costs ~14 cycles, measured).  So a chain of them over k is the
+// reference's fold, acc = acc + t * b in k order, for every output at once,
+// at twice the vector fma rate, with the vector unit left for the operands.
+//
+// A wave owns 64 weight rows x 16 columns.  Operand a is lane L's row
+// m0 + L (block g = L / 16 holds rows 16g .. 16g + 15); operand b is the
+// 16 columns, broadcast from one 16-lane group to all four blocks by the
+// BLGP field (4 + q: group q), so one b register carries four K columns:
+// lane 16q + j holds b(k0 + 4q + r, n0 + j) in register r of a group of 16
+// columns of K.  Trits come from a 256-entry LDS table (byte -> five
+// floats).  A workgroup is four such waves on consecutive row blocks of the
+// same 16 columns: b is staged once per workgroup in LDS (three buffers,
+// two chunks ahead), each wave's packed bytes are loaded one chunk ahead,
+// and one barrier per chunk orders the staging, over LDS only so that it
+// does not wait for the loads in flight.  K advances 80 columns (16 packed
+// bytes per row) per chunk.
+//
+// The accumulator of output (m0 + 16(v / 4) + 4(L / 16) + v % 4, n0 + L % 16)
+// is register v of lane L.  Zero trits: fma(0, b, acc) = acc for finite b
+// (acc is never -0); a chunk whose b holds an Inf or NaN in this wave's
+// columns is done instead on the vector unit, element by element, with zero
+// trits skipped (the reference's step, bit for bit).
+constexpr int kMfK = 80;             // K columns per chunk
+constexpr int kMfB = kMfK / 5;       // packed bytes per row and chunk
+constexpr int kMfG = kMfK / 16;      // groups of 16 K columns (one b register of four per lane group)
+constexpr int kMfW = kMfB / 4 + 1;   // dwords around a row's bytes of a chunk
+static_assert(kMfK % 80 == 0, "whole bytes and b groups per chunk");
+constexpr int kMfWaves = 4;
+constexpr int kMfThreads = kMfWaves * kWave;
+constexpr int kMfStage = (kMfG * 4 * 16 + kMfThreads - 1) / kMfThreads;  // 16-byte b groups per thread and chunk
+
+struct MfBytes {
+    uint32_t w[kMfB / 4];
+};
+
+// A chunk whose b holds an Inf or NaN, element by element on the vector
+// unit with zero trits skipped (the reference's step).  Output v of lane L is
+// row 16 (v / 4) + 4 (L / 16) + v % 4 of the wave's block, whose trit is that
+// lane's a operand, and column L % 16, whose b is in lanes 16 q' + L % 16.
+// Kept out of line: it runs only for such chunks.
+__device__ __noinline__ f32x16 mf_slow_chunk(f32x16 acc, const float* tl, const f32x4* bsb, MfBytes by, int lane) {
+    const int q = lane >> 4, j = lane & 15;
+    for (int jb = 0; jb < kMfB; ++jb) {
+        const uint32_t bv = (by.w[jb >> 2] >> (8 * (jb & 3))) & 0xffu;
+        for (int d = 0; d < 5; ++d) {
+            const int kk = 5 * jb + d;
+            const float tv = tl[8 * bv + d];
+            const int g = kk >> 4, qq = (kk >> 2) & 3, r = kk & 3;
+            const f32x4 bgv = bsb[(g * 4 + q) * 16 + j];
+            float bsel = 0.0f;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                if (rr == r) bsel = bgv[rr];
+            const float bk = __shfl(bsel, 16 * qq + j, kWave);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const float te = __shfl(tv, 16 * (v >> 2) + 4 * q + (v & 3), kWave);
+                if (te != 0.0f) acc[v] = __builtin_fmaf(te, bk, acc[v]);
+            }
+        }
+    }
+    return acc;
+}
+
+template <bool TM>
+__global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Args p) {
+    // byte v -> its five trits as floats at [8 v + d] (bytes >= 243: zero
+    // trits).  Measured faster than int8 entries converted on the vector
+    // unit, even replicated against bank conflicts (6912 x 4096 x 2560:
+    // 1239 against 1401 us): the conversions cost MFMA issue slots.
+    __shared__ __attribute__((aligned(16))) float tl[256 * 8];
+    // b of a chunk, three buffers (chunk c in c % 3, staged two chunks
+    // ahead so that the next chunk's entries can be read before the
+    // barrier that ends a chunk): group g (16 columns of K), lane group
+    // q, column j -> b(kc + 16 g + 4 q + r, n0 + j) for r = 0..3 as one
+    // 16-byte entry at [g][q][j] (a lane reads its own entry: conflict-free)
+    __shared__ f32x4 bst[3][kMfG][4][16];
+    __shared__ uint32_t bbad[3][kMfWaves];  // per wave: its staged b held an Inf or NaN
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(t / kWave);
+    {
+        uint32_t x = (uint32_t)t;
+        float* e = tl + 8 * t;
+#pragma unroll
+        for (int d = 0; d < 5; ++d) {
+            e[d] = t >= 243 ? 0.0f : (float)((int)(x % 3u) - 1);
+            x /= 3u;
+        }
+        e[5] = e[6] = e[7] = 0.0f;
+    }
+    const uint32_t m0 = (blockIdx.x * kMfWaves + wave) * kWave;
+    const uint32_t n0 = blockIdx.y * 16;
+    const int q = lane >> 4, j = lane & 15;
+    const uint32_t col = n0 + (uint32_t)j;
+    // b staging: entry e = [g][qq][jj] of the chunk; thread t takes entries
+    // t, t + 256 (320 per chunk)
+    auto stage_load = [&](uint32_t kc, f32x4 (&v)[kMfStage]) {
+        const bool full = kc + kMfK <= p.k;
+#pragma unroll
+        for (int u = 0; u < kMfStage; ++u) {
+            const int e = t + kMfThreads * u;
+            v[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (e < kMfG * 4 * 16) {
+                const int g = e >> 6, qq = (e >> 4) & 3, jj = e & 15;
+                const uint32_t k4 = kc + 16u * g + 4u * qq, cl = n0 + (uint32_t)jj;
+                if (cl < p.n) {
+                    if (TM) {
+                        const float* src = p.b + (uint64_t)cl * p.bn + (full || k4 < p.k ? k4 : 0u);
+                        if (full) {
+                            v[u] = __builtin_bit_cast(f32x4, (u32x4)*reinterpret_cast<const u32x4_a4*>(src));
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) v[u][r] = k4 + r < p.k ? src[r] : 0.0f;
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const uint32_t kk = k4 + r;
+                            v[u][r] = (full || kk < p.k) ? p.b[(uint64_t)kk * p.bk + cl] : 0.0f;
+                        }
+                    }
+                }
+            }
+        }
+    };
+    auto stage_store = [&](int buf, const f32x4 (&v)[kMfStage]) {
+        bool bad = false;
+#pragma unroll
+        for (int u = 0; u < kMfStage; ++u) {
+            const int e = t + kMfThreads * u;
+            if (e < kMfG * 4 * 16) {
+                reinterpret_cast<f32x4*>(bst[buf])[e] = v[u];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) bad |= !__builtin_isfinite(v[u][r]);
+            }
+        }
+        const uint64_t bl = __ballot(bad);
+        if (lane == 0) bbad[buf][wave] = bl != 0 ? 1u : 0u;
+    };
+    // packed bytes of row m0 + lane: the kMfB bytes of a chunk from the
+    // dword boundary below them (kMfW dwords, shifted); bytes past the row meet b = 0
+    // (k >= K); the range check returns zeros past the matrix, and the
+    // matrix's partial last dword is read byte by byte
+    const int a_bytes = (int)((uint64_t)p.m * p.kp);  // below 2^31 (checked by the launcher)
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)p.a, (short)0, a_bytes, kBufWord3);
+    const uint32_t arow = min(m0 + (uint32_t)lane, p.m - 1u) * p.kp;
+    auto load_a = [&](uint32_t kc, uint32_t (&w)[kMfW]) {
+        const uint32_t o4 = (arow + kc / 5u) & ~3u;
+        if (o4 + 4u * kMfW <= (uint32_t)a_bytes) {
+#pragma unroll
+            for (int h = 0; h < kMfB / 16; ++h) {
+                const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, o4 + 16u * h, 0, 0));
+                w[4 * h] = v[0]; w[4 * h + 1] = v[1]; w[4 * h + 2] = v[2]; w[4 * h + 3] = v[3];
+            }
+            w[kMfW - 1] = __builtin_amdgcn_raw_buffer_load_b32(ra, o4 + 16u * (kMfB / 16), 0, 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < kMfW; ++i) {
+                const uint32_t o = o4 + 4u * i;
+                uint32_t v = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(ra, o + b, 0, 0) << (8 * b);
+                w[i] = v;
+            }
+        }
+    };
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    uint32_t wn[kMfW] = {};
+    f32x4 sv[kMfStage];
+    if (p.k > 0) {
+        stage_load(0, sv);
+        stage_store(0, sv);
+        stage_load(kMfK, sv);
+        stage_store(1, sv);
+        load_a(0, wn);
+        stage_load(2 * kMfK, sv);  // past K: zeros
+    }
+    __syncthreads();  // the table and the b of chunks 0 and 1
+    // Waves past M still stage b and meet every barrier; they skip the MFMAs.
+    const bool live = m0 < p.m;
+    // chunk c's operands, read before the barrier that ends chunk c - 1:
+    // its first b entry, its kMfB bytes and the trits of its first two
+    // bytes.  Byte jb's trits are read two bytes ahead of its MFMAs and a b
+    // group's entry one group ahead, each read placed between MFMAs.
+    f32x4 bq[2];  // b entries of groups g (bq[g % 2]) and g + 1
+    uint32_t by[kMfB / 4];
+    f32x4 tq[3];  // trits 0..3 of byte jb in tq[jb % 3], trit 4 in t4[jb % 3]
+    float t4[3];
+    auto issue = [&](int jb) {
+        const uint32_t v = (by[jb >> 2] >> (8 * (jb & 3))) & 0xffu;
+        tq[jb % 3] = *reinterpret_cast<const f32x4*>(tl + 8 * v);
+        t4[jb % 3] = tl[8 * v + 4];
+    };
+    auto prep = [&](uint32_t kc, uint32_t bufc) {
+        bq[0] = bst[bufc][0][q][j];
+        const uint32_t sh = (arow + kc / 5u) & 3u;
+#pragma unroll
+        for (int i = 0; i < kMfB / 4; ++i) by[i] = __builtin_amdgcn_alignbyte(wn[i + 1], wn[i], sh);
+        issue(0);
+        issue(1);
+    };
+    if (p.k > 0) prep(0, 0);
+    uint32_t buf = 0;
+    for (uint32_t kc = 0; kc < p.k; kc += kMfK, buf = buf == 2u ? 0u : buf + 1u) {
+        if (kc + kMfK < p.k) load_a(kc + kMfK, wn);
+        const bool bad = (bbad[buf][0] | bbad[buf][1] | bbad[buf][2] | bbad[buf][3]) != 0u;
+        if (live && !bad) {
+#pragma unroll
+            for (int jb = 0; jb < kMfB; ++jb) {
+#pragma unroll
+                for (int d = 0; d < 5; ++d) {
+                    const int kk = 5 * jb + d;  // column of the chunk
+                    const float tv = d < 4 ? tq[jb % 3][d] : t4[jb % 3];
+                    const int g = kk >> 4, qq = (kk >> 2) & 3, r = kk & 3;
+                    const float bv = bq[g & 1][r];
+                    __builtin_amdgcn_sched_barrier(0);
+                    switch (qq) {
+                        case 0: acc = __builtin_amdgcn_mfma_f32_16x16x1f32(tv, bv, acc, 0, 0, 4); break;
+                        case 1: acc = __builtin_amdgcn_mfma_f32_16x16x1f32(tv, bv, acc, 0, 0, 5); break;
+                        case 2: acc = __builtin_amdgcn_mfma_f32_16x16x1f32(tv, bv, acc, 0, 0, 6); break;
+                        default: acc = __builtin_amdgcn_mfma_f32_16x16x1f32(tv, bv, acc, 0, 0, 7); break;
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    if ((kk & 15) == 0 && g + 1 < kMfG) bq[(g + 1) & 1] = bst[buf][g + 1][q][j];
+                    if (d == 0 && jb + 2 < kMfB) issue(jb + 2);
+                }
+            }
+        } else if (live) {
+            MfBytes bb;
+#pragma unroll
+            for (int i = 0; i < kMfB / 4; ++i) bb.w[i] = by[i];
+            acc = mf_slow_chunk(acc, tl, &bst[buf][0][0][0], bb, lane);
+        }
+        // chunk c + 2's b into its buffer (read after the barrier), chunk
+        // c + 3's loads, and chunk c + 1's operands (its buffer was written
+        // before the last barrier)
+        if (kc + 2 * kMfK < p.k) {
+            stage_store(buf == 0u ? 2u : buf - 1u, sv);  // buffer (c + 2) % 3
+            stage_load(kc + 3 * kMfK, sv);
+        }
+        if (kc + kMfK < p.k) prep(kc + kMfK, buf == 2u ? 0u : buf + 1u);
+        // a barrier over LDS only: the global loads in flight are this
+        // thread's own registers
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    }
+    if (!live || col >= p.n) return;
+#pragma unroll
+    for (int gb = 0; gb < 4; ++gb) {
+        const uint32_t mr = m0 + 16u * gb + 4u * q;  // rows mr .. mr + 3: registers 4 gb .. 4 gb + 3
+        if (p.trans && mr + 3 < p.m && (p.ldt & 3u) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15u) == 0) {
+            f32x4 o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = add_bias(p.bias, acc[4 * gb + i] * p.sa[mr + i], mr + i);
+            *reinterpret_cast<f32x4*>(p.c + out_idx(p, mr, col)) = o;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (mr + i < p.m) p.c[out_idx(p, mr + i, col)] = add_bias(p.bias, acc[4 * gb + i] * p.sa[mr + i], mr + i);
+        }
+    }
+}
+
+// The matrix-core kernel where its waves (64 rows x 16 columns each, one
+// dependent chain of k MFMAs) give most SIMDs one: with fewer, the vector
+// kernel's shorter chains win (measured: 6912 x 128 x 2560 83 against
+// 103 us, 6912 x 64 x 2560 76-82 against 68-70, 2560 x 256 x 6912 214
+// against 209; from 1024 columns about 2x).
+constexpr uint64_t kMfMinWaves = 768;
+static bool f32_use_mfma(uint64_t m, uint64_t n, uint64_t k) {
+    return k > 0 && k < (1ull << 31) && ((m + 63) / 64) * ((n + 15) / 16) >= kMfMinWaves;
+}
+
+template <bool TM>
+static int launch_f32_mfma(uint64_t m, uint64_t n, hipStream_t s, const TernF32Args& p) {
+    const uint64_t bx = (m + kMfWaves * kWave - 1) / (kMfWaves * kWave), by = (n + 15) / 16;
+    if (bx > 0x7fffffffull || by > 65535) return KORE_HIP_ERR_OVERFLOW;
+    hipLaunchKernelGGL(ternary_f32_mfma_kernel<TM>, dim3((uint32_t)bx, (uint32_t)by), dim3(kMfWaves * kWave), 0, s, p);
+    return launch_status();
+}
+
 // One to four columns (decode steps), any row alignment.  The
 // fold is a chain of k dependent f32 operations per output, so its floor is k
 // times the latency of one dependent vector operation (about 8 cycles for a
@@ -2412,6 +2705,11 @@ static int ternary_f32_run(const uint8_t* a_packed, const float* a_scales, const
             q.m = (uint32_t)std::min<uint64_t>(span, m - r0);
             q.c += trans ? r0 : r0 * n;  // c[n, m]: columns r0 .. of every row, row stride m
             if (bias) q.bias += r0;
+            if (f32_use_mfma(q.m, n, k)) {
+                const int st = tm ? launch_f32_mfma<true>(q.m, n, s, q) : launch_f32_mfma<false>(q.m, n, s, q);
+                if (st != KORE_HIP_OK) return st;
+                continue;
+            }
             const int st = tm ? (ct <= 16 ? launch_f32_rows<16, true>(q.m, n, s, q)
                                  : ct == 32 ? launch_f32_rows<32, true>(q.m, n, s, q)
                                             : launch_f32_rows<64, true>(q.m, n, s, q))

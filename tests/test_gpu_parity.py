@@ -1071,6 +1071,52 @@ def test_ternary_matmul_f32_subnormal_activations(n):
     got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
     assert_bitexact(got, want, f"ternary_matmul_f32 subnormal n={n}")
 
+# Shapes that give the fp32 matrix-core kernel (64 rows x 16 columns per
+# wave) at least 768 waves: whole and ragged row blocks, column groups and
+# 80-column chunks, odd packed-row lengths (unaligned rows), K of one byte.
+TERN_F32_MFMA_SHAPES = [(6912, 128, 2560), (3000, 300, 403), (2049, 500, 81), (6200, 130, 1), (5000, 200, 5),
+                        (12288, 64, 161), (777, 1030, 333)]
+
+
+@pytest.mark.parametrize("m,n,k", TERN_F32_MFMA_SHAPES)
+def test_ternary_matmul_f32_matrix_cores(m, n, k):
+    """The f32-activation ternary_matmul on the fp32 matrix cores (each
+    v_mfma_f32_16x16x1_4b_f32 step one fused multiply-add per output, in k
+    order): bit-exact against the oracle's sequential fold on arbitrary
+    packed bytes."""
+    from inputs import raw_packed
+
+    log(f"ternary_matmul_f32 matrix cores m={m} n={n} k={k}")
+    p = raw_packed(m, k, 7 * m + k)
+    sa = normal((m,), 13, 1.0, 0.1)
+    b = normal((k, n), 14)
+    b *= np.exp2(np.random.default_rng(k).integers(-30, 30, size=(k, 1))).astype(np.float32)
+    got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
+    assert_bitexact(got, oracle.ternary_matmul(p, sa, b, m, n, k), "ternary_matmul_f32 matrix cores")
+
+
+def test_ternary_matmul_f32_matrix_cores_nonfinite_and_subnormal():
+    """Matrix-core path: Inf/NaN activations in some chunks and columns only
+    (those chunks run element by element with zero trits skipped), finite
+    activations whose sums overflow, subnormal activations and signed zeros
+    (gradual underflow in every step): bit-exact against the oracle,
+    non-finite outputs included."""
+    from inputs import raw_packed
+
+    m, n, k = 6500, 128, 803
+    log(f"ternary_matmul_f32 matrix cores non-finite/subnormal m={m} n={n} k={k}")
+    p, sa = raw_packed(m, k, 71), normal((m,), 72, 1.0, 0.1)
+    b = normal((k, n), 73)
+    b[100:180] *= np.float32(1e-39)            # a whole chunk of subnormals
+    b[300:303, 5] = np.float32(-0.0)
+    b[5, 0] = np.inf; b[250, n - 1] = -np.inf; b[777, 17] = np.nan; b[500, 64] = np.inf
+    b[400:404, 3] = 3e38
+    want = oracle.ternary_matmul(p, sa, b, m, n, k)
+    assert np.isfinite(want).any() and not np.isfinite(want).all()
+    got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
+    assert_bitexact(got, want, "ternary_matmul_f32 matrix cores non-finite/subnormal")
+
+
 @pytest.mark.parametrize("seed", range(20))
 def test_ternary_matmuls_random_shapes(seed):
     """Seeded random shapes and base offsets for both ternary matmuls, so that
