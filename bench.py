@@ -46,6 +46,8 @@ MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
 # MI355X vector fp32 FMA without packed math: 256 CUs x 4 SIMDs x 16 lanes x
 # 2 flops x 2.4 GHz
 VALU_F32_PEAK_TFLOPS = 78.6
+# MI355X dense fp32 MFMA: 157.3 TFLOP/s
+MFMA_F32_PEAK_TFLOPS = 157.3
 MALL_BYTES = 256 << 20
 # The headline workload: BASELINE.json's largest single-GPU config.
 HEADLINE = "swiglu"
@@ -574,15 +576,20 @@ class TernaryF32(Workload):
     """BitLinear matmul on f32 activations (kore_hip_ternary_matmul_f32, the
     reference's ternary_matmul as BitLinear::forward calls it): the same
     2560 -> 6912 weights on a decode batch.  Every output is the reference's
-    sequential f32 fold over K (bit-exact), one fma per term and lane, so the
-    kernel is bound by vector issue along the K chain; reported as fp32 FMA
-    throughput (2 flops per term) next to the bytes."""
-    bound = "valu"
+    sequential f32 fold over K (bit-exact).  Decode batches run one fma per
+    term and lane on the vector unit; where the shape gives the matrix-core
+    kernel enough waves (prefill, large batches) each fold step is one
+    v_mfma_f32_16x16x1_4b_f32 step.  Reported as fp32 throughput (2 flops per
+    term) against the vector fma or the fp32 MFMA peak, next to the bytes."""
 
     def __init__(self, m=6912, n=1, k=2560, layer=False):
         self.m, self.n, self.k = m, n, k
         self.layer = layer
-        self.kernel = "ternary_f32_pipe_kernel" if n <= 4 else "ternary_f32_rows_kernel"
+        # the library's dispatch (ternary.hip: kRowsMinCols, kMfMinWaves)
+        mfma = ((m + 63) // 64) * ((n + 15) // 16) >= 768
+        self.bound = "mfma_f32" if mfma else "valu"
+        self.kernel = ("ternary_f32_mfma_kernel" if mfma else
+                       "ternary_f32_pipe_kernel" if n <= 4 else "ternary_f32_rows_kernel")
         self.kp = (k + 4) // 5
         self.name = f"{'bit_linear_f32' if layer else 'ternary_f32'}_{m}x{n}x{k}"
         self.tokens = n
@@ -621,7 +628,7 @@ class TernaryF32(Workload):
         import oracle
         from inputs import normal, raw_packed
 
-        m = 512
+        m = 512 if self.n <= 64 else max(8, 512 * 64 // self.n)
         p, b = raw_packed(m, self.k, 1), normal((self.k, self.n), 2)
         sa = np.ones(m, np.float32)
         return (lambda: oracle.ternary_matmul(p, sa, b, m, self.n, self.k)), \
@@ -752,7 +759,8 @@ def all_workloads():
             RmsNormBackward(), TernaryI8(), TernaryI8(2560, 4096, 6912), TernaryI8(6912, 64, 2560),
             TernaryI8(6912, 1, 2560), TernaryI8(6912, 4096, 2560, layer=True), TernaryI8(2560, 4096, 6912, layer=True),
             TernaryI8(6912, 64, 2560, layer=True), TernaryF32(), TernaryF32(6912, 16, 2560), TernaryF32(6912, 64, 2560),
-            TernaryF32(6912, 1, 2560, layer=True), TernaryF32(6912, 64, 2560, layer=True), PackTernary(),
+            TernaryF32(6912, 1, 2560, layer=True), TernaryF32(6912, 64, 2560, layer=True), TernaryF32(6912, 1024, 2560),
+            TernaryF32(6912, 4096, 2560, layer=True), PackTernary(),
             PackTernary(2560, 6912), Copy()]
 
 
@@ -915,6 +923,8 @@ def main():
             r.update({"bound": w.bound, "ops_per_launch": w.ops, "achieved_tops": round(tops, 3)})
             if w.bound == "mfma":
                 r["frac_of_mfma_peak"] = round(tops / MFMA_I8_PEAK_TOPS, 4)
+            elif w.bound == "mfma_f32":
+                r["frac_of_mfma_f32_peak"] = round(tops / MFMA_F32_PEAK_TFLOPS, 4)
             else:
                 r["frac_of_valu_f32_peak"] = round(tops / VALU_F32_PEAK_TFLOPS, 4)
         if w.name in traffic:
@@ -935,6 +945,8 @@ def main():
         extra = ""
         if w.ops and w.bound == "mfma":
             extra = f", {r['achieved_tops']} TOPS ({100 * r['frac_of_mfma_peak']:.1f}% of the int8 MFMA peak)"
+        elif w.ops and w.bound == "mfma_f32":
+            extra = f", {r['achieved_tops']} TFLOP/s ({100 * r['frac_of_mfma_f32_peak']:.1f}% of the fp32 MFMA peak)"
         elif w.ops:
             extra = f", {r['achieved_tops']} TFLOP/s ({100 * r['frac_of_valu_f32_peak']:.1f}% of the fp32 FMA peak)"
         print(f"[bench] {w.name}: {r['kernel_us']} us, {r['achieved_gbs']} GB/s ({100 * r['frac_of_peak']:.1f}% "
@@ -980,6 +992,7 @@ SUMMARY = [("floor: empty launch", "launch_floor"),
            ("next: ternary i8 6912x4096x2560", "ternary_i8_6912x4096x2560"),
            ("next: BitLinear layer i8 6912x4096x2560", "bit_linear_i8_6912x4096x2560"),
            ("next: ternary i8 2560x4096x6912", "ternary_i8_2560x4096x6912"),
+           ("next: BitLinear layer f32 6912x4096x2560 (fp32 MFMA)", "bit_linear_f32_6912x4096x2560"),
            ("cfg0 RMSNorm 32x2048", "rms_norm_32x2048"), ("cfg1 RoPE Q+K half-split", "rope_qk"),
            ("cfg1 RoPE Q+K interleaved", "rope_qk_interleaved"), ("cfg2 SwiGLU 16384x14336", "swiglu"),
            ("cfg2 GELU 16384x14336", "gelu"), ("cfg3 Embedding 8192x4096", "embedding"),
@@ -1014,6 +1027,8 @@ def print_summary(results):
                 tail += f", {r['kernel_us'] / same:.2f}x its shape's read/write floor per launch"
         if "achieved_tops" in r and r.get("bound") == "mfma":
             tail += f" | {r['achieved_tops']} TOPS ({100 * r['frac_of_mfma_peak']:.1f}% int8 MFMA)"
+        elif "achieved_tops" in r and r.get("bound") == "mfma_f32":
+            tail += f" | {r['achieved_tops']} TFLOP/s ({100 * r['frac_of_mfma_f32_peak']:.1f}% fp32 MFMA)"
         out.append(f"[summary] {label}: {r['kernel_us']}{g} | {r['achieved_gbs']} | {100 * r['frac_of_peak']:.1f}% | "
                    f"{r['ns_per_token']} | {cpu_s}{tail}")
     print("\n".join(out), file=sys.stderr, flush=True)
