@@ -1095,6 +1095,21 @@ def test_ternary_matmul_f32_matrix_cores(m, n, k):
     assert_bitexact(got, oracle.ternary_matmul(p, sa, b, m, n, k), "ternary_matmul_f32 matrix cores")
 
 
+@pytest.mark.parametrize("oa,ob", [(1, 4), (3, 12)])
+def test_ternary_matmul_f32_matrix_cores_unaligned(oa, ob):
+    """Matrix-core path with the packed matrix and the activations at odd
+    offsets (packed rows of any alignment, b 4-byte aligned only):
+    bit-exact against the oracle."""
+    from inputs import raw_packed
+
+    m, n, k = 3100, 260, 419
+    log(f"ternary_matmul_f32 matrix cores unaligned a+{oa} b+{ob} m={m} n={n} k={k}")
+    p, sa, b = raw_packed(m, k, 81), normal((m,), 82, 1.0, 0.1), normal((k, n), 83)
+    got = down(rocm.rocm_ternary_matmul_f32(DEV, _offset_buffer(p, oa), up(sa), _offset_buffer(b, ob), m, n, k),
+               np.float32, (m, n))
+    assert_bitexact(got, oracle.ternary_matmul(p, sa, b, m, n, k), "ternary_matmul_f32 matrix cores unaligned")
+
+
 def test_ternary_matmul_f32_matrix_cores_nonfinite_and_subnormal():
     """Matrix-core path: Inf/NaN activations in some chunks and columns only
     (those chunks run element by element with zero trits skipped), finite
