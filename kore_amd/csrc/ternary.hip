@@ -2517,6 +2517,345 @@ static void launch_mfma(bool aligned_a, bool aligned_b, dim3 grid, hipStream_t s
     if (p.trans) launch_mfma_t<kSplit, true>(aligned_a, aligned_b, grid, s, p);
     else launch_mfma_t<kSplit, false>(aligned_a, aligned_b, grid, s, p);
 }
+// Two-workgroups-per-CU path (the wide path's shapes): a workgroup owns a
+// 256 (m) x 128 (n) output tile, wave w its weight rows [64 w, 64 w + 64)
+// against the tile's 128 code rows: 2 x 4 MFMA tiles of 32 x 32 (128 int32
+// accumulators per lane), 128 VGPRs + 128 AGPRs, so that each SIMD runs one
+// wave of each of two workgroups.  A v_mfma_i32_32x32x32_i8 issues every 32
+// cycles, but the vector and LDS instructions a wave issues between its own
+// MFMAs (the trit decode, operand reads, code loads) delay its next one
+// (measured: one wave per SIMD with three VALU and one LDS read per MFMA
+// reaches 2.4 POP/s, two waves 3.2): with two waves per SIMD one wave's
+// MFMAs cover the other's operand work, and one workgroup's epilogue the
+// other's K loop.  Per 160-column K step a wave first decodes its two rows'
+// 32 packed bytes into the step's A operands (the other wave on its SIMD
+// runs MFMAs meanwhile), then runs 40 MFMAs with the code operands read one
+// group ahead and the next step's code tile loaded into the other buffer by
+// direct global -> LDS loads; one barrier per step.  The byte -> five-trit
+// table is held in 16 copies (copy c for lanes c, c + 16, c + 32, c + 48).
+// Code tile, K order, masking of trits past k, the alignment of packed rows
+// and the output layouts as in the wide path.
+constexpr int kW2N = 128;
+constexpr int kW2NJ = kW2N / 32;
+constexpr int kW2Copies = 16;
+constexpr size_t kW2BBytes = (size_t)kW2N * kWdPitch;                      // one code tile
+constexpr size_t kW2Loop = 2 * kW2BBytes + 256 * kW2Copies * 8;           // code tiles + table
+constexpr int kW2EpPitch = kW2N + 8;                                      // epilogue slab pitch (floats)
+constexpr size_t kW2Epi = (size_t)4 * 32 * kW2EpPitch * 4;
+constexpr size_t kW2Lds = kW2Loop > kW2Epi ? kW2Loop : kW2Epi;
+constexpr int kW2Slots = (int)(kW2BBytes / 16 / 4);                       // 16-byte code slots per wave
+constexpr int kW2Dma = (kW2Slots + kWave - 1) / kWave;
+constexpr uint64_t kW2MaxSteps = 16;  // K steps up to which it beats the wide path
+static_assert(kW2Lds * 2 <= 160 * 1024, "two workgroups per CU");
+
+template <bool kAlignedA, bool kTrans>
+__global__ __launch_bounds__(256, 2) void ternary_i8_w2_kernel(TernArgs p) {
+    constexpr int NJ = kW2NJ, kN = kW2N;
+    constexpr size_t kBB = kW2BBytes;
+    constexpr int kSl = kW2Slots, kDm = kW2Dma;
+    extern __shared__ __attribute__((aligned(16))) uint8_t wlds[];
+    uint64_t* lut = reinterpret_cast<uint64_t*>(wlds + 2 * kBB);
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    const int r = lane & 31, h = lane >> 5;
+    // tile order as in the wide path (panels of n-tiles per XCD)
+    const uint32_t tm_n = (p.m + kWdM - 1) / kWdM, tn_n = (p.n + kN - 1) / kN;
+    const uint32_t ntiles = tm_n * tn_n;
+    const uint32_t per = (ntiles + kXcds - 1) / kXcds;
+    const uint32_t work = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+    if (work >= ntiles) return;  // whole workgroup: no barrier reached yet
+    const uint32_t pw = (tn_n + kXcds - 1) / kXcds;
+    const uint32_t panel = work / (tm_n * pw), within = work % (tm_n * pw);
+    const uint32_t pwid = min(pw, tn_n - panel * pw);
+    const uint32_t m0 = (within / pwid) * kWdM, n0 = (panel * pw + within % pwid) * kN;
+
+    // table: entry e, copy c at u64 index e * 16 + c, filled in a rotated order
+    {
+        const uint64_t v = trit_lut_entry((uint32_t)t);
+#pragma unroll 4
+        for (int c2 = 0; c2 < kW2Copies; ++c2) lut[t * kW2Copies + ((c2 + t) & (kW2Copies - 1))] = v;
+    }
+    const uint64_t* lut_lane = lut + (lane & (kW2Copies - 1));
+
+    const uint32_t nkt = (p.k + kTmK - 1) / kTmK;
+    const uint8_t* arow[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t m = min(m0 + 64 * wave + 32 * i + r, p.m - 1u);
+        arow[i] = p.a + (uint64_t)m * p.kp;
+    }
+    const uintptr_t a_hi = reinterpret_cast<uintptr_t>(p.a) + (uintptr_t)p.m * p.kp;
+    uint32_t sh[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) sh[i] = (uint32_t)(reinterpret_cast<uintptr_t>(arow[i]) & 3u);
+    // this lane's 16 packed bytes of step kt per row (the 20 bytes from the
+    // dword boundary below them for unaligned rows; byte by byte only where
+    // they would pass the matrix's end)
+    auto load_a = [&](uint32_t kt, u32x4 (&av)[2], uint32_t (&ae)[2]) {
+        const uint32_t ab = kt * kTmKp + 16u * h;
+        const uint32_t abc = ab < p.kp ? ab : 0u;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            if (kAlignedA) {
+                av[i] = *reinterpret_cast<const u32x4*>(arow[i] + abc);
+                continue;
+            }
+            const uintptr_t w0 = reinterpret_cast<uintptr_t>(arow[i] + abc) & ~(uintptr_t)3;
+            if (__builtin_expect(w0 + 20u <= a_hi, 1)) {
+                av[i] = *reinterpret_cast<const u32x4_a4*>(w0);
+                ae[i] = *reinterpret_cast<const uint32_t*>(w0 + 16);
+            } else {
+                uint32_t w[5];
+#pragma unroll
+                for (int q = 0; q < 5; ++q) {
+                    w[q] = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uintptr_t o = w0 + 4 * q + e;
+                        w[q] |= (o < a_hi ? (uint32_t)*reinterpret_cast<const uint8_t*>(o) : 0u) << (8 * e);
+                    }
+                }
+                av[i] = u32x4{w[0], w[1], w[2], w[3]};
+                ae[i] = w[4];
+            }
+        }
+    };
+    // code slots of this wave: slot s (16 bytes) of a tile is row s / 11,
+    // piece s % 11 (piece 10: the row's padding, filled with piece 0)
+    // (the piece's byte offset bp16 is recomputed where it is used: registers)
+    uint32_t boff[kDm];
+    auto bp16_of = [&](int g) {
+        const int piece = (kSl * wave + kWave * g + lane) % 11;
+        return piece < 10 ? 16u * (uint32_t)piece : 0u;
+    };
+#pragma unroll
+    for (int g = 0; g < kDm; ++g) {
+        const int slot = kSl * wave + kWave * g + lane;
+        const uint32_t rowc = min(n0 + (uint32_t)(slot / 11), p.n - 1u);
+        boff[g] = rowc * p.k + bp16_of(g);
+    }
+    const bool k_tail = p.k % kTmK != 0;
+    auto dma_one = [&](uint32_t kt, uint32_t buf, int g) {
+        const int8_t* base = p.q + (uint64_t)kt * kTmK;
+        const uint32_t rem = p.k - kt * kTmK;
+        uint8_t* dst = wlds + buf * kBB + (size_t)kSl * 16 * wave + kWave * 16 * g;
+        uint32_t off = boff[g];
+        if (k_tail) {
+            const uint32_t b16 = bp16_of(g);
+            if (b16 >= rem) off -= b16;
+        }
+        if (kSl % kWave == 0 || g < kDm - 1 || kWave * g + lane < kSl)
+            __builtin_amdgcn_global_load_lds((glb_vptr)(base + off), (lds_vptr)dst, 16, 0, 0);
+    };
+
+    i32x16 acc[2][NJ];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0;
+
+    auto read_b = [&](uint32_t buf, int s, i32x4 (&bf)[NJ]) {
+        const uint8_t* bb = wlds + buf * kBB + r * kWdPitch + 80 * h + 16 * s;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) bf[j] = *reinterpret_cast<const i32x4*>(bb + 32 * j * kWdPitch);
+    };
+    // step kt's A operands: its bytes decoded into five 32-deep MFMA steps
+    // (lane half h: columns 80 h .. 80 h + 79), trits past k zeroed
+    auto decode = [&](uint32_t kt, const u32x4 (&avr)[2], const uint32_t (&aer)[2], uint32_t (&dec)[2][20]) {
+        u32x4 av[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            if (kAlignedA) {
+                av[i] = avr[i];
+            } else {
+                av[i] = u32x4{__builtin_amdgcn_alignbyte(avr[i][1], avr[i][0], sh[i]),
+                              __builtin_amdgcn_alignbyte(avr[i][2], avr[i][1], sh[i]),
+                              __builtin_amdgcn_alignbyte(avr[i][3], avr[i][2], sh[i]),
+                              __builtin_amdgcn_alignbyte(aer[i], avr[i][3], sh[i])};
+            }
+        }
+        // eight table reads in flight at a time (registers: two waves per SIMD)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int d = 0; d < 20; ++d) dec[i][d] = 0;
+#pragma unroll
+            for (int b0 = 0; b0 < 16; b0 += 8) {
+                uint64_t tv[8];
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    const uint32_t byte = (av[i][(b0 + b) >> 2] >> (8 * ((b0 + b) & 3))) & 0xffu;
+                    tv[b] = lut_lane[byte * kW2Copies];
+                }
+#pragma unroll
+                for (int b = 0; b < 8; ++b) splice_trits(dec[i], b0 + b, tv[b]);
+            }
+        }
+        if (k_tail && kt + 1 == nkt) {
+            const int rem = (int)p.k - (int)(kt * kTmK) - 80 * h;
+#pragma unroll
+            for (int d = 0; d < 20; ++d) {
+                const int keep = rem - 4 * d;
+                const uint32_t msk = keep >= 4 ? 0xffffffffu : (keep <= 0 ? 0u : (0xffffffffu >> (8 * (4 - keep))));
+#pragma unroll
+                for (int i = 0; i < 2; ++i) dec[i][d] &= msk;
+            }
+        }
+    };
+    // the next step's code loads spread over MFMA groups 0 .. 2 (2 + 2 + 2)
+    constexpr int kDmaAt[6] = {0, (kDm + 2) / 3, 2 * ((kDm + 2) / 3), kDm, kDm, kDm};
+    // (the code operands are read at the start of their group, not a group
+    // ahead: registers; the other wave on the SIMD covers the wait)
+    auto mgroup = [&](auto S_, uint32_t kt, const uint32_t (&cur)[2][20]) {
+        constexpr int s = decltype(S_)::value;
+        constexpr int dlo = kDmaAt[s], dhi = kDmaAt[s + 1];
+        i32x4 bc[NJ];
+        read_b(kt & 1u, s, bc);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const i32x4 af = {(int)cur[i][4 * s], (int)cur[i][4 * s + 1], (int)cur[i][4 * s + 2],
+                              (int)cur[i][4 * s + 3]};
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) acc[i][j] = mfma_wq<kTrans>(af, bc[j], acc[i][j]);
+        }
+        if (kt + 1 < nkt) {
+#pragma unroll
+            for (int g = dlo; g < dhi; ++g) dma_one(kt + 1, (kt + 1) & 1u, g);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
+    using S4 = std::integral_constant<int, 4>;
+    uint32_t cur[2][20];
+    auto kstep = [&](uint32_t kt, u32x4 (&av)[2], uint32_t (&ae)[2]) {
+        decode(kt, av, ae, cur);
+        if (kt + 2 < nkt) load_a(kt + 2, av, ae);
+        mgroup(S0(), kt, cur);
+        mgroup(S1(), kt, cur);
+        mgroup(S2(), kt, cur);
+        mgroup(S3(), kt, cur);
+        mgroup(S4(), kt, cur);
+        // this wave's code loads for step kt + 1 have landed and every wave
+        // is done reading buffer kt & 1 before anyone passes the barrier
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    };
+
+    u32x4 ava[2], avb[2];
+    uint32_t aea[2] = {0u, 0u}, aeb[2] = {0u, 0u};
+    load_a(0, ava, aea);
+    if (nkt > 1) load_a(1, avb, aeb);
+#pragma unroll
+    for (int g = 0; g < kDm; ++g) dma_one(0, 0, g);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // table filled, first code tile staged
+    uint32_t kt = 0;
+    for (; kt + 1 < nkt; kt += 2) {
+        kstep(kt, ava, aea);
+        kstep(kt + 1, avb, aeb);
+    }
+    if (kt < nkt) kstep(kt, ava, aea);
+
+    // Epilogue as in the wide path: ((float)acc * sa[m]) * sq[n] (+ bias[m])
+    // through per-wave LDS slabs, whole output rows per store instruction.
+    if constexpr (kTrans) {
+        constexpr int kTp = 72;
+        float* slab = reinterpret_cast<float*>(wlds) + wave * 32 * kTp;
+        float* sqs = reinterpret_cast<float*>(wlds) + 4 * 32 * kTp;
+        if (t < kN) sqs[t] = p.sq[min(n0 + (uint32_t)t, p.n - 1u)];
+        __syncthreads();
+        const uint32_t mw = m0 + 64 * wave;
+        float sam[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) sam[i] = p.sa[min(mw + 32 * i + r, p.m - 1u)];
+        const uint32_t mc = mw + 4 * (lane & 15);
+        const bool vec_out = (p.m & 3u) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15u) == 0;
+        f32x4 bias4 = {0.f, 0.f, 0.f, 0.f};
+        if (p.bias) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) bias4[u] = p.bias[min(mc + u, p.m - 1u)];
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int row = 8 * (q >> 2) + 4 * h + (q & 3);
+#pragma unroll
+                for (int i = 0; i < 2; ++i) slab[row * kTp + 32 * i + r] = (float)acc[i][j][q] * sam[i];
+            }
+            wave_lds_sync();
+#pragma unroll
+            for (int it = 0; it < 8; ++it) {
+                const int row = 4 * it + (lane >> 4);
+                const uint32_t n = n0 + 32 * j + row;
+                if (n >= p.n) continue;
+                const float sqn = sqs[32 * j + row];
+                f32x4 v = *reinterpret_cast<const f32x4*>(slab + row * kTp + 4 * (lane & 15));
+                v = v * sqn;
+                if (p.bias) v = v + bias4;
+                float* crow = p.c + (uint64_t)n * p.m;
+                if (vec_out && mc + 3 < p.m) {
+                    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(crow + mc));
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (mc + u < p.m) crow[mc + u] = v[u];
+                }
+            }
+            wave_lds_sync();  // the slab is rewritten for the next j
+        }
+        return;
+    }
+    float sqn[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) sqn[j] = p.sq[min(n0 + 32 * j + r, p.n - 1u)];
+    float* slab = reinterpret_cast<float*>(wlds) + wave * 32 * kW2EpPitch;
+    const bool vec_out = (p.n & 3u) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15u) == 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t mb = m0 + 64 * wave + 32 * i;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int row = 8 * (q >> 2) + 4 * h + (q & 3);
+            const float sam = p.sa[min(mb + row, p.m - 1u)];
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) slab[row * kW2EpPitch + 32 * j + r] = ((float)acc[i][j][q] * sam) * sqn[j];
+        }
+        wave_lds_sync();
+        // 32 lanes cover a 128-float row: two rows per store instruction
+        for (int rb = 0; rb < 32; rb += 2) {
+            const int row = rb + (lane >> 5), col = 4 * (lane & 31);
+            const uint32_t m = mb + row;
+            if (m >= p.m) continue;
+            f32x4 v = *reinterpret_cast<const f32x4*>(slab + row * kW2EpPitch + col);
+            if (p.bias) v = v + p.bias[m];
+            float* crow = p.c + (uint64_t)m * p.n;
+            const uint32_t nc = n0 + col;
+            if (vec_out && nc + 3 < p.n) {
+                __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(crow + nc));
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (nc + u < p.n) crow[nc + u] = v[u];
+            }
+        }
+        wave_lds_sync();
+    }
+}
+
+template <bool kTrans>
+static void launch_w2_t(bool aligned_a, dim3 g, hipStream_t s, const TernArgs& p) {
+    if (aligned_a) hipLaunchKernelGGL((ternary_i8_w2_kernel<true, kTrans>), g, dim3(256), kW2Lds, s, p);
+    else hipLaunchKernelGGL((ternary_i8_w2_kernel<false, kTrans>), g, dim3(256), kW2Lds, s, p);
+}
+
 template <int NJ, bool kTrans>
 static void launch_wide_t(bool aligned_a, dim3 g, hipStream_t s, const TernArgs& p) {
     if (aligned_a)
@@ -2610,6 +2949,21 @@ static int ternary_i8_run(const uint8_t* a_packed, const float* a_scales, const 
         if (per * kXcds > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
         const dim3 g((uint32_t)(per * kXcds));
         const bool al = kp % 16 == 0 && aligned16(a_packed);
+        // Few K steps on 256 x 256 tiles: 256 x 128 tiles, two workgroups per
+        // CU, so one workgroup's epilogue (an HBM write burst of a whole tile)
+        // and its first K step overlap the other's matrix-core work.
+        // (measured: 6912 x 4096 x 2560 106 -> 92 us, 8192 x 8192 x 2560 203
+        // -> 177, 6912 x 4096 x 640 44.7 -> 35.4; at 26 K steps no gain:
+        // 4096 x 4096 x 4096 74.5 -> 76.5; on 192-wide tiles a loss:
+        // 2560 x 4096 x 6912 92 -> 105)
+        if (!n192 && (k + kTmK - 1) / kTmK <= kW2MaxSteps) {
+            const uint64_t per2 = (((m + kWdM - 1) / kWdM) * ((n + kW2N - 1) / kW2N) + kXcds - 1) / kXcds;
+            if (per2 * kXcds > 0x7fffffffull) return KORE_HIP_ERR_OVERFLOW;
+            const dim3 g2((uint32_t)(per2 * kXcds));
+            if (p.trans) launch_w2_t<true>(al, g2, s, p);
+            else launch_w2_t<false>(al, g2, s, p);
+            return launch_status();
+        }
         if (n192) launch_wide<6>(al, g, s, p);
         else launch_wide<8>(al, g, s, p);
         return launch_status();

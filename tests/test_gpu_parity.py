@@ -778,9 +778,10 @@ def test_ternary_matmul_i8_small_n(m, n, k):
                                    (4096, 3072, 160), (300, 49152, 160), (49200, 300, 160)])
 def test_ternary_matmul_i8_wide_tiles(m, n, k):
     """The wide path (at least 144 output tiles of 256 x 256, 16-byte packed
-    rows; per-lane table decode): whole and ragged tiles, a partial last K
-    step (k % 160 != 0), a partial single step and a whole one; bit-exact against the oracle on
-    arbitrary packed bytes (bytes >= 243 included)."""
+    rows; at these few K steps 256 x 128 tiles, two workgroups per CU):
+    whole and ragged tiles, a partial last K step (k % 160 != 0), a partial
+    single step and a whole one; bit-exact against the oracle on arbitrary
+    packed bytes (bytes >= 243 included)."""
     from inputs import int8_codes, raw_packed
 
     log(f"ternary_matmul_i8 wide m={m} n={n} k={k}")
@@ -871,13 +872,14 @@ def test_ternary_matmul_i8_full_size_and_pipeline():
 
 
 @pytest.mark.parametrize("m,n,k", [(2560, 4096, 6912), (6912, 1024, 2563), (2560, 3900, 1280), (3072, 3072, 1360),
-                                   (2600, 4100, 1296)])
+                                   (2600, 4100, 1296), (4096, 4096, 2720), (4096, 4000, 2736)])
 def test_ternary_matmul_i8_full_size_unaligned(m, n, k):
     """Full-size shapes: the FFN down-projection 6912 -> 2560 on 4096 tokens
     (1383-byte packed rows, 256 x 192 wide tiles), K = 2563 (code rows not
     16-byte aligned: the tile kernel's window code loads), and 256 x 192 tiles
-    with a partial last column tile, aligned and unaligned packed rows;
-    bit-exact against an f64 GEMM of the decoded trits (exact for these
+    with a partial last column tile, aligned and unaligned packed rows; 256 x
+    256 tiles with more than 16 K steps (the one-workgroup-per-CU kernel that
+    two-workgroup 256 x 128 tiles replace at fewer steps); bit-exact against an f64 GEMM of the decoded trits (exact for these
     integer sums) with the same f32 epilogue."""
     from inputs import int8_codes, ternary_weights
 
