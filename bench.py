@@ -506,7 +506,14 @@ class TernaryI8(Workload):
         elif n <= 64:
             self.kernel = "ternary_i8_skinny_kernel"
         elif ((m + 255) // 256) * ((n + 255) // 256) >= 144:
-            self.kernel = "ternary_i8_wide_kernel"
+            # the library's choice among its wide-path kernels: 256 x 192 tiles
+            # when their rounds of 256 CUs are fewer (at >= 8 K steps), else
+            # 256 x 128 tiles two workgroups per CU at <= 16 K steps
+            t256 = ((m + 255) // 256) * ((n + 255) // 256)
+            t192 = ((m + 255) // 256) * ((n + 191) // 192)
+            steps = (k + 159) // 160
+            n192 = 4 * ((t192 + 255) // 256) < 5 * ((t256 + 255) // 256) and steps >= 8
+            self.kernel = "ternary_i8_w2_kernel" if not n192 and steps <= 16 else "ternary_i8_wide_kernel"
         self.tokens = n
         self.ops = 2 * m * n * k
         self.bytes = m * self.kp + n * k + 4 * m * n + 4 * (m + n) + (4 * m if layer else 0)
