@@ -594,8 +594,12 @@ class TernaryF32(Workload):
         self.layer = layer
         # the library's dispatch (ternary.hip: kRowsMinCols, kMfMinWaves)
         mfma = ((m + 63) // 64) * ((n + 15) // 16) >= 768
-        self.bound = "mfma_f32" if mfma else "valu"
-        self.kernel = ("ternary_f32_mfma_kernel" if mfma else
+        # the library's dispatch: the 4 x 4 x 1 matrix-core kernel for the
+        # layer (token-major input) at 41-192 tokens where the 16 x 16 one
+        # does not run (packed rows of k <= 7680 columns)
+        mf4 = layer and not mfma and 41 <= n <= 192 and k <= 7680
+        self.bound = "mfma_f32" if mfma or mf4 else "valu"
+        self.kernel = ("ternary_f32_mfma_kernel" if mfma else "ternary_f32_mf4_kernel" if mf4 else
                        "ternary_f32_pipe_kernel" if n <= 4 else "ternary_f32_rows_kernel")
         self.kp = (k + 4) // 5
         self.name = f"{'bit_linear_f32' if layer else 'ternary_f32'}_{m}x{n}x{k}"

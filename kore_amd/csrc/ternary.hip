@@ -2027,6 +2027,340 @@ static int launch_f32_mfma(uint64_t m, uint64_t n, hipStream_t s, const TernF32A
     return launch_status();
 }
 
+// Decode batches (a few dozen columns) on the fp32 matrix cores with the
+// 4 x 4 x 1 form: v_mfma_f32_4x4x1_16b_f32 runs 16 blocks of 4 x 4 outputs,
+// each output one fused multiply-add with a single rounding per K column,
+// like the 16 x 16 form (checked on the GPU against fmaf chains of 3000
+// steps on random operands with denormals: no difference).  A dependent
+// chain of them issues one step per ~15 cycles (measured back to back; an
+// instruction between two steps of a chain costs ~13 more; two chains
+// interleaved, ~10 per step each), so a wave owning 4 weight rows x 64
+// columns per chain has a chain 4x shorter per K column than the 64 x 16
+// waves of the 16 x 16 form, and a decode batch gets more chains to spread
+// over the SIMDs.
+//
+// Operands (lane L, block L / 4; layout measured on the GPU): b = b(k, n0 +
+// L); output register v of lane L is (row v of the chain, n0 + L).  The
+// trits need no data movement: per 80-column chunk lane 4 j + r decodes
+// packed byte j of the chunk of the chain's row r (its five trits as
+// floats, one LDS table entry), and the MFMA of column 5 j + d takes trit d
+// from block j's lanes for all 16 blocks (CBSZ = 4, ABID = j).  CH chains
+// per wave (rows m0 .. m0 + 4 CH - 1) share each b read.  A workgroup is
+// 8 / CH waves on 32 consecutive rows of the same 64 columns.  Its rows'
+// packed bytes (one contiguous range) are copied into LDS at the start; b is
+// staged per chunk in LDS (per column, K contiguous, pitch 84 floats: a
+// lane's 16-byte reads of its own column hit 16 distinct bank groups per 16
+// lanes), three buffers, its global loads issued two chunks ahead.  A chunk
+// runs as four bursts of 20 K columns with nothing between the MFMAs; the
+// next burst's b entries are read before the current burst, the next
+// chunk's trits before the barrier that ends the chunk.  Zero trits and
+// non-finite b as in the 16 x 16 kernel: a chunk whose staged b holds an
+// Inf or NaN is folded element by element with zero trits skipped.
+constexpr int kM4K = 80;                 // K columns per chunk
+constexpr int kM4Rows = 32;              // rows per workgroup
+constexpr int kM4Pitch4 = kM4K / 4 + 1;  // 16-byte entries per staged column
+constexpr int kM4Pieces = kWave * kM4K / 4;  // 16-byte pieces of b per chunk
+constexpr uint32_t kM4MaxSlice = 48 * 1024;  // bytes of packed rows a workgroup holds in LDS
+
+// One step of a 4 x 4 x 1 chain whose trit operand is block j's (CBSZ = 4,
+// ABID = j: one block's four lanes broadcast to all sixteen).
+__device__ __forceinline__ f32x4 mf4_step(float a, float b, f32x4 c, int j) {
+    switch (j) {
+        case 0: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 0, 0);
+        case 1: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 1, 0);
+        case 2: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 2, 0);
+        case 3: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 3, 0);
+        case 4: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 4, 0);
+        case 5: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 5, 0);
+        case 6: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 6, 0);
+        case 7: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 7, 0);
+        case 8: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 8, 0);
+        case 9: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 9, 0);
+        case 10: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 10, 0);
+        case 11: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 11, 0);
+        case 12: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 12, 0);
+        case 13: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 13, 0);
+        case 14: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 14, 0);
+        default: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 15, 0);
+    }
+}
+
+template <bool TM, int CH>
+__global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32Args p) {
+    constexpr int W = 8 / CH;
+    constexpr int kThreads = W * kWave;
+    constexpr int kStage = (kM4Pieces + kThreads - 1) / kThreads;
+    __shared__ __attribute__((aligned(16))) float tl[256 * 8];
+    __shared__ f32x4 bs[3][kWave][kM4Pitch4];
+    __shared__ uint32_t bbad[3][W];
+    extern __shared__ uint32_t araw[];  // the workgroup's packed rows, from a dword boundary
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(t / kWave);
+    for (int i = t; i < 256; i += kThreads) {
+        uint32_t x = (uint32_t)i;
+        float* e = tl + 8 * i;
+#pragma unroll
+        for (int d = 0; d < 5; ++d) {
+            e[d] = i >= 243 ? 0.0f : (float)((int)(x % 3u) - 1);
+            x /= 3u;
+        }
+        e[5] = e[6] = e[7] = 0.0f;
+    }
+    const uint32_t r0 = blockIdx.x * kM4Rows;  // the workgroup's first row
+    const uint32_t m0 = r0 + 4u * CH * wave;   // the wave's first row
+    const uint32_t n0 = blockIdx.y * kWave;
+    const uint32_t col = n0 + (uint32_t)lane;
+    // the packed rows r0 .. r0 + 31 (past the matrix: zeros)
+    const int a_bytes = (int)((uint64_t)p.m * p.kp);
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)p.a, (short)0, a_bytes, kBufWord3);
+    const uint32_t s_beg = r0 * p.kp, d0 = s_beg & ~3u, s_off = s_beg - d0;
+    const uint32_t nwords = (s_off + kM4Rows * p.kp + 3u) / 4u;
+    for (uint32_t i = (uint32_t)t; i < nwords; i += kThreads) {
+        // a dword that straddles the end of the matrix reads as zero from the
+        // range-checked resource: its bytes are read one by one
+        const uint32_t o = d0 + 4u * i;
+        uint32_t v;
+        if (o + 4u <= (uint32_t)a_bytes) {
+            v = __builtin_amdgcn_raw_buffer_load_b32(ra, o, 0, 0);
+        } else {
+            v = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(ra, o + b, 0, 0) << (8 * b);
+        }
+        araw[i] = v;
+    }
+    // b staging, piece e of a chunk: token-major b, column e / 20 and K
+    // columns 4 (e % 20) .. + 3; [K, N] b, K column e / 16 and columns
+    // 4 (e % 16) .. + 3
+    const bool nvec = !TM && (p.n & 3u) == 0 && (reinterpret_cast<uintptr_t>(p.b) & 15u) == 0;
+    auto stage_load = [&](uint32_t kc, f32x4 (&v)[kStage]) {
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int e = t + kThreads * u;
+            v[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (e < kM4Pieces) {
+                if (TM) {
+                    const uint32_t cl = n0 + (uint32_t)(e / (kM4K / 4)), k4 = kc + 4u * (uint32_t)(e % (kM4K / 4));
+                    if (cl < p.n) {
+                        if (k4 + 4 <= p.k) {
+                            v[u] = __builtin_bit_cast(f32x4, (u32x4)*reinterpret_cast<const u32x4_a4*>(p.b + (uint64_t)cl * p.bn + k4));
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) v[u][r] = k4 + r < p.k ? p.b[(uint64_t)cl * p.bn + k4 + r] : 0.0f;
+                        }
+                    }
+                } else {
+                    const uint32_t kk = kc + (uint32_t)(e / 16), c4 = n0 + 4u * (uint32_t)(e % 16);
+                    if (kk < p.k) {
+                        const float* src = p.b + (uint64_t)kk * p.bk;
+                        if (nvec && c4 + 4 <= p.n) {
+                            v[u] = *reinterpret_cast<const f32x4*>(src + c4);
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) v[u][r] = c4 + r < p.n ? src[c4 + r] : 0.0f;
+                        }
+                    }
+                }
+            }
+        }
+    };
+    auto stage_store = [&](uint32_t buf, const f32x4 (&v)[kStage]) {
+        bool bad = false;
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int e = t + kThreads * u;
+            if (e < kM4Pieces) {
+                if (TM) {
+                    bs[buf][e / (kM4K / 4)][e % (kM4K / 4)] = v[u];
+                } else {
+                    const int kk = e / 16, c4 = 4 * (e % 16);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) bs[buf][c4 + r][kk >> 2][kk & 3] = v[u][r];
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) bad |= !__builtin_isfinite(v[u][r]);
+            }
+        }
+        const uint64_t bl = __ballot(bad);
+        if (lane == 0) bbad[buf][wave] = bl != 0 ? 1u : 0u;
+    };
+    f32x4 acc[CH];
+#pragma unroll
+    for (int h = 0; h < CH; ++h) acc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 sv0[kStage], sv1[kStage];
+    if (p.k > 0) {
+        stage_load(0, sv0);
+        stage_store(0, sv0);
+        stage_load(kM4K, sv0);
+        stage_store(1, sv0);
+        stage_load(2 * kM4K, sv0);  // past K: zeros
+        stage_load(3 * kM4K, sv1);
+    }
+    __syncthreads();  // the table, the packed rows and the b of chunks 0 and 1
+    const bool live = m0 < p.m;
+    // lane 4 j + r: byte j of the chunk of chain h's row r
+    const uint8_t* abytes = reinterpret_cast<const uint8_t*>(araw);
+    const uint32_t aoff = s_off + (4u * CH * wave + (uint32_t)(lane & 3)) * p.kp + (uint32_t)(lane >> 2);
+    f32x4 tq[CH], tqn[CH];  // trits 0..3 of this lane's byte, per chain (this chunk, the next)
+    float t4[CH], t4n[CH];  // trit 4
+    auto load_trits = [&](uint32_t kc, f32x4 (&q)[CH], float (&q4)[CH]) {
+#pragma unroll
+        for (int h = 0; h < CH; ++h) {
+            const uint32_t v = abytes[aoff + 4u * h * p.kp + kc / 5u];
+            q[h] = *reinterpret_cast<const f32x4*>(tl + 8 * v);
+            q4[h] = tl[8 * v + 4];
+        }
+    };
+    auto chunk_bad = [&](uint32_t buf) {
+        bool bad = false;
+#pragma unroll
+        for (int w = 0; w < W; ++w) bad |= bbad[buf][w] != 0u;
+        return bad;
+    };
+    f32x4 bq[2][5];  // b entries of a burst (20 K columns)
+    auto read_b = [&](f32x4 (&q)[5], uint32_t buf, int bi) {
+#pragma unroll
+        for (int g = 0; g < 5; ++g) q[g] = bs[buf][lane][5 * bi + g];
+    };
+    bool bad = false, badn = false;
+    if (p.k > 0) {
+        load_trits(0, tq, t4);
+        read_b(bq[0], 0, 0);
+        bad = chunk_bad(0);
+    }
+    // one chunk: its bursts, chunk c + 2's b into its buffer (loaded two
+    // chunks ago into svc), chunk c + 4's loads into svc, chunk c + 1's
+    // trits and first b entries, and a barrier over LDS only (the loads in
+    // flight are this thread's own registers)
+    auto chunk = [&](uint32_t kc, uint32_t buf, f32x4 (&svc)[kStage]) {
+        const uint32_t nbuf = buf == 2u ? 0u : buf + 1u;
+        const bool more = kc + kM4K < p.k;
+        // chunk c + 1's trits, first b entries and flag: its buffer was
+        // written before the last barrier, so they are read during the last
+        // burst of chunk c
+        auto read_next = [&]() {
+            if (more) {
+                load_trits(kc + kM4K, tqn, t4n);
+                read_b(bq[0], nbuf, 0);
+                badn = chunk_bad(nbuf);
+            }
+        };
+        if (live && !bad) {
+#pragma unroll
+            for (int bi = 0; bi < 4; ++bi) {
+                if (bi < 3) read_b(bq[(bi + 1) & 1], buf, bi + 1);
+                else read_next();
+                const f32x4(&q)[5] = bq[bi & 1];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                    for (int d = 0; d < 5; ++d) {
+                        const int kk = 5 * u + d;
+#pragma unroll
+                        for (int h = 0; h < CH; ++h)
+                            acc[h] = mf4_step(d < 4 ? tq[h][d] : t4[h], q[kk >> 2][kk & 3], acc[h], 4 * bi + u);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+          if (live) {
+            // The reference's step, element by element: output v of lane L
+            // is row v of chain h, whose trit d of byte j lane 4 j + v holds.
+            for (int kk = 0; kk < kM4K; ++kk) {
+                const int j = kk / 5, d = kk % 5;
+                const float bk = bs[buf][lane][kk >> 2][kk & 3];
+#pragma unroll
+                for (int h = 0; h < CH; ++h) {
+                    float tv = t4[h];
+#pragma unroll
+                    for (int dd = 0; dd < 4; ++dd)
+                        if (dd == d) tv = tq[h][dd];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float te = __shfl(tv, 4 * j + r, kWave);
+                        if (te != 0.0f) acc[h][r] = __builtin_fmaf(te, bk, acc[h][r]);
+                    }
+                }
+            }
+          }
+          read_next();
+        }
+        if (kc + 2 * kM4K < p.k) {
+            stage_store(buf == 0u ? 2u : buf - 1u, svc);  // buffer (c + 2) % 3
+            stage_load(kc + 4 * kM4K, svc);
+        }
+#pragma unroll
+        for (int h = 0; h < CH; ++h) {
+            tq[h] = tqn[h];
+            t4[h] = t4n[h];
+        }
+        bad = badn;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    };
+    uint32_t buf = 0;
+    for (uint32_t kc = 0; kc < p.k; kc += 2 * kM4K) {
+        chunk(kc, buf, sv0);
+        buf = buf == 2u ? 0u : buf + 1u;
+        if (kc + kM4K >= p.k) break;
+        chunk(kc + kM4K, buf, sv1);
+        buf = buf == 2u ? 0u : buf + 1u;
+    }
+    if (!live || col >= p.n) return;
+#pragma unroll
+    for (int h = 0; h < CH; ++h) {
+        const uint32_t mr = m0 + 4u * h;
+        if (mr >= p.m) break;
+        if (p.trans && mr + 3 < p.m && (p.ldt & 3u) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15u) == 0) {
+            f32x4 out;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) out[r] = add_bias(p.bias, acc[h][r] * p.sa[mr + r], mr + r);
+            *reinterpret_cast<f32x4*>(p.c + out_idx(p, mr, col)) = out;
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (mr + r < p.m) p.c[out_idx(p, mr + r, col)] = add_bias(p.bias, acc[h][r] * p.sa[mr + r], mr + r);
+        }
+    }
+}
+
+// Bytes of the packed-row slice a workgroup copies into LDS (0: too long for
+// this kernel).
+static uint32_t f32_mf4_slice(uint64_t kp) {
+    const uint64_t words = (3u + kM4Rows * kp + 3u) / 4u;
+    return words * 4u <= kM4MaxSlice ? (uint32_t)(words * 4u) : 0u;
+}
+
+// Where the 4 x 4 kernel runs: token-major b (BitLinear::forward's input
+// as stored), 41 to 192 columns, and no 16 x 16 launch for the shape.
+// Measured (HIP events, bit_linear_f32): 6912 x {48, 64, 96} x 2560 49, 51,
+// 98 us against 70, 70, 107 for the row-broadcast kernel; 2560 x {96, 128,
+// 192} x 6912 129, 132, 134 against 170, 172, 195; 48 and 64 columns at
+// 2560 x 6912 within 3% (124-128 against 123-125); 24 and 32 columns
+// slower (47-49 against 38-39 us at 6912 x 2560: the 64-column waves are
+// half empty).  Its [K, N] staging (scalar LDS writes per column) makes the
+// plain ternary_matmul slower at most of these shapes, so that layout keeps
+// the row-broadcast kernel.  Two chains per wave (8 rows, each b read shared
+// by both) measured 10-20% slower: one wave per SIMD then has nothing to
+// hide its own LDS waits and barriers behind.
+static bool f32_use_mf4(uint64_t m, uint64_t n, uint64_t k, uint64_t kp) {
+    return k > 0 && n >= 41 && n <= 192 && !f32_use_mfma(m, n, k) && f32_mf4_slice(kp) != 0;
+}
+
+template <bool TM, int CH>
+static int launch_f32_mf4(uint64_t m, uint64_t n, hipStream_t s, const TernF32Args& p) {
+    const uint64_t bx = (m + kM4Rows - 1) / kM4Rows, by = (n + kWave - 1) / kWave;
+    if (bx > 0x7fffffffull || by > 65535) return KORE_HIP_ERR_OVERFLOW;
+    const uint32_t lds = f32_mf4_slice(p.kp);
+    if (lds == 0) return KORE_HIP_ERR_BAD_DIM;
+    hipLaunchKernelGGL((ternary_f32_mf4_kernel<TM, CH>), dim3((uint32_t)bx, (uint32_t)by), dim3(8 / CH * kWave), lds, s, p);
+    return launch_status();
+}
+
 // One to four columns (decode steps), any row alignment.  The
 // fold is a chain of k dependent f32 operations per output, so its floor is k
 // times the latency of one dependent vector operation (about 8 cycles for a
@@ -3060,6 +3394,11 @@ static int ternary_f32_run(const uint8_t* a_packed, const float* a_scales, const
             q.m = (uint32_t)std::min<uint64_t>(span, m - r0);
             q.c += trans ? r0 : r0 * n;  // c[n, m]: columns r0 .. of every row, row stride m
             if (bias) q.bias += r0;
+            if (tm && f32_use_mf4(q.m, n, k, kp)) {
+                const int st = launch_f32_mf4<true, 1>(q.m, n, s, q);
+                if (st != KORE_HIP_OK) return st;
+                continue;
+            }
             if (f32_use_mfma(q.m, n, k)) {
                 const int st = tm ? launch_f32_mfma<true>(q.m, n, s, q) : launch_f32_mfma<false>(q.m, n, s, q);
                 if (st != KORE_HIP_OK) return st;

@@ -226,3 +226,39 @@ def test_bit_linear_unaligned_buffers(off):
     got = yt[off // 4: off // 4 + batch * m].cpu().numpy().reshape(batch, m)
     assert_bitexact(got[:16], oracle.bit_linear_forward(p, sa, x[:16], bias, m, 16, k), "bit_linear_f32 unaligned")
     assert torch.isnan(yt[:off // 4]).all() and torch.isnan(yt[off // 4 + batch * m:]).all()
+
+
+@pytest.mark.parametrize("m,batch,k", [(2049, 48, 2563), (130, 96, 1203), (557, 192, 6912), (33, 41, 85),
+                                       (1001, 64, 80), (4097, 100, 1283)])
+def test_bit_linear_f32_matrix_core_decode_batches(m, batch, k):
+    """The 4 x 4 x 1 matrix-core kernel that takes the f32 layer at 41-192
+    tokens (token-major input): ragged row groups (m % 4 == 1, where the
+    packed matrix ends inside a dword), partial last column tiles, K not a
+    multiple of the 80-column chunk or of 5, up to 6912 columns of packed
+    rows held in LDS; with Inf, NaN and subnormal inputs in some tokens (their
+    chunks fold element by element, zero trits skipped).  Bit-exact against
+    the oracle's composition on the tokens it finishes in seconds and against
+    the device's ternary_matmul_f32 on x^T (another kernel) on every token."""
+    log(f"bit_linear_f32 4x4 matrix cores m={m} batch={batch} k={k}")
+    p = raw_packed(m, k, 5 * m + k)
+    sa = normal((m,), 50, 1.0, 0.1)
+    bias = normal((m,), 51)
+    x = normal((batch, k), 52)
+    r = np.random.default_rng(m + batch)
+    x[1, r.integers(0, k, 3)] = np.inf
+    x[2, r.integers(0, k, 2)] = -np.inf
+    x[3, r.integers(0, k, 2)] = np.nan
+    x[4] = (x[4] * 1e-39).astype(np.float32)  # subnormal
+    bp, bs, bb = up(p), up(sa), up(bias)
+    got = down(rocm.rocm_bit_linear_f32(DEV, bp, bs, up(x), bb, m, batch, k), np.float32, (batch, m))
+    tok = slice(0, min(batch, max(8, 100_000_000 // max(1, m * k))))
+    xs = x[tok]
+    assert_bitexact(got[tok], oracle.bit_linear_forward(p, sa, xs, bias, m, xs.shape[0], k),
+                    "bit_linear_f32 4x4 matrix cores vs oracle")
+    xt = torch.from_numpy(x).cuda().t().contiguous()
+    c = rocm.rocm_ternary_matmul_f32(DEV, bp, bs, HipBuffer.from_tensor(xt), m, batch, k)
+    ct = torch.from_numpy(down(c, np.float32, (m, batch))).cuda()
+    want = ct.t().contiguous() + torch.from_numpy(bias).cuda()[None, :]
+    gt = torch.from_numpy(got).cuda()
+    same = (gt == want) | (torch.isnan(gt) & torch.isnan(want))
+    assert bool(same.all()), f"bit_linear_f32 4x4 matrix cores vs ternary_matmul_f32: {int((~same).sum())} differ"
