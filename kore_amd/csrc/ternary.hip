@@ -42,9 +42,12 @@
 // output, the reference loop order.
 //
 // kore_hip_ternary_matmul_f32: the reference's f32-activation ternary_matmul,
-// a sequential fold per output (at the end): ternary_f32_rows_kernel for five
-// columns and more, ternary_f32_pipe_kernel for one to four columns,
-// ternary_f32_seq_kernel for K = 0 and matrices of fewer than 20 packed bytes.
+// a sequential fold per output (at the end): ternary_f32_mfma_kernel (fp32
+// matrix cores, 16 x 16 x 1) for prefill-sized shapes,
+// ternary_f32_mf4_kernel (4 x 4 x 1) for the layer's token-major input at
+// 41-192 tokens, ternary_f32_rows_kernel for five columns and more,
+// ternary_f32_pipe_kernel for one to four columns, ternary_f32_seq_kernel for
+// K = 0 and matrices of fewer than 20 packed bytes.
 #include <algorithm>
 #include <type_traits>
 
@@ -2115,7 +2118,9 @@ __global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32
     const int a_bytes = (int)((uint64_t)p.m * p.kp);
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)p.a, (short)0, a_bytes, kBufWord3);
     const uint32_t s_beg = r0 * p.kp, d0 = s_beg & ~3u, s_off = s_beg - d0;
-    const uint32_t nwords = (s_off + kM4Rows * p.kp + 3u) / 4u;
+    // (+ 4 words: the last chunk's trit reads of row 31 reach up to 15 bytes
+    // past the slice; past the matrix they read zeros)
+    const uint32_t nwords = (s_off + kM4Rows * p.kp + 3u) / 4u + 4u;
     for (uint32_t i = (uint32_t)t; i < nwords; i += kThreads) {
         // a dword that straddles the end of the matrix reads as zero from the
         // range-checked resource: its bytes are read one by one
@@ -2331,7 +2336,7 @@ __global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32
 // Bytes of the packed-row slice a workgroup copies into LDS (0: too long for
 // this kernel).
 static uint32_t f32_mf4_slice(uint64_t kp) {
-    const uint64_t words = (3u + kM4Rows * kp + 3u) / 4u;
+    const uint64_t words = (3u + kM4Rows * kp + 3u) / 4u + 4u;
     return words * 4u <= kM4MaxSlice ? (uint32_t)(words * 4u) : 0u;
 }
 
