@@ -262,3 +262,33 @@ def test_bit_linear_f32_matrix_core_decode_batches(m, batch, k):
     gt = torch.from_numpy(got).cuda()
     same = (gt == want) | (torch.isnan(gt) & torch.isnan(want))
     assert bool(same.all()), f"bit_linear_f32 4x4 matrix cores vs ternary_matmul_f32: {int((~same).sum())} differ"
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_bit_linear_f32_matrix_core_random_shapes(seed):
+    """Random shapes across the 4 x 4 x 1 kernel's range (41-192 tokens, up to
+    7680 input features, any row count): bit-exact against the oracle on the
+    first tokens and against ternary_matmul_f32 on x^T (the row-broadcast or
+    16 x 16 kernel, never this one) on every token."""
+    r = np.random.default_rng(1000 + seed)
+    m = int(r.integers(1, 3000))
+    batch = int(r.integers(41, 193))
+    k = int(r.integers(1, 7681))
+    log(f"bit_linear_f32 4x4 random seed={seed} m={m} batch={batch} k={k}")
+    p = raw_packed(m, k, 11 * seed + 3)
+    sa = normal((m,), 60 + seed, 1.0, 0.1)
+    bias = normal((m,), 70 + seed) if seed % 2 == 0 else None
+    x = normal((batch, k), 80 + seed)
+    bp, bs = up(p), up(sa)
+    bb = up(bias) if bias is not None else None
+    got = down(rocm.rocm_bit_linear_f32(DEV, bp, bs, up(x), bb, m, batch, k), np.float32, (batch, m))
+    tok = slice(0, min(batch, max(2, 50_000_000 // max(1, m * k))))
+    xs = x[tok]
+    assert_bitexact(got[tok], oracle.bit_linear_forward(p, sa, xs, bias, m, xs.shape[0], k),
+                    f"bit_linear_f32 4x4 random seed={seed}")
+    xt = torch.from_numpy(x).cuda().t().contiguous()
+    c = rocm.rocm_ternary_matmul_f32(DEV, bp, bs, HipBuffer.from_tensor(xt), m, batch, k)
+    want = torch.from_numpy(down(c, np.float32, (m, batch))).cuda().t().contiguous()
+    if bias is not None:
+        want = want + torch.from_numpy(bias).cuda()[None, :]
+    assert torch.equal(torch.from_numpy(got).cuda(), want), f"bit_linear_f32 4x4 random seed={seed} vs composition"
