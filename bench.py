@@ -594,10 +594,11 @@ class TernaryF32(Workload):
         self.layer = layer
         # the library's dispatch (ternary.hip: kRowsMinCols, kMfMinWaves)
         mfma = ((m + 63) // 64) * ((n + 15) // 16) >= 768
-        # the library's dispatch: the 4 x 4 x 1 matrix-core kernel for the
-        # layer (token-major input) at 41-192 tokens where the 16 x 16 one
-        # does not run (packed rows of k <= 7680 columns)
-        mf4 = layer and not mfma and 41 <= n <= 192 and k <= 7680
+        # the library's dispatch: the 4 x 4 x 1 matrix-core kernel where the
+        # 16 x 16 one does not run (packed rows of k <= 7680 columns): the
+        # layer (token-major input) at 41-192 tokens, [K, N] b at 41-64
+        # tokens on at least 4096 rows
+        mf4 = not mfma and k <= 7680 and (41 <= n <= 192 if layer else (41 <= n <= 64 and m >= 4096))
         self.bound = "mfma_f32" if mfma or mf4 else "valu"
         self.kernel = ("ternary_f32_mfma_kernel" if mfma else "ternary_f32_mf4_kernel" if mf4 else
                        "ternary_f32_pipe_kernel" if n <= 4 else "ternary_f32_rows_kernel")

@@ -2135,10 +2135,11 @@ __global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32
         }
         araw[i] = v;
     }
-    // b staging, piece e of a chunk: token-major b, column e / 20 and K
-    // columns 4 (e % 20) .. + 3; [K, N] b, K column e / 16 and columns
-    // 4 (e % 16) .. + 3
-    const bool nvec = !TM && (p.n & 3u) == 0 && (reinterpret_cast<uintptr_t>(p.b) & 15u) == 0;
+    // b staging, piece e of a chunk = one 16-byte entry of the LDS tile:
+    // token-major b, column e / 20 and K columns 4 (e % 20) .. + 3 (one
+    // 16-byte load along the column's row); [K, N] b, column e % 64 and K
+    // columns 4 (e / 64) .. + 3 (four loads, each a wave-wide 256-byte piece
+    // of a row of b)
     auto stage_load = [&](uint32_t kc, f32x4 (&v)[kStage]) {
 #pragma unroll
         for (int u = 0; u < kStage; ++u) {
@@ -2156,15 +2157,11 @@ __global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32
                         }
                     }
                 } else {
-                    const uint32_t kk = kc + (uint32_t)(e / 16), c4 = n0 + 4u * (uint32_t)(e % 16);
-                    if (kk < p.k) {
-                        const float* src = p.b + (uint64_t)kk * p.bk;
-                        if (nvec && c4 + 4 <= p.n) {
-                            v[u] = *reinterpret_cast<const f32x4*>(src + c4);
-                        } else {
+                    const uint32_t cl = n0 + (uint32_t)(e % kWave), k4 = kc + 4u * (uint32_t)(e / kWave);
+                    if (cl < p.n) {
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) v[u][r] = c4 + r < p.n ? src[c4 + r] : 0.0f;
-                        }
+                        for (int r = 0; r < 4; ++r)
+                            v[u][r] = k4 + r < p.k ? p.b[(uint64_t)(k4 + r) * p.bk + (uint64_t)cl * p.bn] : 0.0f;
                     }
                 }
             }
@@ -2176,13 +2173,8 @@ __global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32
         for (int u = 0; u < kStage; ++u) {
             const int e = t + kThreads * u;
             if (e < kM4Pieces) {
-                if (TM) {
-                    bs[buf][e / (kM4K / 4)][e % (kM4K / 4)] = v[u];
-                } else {
-                    const int kk = e / 16, c4 = 4 * (e % 16);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) bs[buf][c4 + r][kk >> 2][kk & 3] = v[u][r];
-                }
+                if (TM) bs[buf][e / (kM4K / 4)][e % (kM4K / 4)] = v[u];
+                else bs[buf][e % kWave][e / kWave] = v[u];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) bad |= !__builtin_isfinite(v[u][r]);
             }
@@ -2347,13 +2339,15 @@ static uint32_t f32_mf4_slice(uint64_t kp) {
 // 192} x 6912 129, 132, 134 against 170, 172, 195; 48 and 64 columns at
 // 2560 x 6912 within 3% (124-128 against 123-125); 24 and 32 columns
 // slower (47-49 against 38-39 us at 6912 x 2560: the 64-column waves are
-// half empty).  Its [K, N] staging (scalar LDS writes per column) makes the
-// plain ternary_matmul slower at most of these shapes, so that layout keeps
-// the row-broadcast kernel.  Two chains per wave (8 rows, each b read shared
-// by both) measured 10-20% slower: one wave per SIMD then has nothing to
-// hide its own LDS waits and barriers behind.
-static bool f32_use_mf4(uint64_t m, uint64_t n, uint64_t k, uint64_t kp) {
-    return k > 0 && n >= 41 && n <= 192 && !f32_use_mfma(m, n, k) && f32_mf4_slice(kp) != 0;
+// half empty).  With [K, N] b (the plain ternary_matmul; four row loads per
+// staged entry) it wins only at 41-64 columns on tall matrices: 6912 x
+// {41, 48, 64} x 2560 61 us against 69, 66, 66; 2560 x 64 x 6912 155 against
+// 110, 6912 x 96 x 2560 120 against 102.  Two chains per wave (8 rows, each
+// b read shared by both) measured 10-20% slower: one wave per SIMD then has
+// nothing to hide its own LDS waits and barriers behind.
+static bool f32_use_mf4(uint64_t m, uint64_t n, uint64_t k, uint64_t kp, bool tm) {
+    if (k == 0 || n < 41 || f32_use_mfma(m, n, k) || f32_mf4_slice(kp) == 0) return false;
+    return tm ? n <= 192 : (n <= 64 && m >= 4096);
 }
 
 template <bool TM, int CH>
@@ -3399,8 +3393,8 @@ static int ternary_f32_run(const uint8_t* a_packed, const float* a_scales, const
             q.m = (uint32_t)std::min<uint64_t>(span, m - r0);
             q.c += trans ? r0 : r0 * n;  // c[n, m]: columns r0 .. of every row, row stride m
             if (bias) q.bias += r0;
-            if (tm && f32_use_mf4(q.m, n, k, kp)) {
-                const int st = launch_f32_mf4<true, 1>(q.m, n, s, q);
+            if (f32_use_mf4(q.m, n, k, kp, tm)) {
+                const int st = tm ? launch_f32_mf4<true, 1>(q.m, n, s, q) : launch_f32_mf4<false, 1>(q.m, n, s, q);
                 if (st != KORE_HIP_OK) return st;
                 continue;
             }

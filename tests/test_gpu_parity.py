@@ -1411,3 +1411,25 @@ def test_norm_family_adversarial_rows_bit_exact(cols):
     wq, ws = oracle.rms_norm_quant_i8(x, g, 1e-6)
     assert down(q, np.int8, (rows, cols)).tobytes() == wq.tobytes(), f"prequant codes adversarial {cols}"
     assert down(s, np.float32, (rows,)).tobytes() == ws.tobytes(), f"prequant scales adversarial {cols}"
+
+
+@pytest.mark.parametrize("m,n,k", [(6912, 64, 2560), (4097, 48, 1283), (5000, 41, 85), (4100, 64, 7680)])
+def test_ternary_matmul_f32_matrix_core_decode_batches(m, n, k):
+    """ternary_matmul_f32 with [K, N] b at 41-64 columns on tall matrices (the
+    4 x 4 x 1 matrix-core kernel): bit-exact against the oracle on every
+    output, with Inf, NaN and subnormal activations in some columns (their
+    chunks fold element by element, zero trits skipped), ragged row groups
+    and K not a multiple of the 80-column chunk."""
+    from inputs import raw_packed
+
+    log(f"ternary_matmul_f32 4x4 matrix cores m={m} n={n} k={k}")
+    p = raw_packed(m, k, m + 13 * k)
+    sa = normal((m,), 90, 1.0, 0.1)
+    b = normal((k, n), 91)
+    r = np.random.default_rng(m + n)
+    b[r.integers(0, k, 2), 1] = np.inf
+    b[r.integers(0, k, 2), 2] = -np.inf
+    b[r.integers(0, k, 1), 3] = np.nan
+    b[:, 4] = (b[:, 4] * 1e-39).astype(np.float32)
+    got = down(rocm.rocm_ternary_matmul_f32(DEV, up(p), up(sa), up(b), m, n, k), np.float32, (m, n))
+    assert_bitexact(got, oracle.ternary_matmul(p, sa, b, m, n, k), "ternary_matmul_f32 4x4 matrix cores")
