@@ -138,16 +138,10 @@ __global__ __launch_bounds__(kEwBlock) void unary_vec_kernel(const f32x4* __rest
     }
 }
 
-// Workgroups are dispatched to the 8 XCDs round-robin by index, so block b
-// runs on XCD b % 8.  The binary streams give each XCD one contiguous range
-// of tiles (XCD x: tiles [x q + min(x, r), ...) of its share q + (x < r),
-// q = blocks / 8, r = blocks % 8; a bijection on the tiles): SwiGLU 16384 x
+// The binary streams give each XCD one contiguous range of tiles
+// (xcd_tile): SwiGLU 16384 x
 // 14336 433 -> 426 us (81.3 -> 82.8% of 8 TB/s, two runs alike).  The
 // unary streams keep the plain order (GELU 276 -> 282 us with it).
-__device__ __forceinline__ uint64_t xcd_tile(uint64_t b, uint64_t nb) {
-    const uint64_t x = b % 8u, q = nb / 8u, r = nb % 8u;
-    return x * q + (x < r ? x : r) + b / 8u;
-}
 
 template <class Op>
 __global__ __launch_bounds__(kEwBlock) void binary_vec_kernel(const f32x4* __restrict__ a,

@@ -23,6 +23,15 @@ __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
 // Streaming loads/stores: data touched once.  The nontemporal hint keeps
 // the 2+ GB element-wise streams from evicting reusable lines in L2/MALL.
+// Workgroups are dispatched to the 8 XCDs round-robin by index, so block b
+// runs on XCD b % 8.  xcd_tile(b, nb) gives XCD x one contiguous range of the
+// nb tiles: [x q + min(x, r), ...) of its share q + (x < r), q = nb / 8,
+// r = nb % 8 -- a bijection on [0, nb).
+__device__ __forceinline__ uint64_t xcd_tile(uint64_t b, uint64_t nb) {
+    const uint64_t x = b % 8u, q = nb / 8u, r = nb % 8u;
+    return x * q + (x < r ? x : r) + b / 8u;
+}
+
 __device__ __forceinline__ f32x4 ld_stream(const f32x4* p) {
     return __builtin_nontemporal_load(p);
 }
