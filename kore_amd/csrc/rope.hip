@@ -161,9 +161,8 @@ __global__ __launch_bounds__(kRopeLaneBlock) void rope_lane_kernel(RopeTensor t0
                                                                 uint32_t blocks_tok) {
     extern __shared__ f32x4 cs_raw[];  // [D/2] (cos, sin)
     float2* cs = reinterpret_cast<float2*>(cs_raw);
-    const uint64_t bxr = blockIdx.x;
-    const uint64_t token = bxr / blocks_tok;
-    const uint32_t bt = (uint32_t)(bxr % blocks_tok);
+    const uint64_t token = blockIdx.x / blocks_tok;
+    const uint32_t bt = blockIdx.x % blocks_tok;
     const bool first_t = bt < blocks0;
     const RopeTensor& tt = first_t ? t0 : t1;
     const uint32_t row4 = tt.heads * (head_dim >> 2);  // float4 per token row
