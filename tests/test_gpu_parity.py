@@ -275,7 +275,9 @@ def test_prequant_huge_weights_overflowing_numerator(cols):
 
 
 # ------------------------------------------------------------- activations
-ACT_SIZES = [1, 3, 4, 5, 255, 1024, 1027, (1 << 20) + 3]
+# (13 * 512 + 3 and 2049 * 512 - 5: block counts that do not divide over the
+# 8 XCDs, for the binary kernels' per-XCD tile order)
+ACT_SIZES = [1, 3, 4, 5, 255, 1024, 1027, 13 * 512 + 3, (1 << 20) + 3, 2049 * 512 - 5]
 
 
 def special_values():
