@@ -61,7 +61,9 @@ __global__ __launch_bounds__(kEmbBlock) void embedding_vec_kernel(const f32x4* _
 // workgroups that each move one contiguous row chunk keep the most
 // independent requests in flight (measured on MI355X: a 1 GiB gather-copy
 // runs at 74.6% of 8 TB/s with 256-thread chunks, 81.5% with 1024, and
-// worse with several tokens per workgroup).
+// worse with several tokens per workgroup).  Table rows are read through the
+// caches (repeated ids hit them); nontemporal table loads measured slower
+// (8192 x 4096 from a 128256-row table: 43.6 -> 44.7 us).
 template <typename Id>
 __global__ __launch_bounds__(kEmbMaxBlock) void embedding_vec1_kernel(const f32x4* __restrict__ table,
                                                                       const Id* __restrict__ ids,
