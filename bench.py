@@ -595,10 +595,10 @@ class TernaryF32(Workload):
         # the library's dispatch (ternary.hip: kRowsMinCols, kMfMinWaves)
         mfma = ((m + 63) // 64) * ((n + 15) // 16) >= 768
         # the library's dispatch: the 4 x 4 x 1 matrix-core kernel where the
-        # 16 x 16 one does not run (packed rows of k <= 7680 columns): the
-        # layer (token-major input) at 41-192 tokens, [K, N] b at 41-64
-        # tokens on at least 4096 rows
-        mf4 = not mfma and k <= 7680 and (41 <= n <= 192 if layer else (41 <= n <= 64 and m >= 4096))
+        # 16 x 16 one does not run: 41-192 tokens, k >= 2560 (up to 7675), at
+        # least 1024 waves of 4 rows x 64 tokens
+        slice_ok = ((3 + 32 * ((k + 4) // 5) + 3) // 4 + 4) * 4 <= 48 * 1024  # the workgroup's packed rows fit its LDS
+        mf4 = not mfma and slice_ok and k >= 2560 and 41 <= n <= 192 and (m + 3) // 4 * ((n + 63) // 64) >= 1024
         self.bound = "mfma_f32" if mfma or mf4 else "valu"
         self.kernel = ("ternary_f32_mfma_kernel" if mfma else "ternary_f32_mf4_kernel" if mf4 else
                        "ternary_f32_pipe_kernel" if n <= 4 else "ternary_f32_rows_kernel")

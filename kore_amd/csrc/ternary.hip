@@ -2140,7 +2140,44 @@ __global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32
     // 16-byte load along the column's row); [K, N] b, column e % 64 and K
     // columns 4 (e / 64) .. + 3 (four loads, each a wave-wide 256-byte piece
     // of a row of b)
+    // Whole chunks load through a range-checked resource at per-thread byte
+    // offsets fixed for the kernel (no 64-bit address arithmetic, no
+    // branches: a column past n, or a piece past the chunk, sits out of
+    // range and reads zeros); b is below 6 MB here (n <= 192, k <= 7680).
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p.b, (short)0, (int)((uint64_t)p.n * p.k * 4u), kBufWord3);
+    constexpr uint32_t kOut = 0x80000000u;  // an offset past any b this kernel takes
+    uint32_t boff[kStage];
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) {
+        const int e = t + kThreads * u;
+        boff[u] = kOut;
+        if (e < kM4Pieces) {
+            if (TM) {
+                const uint32_t cl = n0 + (uint32_t)(e / (kM4K / 4)), q4 = 4u * (uint32_t)(e % (kM4K / 4));
+                if (cl < p.n) boff[u] = (cl * p.k + q4) * 4u;
+            } else {
+                const uint32_t cl = n0 + (uint32_t)(e % kWave), q4 = 4u * (uint32_t)(e / kWave);
+                if (cl < p.n) boff[u] = (q4 * p.n + cl) * 4u;
+            }
+        }
+    }
     auto stage_load = [&](uint32_t kc, f32x4 (&v)[kStage]) {
+        if (kc + kM4K <= p.k) {
+#pragma unroll
+            for (int u = 0; u < kStage; ++u) {
+                if (TM) {
+                    v[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, boff[u] + 4u * kc, 0, 0));
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        v[u][r] = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rb, boff[u] + 4u * (kc + r) * p.n, 0, 0));
+                }
+            }
+            return;
+        }
+        // the last, partial chunk: element by element, zeros past k
 #pragma unroll
         for (int u = 0; u < kStage; ++u) {
             const int e = t + kThreads * u;
@@ -2332,22 +2369,26 @@ static uint32_t f32_mf4_slice(uint64_t kp) {
     return words * 4u <= kM4MaxSlice ? (uint32_t)(words * 4u) : 0u;
 }
 
-// Where the 4 x 4 kernel runs: token-major b (BitLinear::forward's input
-// as stored), 41 to 192 columns, and no 16 x 16 launch for the shape.
-// Measured (HIP events, bit_linear_f32): 6912 x {48, 64, 96} x 2560 49, 51,
-// 98 us against 70, 70, 107 for the row-broadcast kernel; 2560 x {96, 128,
-// 192} x 6912 129, 132, 134 against 170, 172, 195; 48 and 64 columns at
-// 2560 x 6912 within 3% (124-128 against 123-125); 24 and 32 columns
-// slower (47-49 against 38-39 us at 6912 x 2560: the 64-column waves are
-// half empty).  With [K, N] b (the plain ternary_matmul; four row loads per
-// staged entry) it wins only at 41-64 columns on tall matrices: 6912 x
-// {41, 48, 64} x 2560 61 us against 69, 66, 66; 2560 x 64 x 6912 155 against
-// 110, 6912 x 96 x 2560 120 against 102.  Two chains per wave (8 rows, each
-// b read shared by both) measured 10-20% slower: one wave per SIMD then has
-// nothing to hide its own LDS waits and barriers behind.
-static bool f32_use_mf4(uint64_t m, uint64_t n, uint64_t k, uint64_t kp, bool tm) {
-    if (k == 0 || n < 41 || f32_use_mfma(m, n, k) || f32_mf4_slice(kp) == 0) return false;
-    return tm ? n <= 192 : (n <= 64 && m >= 4096);
+// Where the 4 x 4 kernel runs: 41 to 192 columns, K from 2560 (its fixed
+// costs -- the packed-row copy, the staging prologue -- spread over enough
+// chunks), at least 1024 waves of 4 rows x 64 columns, and no 16 x 16
+// launch for the shape; both layouts of b.  Measured (HIP events; the
+// row-broadcast kernel in the same run), token-major b (the layer) and
+// [K, N] b (the plain ternary_matmul):
+//   6912 x 64 x 2560: 46.1 and 48.0 us against 70 and 66 (1728 waves);
+//   6912 x 96 x 2560: 89.9 and 94.0 against 107 and 102;
+//   2560 x {96, 128, 192} x 6912: 118-123 and 124-128 against 143-195
+//   (1280-1920 waves);
+//   2560 x 64 x 6912 (640 waves): 118.6 and 123.5 against 125 and 109;
+//   2048 x 64 x 2048 (512 waves): 39.7 against 26.0 ([K, N]);
+//   24 and 32 columns: 47-49 against 38-39 us at 6912 x 2560 (the 64-column
+//   waves half empty).
+// Two chains per wave (8 rows, each b read shared by both) measured 10-20%
+// slower: one wave per SIMD then has nothing to hide its own LDS waits and
+// barriers behind.
+static bool f32_use_mf4(uint64_t m, uint64_t n, uint64_t k, uint64_t kp) {
+    if (n < 41 || n > 192 || k < 2560 || f32_use_mfma(m, n, k) || f32_mf4_slice(kp) == 0) return false;
+    return (m + 3) / 4 * ((n + kWave - 1) / kWave) >= 1024;
 }
 
 template <bool TM, int CH>
@@ -3393,7 +3434,7 @@ static int ternary_f32_run(const uint8_t* a_packed, const float* a_scales, const
             q.m = (uint32_t)std::min<uint64_t>(span, m - r0);
             q.c += trans ? r0 : r0 * n;  // c[n, m]: columns r0 .. of every row, row stride m
             if (bias) q.bias += r0;
-            if (f32_use_mf4(q.m, n, k, kp, tm)) {
+            if (f32_use_mf4(q.m, n, k, kp)) {
                 const int st = tm ? launch_f32_mf4<true, 1>(q.m, n, s, q) : launch_f32_mf4<false, 1>(q.m, n, s, q);
                 if (st != KORE_HIP_OK) return st;
                 continue;

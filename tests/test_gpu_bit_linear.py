@@ -228,14 +228,14 @@ def test_bit_linear_unaligned_buffers(off):
     assert torch.isnan(yt[:off // 4]).all() and torch.isnan(yt[off // 4 + batch * m:]).all()
 
 
-@pytest.mark.parametrize("m,batch,k", [(2049, 48, 2563), (130, 96, 1203), (557, 192, 6912), (33, 41, 85),
-                                       (1001, 64, 80), (4097, 100, 1283)])
+@pytest.mark.parametrize("m,batch,k", [(4097, 48, 2563), (2049, 130, 2605), (1500, 192, 6912), (4100, 41, 2560),
+                                       (6000, 64, 3201)])
 def test_bit_linear_f32_matrix_core_decode_batches(m, batch, k):
     """The 4 x 4 x 1 matrix-core kernel that takes the f32 layer at 41-192
-    tokens (token-major input): ragged row groups (m % 4 == 1, where the
-    packed matrix ends inside a dword), partial last column tiles, K not a
-    multiple of the 80-column chunk or of 5, up to 6912 columns of packed
-    rows held in LDS; with Inf, NaN and subnormal inputs in some tokens (their
+    tokens (token-major input; K >= 2560 and at least 1024 waves of 4 rows x
+    64 tokens): ragged row groups (m % 4 == 1, where the packed matrix ends
+    inside a dword), partial last column tiles, K not a multiple of the
+    80-column chunk or of 5, 6912 columns of packed rows held in LDS; with Inf, NaN and subnormal inputs in some tokens (their
     chunks fold element by element, zero trits skipped).  Bit-exact against
     the oracle's composition on the tokens it finishes in seconds and against
     the device's ternary_matmul_f32 on x^T (another kernel) on every token."""
@@ -266,14 +266,15 @@ def test_bit_linear_f32_matrix_core_decode_batches(m, batch, k):
 
 @pytest.mark.parametrize("seed", range(6))
 def test_bit_linear_f32_matrix_core_random_shapes(seed):
-    """Random shapes across the 4 x 4 x 1 kernel's range (41-192 tokens, up to
-    7680 input features, any row count): bit-exact against the oracle on the
+    """Random shapes across the 4 x 4 x 1 kernel's range (41-192 tokens,
+    2560-7680 input features, at least 1024 waves): bit-exact against the oracle on the
     first tokens and against ternary_matmul_f32 on x^T (the row-broadcast or
     16 x 16 kernel, never this one) on every token."""
     r = np.random.default_rng(1000 + seed)
-    m = int(r.integers(1, 3000))
     batch = int(r.integers(41, 193))
-    k = int(r.integers(1, 7681))
+    tiles = (batch + 63) // 64
+    m = int(r.integers(4096 // tiles, 4096 // tiles + 2000))  # at least 1024 waves of 4 rows x 64 tokens
+    k = int(r.integers(2560, 7681))
     log(f"bit_linear_f32 4x4 random seed={seed} m={m} batch={batch} k={k}")
     p = raw_packed(m, k, 11 * seed + 3)
     sa = normal((m,), 60 + seed, 1.0, 0.1)

@@ -1415,10 +1415,11 @@ def test_norm_family_adversarial_rows_bit_exact(cols):
     assert down(s, np.float32, (rows,)).tobytes() == ws.tobytes(), f"prequant scales adversarial {cols}"
 
 
-@pytest.mark.parametrize("m,n,k", [(6912, 64, 2560), (4097, 48, 1283), (5000, 41, 85), (4100, 64, 7680)])
+@pytest.mark.parametrize("m,n,k", [(6912, 64, 2560), (4097, 48, 2563), (2600, 100, 2600), (4100, 64, 7680),
+                                   (1500, 192, 6912)])
 def test_ternary_matmul_f32_matrix_core_decode_batches(m, n, k):
-    """ternary_matmul_f32 with [K, N] b at 41-64 columns on tall matrices (the
-    4 x 4 x 1 matrix-core kernel): bit-exact against the oracle on every
+    """ternary_matmul_f32 with [K, N] b on the 4 x 4 x 1 matrix-core kernel
+    (41-192 columns, K >= 2560, at least 1024 waves of 4 rows x 64 columns): bit-exact against the oracle on every
     output, with Inf, NaN and subnormal activations in some columns (their
     chunks fold element by element, zero trits skipped), ragged row groups
     and K not a multiple of the 80-column chunk."""
