@@ -2379,7 +2379,9 @@ static uint32_t f32_mf4_slice(uint64_t kp) {
 //   6912 x 96 x 2560: 89.9 and 94.0 against 107 and 102;
 //   2560 x {96, 128, 192} x 6912: 118-123 and 124-128 against 143-195
 //   (1280-1920 waves);
-//   2560 x 64 x 6912 (640 waves): 118.6 and 123.5 against 125 and 109;
+//   2560 x 64 x 6912 (640 waves): 118 and 124 against 116 and 103-109;
+//   2048 x 64 x 6912 (512 waves): 118 (token-major) against 78: below 1024
+//   waves a SIMD runs one wave, whose chain time does not shrink with m;
 //   2048 x 64 x 2048 (512 waves): 39.7 against 26.0 ([K, N]);
 //   24 and 32 columns: 47-49 against 38-39 us at 6912 x 2560 (the 64-column
 //   waves half empty).
