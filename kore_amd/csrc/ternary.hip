@@ -2088,9 +2088,9 @@ __device__ __forceinline__ f32x4 mf4_step(float a, float b, f32x4 c, int j) {
     }
 }
 
-template <bool TM, int CH>
-__global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32Args p) {
-    constexpr int W = 8 / CH;
+template <bool TM, int CH, int W>
+__global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args p) {
+    constexpr int kRows = 4 * CH * W;  // rows per workgroup
     constexpr int kThreads = W * kWave;
     constexpr int kStage = (kM4Pieces + kThreads - 1) / kThreads;
     __shared__ __attribute__((aligned(16))) float tl[256 * 8];
@@ -2110,7 +2110,7 @@ __global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32
         }
         e[5] = e[6] = e[7] = 0.0f;
     }
-    const uint32_t r0 = blockIdx.x * kM4Rows;  // the workgroup's first row
+    const uint32_t r0 = blockIdx.x * kRows;  // the workgroup's first row
     const uint32_t m0 = r0 + 4u * CH * wave;   // the wave's first row
     const uint32_t n0 = blockIdx.y * kWave;
     const uint32_t col = n0 + (uint32_t)lane;
@@ -2120,7 +2120,7 @@ __global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32
     const uint32_t s_beg = r0 * p.kp, d0 = s_beg & ~3u, s_off = s_beg - d0;
     // (+ 4 words: the last chunk's trit reads of row 31 reach up to 15 bytes
     // past the slice; past the matrix they read zeros)
-    const uint32_t nwords = (s_off + kM4Rows * p.kp + 3u) / 4u + 4u;
+    const uint32_t nwords = (s_off + kRows * p.kp + 3u) / 4u + 4u;
     for (uint32_t i = (uint32_t)t; i < nwords; i += kThreads) {
         // a dword that straddles the end of the matrix reads as zero from the
         // range-checked resource: its bytes are read one by one
@@ -2140,10 +2140,12 @@ __global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32
     // 16-byte load along the column's row); [K, N] b, column e % 64 and K
     // columns 4 (e / 64) .. + 3 (four loads, each a wave-wide 256-byte piece
     // of a row of b)
-    // Whole chunks load through a range-checked resource at per-thread byte
+    // Chunks load through a range-checked resource at per-thread byte
     // offsets fixed for the kernel (no 64-bit address arithmetic, no
     // branches: a column past n, or a piece past the chunk, sits out of
-    // range and reads zeros); b is below 6 MB here (n <= 192, k <= 7680).
+    // range and reads zeros; the resource checks each dword, so a 16-byte
+    // load that straddles the end of b keeps its dwords before the end); b
+    // is below 6 MB here (n <= 192, k <= 7680).
     const __amdgpu_buffer_rsrc_t rb =
         __builtin_amdgcn_make_buffer_rsrc((void*)p.b, (short)0, (int)((uint64_t)p.n * p.k * 4u), kBufWord3);
     constexpr uint32_t kOut = 0x80000000u;  // an offset past any b this kernel takes
@@ -2162,45 +2164,31 @@ __global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32
             }
         }
     }
+    // Every chunk, the partial last one and those past K included, issues
+    // the same loads, so that the wait before a staged chunk's LDS store
+    // counts only that chunk's loads (the compiler tracks the loads in
+    // flight across the loop exactly): [K, N] b past K lies past the end of
+    // b (zeros); token-major b past K reads the next column's values (or
+    // past the end: zeros), which the partial chunk replaces by zeros and
+    // the chunks past K never store.
     auto stage_load = [&](uint32_t kc, f32x4 (&v)[kStage]) {
-        if (kc + kM4K <= p.k) {
-#pragma unroll
-            for (int u = 0; u < kStage; ++u) {
-                if (TM) {
-                    v[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, boff[u] + 4u * kc, 0, 0));
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        v[u][r] = __builtin_bit_cast(
-                            float, __builtin_amdgcn_raw_buffer_load_b32(rb, boff[u] + 4u * (kc + r) * p.n, 0, 0));
-                }
-            }
-            return;
-        }
-        // the last, partial chunk: element by element, zeros past k
 #pragma unroll
         for (int u = 0; u < kStage; ++u) {
-            const int e = t + kThreads * u;
-            v[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (e < kM4Pieces) {
-                if (TM) {
-                    const uint32_t cl = n0 + (uint32_t)(e / (kM4K / 4)), k4 = kc + 4u * (uint32_t)(e % (kM4K / 4));
-                    if (cl < p.n) {
-                        if (k4 + 4 <= p.k) {
-                            v[u] = __builtin_bit_cast(f32x4, (u32x4)*reinterpret_cast<const u32x4_a4*>(p.b + (uint64_t)cl * p.bn + k4));
-                        } else {
+            if (TM) {
+                v[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, boff[u] + 4u * kc, 0, 0));
+            } else {
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) v[u][r] = k4 + r < p.k ? p.b[(uint64_t)cl * p.bn + k4 + r] : 0.0f;
-                        }
-                    }
-                } else {
-                    const uint32_t cl = n0 + (uint32_t)(e % kWave), k4 = kc + 4u * (uint32_t)(e / kWave);
-                    if (cl < p.n) {
+                for (int r = 0; r < 4; ++r)
+                    v[u][r] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(rb, boff[u] + 4u * (kc + r) * p.n, 0, 0));
+            }
+        }
+        if (TM && kc + kM4K > p.k) {
 #pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            v[u][r] = k4 + r < p.k ? p.b[(uint64_t)(k4 + r) * p.bk + (uint64_t)cl * p.bn] : 0.0f;
-                    }
-                }
+            for (int u = 0; u < kStage; ++u) {
+                const uint32_t k4 = kc + 4u * (uint32_t)((t + kThreads * u) % (kM4K / 4));
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[u][r] = k4 + r < p.k ? v[u][r] : 0.0f;
             }
         }
     };
@@ -2228,7 +2216,7 @@ __global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32
         stage_store(0, sv0);
         stage_load(kM4K, sv0);
         stage_store(1, sv0);
-        stage_load(2 * kM4K, sv0);  // past K: zeros
+        stage_load(2 * kM4K, sv0);  // stored by chunk 0 where chunk 2 exists
         stage_load(3 * kM4K, sv1);
     }
     __syncthreads();  // the table, the packed rows and the b of chunks 0 and 1
@@ -2238,53 +2226,68 @@ __global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32
     const uint32_t aoff = s_off + (4u * CH * wave + (uint32_t)(lane & 3)) * p.kp + (uint32_t)(lane >> 2);
     f32x4 tq[CH], tqn[CH];  // trits 0..3 of this lane's byte, per chain (this chunk, the next)
     float t4[CH], t4n[CH];  // trit 4
-    auto load_trits = [&](uint32_t kc, f32x4 (&q)[CH], float (&q4)[CH]) {
+    auto trit_bytes = [&](uint32_t kc, uint32_t (&v)[CH]) {
+#pragma unroll
+        for (int h = 0; h < CH; ++h) v[h] = abytes[aoff + 4u * h * p.kp + kc / 5u];
+    };
+    auto trit_table = [&](const uint32_t (&v)[CH], f32x4 (&q)[CH], float (&q4)[CH]) {
 #pragma unroll
         for (int h = 0; h < CH; ++h) {
-            const uint32_t v = abytes[aoff + 4u * h * p.kp + kc / 5u];
-            q[h] = *reinterpret_cast<const f32x4*>(tl + 8 * v);
-            q4[h] = tl[8 * v + 4];
+            q[h] = *reinterpret_cast<const f32x4*>(tl + 8 * v[h]);
+            q4[h] = tl[8 * v[h] + 4];
         }
     };
-    auto chunk_bad = [&](uint32_t buf) {
-        bool bad = false;
+    auto chunk_flags = [&](uint32_t buf, uint32_t (&f)[W]) {
 #pragma unroll
-        for (int w = 0; w < W; ++w) bad |= bbad[buf][w] != 0u;
-        return bad;
+        for (int w = 0; w < W; ++w) f[w] = bbad[buf][w];
+    };
+    auto any_flag = [&](const uint32_t (&f)[W]) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int w = 0; w < W; ++w) x |= f[w];
+        return x != 0u;
     };
     f32x4 bq[2][5];  // b entries of a burst (20 K columns)
     auto read_b = [&](f32x4 (&q)[5], uint32_t buf, int bi) {
 #pragma unroll
         for (int g = 0; g < 5; ++g) q[g] = bs[buf][lane][5 * bi + g];
     };
-    bool bad = false, badn = false;
+    bool bad = false;
     if (p.k > 0) {
-        load_trits(0, tq, t4);
+        uint32_t tb[CH], fl[W];
+        trit_bytes(0, tb);
+        trit_table(tb, tq, t4);
         read_b(bq[0], 0, 0);
-        bad = chunk_bad(0);
+        chunk_flags(0, fl);
+        bad = any_flag(fl);
     }
-    // one chunk: its bursts, chunk c + 2's b into its buffer (loaded two
-    // chunks ago into svc), chunk c + 4's loads into svc, chunk c + 1's
-    // trits and first b entries, and a barrier over LDS only (the loads in
-    // flight are this thread's own registers)
+    // One chunk: its four bursts and, spread over them so that no LDS wait
+    // stands before a burst's MFMAs, chunk c + 1's trit bytes (burst 0),
+    // its trits from the table and its Inf/NaN flags (burst 2), chunk c + 2's
+    // b into its buffer (loaded two chunks ago into svc; that buffer was last
+    // read in chunk c - 1, before the last barrier) and chunk c + 1's first
+    // b entries (burst 3); then chunk c + 4's loads into svc and a barrier
+    // over LDS only (the loads in flight are this thread's own registers).
+    // On the last chunk the next-chunk reads re-read this chunk's (valid
+    // addresses, results unused), so that no branch joins before a burst.
     auto chunk = [&](uint32_t kc, uint32_t buf, f32x4 (&svc)[kStage]) {
         const uint32_t nbuf = buf == 2u ? 0u : buf + 1u;
-        const bool more = kc + kM4K < p.k;
-        // chunk c + 1's trits, first b entries and flag: its buffer was
-        // written before the last barrier, so they are read during the last
-        // burst of chunk c
-        auto read_next = [&]() {
-            if (more) {
-                load_trits(kc + kM4K, tqn, t4n);
-                read_b(bq[0], nbuf, 0);
-                badn = chunk_bad(nbuf);
-            }
-        };
+        const uint32_t kn = kc + kM4K < p.k ? kc + kM4K : kc;
+        const bool store = kc + 2 * kM4K < p.k;
+        uint32_t tb[CH], fl[W];
         if (live && !bad) {
 #pragma unroll
             for (int bi = 0; bi < 4; ++bi) {
                 if (bi < 3) read_b(bq[(bi + 1) & 1], buf, bi + 1);
-                else read_next();
+                if (bi == 0) trit_bytes(kn, tb);
+                if (bi == 2) {
+                    trit_table(tb, tqn, t4n);
+                    chunk_flags(nbuf, fl);
+                }
+                if (bi == 3) {
+                    if (store) stage_store(buf == 0u ? 2u : buf - 1u, svc);  // buffer (c + 2) % 3
+                    read_b(bq[0], nbuf, 0);
+                }
                 const f32x4(&q)[5] = bq[bi & 1];
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -2320,18 +2323,19 @@ __global__ __launch_bounds__(8 / CH * kWave) void ternary_f32_mf4_kernel(TernF32
                 }
             }
           }
-          read_next();
+          trit_bytes(kn, tb);
+          trit_table(tb, tqn, t4n);
+          chunk_flags(nbuf, fl);
+          if (store) stage_store(buf == 0u ? 2u : buf - 1u, svc);
+          read_b(bq[0], nbuf, 0);
         }
-        if (kc + 2 * kM4K < p.k) {
-            stage_store(buf == 0u ? 2u : buf - 1u, svc);  // buffer (c + 2) % 3
-            stage_load(kc + 4 * kM4K, svc);
-        }
+        stage_load(kc + 4 * kM4K, svc);
 #pragma unroll
         for (int h = 0; h < CH; ++h) {
             tq[h] = tqn[h];
             t4[h] = t4n[h];
         }
-        bad = badn;
+        bad = any_flag(fl);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
@@ -2393,14 +2397,23 @@ static bool f32_use_mf4(uint64_t m, uint64_t n, uint64_t k, uint64_t kp) {
     return (m + 3) / 4 * ((n + kWave - 1) / kWave) >= 1024;
 }
 
-template <bool TM, int CH>
-static int launch_f32_mf4(uint64_t m, uint64_t n, hipStream_t s, const TernF32Args& p) {
-    const uint64_t bx = (m + kM4Rows - 1) / kM4Rows, by = (n + kWave - 1) / kWave;
+template <bool TM, int CH, int W>
+static int launch_f32_mf4_w(uint64_t m, uint64_t n, hipStream_t s, const TernF32Args& p) {
+    const uint64_t bx = (m + 4 * CH * W - 1) / (4 * CH * W), by = (n + kWave - 1) / kWave;
     if (bx > 0x7fffffffull || by > 65535) return KORE_HIP_ERR_OVERFLOW;
     const uint32_t lds = f32_mf4_slice(p.kp);
     if (lds == 0) return KORE_HIP_ERR_BAD_DIM;
-    hipLaunchKernelGGL((ternary_f32_mf4_kernel<TM, CH>), dim3((uint32_t)bx, (uint32_t)by), dim3(8 / CH * kWave), lds, s, p);
+    hipLaunchKernelGGL((ternary_f32_mf4_kernel<TM, CH, W>), dim3((uint32_t)bx, (uint32_t)by), dim3(W * kWave), lds, s, p);
     return launch_status();
+}
+
+template <bool TM>
+static int launch_f32_mf4(uint64_t m, uint64_t n, hipStream_t s, const TernF32Args& p) {
+#ifndef KORE_MF4_W
+    return launch_f32_mf4_w<TM, 1, 8>(m, n, s, p);
+#else
+    return launch_f32_mf4_w<TM, 1, KORE_MF4_W>(m, n, s, p);
+#endif
 }
 
 // One to four columns (decode steps), any row alignment.  The
@@ -3437,7 +3450,7 @@ static int ternary_f32_run(const uint8_t* a_packed, const float* a_scales, const
             q.c += trans ? r0 : r0 * n;  // c[n, m]: columns r0 .. of every row, row stride m
             if (bias) q.bias += r0;
             if (f32_use_mf4(q.m, n, k, kp)) {
-                const int st = tm ? launch_f32_mf4<true, 1>(q.m, n, s, q) : launch_f32_mf4<false, 1>(q.m, n, s, q);
+                const int st = tm ? launch_f32_mf4<true>(q.m, n, s, q) : launch_f32_mf4<false>(q.m, n, s, q);
                 if (st != KORE_HIP_OK) return st;
                 continue;
             }
