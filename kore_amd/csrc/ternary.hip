@@ -2065,6 +2065,12 @@ constexpr int kM4Pitch4 = kM4K / 4 + 1;  // 16-byte entries per staged column
 constexpr int kM4Pieces = kWave * kM4K / 4;  // 16-byte pieces of b per chunk
 constexpr uint32_t kM4MaxSlice = 48 * 1024;  // bytes of packed rows a workgroup holds in LDS
 
+// 16 bytes per lane from a range-checked resource straight into LDS (lane
+// L's at dst + 16 L; dst wave-uniform).
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, lds_vptr dst, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
+}
+
 // One step of a 4 x 4 x 1 chain whose trit operand is block j's (CBSZ = 4,
 // ABID = j: one block's four lanes broadcast to all sixteen).
 __device__ __forceinline__ f32x4 mf4_step(float a, float b, f32x4 c, int j) {
@@ -2095,7 +2101,6 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
     constexpr int kStage = (kM4Pieces + kThreads - 1) / kThreads;
     __shared__ __attribute__((aligned(16))) float tl[256 * 8];
     __shared__ f32x4 bs[3][kWave][kM4Pitch4];
-    __shared__ uint32_t bbad[3][W];
     extern __shared__ uint32_t araw[];  // the workgroup's packed rows, from a dword boundary
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
@@ -2135,89 +2140,95 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
         }
         araw[i] = v;
     }
-    // b staging, piece e of a chunk = one 16-byte entry of the LDS tile:
-    // token-major b, column e / 20 and K columns 4 (e % 20) .. + 3 (one
-    // 16-byte load along the column's row); [K, N] b, column e % 64 and K
-    // columns 4 (e / 64) .. + 3 (four loads, each a wave-wide 256-byte piece
-    // of a row of b)
-    // Chunks load through a range-checked resource at per-thread byte
-    // offsets fixed for the kernel (no 64-bit address arithmetic, no
-    // branches: a column past n, or a piece past the chunk, sits out of
-    // range and reads zeros; the resource checks each dword, so a 16-byte
-    // load that straddles the end of b keeps its dwords before the end); b
-    // is below 6 MB here (n <= 192, k <= 7680).
+    // b staging.  b is below 6 MB here (n <= 192, k <= 7680) and loads
+    // through a range-checked resource at 32-bit byte offsets fixed for the
+    // kernel: a column past n sits past the end of b and reads zeros, and
+    // the resource checks each dword.
+    //  - token-major b: the LDS tile is [column][21 entries of 16 bytes]
+    //    (20 used), i.e. 21 rows of 64 16-byte slots per chunk, and slot s
+    //    holds column s / 21, K columns 4 (s % 21) .. + 3 of the chunk (the
+    //    unused entry reloads entry 19).  Wave w loads rows w, w + W, w + 2W
+    //    straight into LDS (buffer loads with the LDS bit: no registers, no
+    //    LDS stores), issued two chunks ahead; the wait for them is an
+    //    explicit vmcnt before the chunk's barrier.
+    //  - [K, N] b: piece e = column e % 64, K columns 4 (e / 64) .. + 3 (four
+    //    loads, each a wave-wide 256-byte piece of a row of b), through
+    //    registers into the same tile, loaded two chunks ahead.
+    // Past K: [K, N] b lies past the end of b (zeros); token-major b reads
+    // the next column's values, whose trits are zero (masked for the partial
+    // last chunk).  Every chunk issues the same loads, chunks past K
+    // included, so the waits count only the loads they are for.
     const __amdgpu_buffer_rsrc_t rb =
         __builtin_amdgcn_make_buffer_rsrc((void*)p.b, (short)0, (int)((uint64_t)p.n * p.k * 4u), kBufWord3);
     constexpr uint32_t kOut = 0x80000000u;  // an offset past any b this kernel takes
-    uint32_t boff[kStage];
+    constexpr int kTmRows = kM4Pitch4;      // LDS-DMA rows of 64 slots per chunk
+    constexpr int kDmaMax = (kTmRows + W - 1) / W;
+    const int ndma = (kTmRows - (int)wave + W - 1) / W;  // this wave's rows (wave-uniform)
+    uint32_t boff[TM ? kDmaMax : kStage];
+    if constexpr (TM) {
 #pragma unroll
-    for (int u = 0; u < kStage; ++u) {
-        const int e = t + kThreads * u;
-        boff[u] = kOut;
-        if (e < kM4Pieces) {
-            if (TM) {
-                const uint32_t cl = n0 + (uint32_t)(e / (kM4K / 4)), q4 = 4u * (uint32_t)(e % (kM4K / 4));
-                if (cl < p.n) boff[u] = (cl * p.k + q4) * 4u;
-            } else {
-                const uint32_t cl = n0 + (uint32_t)(e % kWave), q4 = 4u * (uint32_t)(e / kWave);
-                if (cl < p.n) boff[u] = (q4 * p.n + cl) * 4u;
-            }
+        for (int u = 0; u < kDmaMax; ++u) {
+            const uint32_t sl = (uint32_t)(kWave * ((int)wave + W * u) + lane);
+            const uint32_t cl = n0 + sl / (uint32_t)kM4Pitch4, j = sl % (uint32_t)kM4Pitch4;
+            boff[u] = cl < p.n ? (cl * p.k + 4u * (j < 20u ? j : 19u)) * 4u : kOut;
         }
-    }
-    // Every chunk, the partial last one and those past K included, issues
-    // the same loads, so that the wait before a staged chunk's LDS store
-    // counts only that chunk's loads (the compiler tracks the loads in
-    // flight across the loop exactly): [K, N] b past K lies past the end of
-    // b (zeros); token-major b past K reads the next column's values (or
-    // past the end: zeros), which the partial chunk replaces by zeros and
-    // the chunks past K never store.
-    auto stage_load = [&](uint32_t kc, f32x4 (&v)[kStage]) {
-#pragma unroll
-        for (int u = 0; u < kStage; ++u) {
-            if (TM) {
-                v[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, boff[u] + 4u * kc, 0, 0));
-            } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    v[u][r] = __builtin_bit_cast(
-                        float, __builtin_amdgcn_raw_buffer_load_b32(rb, boff[u] + 4u * (kc + r) * p.n, 0, 0));
-            }
-        }
-        if (TM && kc + kM4K > p.k) {
-#pragma unroll
-            for (int u = 0; u < kStage; ++u) {
-                const uint32_t k4 = kc + 4u * (uint32_t)((t + kThreads * u) % (kM4K / 4));
-#pragma unroll
-                for (int r = 0; r < 4; ++r) v[u][r] = k4 + r < p.k ? v[u][r] : 0.0f;
-            }
-        }
-    };
-    auto stage_store = [&](uint32_t buf, const f32x4 (&v)[kStage]) {
-        bool bad = false;
+    } else {
 #pragma unroll
         for (int u = 0; u < kStage; ++u) {
             const int e = t + kThreads * u;
-            if (e < kM4Pieces) {
-                if (TM) bs[buf][e / (kM4K / 4)][e % (kM4K / 4)] = v[u];
-                else bs[buf][e % kWave][e / kWave] = v[u];
+            const uint32_t cl = n0 + (uint32_t)(e % kWave), q4 = 4u * (uint32_t)(e / kWave);
+            boff[u] = e < kM4Pieces && cl < p.n ? (q4 * p.n + cl) * 4u : kOut;
+        }
+    }
+    auto dma_chunk = [&](uint32_t kc, uint32_t buf) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) bad |= !__builtin_isfinite(v[u][r]);
+        for (int u = 0; u < kDmaMax; ++u) {
+            if (u < kDmaMax - 1 || u < ndma) {
+                lds_load16(rb, (lds_vptr)((char*)&bs[buf][0][0] + 1024 * ((int)wave + W * u)), boff[u], 4u * kc);
             }
         }
-        const uint64_t bl = __ballot(bad);
-        if (lane == 0) bbad[buf][wave] = bl != 0 ? 1u : 0u;
+    };
+    // the wait for the LDS loads of all but the last `pending` chunks issued
+    auto dma_wait = [&](bool pending) {
+        if (!pending) {
+            __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+        } else if (ndma == kDmaMax) {
+            __builtin_amdgcn_s_waitcnt(0xF70 | kDmaMax);
+        } else {
+            __builtin_amdgcn_s_waitcnt(0xF70 | (kDmaMax - 1));
+        }
+    };
+    auto stage_load = [&](uint32_t kc, f32x4 (&v)[kStage]) {
+#pragma unroll
+        for (int u = 0; u < kStage; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                v[u][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, boff[u] + 4u * (kc + r) * p.n, 0, 0));
+    };
+    auto stage_store = [&](uint32_t buf, const f32x4 (&v)[kStage]) {
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int e = t + kThreads * u;
+            if (e < kM4Pieces) bs[buf][e % kWave][e / kWave] = v[u];
+        }
     };
     f32x4 acc[CH];
 #pragma unroll
     for (int h = 0; h < CH; ++h) acc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    f32x4 sv0[kStage], sv1[kStage];
+    f32x4 sv0[TM ? 1 : kStage], sv1[TM ? 1 : kStage];
     if (p.k > 0) {
-        stage_load(0, sv0);
-        stage_store(0, sv0);
-        stage_load(kM4K, sv0);
-        stage_store(1, sv0);
-        stage_load(2 * kM4K, sv0);  // stored by chunk 0 where chunk 2 exists
-        stage_load(3 * kM4K, sv1);
+        if constexpr (TM) {
+            dma_chunk(0, 0);
+            dma_chunk(kM4K, 1);
+            dma_wait(false);
+        } else {
+            stage_load(0, sv0);
+            stage_store(0, sv0);
+            stage_load(kM4K, sv0);
+            stage_store(1, sv0);
+            stage_load(2 * kM4K, sv0);  // stored by chunk 0 where chunk 2 exists
+            stage_load(3 * kM4K, sv1);
+        }
     }
     __syncthreads();  // the table, the packed rows and the b of chunks 0 and 1
     const bool live = m0 < p.m;
@@ -2230,62 +2241,104 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
 #pragma unroll
         for (int h = 0; h < CH; ++h) v[h] = abytes[aoff + 4u * h * p.kp + kc / 5u];
     };
-    auto trit_table = [&](const uint32_t (&v)[CH], f32x4 (&q)[CH], float (&q4)[CH]) {
+    // the trits of chunk kc (zero past K: the packed matrix's last byte of a
+    // row may hold any digits there, and token-major b is not zero there)
+    auto trit_table = [&](uint32_t kc, const uint32_t (&v)[CH], f32x4 (&q)[CH], float (&q4)[CH]) {
 #pragma unroll
         for (int h = 0; h < CH; ++h) {
             q[h] = *reinterpret_cast<const f32x4*>(tl + 8 * v[h]);
             q4[h] = tl[8 * v[h] + 4];
         }
-    };
-    auto chunk_flags = [&](uint32_t buf, uint32_t (&f)[W]) {
+        if (kc + kM4K > p.k) {
+            const uint32_t k0 = kc + 5u * (uint32_t)(lane >> 2);
 #pragma unroll
-        for (int w = 0; w < W; ++w) f[w] = bbad[buf][w];
-    };
-    auto any_flag = [&](const uint32_t (&f)[W]) {
-        uint32_t x = 0;
+            for (int h = 0; h < CH; ++h) {
 #pragma unroll
-        for (int w = 0; w < W; ++w) x |= f[w];
-        return x != 0u;
+                for (int d = 0; d < 4; ++d) q[h][d] = k0 + d < p.k ? q[h][d] : 0.0f;
+                q4[h] = k0 + 4 < p.k ? q4[h] : 0.0f;
+            }
+        }
+    };
+    auto nonfinite = [&]() {
+        bool nf = false;
+#pragma unroll
+        for (int h = 0; h < CH; ++h)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) nf |= !__builtin_isfinite(acc[h][r]);
+        return __ballot(nf) != 0;
     };
     f32x4 bq[2][5];  // b entries of a burst (20 K columns)
     auto read_b = [&](f32x4 (&q)[5], uint32_t buf, int bi) {
 #pragma unroll
         for (int g = 0; g < 5; ++g) q[g] = bs[buf][lane][5 * bi + g];
     };
-    bool bad = false;
+    // The reference's step over chunk buf, element by element: output v of
+    // lane L is row v of chain h, whose trit d of byte j lane 4 j + v holds.
+    auto slow_chunk = [&](uint32_t buf) {
+        for (int kk = 0; kk < kM4K; ++kk) {
+            const int j = kk / 5, d = kk % 5;
+            const float bk = bs[buf][lane][kk >> 2][kk & 3];
+#pragma unroll
+            for (int h = 0; h < CH; ++h) {
+                float tv = t4[h];
+#pragma unroll
+                for (int dd = 0; dd < 4; ++dd)
+                    if (dd == d) tv = tq[h][dd];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float te = __shfl(tv, 4 * j + r, kWave);
+                    if (te != 0.0f) acc[h][r] = __builtin_fmaf(te, bk, acc[h][r]);
+                }
+            }
+        }
+    };
+    // Inf and NaN: the matrix-core chain adds the zero-trit terms too, which
+    // leave a finite sum unchanged (fma(0, b, s) = s for finite b; s is
+    // never -0) but make it NaN for an infinite or NaN b.  So a chunk after
+    // which some sum of the wave is not finite is folded again from the saved
+    // sums, element by element with zero trits skipped (the reference's step;
+    // a sum that overflowed gives the same result either way), and a wave
+    // whose sums are no longer finite stays on that path.
+    bool stuck = false;
     if (p.k > 0) {
-        uint32_t tb[CH], fl[W];
+        uint32_t tb[CH];
         trit_bytes(0, tb);
-        trit_table(tb, tq, t4);
+        trit_table(0, tb, tq, t4);
         read_b(bq[0], 0, 0);
-        chunk_flags(0, fl);
-        bad = any_flag(fl);
     }
     // One chunk: its four bursts and, spread over them so that no LDS wait
-    // stands before a burst's MFMAs, chunk c + 1's trit bytes (burst 0),
-    // its trits from the table and its Inf/NaN flags (burst 2), chunk c + 2's
-    // b into its buffer (loaded two chunks ago into svc; that buffer was last
-    // read in chunk c - 1, before the last barrier) and chunk c + 1's first
-    // b entries (burst 3); then chunk c + 4's loads into svc and a barrier
-    // over LDS only (the loads in flight are this thread's own registers).
-    // On the last chunk the next-chunk reads re-read this chunk's (valid
-    // addresses, results unused), so that no branch joins before a burst.
-    auto chunk = [&](uint32_t kc, uint32_t buf, f32x4 (&svc)[kStage]) {
-        const uint32_t nbuf = buf == 2u ? 0u : buf + 1u;
+    // stands before a burst's MFMAs, chunk c + 2's b (token-major: its LDS
+    // loads, burst 0; [K, N]: its LDS stores from the registers loaded two
+    // chunks ago, burst 3; the buffer was last read in chunk c - 1, before
+    // the last barrier), chunk c + 1's trit bytes (burst 0), its trits from
+    // the table (burst 2) and its first b entries (burst 3); then the
+    // Inf/NaN check, chunk c + 4's [K, N] loads, the wait for chunk c + 1's
+    // token-major loads and a barrier over LDS only.  On the last chunk the
+    // next-chunk reads re-read this chunk's (valid addresses, results
+    // unused), so that no branch joins before a burst.
+    auto chunk = [&](uint32_t kc, uint32_t buf, f32x4 (&svc)[TM ? 1 : kStage]) {
+        const uint32_t nbuf = buf == 2u ? 0u : buf + 1u, sbuf = buf == 0u ? 2u : buf - 1u;
         const uint32_t kn = kc + kM4K < p.k ? kc + kM4K : kc;
         const bool store = kc + 2 * kM4K < p.k;
-        uint32_t tb[CH], fl[W];
-        if (live && !bad) {
+        uint32_t tb[CH];
+        if (live && !stuck) {
+            f32x4 saved[CH];
+#pragma unroll
+            for (int h = 0; h < CH; ++h) saved[h] = acc[h];
 #pragma unroll
             for (int bi = 0; bi < 4; ++bi) {
                 if (bi < 3) read_b(bq[(bi + 1) & 1], buf, bi + 1);
-                if (bi == 0) trit_bytes(kn, tb);
-                if (bi == 2) {
-                    trit_table(tb, tqn, t4n);
-                    chunk_flags(nbuf, fl);
+                if (bi == 0) {
+                    if constexpr (TM) {
+                        if (store) dma_chunk(kc + 2 * kM4K, sbuf);
+                    }
+                    trit_bytes(kn, tb);
                 }
+                if (bi == 2) trit_table(kn, tb, tqn, t4n);
                 if (bi == 3) {
-                    if (store) stage_store(buf == 0u ? 2u : buf - 1u, svc);  // buffer (c + 2) % 3
+                    if constexpr (!TM) {
+                        if (store) stage_store(sbuf, svc);
+                    }
                     read_b(bq[0], nbuf, 0);
                 }
                 const f32x4(&q)[5] = bq[bi & 1];
@@ -2302,43 +2355,45 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-        } else {
-          if (live) {
-            // The reference's step, element by element: output v of lane L
-            // is row v of chain h, whose trit d of byte j lane 4 j + v holds.
-            for (int kk = 0; kk < kM4K; ++kk) {
-                const int j = kk / 5, d = kk % 5;
-                const float bk = bs[buf][lane][kk >> 2][kk & 3];
+            if (nonfinite()) {
 #pragma unroll
-                for (int h = 0; h < CH; ++h) {
-                    float tv = t4[h];
-#pragma unroll
-                    for (int dd = 0; dd < 4; ++dd)
-                        if (dd == d) tv = tq[h][dd];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float te = __shfl(tv, 4 * j + r, kWave);
-                        if (te != 0.0f) acc[h][r] = __builtin_fmaf(te, bk, acc[h][r]);
-                    }
-                }
+                for (int h = 0; h < CH; ++h) acc[h] = saved[h];
+                slow_chunk(buf);
+                stuck = nonfinite();
             }
-          }
-          trit_bytes(kn, tb);
-          trit_table(tb, tqn, t4n);
-          chunk_flags(nbuf, fl);
-          if (store) stage_store(buf == 0u ? 2u : buf - 1u, svc);
-          read_b(bq[0], nbuf, 0);
+        } else {
+            if (live) {
+                slow_chunk(buf);
+                stuck = nonfinite();
+            }
+            if constexpr (TM) {
+                if (store) dma_chunk(kc + 2 * kM4K, sbuf);
+            } else {
+                if (store) stage_store(sbuf, svc);
+            }
+            trit_bytes(kn, tb);
+            trit_table(kn, tb, tqn, t4n);
+            read_b(bq[0], nbuf, 0);
         }
-        stage_load(kc + 4 * kM4K, svc);
+        if constexpr (!TM) stage_load(kc + 4 * kM4K, svc);
 #pragma unroll
         for (int h = 0; h < CH; ++h) {
             tq[h] = tqn[h];
             t4[h] = t4n[h];
         }
-        bad = any_flag(fl);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        if constexpr (TM) {
+            // no release fence: it would wait for the LDS loads still in
+            // flight for chunk c + 2; this wave's reads of buffer c have
+            // all been consumed, and no wave writes LDS but by those loads
+            __builtin_amdgcn_sched_barrier(0);
+            dma_wait(store);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        }
     };
     uint32_t buf = 0;
     for (uint32_t kc = 0; kc < p.k; kc += 2 * kM4K) {
@@ -2409,11 +2464,7 @@ static int launch_f32_mf4_w(uint64_t m, uint64_t n, hipStream_t s, const TernF32
 
 template <bool TM>
 static int launch_f32_mf4(uint64_t m, uint64_t n, hipStream_t s, const TernF32Args& p) {
-#ifndef KORE_MF4_W
     return launch_f32_mf4_w<TM, 1, 8>(m, n, s, p);
-#else
-    return launch_f32_mf4_w<TM, 1, KORE_MF4_W>(m, n, s, p);
-#endif
 }
 
 // One to four columns (decode steps), any row alignment.  The
