@@ -2100,7 +2100,8 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
     constexpr int kThreads = W * kWave;
     constexpr int kStage = (kM4Pieces + kThreads - 1) / kThreads;
     __shared__ __attribute__((aligned(16))) float tl[256 * 8];
-    __shared__ f32x4 bs[3][kWave][kM4Pitch4];
+    constexpr uint32_t kBufs = TM ? 4u : 3u;  // b tiles in LDS
+    __shared__ f32x4 bs[kBufs][kWave][kM4Pitch4];
     extern __shared__ uint32_t araw[];  // the workgroup's packed rows, from a dword boundary
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
@@ -2149,11 +2150,17 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
     //    holds column s / 21, K columns 4 (s % 21) .. + 3 of the chunk (the
     //    unused entry reloads entry 19).  Wave w loads rows w, w + W, w + 2W
     //    straight into LDS (buffer loads with the LDS bit: no registers, no
-    //    LDS stores), issued two chunks ahead; the wait for them is an
-    //    explicit vmcnt before the chunk's barrier.
+    //    LDS stores).  Four tiles: chunk c + 3's loads are issued in chunk c
+    //    (into the tile chunk c - 1 used) and waited for, by an explicit
+    //    vmcnt, before the barrier that ends chunk c + 1, so that they have
+    //    landed for every wave when chunk c + 1's last burst reads chunk
+    //    c + 2's first b entries.
     //  - [K, N] b: piece e = column e % 64, K columns 4 (e / 64) .. + 3 (four
     //    loads, each a wave-wide 256-byte piece of a row of b), through
-    //    registers into the same tile, loaded two chunks ahead.
+    //    registers into the same tile layout, loaded four chunks ahead and
+    //    stored into LDS two chunks ahead (three tiles).  (Loading [K, N] b
+    //    straight into LDS needs a [K][column] tile, read as two
+    //    ds_read2st64_b32 per four K columns: measured 5% slower.)
     // Past K: [K, N] b lies past the end of b (zeros); token-major b reads
     // the next column's values, whose trits are zero (masked for the partial
     // last chunk).  Every chunk issues the same loads, chunks past K
@@ -2220,7 +2227,8 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
         if constexpr (TM) {
             dma_chunk(0, 0);
             dma_chunk(kM4K, 1);
-            dma_wait(false);
+            dma_chunk(2 * kM4K, 2);
+            dma_wait(true);  // chunks 0 and 1 (chunk 2's: by the end of chunk 0)
         } else {
             stage_load(0, sv0);
             stage_store(0, sv0);
@@ -2230,7 +2238,15 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
             stage_load(3 * kM4K, sv1);
         }
     }
-    __syncthreads();  // the table, the packed rows and the b of chunks 0 and 1
+    // the table, the packed rows and the b of chunks 0 and 1 (token-major b:
+    // no release fence, which would wait for chunk 2's loads too; the
+    // table and the packed rows are LDS stores, waited for by lgkmcnt(0))
+    if constexpr (TM) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+    } else {
+        __syncthreads();
+    }
     const bool live = m0 < p.m;
     // lane 4 j + r: byte j of the chunk of chain h's row r
     const uint8_t* abytes = reinterpret_cast<const uint8_t*>(araw);
@@ -2307,19 +2323,20 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
         read_b(bq[0], 0, 0);
     }
     // One chunk: its four bursts and, spread over them so that no LDS wait
-    // stands before a burst's MFMAs, chunk c + 2's b (token-major: its LDS
-    // loads, burst 0; [K, N]: its LDS stores from the registers loaded two
-    // chunks ago, burst 3; the buffer was last read in chunk c - 1, before
-    // the last barrier), chunk c + 1's trit bytes (burst 0), its trits from
-    // the table (burst 2) and its first b entries (burst 3); then the
-    // Inf/NaN check, chunk c + 4's [K, N] loads, the wait for chunk c + 1's
-    // token-major loads and a barrier over LDS only.  On the last chunk the
+    // stands before a burst's MFMAs, the staging of a later chunk into the
+    // tile chunk c - 1 used (last read before the last barrier; token-major:
+    // chunk c + 3's LDS loads, burst 0; [K, N]: chunk c + 2's LDS stores from
+    // the registers loaded two chunks ago, burst 3), chunk c + 1's trit bytes
+    // (burst 0), its trits from the table (burst 2) and its first b entries
+    // (burst 3); then the Inf/NaN check, chunk c + 4's [K, N] loads, the
+    // wait for chunk c + 2's token-major loads and a barrier over LDS only.  On the last chunk the
     // next-chunk reads re-read this chunk's (valid addresses, results
     // unused), so that no branch joins before a burst.
     auto chunk = [&](uint32_t kc, uint32_t buf, f32x4 (&svc)[TM ? 1 : kStage]) {
-        const uint32_t nbuf = buf == 2u ? 0u : buf + 1u, sbuf = buf == 0u ? 2u : buf - 1u;
+        const uint32_t nbuf = buf + 1u == kBufs ? 0u : buf + 1u, sbuf = buf == 0u ? kBufs - 1u : buf - 1u;
+        const uint32_t kahead = TM ? 3u : 2u;  // the chunk staged into sbuf
         const uint32_t kn = kc + kM4K < p.k ? kc + kM4K : kc;
-        const bool store = kc + 2 * kM4K < p.k;
+        const bool store = kc + kahead * kM4K < p.k;
         uint32_t tb[CH];
         if (live && !stuck) {
             f32x4 saved[CH];
@@ -2330,7 +2347,7 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
                 if (bi < 3) read_b(bq[(bi + 1) & 1], buf, bi + 1);
                 if (bi == 0) {
                     if constexpr (TM) {
-                        if (store) dma_chunk(kc + 2 * kM4K, sbuf);
+                        if (store) dma_chunk(kc + kahead * kM4K, sbuf);
                     }
                     trit_bytes(kn, tb);
                 }
@@ -2367,7 +2384,7 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
                 stuck = nonfinite();
             }
             if constexpr (TM) {
-                if (store) dma_chunk(kc + 2 * kM4K, sbuf);
+                if (store) dma_chunk(kc + kahead * kM4K, sbuf);
             } else {
                 if (store) stage_store(sbuf, svc);
             }
@@ -2383,7 +2400,7 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
         }
         if constexpr (TM) {
             // no release fence: it would wait for the LDS loads still in
-            // flight for chunk c + 2; this wave's reads of buffer c have
+            // flight for chunk c + 3; this wave's reads of buffer c have
             // all been consumed, and no wave writes LDS but by those loads
             __builtin_amdgcn_sched_barrier(0);
             dma_wait(store);
@@ -2398,10 +2415,10 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
     uint32_t buf = 0;
     for (uint32_t kc = 0; kc < p.k; kc += 2 * kM4K) {
         chunk(kc, buf, sv0);
-        buf = buf == 2u ? 0u : buf + 1u;
+        buf = buf + 1u == kBufs ? 0u : buf + 1u;
         if (kc + kM4K >= p.k) break;
         chunk(kc + kM4K, buf, sv1);
-        buf = buf == 2u ? 0u : buf + 1u;
+        buf = buf + 1u == kBufs ? 0u : buf + 1u;
     }
     if (!live || col >= p.n) return;
 #pragma unroll
