@@ -596,9 +596,11 @@ class TernaryF32(Workload):
         mfma = ((m + 63) // 64) * ((n + 15) // 16) >= 768
         # the library's dispatch: the 4 x 4 x 1 matrix-core kernel where the
         # 16 x 16 one does not run: 41-192 tokens, k >= 2560 (up to 7675), at
-        # least 1024 waves of 4 rows x 64 tokens
+        # least 640 waves of 4 rows x 64 tokens for the layer's token-major
+        # input, 1024 for [K, N] b
         slice_ok = ((3 + 32 * ((k + 4) // 5) + 3) // 4 + 4) * 4 <= 48 * 1024  # the workgroup's packed rows fit its LDS
-        mf4 = not mfma and slice_ok and k >= 2560 and 41 <= n <= 192 and (m + 3) // 4 * ((n + 63) // 64) >= 1024
+        mf4 = (not mfma and slice_ok and k >= 2560 and 41 <= n <= 192
+               and (m + 3) // 4 * ((n + 63) // 64) >= (640 if layer else 1024))
         self.bound = "mfma_f32" if mfma or mf4 else "valu"
         self.kernel = ("ternary_f32_mfma_kernel" if mfma else "ternary_f32_mf4_kernel" if mf4 else
                        "ternary_f32_pipe_kernel" if n <= 4 else "ternary_f32_rows_kernel")

@@ -2447,26 +2447,28 @@ static uint32_t f32_mf4_slice(uint64_t kp) {
 
 // Where the 4 x 4 kernel runs: 41 to 192 columns, K from 2560 (its fixed
 // costs -- the packed-row copy, the staging prologue -- spread over enough
-// chunks), at least 1024 waves of 4 rows x 64 columns, and no 16 x 16
-// launch for the shape; both layouts of b.  Measured (HIP events; the
-// row-broadcast kernel in the same run), token-major b (the layer) and
-// [K, N] b (the plain ternary_matmul):
-//   6912 x 64 x 2560: 46.1 and 48.0 us against 70 and 66 (1728 waves);
-//   6912 x 96 x 2560: 89.9 and 94.0 against 107 and 102;
-//   2560 x {96, 128, 192} x 6912: 118-123 and 124-128 against 143-195
-//   (1280-1920 waves);
-//   2560 x 64 x 6912 (640 waves): 118 and 124 against 116 and 103-109;
-//   2048 x 64 x 6912 (512 waves): 118 (token-major) against 78: below 1024
-//   waves a SIMD runs one wave, whose chain time does not shrink with m;
-//   2048 x 64 x 2048 (512 waves): 39.7 against 26.0 ([K, N]);
+// chunks), no 16 x 16 launch for the shape, and at least 640 waves of 4
+// rows x 64 columns with token-major b (the layer), 1024 with [K, N] b (the
+// plain ternary_matmul).  Up to 1024 waves a SIMD runs one wave, whose
+// chain time does not shrink with m, so below that the row-broadcast
+// kernel, whose time does, wins at some m.  Measured (HIP events; the
+// row-broadcast kernel on the same box; layer, then [K, N]):
+//   6912 x 64 x 2560 (1728 waves): 42.2 and 46.0 us against 70 and 66;
+//   6912 x 96 x 2560: 81 and 90 against 107 and 102;
+//   2560 x {96, 192} x 6912 (1280-1920 waves): 105-110 and 116-125 against
+//   143-195;
+//   2560 x 64 x 6912 (640 waves): 104 and 114 against 116 and 104;
+//   3500 x 64 x 4096 (875 waves): 64 and 71 against 67 and 71;
+//   3000 x 64 x 2560 (750 waves): 40.5 and 45.1 against 45.4 and 42.1;
+//   2048 x 64 x 6912 (512 waves): 104 and 114 against 80 and 80;
 //   24 and 32 columns: 47-49 against 38-39 us at 6912 x 2560 (the 64-column
 //   waves half empty).
-// Two chains per wave (8 rows, each b read shared by both) measured 10-20%
-// slower: one wave per SIMD then has nothing to hide its own LDS waits and
-// barriers behind.
-static bool f32_use_mf4(uint64_t m, uint64_t n, uint64_t k, uint64_t kp) {
+// Two chains per wave (8 rows, each b read shared by both; 864 waves at
+// 6912 x 64) measured 5% slower, and workgroups of 7 waves (247 instead of
+// 216 workgroups at 6912 rows, one per CU) 6% slower.
+static bool f32_use_mf4(uint64_t m, uint64_t n, uint64_t k, uint64_t kp, bool tm) {
     if (n < 41 || n > 192 || k < 2560 || f32_use_mfma(m, n, k) || f32_mf4_slice(kp) == 0) return false;
-    return (m + 3) / 4 * ((n + kWave - 1) / kWave) >= 1024;
+    return (m + 3) / 4 * ((n + kWave - 1) / kWave) >= (tm ? 640u : 1024u);
 }
 
 template <bool TM, int CH, int W>
@@ -3517,7 +3519,7 @@ static int ternary_f32_run(const uint8_t* a_packed, const float* a_scales, const
             q.m = (uint32_t)std::min<uint64_t>(span, m - r0);
             q.c += trans ? r0 : r0 * n;  // c[n, m]: columns r0 .. of every row, row stride m
             if (bias) q.bias += r0;
-            if (f32_use_mf4(q.m, n, k, kp)) {
+            if (f32_use_mf4(q.m, n, k, kp, tm)) {
                 const int st = tm ? launch_f32_mf4<true>(q.m, n, s, q) : launch_f32_mf4<false>(q.m, n, s, q);
                 if (st != KORE_HIP_OK) return st;
                 continue;

@@ -229,10 +229,10 @@ def test_bit_linear_unaligned_buffers(off):
 
 
 @pytest.mark.parametrize("m,batch,k", [(4097, 48, 2563), (2049, 130, 2605), (1500, 192, 6912), (4100, 41, 2560),
-                                       (6000, 64, 3201), (4100, 64, 6917)])
+                                       (6000, 64, 3201), (4100, 64, 6917), (2560, 64, 6912), (2600, 41, 2561)])
 def test_bit_linear_f32_matrix_core_decode_batches(m, batch, k):
     """The 4 x 4 x 1 matrix-core kernel that takes the f32 layer at 41-192
-    tokens (token-major input; K >= 2560 and at least 1024 waves of 4 rows x
+    tokens (token-major input; K >= 2560 and at least 640 waves of 4 rows x
     64 tokens): ragged row groups (m % 4 == 1, where the packed matrix ends
     inside a dword), partial last column tiles, K not a multiple of the
     80-column chunk or of 5, 6912 columns of packed rows held in LDS; with Inf, NaN and subnormal inputs in some tokens (their
