@@ -2049,16 +2049,15 @@ static int launch_f32_mfma(uint64_t m, uint64_t n, hipStream_t s, const TernF32A
 // floats, one LDS table entry), and the MFMA of column 5 j + d takes trit d
 // from block j's lanes for all 16 blocks (CBSZ = 4, ABID = j).  CH chains
 // per wave (rows m0 .. m0 + 4 CH - 1) share each b read.  A workgroup is
-// 8 / CH waves on 32 consecutive rows of the same 64 columns.  Its rows'
+// W waves on 4 CH W consecutive rows of the same 64 columns.  Its rows'
 // packed bytes (one contiguous range) are copied into LDS at the start; b is
 // staged per chunk in LDS (per column, K contiguous, pitch 84 floats: a
 // lane's 16-byte reads of its own column hit 16 distinct bank groups per 16
-// lanes), three buffers, its global loads issued two chunks ahead.  A chunk
-// runs as four bursts of 20 K columns with nothing between the MFMAs; the
-// next burst's b entries are read before the current burst, the next
-// chunk's trits before the barrier that ends the chunk.  Zero trits and
-// non-finite b as in the 16 x 16 kernel: a chunk whose staged b holds an
-// Inf or NaN is folded element by element with zero trits skipped.
+// lanes; the staging schedule is described in the kernel).  A chunk runs as
+// four bursts of 20 K columns with nothing between the MFMAs; the next
+// burst's b entries are read before the current burst, the next chunk's
+// trits and first b entries during the chunk.  Inf and NaN b are found
+// from the sums after each chunk (see the kernel).
 constexpr int kM4K = 80;                 // K columns per chunk
 constexpr int kM4Rows = 32;              // rows per workgroup
 constexpr int kM4Pitch4 = kM4K / 4 + 1;  // 16-byte entries per staged column
