@@ -2105,16 +2105,6 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(t / kWave);
-    for (int i = t; i < 256; i += kThreads) {
-        uint32_t x = (uint32_t)i;
-        float* e = tl + 8 * i;
-#pragma unroll
-        for (int d = 0; d < 5; ++d) {
-            e[d] = i >= 243 ? 0.0f : (float)((int)(x % 3u) - 1);
-            x /= 3u;
-        }
-        e[5] = e[6] = e[7] = 0.0f;
-    }
     const uint32_t r0 = blockIdx.x * kRows;  // the workgroup's first row
     const uint32_t m0 = r0 + 4u * CH * wave;   // the wave's first row
     const uint32_t n0 = blockIdx.y * kWave;
@@ -2126,20 +2116,47 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
     // (+ 4 words: the last chunk's trit reads of row 31 reach up to 15 bytes
     // past the slice; past the matrix they read zeros)
     const uint32_t nwords = (s_off + kRows * p.kp + 3u) / 4u + 4u;
-    for (uint32_t i = (uint32_t)t; i < nwords; i += kThreads) {
-        // a dword that straddles the end of the matrix reads as zero from the
-        // range-checked resource: its bytes are read one by one
-        const uint32_t o = d0 + 4u * i;
-        uint32_t v;
-        if (o + 4u <= (uint32_t)a_bytes) {
-            v = __builtin_amdgcn_raw_buffer_load_b32(ra, o, 0, 0);
-        } else {
-            v = 0;
+    // The copy into araw (after the b loads of the first chunks are issued,
+    // below): the words of a batch are all loaded before any is stored, so
+    // the batch costs one load latency (a loop storing each word after its
+    // own load paid one per word).  Words past the matrix read zeros from
+    // the range-checked resource; the word that straddles its end would too,
+    // so its owner thread reads its bytes one by one up front.
+    const uint32_t i_s = (a_bytes & 3) != 0 ? ((uint32_t)a_bytes - d0) / 4u : 0xffffffffu;
+    // One batch, no loop: nwords <= 12288 (48 KB), 24 words per thread; the
+    // loads past nwords read words that are not stored.  The straddling
+    // word's bytes are loaded after the batch's words, so that waiting for
+    // them (loads complete in order) costs nothing beyond the batch.
+    auto copy_rows = [&]() {
+        constexpr int kCopyU = (int)((kM4MaxSlice / 4u + kThreads - 1) / kThreads);
+        uint32_t v[kCopyU];
 #pragma unroll
-            for (int b = 0; b < 4; ++b) v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(ra, o + b, 0, 0) << (8 * b);
+        for (int u = 0; u < kCopyU; ++u)
+            v[u] = __builtin_amdgcn_raw_buffer_load_b32(ra, d0 + 4u * ((uint32_t)t + (uint32_t)(kThreads * u)), 0, 0);
+        uint32_t w_s = 0;
+        if (i_s < nwords && (uint32_t)t == i_s % (uint32_t)kThreads) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                w_s |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(ra, d0 + 4u * i_s + (uint32_t)b, 0, 0) << (8 * b);
         }
-        araw[i] = v;
-    }
+#pragma unroll
+        for (int u = 0; u < kCopyU; ++u) {
+            const uint32_t i = (uint32_t)t + (uint32_t)(kThreads * u);
+            if (i < nwords) araw[i] = i == i_s ? w_s : v[u];
+        }
+    };
+    auto build_table = [&]() {
+        for (int i = t; i < 256; i += kThreads) {
+            uint32_t x = (uint32_t)i;
+            float* e = tl + 8 * i;
+#pragma unroll
+            for (int d = 0; d < 5; ++d) {
+                e[d] = i >= 243 ? 0.0f : (float)((int)(x % 3u) - 1);
+                x /= 3u;
+            }
+            e[5] = e[6] = e[7] = 0.0f;
+        }
+    };
     // b staging.  b is below 6 MB here (n <= 192, k <= 7680) and loads
     // through a range-checked resource at 32-bit byte offsets fixed for the
     // kernel: a column past n sits past the end of b and reads zeros, and
@@ -2222,20 +2239,25 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_mf4_kernel(TernF32Args 
 #pragma unroll
     for (int h = 0; h < CH; ++h) acc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 sv0[TM ? 1 : kStage], sv1[TM ? 1 : kStage];
-    if (p.k > 0) {
-        if constexpr (TM) {
-            dma_chunk(0, 0);
-            dma_chunk(kM4K, 1);
-            dma_chunk(2 * kM4K, 2);
-            dma_wait(true);  // chunks 0 and 1 (chunk 2's: by the end of chunk 0)
-        } else {
-            stage_load(0, sv0);
-            stage_store(0, sv0);
-            stage_load(kM4K, sv0);
-            stage_store(1, sv0);
-            stage_load(2 * kM4K, sv0);  // stored by chunk 0 where chunk 2 exists
-            stage_load(3 * kM4K, sv1);
-        }
+    // the b of the first chunks, then the packed rows and the table while
+    // those loads are in flight
+    if constexpr (TM) {
+        dma_chunk(0, 0);
+        dma_chunk(kM4K, 1);
+        dma_chunk(2 * kM4K, 2);
+    } else {
+        stage_load(0, sv0);
+        stage_load(kM4K, sv1);
+    }
+    copy_rows();
+    build_table();
+    if constexpr (TM) {
+        dma_wait(true);  // chunks 0 and 1 (chunk 2's: by the end of chunk 0)
+    } else {
+        stage_store(0, sv0);
+        stage_store(1, sv1);
+        stage_load(2 * kM4K, sv0);  // stored by chunk 0 where chunk 2 exists
+        stage_load(3 * kM4K, sv1);
     }
     // the table, the packed rows and the b of chunks 0 and 1 (token-major b:
     // no release fence, which would wait for chunk 2's loads too; the
