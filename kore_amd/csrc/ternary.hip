@@ -1767,6 +1767,12 @@ static int launch_f32_rows(uint64_t m, uint64_t n, hipStream_t s, const TernF32A
 // (acc is never -0); a chunk whose b holds an Inf or NaN in this wave's
 // columns is done instead on the vector unit, element by element, with zero
 // trits skipped (the reference's step, bit for bit).
+// 16 bytes per lane from a range-checked resource straight into LDS (lane
+// L's at dst + 16 L; dst wave-uniform).
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, lds_vptr dst, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
+}
+
 constexpr int kMfK = 160;            // K columns per chunk
 constexpr int kMfB = kMfK / 5;       // packed bytes per row and chunk
 constexpr int kMfG = kMfK / 16;      // groups of 16 K columns (one b register of four per lane group)
@@ -1809,8 +1815,9 @@ __device__ __noinline__ f32x16 mf_slow_chunk(f32x16 acc, const float* tl, const 
     return acc;
 }
 
-template <bool TM>
+template <bool TM, bool DMA>
 __global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Args p) {
+    static_assert(TM || !DMA, "LDS-DMA staging is for token-major b");
     // byte v -> its five trits as floats at [8 v + d] (bytes >= 243: zero
     // trits).  Measured faster than int8 entries converted on the vector
     // unit, even replicated against bank conflicts (6912 x 4096 x 2560:
@@ -1885,6 +1892,40 @@ __global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Arg
         const uint64_t bl = __ballot(bad);
         if (lane == 0) bbad[buf][wave] = bl != 0 ? 1u : 0u;
     };
+    // DMA (token-major b, K % 4 == 0, b below 2 GB): the chunk's 640 entries
+    // straight into LDS, 10 loads of 1 KB (64 lanes x 16 bytes; entry e =
+    // 64 g + 16 qq + jj is lane e % 64 of load g), wave w issuing loads w,
+    // w + 4, w + 8, from a range-checked resource at 32-bit offsets fixed
+    // for the kernel: columns past n and entries past K (all four of their
+    // K columns, as K % 4 == 0) read zeros.  Chunk c + 2's loads are issued
+    // at the start of chunk c, into the buffer chunk c - 1 used; the release
+    // fence before the barrier that ends chunk c waits for them (a chunk
+    // lasts far longer than the loads).  No registers, no LDS stores, no
+    // staging flags: Inf/NaN are found from the sums after each chunk.
+    constexpr int kMfDmaRows = kMfG;                            // 1 KB loads per chunk
+    constexpr int kMfDmaMax = (kMfDmaRows + kMfWaves - 1) / kMfWaves;
+    constexpr uint32_t kOutOff = 0x80000000u;                    // an offset past any b this path takes
+    uint32_t doff[kMfDmaMax], dk4[kMfDmaMax];
+    const __amdgpu_buffer_rsrc_t rbd = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.b, (short)0, DMA ? (int)((uint64_t)p.n * p.k * 4u) : 0, kBufWord3);
+    if constexpr (DMA) {
+#pragma unroll
+        for (int u = 0; u < kMfDmaMax; ++u) {
+            const uint32_t g = wave + (uint32_t)(kMfWaves * u);
+            const uint32_t cl = n0 + (uint32_t)(lane & 15);
+            dk4[u] = 16u * g + 4u * (uint32_t)(lane >> 4);  // K column of the entry within its chunk
+            doff[u] = cl < p.n ? (cl * p.k + dk4[u]) * 4u : kOutOff;
+        }
+    }
+    auto dma_chunk = [&](uint32_t kc, uint32_t buf) {
+#pragma unroll
+        for (int u = 0; u < kMfDmaMax; ++u) {
+            const uint32_t g = wave + (uint32_t)(kMfWaves * u);
+            if (u < kMfDmaMax - 1 || g < (uint32_t)kMfDmaRows)
+                lds_load16(rbd, (lds_vptr)(reinterpret_cast<char*>(&bst[buf][0][0][0]) + 1024u * g),
+                           kc + dk4[u] < p.k ? doff[u] : kOutOff, 4u * kc);
+        }
+    };
     // packed bytes of row m0 + lane: the kMfB bytes of a chunk from the
     // dword boundary below them (kMfW dwords, shifted); bytes past the row meet b = 0
     // (k >= K); the range check returns zeros past the matrix, and the
@@ -1918,12 +1959,18 @@ __global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Arg
     uint32_t wn[kMfW] = {};
     f32x4 sv[kMfStage];
     if (p.k > 0) {
-        stage_load(0, sv);
-        stage_store(0, sv);
-        stage_load(kMfK, sv);
-        stage_store(1, sv);
-        load_a(0, wn);
-        stage_load(2 * kMfK, sv);  // past K: zeros
+        if constexpr (DMA) {
+            dma_chunk(0, 0);
+            dma_chunk(kMfK, 1);
+            load_a(0, wn);
+        } else {
+            stage_load(0, sv);
+            stage_store(0, sv);
+            stage_load(kMfK, sv);
+            stage_store(1, sv);
+            load_a(0, wn);
+            stage_load(2 * kMfK, sv);  // past K: zeros
+        }
     }
     __syncthreads();  // the table and the b of chunks 0 and 1
     // Waves past M still stage b and meet every barrier; they skip the MFMAs.
@@ -1951,9 +1998,15 @@ __global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Arg
     };
     if (p.k > 0) prep(0, 0);
     uint32_t buf = 0;
+    bool stuck = false;  // DMA: the wave's sums are no longer all finite
     for (uint32_t kc = 0; kc < p.k; kc += kMfK, buf = buf == 2u ? 0u : buf + 1u) {
+        if constexpr (DMA) {
+            if (kc + 2 * kMfK < p.k) dma_chunk(kc + 2 * kMfK, buf == 0u ? 2u : buf - 1u);
+        }
         if (kc + kMfK < p.k) load_a(kc + kMfK, wn);
-        const bool bad = (bbad[buf][0] | bbad[buf][1] | bbad[buf][2] | bbad[buf][3]) != 0u;
+        const bool bad = DMA ? stuck : (bbad[buf][0] | bbad[buf][1] | bbad[buf][2] | bbad[buf][3]) != 0u;
+        f32x16 saved;
+        if constexpr (DMA) saved = acc;
         if (live && !bad) {
 #pragma unroll
             for (int jb = 0; jb < kMfB; ++jb) {
@@ -1975,16 +2028,36 @@ __global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Arg
                     if (d == 0 && jb + 2 < kMfB) issue(jb + 2);
                 }
             }
-        } else if (live) {
+        }
+        if constexpr (DMA) {
+            // the chain adds the zero-trit terms too: a finite sum is left
+            // unchanged by them, but an Inf or NaN b makes it NaN, so a
+            // chunk after which some sum is not finite is folded again from
+            // the saved sums with zero trits skipped
+            bool nf = false;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) nf |= !__builtin_isfinite(acc[v]);
+            if (live && !bad && __ballot(nf) != 0) {
+                acc = saved;
+                stuck = true;
+            }
+        }
+        if (live && (DMA ? stuck : bad)) {
             MfBytes bb;
 #pragma unroll
             for (int i = 0; i < kMfB / 4; ++i) bb.w[i] = by[i];
             acc = mf_slow_chunk(acc, tl, &bst[buf][0][0][0], bb, lane);
+            if constexpr (DMA) {
+                bool nf = false;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) nf |= !__builtin_isfinite(acc[v]);
+                stuck = __ballot(nf) != 0;
+            }
         }
         // chunk c + 2's b into its buffer (read after the barrier), chunk
         // c + 3's loads, and chunk c + 1's operands (its buffer was written
         // before the last barrier)
-        if (kc + 2 * kMfK < p.k) {
+        if (!DMA && kc + 2 * kMfK < p.k) {
             stage_store(buf == 0u ? 2u : buf - 1u, sv);  // buffer (c + 2) % 3
             stage_load(kc + 3 * kMfK, sv);
         }
@@ -2026,7 +2099,12 @@ template <bool TM>
 static int launch_f32_mfma(uint64_t m, uint64_t n, hipStream_t s, const TernF32Args& p) {
     const uint64_t bx = (m + kMfWaves * kWave - 1) / (kMfWaves * kWave), by = (n + 15) / 16;
     if (bx > 0x7fffffffull || by > 65535) return KORE_HIP_ERR_OVERFLOW;
-    hipLaunchKernelGGL(ternary_f32_mfma_kernel<TM>, dim3((uint32_t)bx, (uint32_t)by), dim3(kMfWaves * kWave), 0, s, p);
+    // token-major b straight into LDS where K % 4 == 0 (no entry straddles
+    // K) and b is below 2 GB (32-bit offsets)
+    if (TM && p.k % 4u == 0 && (uint64_t)p.n * p.k * 4u < 0x7fffffffull)
+        hipLaunchKernelGGL((ternary_f32_mfma_kernel<TM, TM>), dim3((uint32_t)bx, (uint32_t)by), dim3(kMfWaves * kWave), 0, s, p);
+    else
+        hipLaunchKernelGGL((ternary_f32_mfma_kernel<TM, false>), dim3((uint32_t)bx, (uint32_t)by), dim3(kMfWaves * kWave), 0, s, p);
     return launch_status();
 }
 
@@ -2063,12 +2141,6 @@ constexpr int kM4Rows = 32;              // rows per workgroup
 constexpr int kM4Pitch4 = kM4K / 4 + 1;  // 16-byte entries per staged column
 constexpr int kM4Pieces = kWave * kM4K / 4;  // 16-byte pieces of b per chunk
 constexpr uint32_t kM4MaxSlice = 48 * 1024;  // bytes of packed rows a workgroup holds in LDS
-
-// 16 bytes per lane from a range-checked resource straight into LDS (lane
-// L's at dst + 16 L; dst wave-uniform).
-__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, lds_vptr dst, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
-}
 
 // One step of a 4 x 4 x 1 chain whose trit operand is block j's (CBSZ = 4,
 // ABID = j: one block's four lanes broadcast to all sixteen).

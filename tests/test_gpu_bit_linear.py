@@ -264,6 +264,41 @@ def test_bit_linear_f32_matrix_core_decode_batches(m, batch, k):
     assert bool(same.all()), f"bit_linear_f32 4x4 matrix cores vs ternary_matmul_f32: {int((~same).sum())} differ"
 
 
+@pytest.mark.parametrize("m,batch,k", [(2049, 520, 1284), (1100, 1040, 3200), (4096, 770, 2560)])
+def test_bit_linear_f32_prefill_nonfinite(m, batch, k):
+    """The 16 x 16 matrix-core kernel on the layer's token-major input with K
+    a multiple of 4 (b loaded straight into LDS; Inf/NaN found from the sums
+    after each chunk, the chunk refolded with zero trits skipped): tokens with
+    Inf, -Inf, NaN, subnormal and overflowing inputs, bit-exact against the
+    oracle on those tokens and against ternary_matmul_f32 on x^T (the [K, N]
+    staging, which flags non-finite b when staging it) on every token."""
+    log(f"bit_linear_f32 16x16 non-finite m={m} batch={batch} k={k}")
+    p = raw_packed(m, k, 3 * m + k)
+    sa = normal((m,), 90, 1.0, 0.1)
+    bias = normal((m,), 91)
+    x = normal((batch, k), 92)
+    r = np.random.default_rng(m + batch + k)
+    x[0, r.integers(0, k, 2)] = np.inf
+    x[1, r.integers(0, k, 3)] = -np.inf
+    x[2, r.integers(0, k, 1)] = np.nan
+    x[3] = (x[3] * 1e-39).astype(np.float32)  # subnormal
+    x[4] = np.float32(3e38)  # the sums overflow
+    x[batch - 1, k - 1] = np.nan  # the last chunk of the last token
+    bp, bs, bb = up(p), up(sa), up(bias)
+    got = down(rocm.rocm_bit_linear_f32(DEV, bp, bs, up(x), bb, m, batch, k), np.float32, (batch, m))
+    rows = [0, 1, 2, 3, 4, 5, batch - 1]
+    xs = x[rows]
+    assert_bitexact(got[rows], oracle.bit_linear_forward(p, sa, xs, bias, m, len(rows), k),
+                    "bit_linear_f32 16x16 non-finite vs oracle")
+    xt = torch.from_numpy(x).cuda().t().contiguous()
+    c = rocm.rocm_ternary_matmul_f32(DEV, bp, bs, HipBuffer.from_tensor(xt), m, batch, k)
+    ct = torch.from_numpy(down(c, np.float32, (m, batch))).cuda()
+    want = ct.t().contiguous() + torch.from_numpy(bias).cuda()[None, :]
+    gt = torch.from_numpy(got).cuda()
+    same = (gt == want) | (torch.isnan(gt) & torch.isnan(want))
+    assert bool(same.all()), f"bit_linear_f32 16x16 vs ternary_matmul_f32: {int((~same).sum())} differ"
+
+
 @pytest.mark.parametrize("seed", range(6))
 def test_bit_linear_f32_matrix_core_random_shapes(seed):
     """Random shapes across the 4 x 4 x 1 kernel's range (41-192 tokens,
