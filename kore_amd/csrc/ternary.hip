@@ -1791,7 +1791,10 @@ struct MfBytes {
 // row 16 (v / 4) + 4 (L / 16) + v % 4 of the wave's block, whose trit is that
 // lane's a operand, and column L % 16, whose b is in lanes 16 q' + L % 16.
 // Kept out of line: it runs only for such chunks.
-__device__ __noinline__ f32x16 mf_slow_chunk(f32x16 acc, const float* tl, const f32x4* bsb, MfBytes by, int lane) {
+// kmajor: the chunk's b as [K][16 columns] floats instead of [g][q][j]
+// entries.
+__device__ __noinline__ f32x16 mf_slow_chunk(f32x16 acc, const float* tl, const f32x4* bsb, MfBytes by, int lane,
+                                             bool kmajor) {
     const int q = lane >> 4, j = lane & 15;
     for (int jb = 0; jb < kMfB; ++jb) {
         const uint32_t bv = (by.w[jb >> 2] >> (8 * (jb & 3))) & 0xffu;
@@ -1799,12 +1802,17 @@ __device__ __noinline__ f32x16 mf_slow_chunk(f32x16 acc, const float* tl, const 
             const int kk = 5 * jb + d;
             const float tv = tl[8 * bv + d];
             const int g = kk >> 4, qq = (kk >> 2) & 3, r = kk & 3;
-            const f32x4 bgv = bsb[(g * 4 + q) * 16 + j];
-            float bsel = 0.0f;
+            float bk;
+            if (kmajor) {
+                bk = reinterpret_cast<const float*>(bsb)[16 * kk + j];
+            } else {
+                const f32x4 bgv = bsb[(g * 4 + q) * 16 + j];
+                float bsel = 0.0f;
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-                if (rr == r) bsel = bgv[rr];
-            const float bk = __shfl(bsel, 16 * qq + j, kWave);
+                for (int rr = 0; rr < 4; ++rr)
+                    if (rr == r) bsel = bgv[rr];
+                bk = __shfl(bsel, 16 * qq + j, kWave);
+            }
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const float te = __shfl(tv, 16 * (v >> 2) + 4 * q + (v & 3), kWave);
@@ -1817,7 +1825,6 @@ __device__ __noinline__ f32x16 mf_slow_chunk(f32x16 acc, const float* tl, const 
 
 template <bool TM, bool DMA>
 __global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Args p) {
-    static_assert(TM || !DMA, "LDS-DMA staging is for token-major b");
     // byte v -> its five trits as floats at [8 v + d] (bytes >= 243: zero
     // trits).  Measured faster than int8 entries converted on the vector
     // unit, even replicated against bank conflicts (6912 x 4096 x 2560:
@@ -1892,12 +1899,17 @@ __global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Arg
         const uint64_t bl = __ballot(bad);
         if (lane == 0) bbad[buf][wave] = bl != 0 ? 1u : 0u;
     };
-    // DMA (token-major b, K % 4 == 0, b below 2 GB): the chunk's 640 entries
-    // straight into LDS, 10 loads of 1 KB (64 lanes x 16 bytes; entry e =
-    // 64 g + 16 qq + jj is lane e % 64 of load g), wave w issuing loads w,
-    // w + 4, w + 8, from a range-checked resource at 32-bit offsets fixed
-    // for the kernel: columns past n and entries past K (all four of their
-    // K columns, as K % 4 == 0) read zeros.  Chunk c + 2's loads are issued
+    // DMA: the chunk's b straight into LDS, 10 loads of 1 KB (64 lanes x 16
+    // bytes), wave w issuing loads w, w + 4, w + 8, from a range-checked
+    // resource at 32-bit offsets fixed for the kernel (plus a per-chunk
+    // scalar offset).  Token-major b (K % 4 == 0, b below 2 GB): entry e =
+    // 64 g + 16 qq + jj is lane e % 64 of load g; columns past n and
+    // entries past K (all four of their K columns, as K % 4 == 0) read
+    // zeros.  [K, N] b (its offsets below 2^31 up to K + 320): the chunk as
+    // [K][16 columns] floats, load g holding K columns 16 g .. + 15, lane l
+    // K column 16 g + l / 4 and columns 4 (l % 4) .. + 3; K columns past K
+    // read zeros, and a lane's last columns past n read the next K row's
+    // first values (columns whose outputs are not stored).  Chunk c + 2's loads are issued
     // at the start of chunk c, into the buffer chunk c - 1 used; the release
     // fence before the barrier that ends chunk c waits for them (a chunk
     // lasts far longer than the loads).  No registers, no LDS stores, no
@@ -1912,9 +1924,15 @@ __global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Arg
 #pragma unroll
         for (int u = 0; u < kMfDmaMax; ++u) {
             const uint32_t g = wave + (uint32_t)(kMfWaves * u);
-            const uint32_t cl = n0 + (uint32_t)(lane & 15);
-            dk4[u] = 16u * g + 4u * (uint32_t)(lane >> 4);  // K column of the entry within its chunk
-            doff[u] = cl < p.n ? (cl * p.k + dk4[u]) * 4u : kOutOff;
+            if (TM) {
+                const uint32_t cl = n0 + (uint32_t)(lane & 15);
+                dk4[u] = 16u * g + 4u * (uint32_t)(lane >> 4);  // K column of the entry within its chunk
+                doff[u] = cl < p.n ? (cl * p.k + dk4[u]) * 4u : kOutOff;
+            } else {
+                const uint32_t c4 = n0 + 4u * (uint32_t)(lane & 3);
+                dk4[u] = 0u;
+                doff[u] = c4 < p.n ? ((16u * g + (uint32_t)(lane >> 2)) * p.n + c4) * 4u : kOutOff;
+            }
         }
     }
     auto dma_chunk = [&](uint32_t kc, uint32_t buf) {
@@ -1923,7 +1941,7 @@ __global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Arg
             const uint32_t g = wave + (uint32_t)(kMfWaves * u);
             if (u < kMfDmaMax - 1 || g < (uint32_t)kMfDmaRows)
                 lds_load16(rbd, (lds_vptr)(reinterpret_cast<char*>(&bst[buf][0][0][0]) + 1024u * g),
-                           kc + dk4[u] < p.k ? doff[u] : kOutOff, 4u * kc);
+                           !TM || kc + dk4[u] < p.k ? doff[u] : kOutOff, TM ? 4u * kc : 4u * kc * p.n);
         }
     };
     // packed bytes of row m0 + lane: the kMfB bytes of a chunk from the
@@ -1980,6 +1998,12 @@ __global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Arg
     // bytes.  Byte jb's trits are read two bytes ahead of its MFMAs and a b
     // group's entry one group ahead, each read placed between MFMAs.
     f32x4 bq[2];  // b entries of groups g (bq[g % 2]) and g + 1
+    // b(kc + 16 g + 4 q + r, n0 + j) for r = 0..3 from chunk buffer bufc
+    auto b_entry = [&](uint32_t bufc, int g) -> f32x4 {
+        if (TM || !DMA) return bst[bufc][g][q][j];
+        const float* bk = reinterpret_cast<const float*>(&bst[bufc][0][0][0]) + 16 * (16 * g + 4 * q) + j;
+        return f32x4{bk[0], bk[16], bk[32], bk[48]};
+    };
     uint32_t by[kMfB / 4];
     f32x4 tq[3];  // trits 0..3 of byte jb in tq[jb % 3], trit 4 in t4[jb % 3]
     float t4[3];
@@ -1989,7 +2013,7 @@ __global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Arg
         t4[jb % 3] = tl[8 * v + 4];
     };
     auto prep = [&](uint32_t kc, uint32_t bufc) {
-        bq[0] = bst[bufc][0][q][j];
+        bq[0] = b_entry(bufc, 0);
         const uint32_t sh = (arow + kc / 5u) & 3u;
 #pragma unroll
         for (int i = 0; i < kMfB / 4; ++i) by[i] = __builtin_amdgcn_alignbyte(wn[i + 1], wn[i], sh);
@@ -2024,7 +2048,7 @@ __global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Arg
                         default: acc = __builtin_amdgcn_mfma_f32_16x16x1f32(tv, bv, acc, 0, 0, 7); break;
                     }
                     __builtin_amdgcn_sched_barrier(0);
-                    if ((kk & 15) == 0 && g + 1 < kMfG) bq[(g + 1) & 1] = bst[buf][g + 1][q][j];
+                    if ((kk & 15) == 0 && g + 1 < kMfG) bq[(g + 1) & 1] = b_entry(buf, g + 1);
                     if (d == 0 && jb + 2 < kMfB) issue(jb + 2);
                 }
             }
@@ -2046,7 +2070,7 @@ __global__ __launch_bounds__(kMfThreads) void ternary_f32_mfma_kernel(TernF32Arg
             MfBytes bb;
 #pragma unroll
             for (int i = 0; i < kMfB / 4; ++i) bb.w[i] = by[i];
-            acc = mf_slow_chunk(acc, tl, &bst[buf][0][0][0], bb, lane);
+            acc = mf_slow_chunk(acc, tl, &bst[buf][0][0][0], bb, lane, !TM && DMA);
             if constexpr (DMA) {
                 bool nf = false;
 #pragma unroll
@@ -2099,10 +2123,13 @@ template <bool TM>
 static int launch_f32_mfma(uint64_t m, uint64_t n, hipStream_t s, const TernF32Args& p) {
     const uint64_t bx = (m + kMfWaves * kWave - 1) / (kMfWaves * kWave), by = (n + 15) / 16;
     if (bx > 0x7fffffffull || by > 65535) return KORE_HIP_ERR_OVERFLOW;
-    // token-major b straight into LDS where K % 4 == 0 (no entry straddles
-    // K) and b is below 2 GB (32-bit offsets)
-    if (TM && p.k % 4u == 0 && (uint64_t)p.n * p.k * 4u < 0x7fffffffull)
-        hipLaunchKernelGGL((ternary_f32_mfma_kernel<TM, TM>), dim3((uint32_t)bx, (uint32_t)by), dim3(kMfWaves * kWave), 0, s, p);
+    // b straight into LDS: token-major b where K % 4 == 0 (no entry
+    // straddles K) and b is below 2 GB, [K, N] b where its offsets stay below
+    // 2^31 up to two chunks past K (32-bit offsets)
+    const bool dma = TM ? p.k % 4u == 0 && (uint64_t)p.n * p.k * 4u < 0x7fffffffull
+                        : (uint64_t)p.n * (p.k + 2u * kMfK) * 4u < 0x7fffffffull;
+    if (dma)
+        hipLaunchKernelGGL((ternary_f32_mfma_kernel<TM, true>), dim3((uint32_t)bx, (uint32_t)by), dim3(kMfWaves * kWave), 0, s, p);
     else
         hipLaunchKernelGGL((ternary_f32_mfma_kernel<TM, false>), dim3((uint32_t)bx, (uint32_t)by), dim3(kMfWaves * kWave), 0, s, p);
     return launch_status();
