@@ -1444,6 +1444,12 @@ static void launch_f32_seq(int ct, dim3 g, hipStream_t s, const TernF32Args& p) 
 #undef KORE_F32_SEQ
 }
 
+// 16 bytes per lane from a range-checked resource straight into LDS (lane
+// L's at dst + 16 L; dst wave-uniform).
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, lds_vptr dst, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
+}
+
 constexpr uint32_t kRowsW = 4;            // waves per workgroup (b[K, N])
 // Token-major b (the layer's input as stored): a staged chunk is a 320-byte
 // piece of every column, which straddles cache lines, so every workgroup's
@@ -1696,6 +1702,233 @@ __global__ __launch_bounds__(W * kWave) void ternary_f32_rows_kernel(TernF32Args
     }
 }
 
+// The row-broadcast kernel with token-major b loaded straight into LDS
+// (three tiles, chunk c + 2's loads issued in chunk c); the rest as in
+// ternary_f32_rows_kernel above.
+template <int CT, int R, int W>
+__global__ __launch_bounds__(W * kWave) void ternary_f32_rows_dma_kernel(TernF32Args p) {
+    constexpr bool DMA = true;
+    constexpr int KC = 80;                 // K columns per chunk
+    constexpr int NB = KC / 5;             // packed bytes per row and chunk (one per lane of a 16-lane row)
+    constexpr int kPitch = KC + 4;         // floats per column of the staged b: 21 x 16 bytes
+    constexpr int kSlots = kWave / CT;     // row slots of a wave (CT lanes each)
+    constexpr int kThreads = W * kWave;
+    static_assert(NB == 16 && CT % 16 == 0 && kWave % CT == 0, "chunk split");
+    // DMA: token-major b (the layer's input) goes straight into LDS: three
+    // tiles, each a whole number of 1 KB loads (64 lanes x 16 bytes); see
+    // below.
+    constexpr int kDmaRows = (CT * kPitch / 4 + kWave - 1) / kWave;  // 1 KB loads per chunk
+    constexpr int kTileF = DMA ? kDmaRows * kWave * 4 : CT * kPitch;  // floats per tile
+    // b of a chunk, [column][k]: separate arrays, so that with the loop
+    // unrolled over them the compiler sees which one a read and a load into
+    // LDS touch (a read waits only for loads into its own tile)
+    __shared__ __attribute__((aligned(16))) float bs0[kTileF];
+    __shared__ __attribute__((aligned(16))) float bs1[kTileF];
+    __shared__ __attribute__((aligned(16))) float bs2[kTileF];
+    __shared__ float tlut[5 * 256];  // digit d of byte v -> trit as float at [d * 256 + v]; v >= 243: 0
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(t / kWave);
+    for (int v = t; v < 256; v += kThreads) {
+        uint32_t x = (uint32_t)v;
+#pragma unroll
+        for (int d = 0; d < 5; ++d) {
+            tlut[d * 256 + v] = v >= 243 ? 0.0f : (float)((int)(x % 3u) - 1);
+            x /= 3u;
+        }
+    }
+    __syncthreads();  // the table is read before the first chunk's barrier
+    const uint32_t col0 = blockIdx.y * CT;
+    const uint32_t col = col0 + (uint32_t)(lane % CT);
+    // row slot lane / CT of the wave owns rows row0 .. row0 + R - 1
+    const uint32_t row0 = ((blockIdx.x * W + wave) * kSlots + (uint32_t)(lane / CT)) * R;
+    // DMA staging (token-major b): slot s of a tile (16 bytes) holds column
+    // s / 21, K columns 4 (s % 21) .. + 3 of the chunk ([column][84 floats],
+    // the layout above; entry 20 of a column, its padding, reloads entry
+    // 19, and slots past the tile's columns read zeros).  Wave w issues the
+    // loads of rows w, w + W, ... of the tile through a resource based at the
+    // tile's first column, at 32-bit offsets fixed for the kernel plus a
+    // per-chunk scalar offset (the launcher takes this path where the tile's
+    // 64 columns hold below 2^31 bytes).  Past K a column reads the next one's values: the partial
+    // last chunk's trits past K are masked to zero instead.  Chunk c + 2's
+    // loads are issued in chunk c (into the tile chunk c - 1 used; issued
+    // past K too, into a tile no chunk reads) and waited for, with an
+    // explicit vmcnt, before the barrier that ends chunk c + 1.
+    // Every wave issues kDmaMax loads per chunk (a wave short of rows
+    // reloads another wave's row: the same bytes to the same place), so that
+    // the compiler's count of the loads in flight is the same on every path.
+    constexpr int kDmaMax = (kDmaRows + W - 1) / W;
+    auto dma_row = [&](int u) { return (uint32_t)(((int)wave + W * u) % kDmaRows); };
+    uint32_t doff[kDmaMax];
+    const uint32_t tile_cols = p.n - col0 < (uint32_t)CT ? p.n - col0 : (uint32_t)CT;
+    const __amdgpu_buffer_rsrc_t rbd = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.b + (DMA ? (uint64_t)col0 * p.k : 0u)), (short)0, DMA ? (int)(tile_cols * p.k * 4u) : 0, kBufWord3);
+    if constexpr (DMA) {
+#pragma unroll
+        for (int u = 0; u < kDmaMax; ++u) {
+            const uint32_t sl = (uint32_t)kWave * dma_row(u) + (uint32_t)lane;
+            const uint32_t cl = sl / (uint32_t)(kPitch / 4), j = sl % (uint32_t)(kPitch / 4);
+            doff[u] = cl < tile_cols ? (cl * p.k + 4u * (j < 20u ? j : 19u)) * 4u : 0x80000000u;
+        }
+    }
+    auto dma_chunk = [&](uint32_t kc, float* tile) {
+#pragma unroll
+        for (int u = 0; u < kDmaMax; ++u)
+            lds_load16(rbd, (lds_vptr)(reinterpret_cast<char*>(tile) + 1024u * dma_row(u)), doff[u], 4u * kc);
+    };
+    // byte lane % 16 of the chunk for each row.  Past the row's end the byte
+    // is the next row's (or 0 past the matrix, by the range check): its
+    // trits meet only b past K, which is zero, and fma(t, 0, acc) = acc.
+    const int a_bytes = (int)((uint64_t)p.m * p.kp);  // below 2^31 (checked by the launcher)
+    uint32_t aoff[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) aoff[i] = min(row0 + i, p.m - 1) * p.kp + (uint32_t)(lane & (NB - 1));
+    auto load_pb = [&](uint32_t kc, uint32_t (&pb)[R]) {
+        const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)p.a, (short)0, a_bytes, kBufWord3);
+#pragma unroll
+        for (int i = 0; i < R; ++i) pb[i] = __builtin_amdgcn_raw_buffer_load_b8(ra, aoff[i] + kc / 5u, 0, 0);
+    };
+    uint32_t pbn[R];
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = 0.0f;
+    if (p.k > 0) {
+        load_pb(0, pbn);
+        dma_chunk(0, bs0);
+        dma_chunk(KC, bs1);
+        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): chunks 0 and 1
+        __builtin_amdgcn_s_barrier();
+    }
+    bool slow = false;  // wave-uniform: a row's sum is Inf or NaN
+    // one chunk: its b in tile bb; with DMA, chunk c + 2's loads into tile nb2
+    auto chunk = [&](uint32_t kc, float* bb, float* nb2) {
+        // this chunk's trits: lane L holds the five of byte L % 16 of each row
+        uint32_t pbc[R];
+        float tr[R][5];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            pbc[i] = pbn[i];
+#pragma unroll
+            for (int d = 0; d < 5; ++d) tr[i][d] = tlut[d * 256 + pbn[i]];
+        }
+        if (DMA && kc + KC > p.k) {
+            // the partial last chunk: trits past K are zero (b there is the
+            // next column's)
+            const uint32_t k0 = kc + 5u * (uint32_t)(lane & (NB - 1));
+#pragma unroll
+            for (int i = 0; i < R; ++i)
+#pragma unroll
+                for (int d = 0; d < 5; ++d) tr[i][d] = k0 + d < p.k ? tr[i][d] : 0.0f;
+        }
+        if constexpr (DMA) {
+            // issued for every chunk, past K too (range-checked reads into a
+            // tile no chunk reads), so that the waits count only the loads
+            // they are for
+            load_pb(kc + KC, pbn);
+            dma_chunk(kc + 2 * KC, nb2);
+        }
+        const f32x4* bc = reinterpret_cast<const f32x4*>(bb + (lane % CT) * kPitch);
+        if (!slow) {
+            // K advances 20 columns (4 bytes, 5 float4 of b) per group; the
+            // next group's b is read before this group's fmas
+            float saved[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) saved[i] = acc[i];
+            f32x4 bcur[5], bnxt[5];
+#pragma unroll
+            for (int q = 0; q < 5; ++q) bcur[q] = bc[q];
+            auto group = [&](auto gc) {
+                constexpr int G = decltype(gc)::value;
+                if (G < 3) {
+#pragma unroll
+                    for (int q = 0; q < 5; ++q) bnxt[q] = bc[5 * (G + 1) + q];
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                const float* bf = reinterpret_cast<const float*>(bcur);
+                auto byte = [&](auto jc) {
+                    constexpr int j = decltype(jc)::value;  // byte of the group
+#pragma unroll
+                    for (int d = 0; d < 5; ++d)
+#pragma unroll
+                        for (int i = 0; i < R; ++i) acc[i] = fmac_trit<4 * G + j>(acc[i], tr[i][d], bf[5 * j + d]);
+                };
+                byte(std::integral_constant<int, 0>{});
+                byte(std::integral_constant<int, 1>{});
+                byte(std::integral_constant<int, 2>{});
+                byte(std::integral_constant<int, 3>{});
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int q = 0; q < 5; ++q) bcur[q] = bnxt[q];
+            };
+            group(std::integral_constant<int, 0>{});
+            group(std::integral_constant<int, 1>{});
+            group(std::integral_constant<int, 2>{});
+            group(std::integral_constant<int, 3>{});
+            // An Inf or NaN b turns the sum it enters Inf or NaN (fma(0, Inf,
+            // acc) included), and so does an overflow: redo the chunk with
+            // zero trits skipped from the saved sums, and keep doing so.
+            bool nf = false;
+#pragma unroll
+            for (int i = 0; i < R; ++i) nf |= !__builtin_isfinite(acc[i]);
+            if (__builtin_expect(__ballot(nf) != 0, 0)) {
+                slow = true;
+#pragma unroll
+                for (int i = 0; i < R; ++i) acc[i] = saved[i];
+            }
+        }
+        if (slow) {
+            const uint32_t kn = min((uint32_t)KC, p.k - kc);
+            const float* bf = bb + (lane % CT) * kPitch;
+            for (uint32_t ki = 0; ki < kn; ++ki) {
+                const float bv = bf[ki];
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    // byte ki / 5 of the row, held by lane ki / 5 of this lane's 16-lane row
+                    const uint32_t byte = (uint32_t)__shfl((int)pbc[i], (lane & ~15) + (int)(ki / 5u), kWave);
+                    const float trv = tlut[(ki % 5u) * 256u + byte];
+                    if (trv != 0.0f) acc[i] = __builtin_fmaf(trv, bv, acc[i]);
+                }
+            }
+        }
+        if constexpr (DMA) {
+            // chunk c + 1's loads (and the packed bytes) landed for every
+            // wave, and this chunk's tile read by all, before the next chunk;
+            // no release fence (it would wait for chunk c + 2's loads too)
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(0xF70 | kDmaMax);  // all but chunk c + 2's loads
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    if constexpr (DMA) {
+        // unrolled over the three tiles: chunk c in tile c % 3
+        for (uint32_t kc = 0; kc < p.k; kc += 3 * KC) {
+            chunk(kc, bs0, bs2);
+            if (kc + KC >= p.k) break;
+            chunk(kc + KC, bs1, bs0);
+            if (kc + 2 * KC >= p.k) break;
+            chunk(kc + 2 * KC, bs2, bs1);
+        }
+    }
+    // no LDS load may still be in flight when the workgroup's LDS is released
+    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0xF70);
+    if (col < p.n) {
+        // c[n, m] with four rows per lane: the lane's rows are four
+        // consecutive floats of one output row, stored as one 16-byte write
+        if (R == 4 && p.trans && row0 + 3 < p.m && (p.ldt & 3u) == 0 &&
+            (reinterpret_cast<uintptr_t>(p.c) & 15u) == 0) {
+            f32x4 v;
+#pragma unroll
+            for (int i = 0; i < R && i < 4; ++i) v[i] = add_bias(p.bias, acc[i] * p.sa[row0 + i], row0 + i);
+            *reinterpret_cast<f32x4*>(p.c + out_idx(p, row0, col)) = v;
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+            if (row0 + i < p.m) p.c[out_idx(p, row0 + i, col)] = add_bias(p.bias, acc[i] * p.sa[row0 + i], row0 + i);
+    }
+}
+
 // Rows per lane: 4 for 64-column tiles and 2 for narrower ones (b read from
 // LDS once per R rows; measured: 16- and 32-column tiles ran 6-12% slower
 // with 4 than with 2 at every m tried, 64-column tiles 8-20% faster) while
@@ -1726,14 +1959,23 @@ static int launch_f32_rows(uint64_t m, uint64_t n, hipStream_t s, const TernF32A
     const uint64_t bx = (m + rows - 1) / rows;
     if (bx > 0x7fffffffull || gy > 65535) return KORE_HIP_ERR_OVERFLOW;
     const dim3 gr((uint32_t)bx, (uint32_t)gy), blk(W * kWave);
+    // token-major b straight into LDS where a 64-column tile of it holds
+    // below 2^31 bytes (the kernel's 32-bit offsets)
+    const bool dma = TM && (uint64_t)CT * p.k * 4u < 0x80000000ull;
+#define KORE_ROWS_LAUNCH(RR)                                                                   \
+    do {                                                                                       \
+        if (dma) hipLaunchKernelGGL((ternary_f32_rows_dma_kernel<CT, RR, W>), gr, blk, 0, s, p);        \
+        else hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, RR, W, TM>), gr, blk, 0, s, p);            \
+    } while (0)
     if constexpr (CT == 64) {
-        if (r == 4) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 4, W, TM>), gr, blk, 0, s, p);
-        else if (r == 5) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 5, W, TM>), gr, blk, 0, s, p);
-        else if (r == 7) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 7, W, TM>), gr, blk, 0, s, p);
+        if (r == 4) KORE_ROWS_LAUNCH(4);
+        else if (r == 5) KORE_ROWS_LAUNCH(5);
+        else if (r == 7) KORE_ROWS_LAUNCH(7);
         if (r >= 4) return launch_status();
     }
-    if (r == 2) hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 2, W, TM>), gr, blk, 0, s, p);
-    else hipLaunchKernelGGL((ternary_f32_rows_kernel<CT, 1, W, TM>), gr, blk, 0, s, p);
+    if (r == 2) KORE_ROWS_LAUNCH(2);
+    else KORE_ROWS_LAUNCH(1);
+#undef KORE_ROWS_LAUNCH
     return launch_status();
 }
 
@@ -1767,12 +2009,6 @@ static int launch_f32_rows(uint64_t m, uint64_t n, hipStream_t s, const TernF32A
 // (acc is never -0); a chunk whose b holds an Inf or NaN in this wave's
 // columns is done instead on the vector unit, element by element, with zero
 // trits skipped (the reference's step, bit for bit).
-// 16 bytes per lane from a range-checked resource straight into LDS (lane
-// L's at dst + 16 L; dst wave-uniform).
-__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, lds_vptr dst, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
-}
-
 constexpr int kMfK = 160;            // K columns per chunk
 constexpr int kMfB = kMfK / 5;       // packed bytes per row and chunk
 constexpr int kMfG = kMfK / 16;      // groups of 16 K columns (one b register of four per lane group)
