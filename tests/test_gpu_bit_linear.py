@@ -264,15 +264,18 @@ def test_bit_linear_f32_matrix_core_decode_batches(m, batch, k):
     assert bool(same.all()), f"bit_linear_f32 4x4 matrix cores vs ternary_matmul_f32: {int((~same).sum())} differ"
 
 
-@pytest.mark.parametrize("m,batch,k", [(2049, 520, 1284), (1100, 1040, 3200), (4096, 770, 2560)])
+@pytest.mark.parametrize("m,batch,k", [(2049, 520, 1284), (1100, 1040, 3200), (4096, 770, 2560),
+                                       (13824, 40, 2560), (3000, 24, 1283), (2500, 12, 3203)])
 def test_bit_linear_f32_prefill_nonfinite(m, batch, k):
-    """The 16 x 16 matrix-core kernel on the layer's token-major input with K
-    a multiple of 4 (b loaded straight into LDS; Inf/NaN found from the sums
-    after each chunk, the chunk refolded with zero trits skipped): tokens with
-    Inf, -Inf, NaN, subnormal and overflowing inputs, bit-exact against the
-    oracle on those tokens and against ternary_matmul_f32 on x^T (the [K, N]
-    staging, which flags non-finite b when staging it) on every token."""
-    log(f"bit_linear_f32 16x16 non-finite m={m} batch={batch} k={k}")
+    """The kernels that load the layer's token-major input straight into LDS
+    and find Inf/NaN from the sums after each chunk (the chunk refolded with
+    zero trits skipped): the 16 x 16 matrix-core kernel (K a multiple of 4)
+    and the row-broadcast kernel in 64-, 32- and 16-column tiles (7, 2 and 2
+    rows per lane; partial last chunks).  Tokens with Inf, -Inf, NaN,
+    subnormal and overflowing inputs, bit-exact against the oracle on those
+    tokens and against ternary_matmul_f32 on x^T (other staging) on every
+    token."""
+    log(f"bit_linear_f32 LDS-loaded input, non-finite m={m} batch={batch} k={k}")
     p = raw_packed(m, k, 3 * m + k)
     sa = normal((m,), 90, 1.0, 0.1)
     bias = normal((m,), 91)
